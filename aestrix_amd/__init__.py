@@ -1,0 +1,27 @@
+"""aestrix_amd -- MI355X-native (gfx950) MLX-format affine 4-bit quantized linear.
+
+The hot path of the reference's FLUX.2 klein runtime: quantized Linear layers
+with uint32 words of eight low-nibble-first 4-bit codes, one bf16 (scale, bias)
+per 64 K elements, w = scale * q + bias.  Three hand-written HIP kernels behind
+the C ABI of ``include/imq.h`` (``aestrix_amd/libimq.so``):
+
+* ``dequantize``        -- standalone, bit-exact, HBM-bound
+* ``qgemv``             -- M <= 16, register dequant, no MFMA, HBM-bound
+* ``qgemm``             -- dense M, dequant fused into bf16 MFMA tiles
+
+``quantized_matmul`` dispatches between the two matmul regimes.
+"""
+
+from ._lib import ImqError, ImqInvalid, ImqLibraryMissing, ImqUnsupported  # noqa: F401
+from .ops import (  # noqa: F401
+    BITS,
+    GROUP_SIZE,
+    Q,
+    QuantizedLinear,
+    context,
+    dequantize,
+    qgemm,
+    qgemv,
+    qmm,
+    quantized_matmul,
+)

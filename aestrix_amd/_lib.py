@@ -1,0 +1,102 @@
+"""ctypes binding of the C ABI in ``include/imq.h`` (``aestrix_amd/libimq.so``).
+
+The library is built in-tree by ``aestrix_amd/build.py``.  Loading never
+builds and never falls back: a missing library raises ``ImqLibraryMissing``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "libimq.so")
+
+IMQ_OK = 0
+IMQ_EINVAL = 1
+IMQ_EUNSUPPORTED = 2
+IMQ_EHIP = 3
+IMQ_ENOMEM = 4
+
+IMQ_BF16 = 0
+IMQ_F16 = 1
+IMQ_F32 = 2
+
+# Every entry point the header declares, with its ctypes signature.
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_sz = ctypes.c_size_t
+_QMM = [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]
+SIGNATURES = {
+    "imq_abi_version": ([], _i),
+    "imq_status_string": ([_i], ctypes.c_char_p),
+    "imq_create": ([_i, ctypes.POINTER(_p)], _i),
+    "imq_destroy": ([_p], _i),
+    "imq_last_error": ([_p], ctypes.c_char_p),
+    "imq_stream_create": ([_p, ctypes.POINTER(_p)], _i),
+    "imq_stream_destroy": ([_p, _p], _i),
+    "imq_stream_sync": ([_p, _p], _i),
+    "imq_malloc": ([_p, _sz, ctypes.POINTER(_p)], _i),
+    "imq_free": ([_p, _p], _i),
+    "imq_memcpy_h2d": ([_p, _p, _p, _sz, _p], _i),
+    "imq_memcpy_d2h": ([_p, _p, _p, _sz, _p], _i),
+    "imq_dequantize": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
+    "imq_qmm_t": (_QMM, _i),
+    "imq_qgemv": (_QMM, _i),
+    "imq_qgemm": (_QMM, _i),
+}
+
+
+class ImqLibraryMissing(RuntimeError):
+    """libimq.so is not built; run ``python -m aestrix_amd.build``."""
+
+
+class ImqError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{_status_name(status)}: {message}")
+        self.status = status
+
+
+class ImqInvalid(ImqError, ValueError):
+    pass
+
+
+class ImqUnsupported(ImqError, NotImplementedError):
+    pass
+
+
+def _status_name(status: int) -> str:
+    return {0: "IMQ_OK", 1: "IMQ_EINVAL", 2: "IMQ_EUNSUPPORTED", 3: "IMQ_EHIP",
+            4: "IMQ_ENOMEM"}.get(status, f"status {status}")
+
+
+_lib = None
+
+
+def load():
+    """Load libimq.so (no compute call is made)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImqLibraryMissing(
+                f"{LIB_PATH} is not built; run `python -m aestrix_amd.build` "
+                "(there is no CPU fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (argtypes, restype) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
+        _lib = L
+    return _lib
+
+
+def check(status: int, ctx) -> None:
+    if status == IMQ_OK:
+        return
+    msg = load().imq_last_error(ctx)
+    text = msg.decode() if msg else ""
+    if status == IMQ_EINVAL:
+        raise ImqInvalid(status, text)
+    if status == IMQ_EUNSUPPORTED:
+        raise ImqUnsupported(status, text)
+    raise ImqError(status, text)

@@ -1,0 +1,258 @@
+// capi.cpp -- the C ABI of include/imq.h over the gfx950 kernels.
+//
+// Error conventions follow the reference's engine: misuse is reported, never
+// crashes (the reference throws SpikeError.missingTensor / .metal,
+// Sources/ImarelloDirect/DirectQmmSpike.swift:17-19, and checks the command
+// buffer error after the wait, Sources/ImarelloDirect/DirectDiTStep.swift:968-970).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <new>
+#include <string>
+
+#include "imq.h"
+#include "imq_kernels.hpp"
+
+struct imq_ctx {
+  int device = 0;
+  mutable std::mutex mu;
+  std::string err;
+};
+
+namespace {
+
+thread_local std::string g_create_error;  // failures before a context exists
+
+int fail(imq_ctx* ctx, int status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (ctx) {
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    ctx->err = buf;
+  } else {
+    g_create_error = buf;
+  }
+  return status;
+}
+
+int hip_fail(imq_ctx* ctx, hipError_t e, const char* what) {
+  return fail(ctx, IMQ_EHIP, "%s: %s (hipError %d)", what, hipGetErrorString(e), (int)e);
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int bind_device(imq_ctx* ctx) {
+  const hipError_t e = hipSetDevice(ctx->device);
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, "hipSetDevice");
+}
+
+// Shared validation of the quantized-matmul entry points.
+int check_qmm(imq_ctx* ctx, const char* fn, const uint32_t* w, const void* s, const void* b,
+              const void* x, void* y, int k, int n, int m, int group_size, int bits,
+              imq_dtype dtype) {
+  if (!ctx) return fail(nullptr, IMQ_EINVAL, "%s: null context", fn);
+  if (!w || !s || !b || !x || !y)
+    return fail(ctx, IMQ_EINVAL, "%s: null device pointer (w=%p scales=%p biases=%p x=%p y=%p)",
+                fn, (const void*)w, s, b, x, y);
+  if (group_size != 64)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: group_size %d (only 64 is provided)", fn, group_size);
+  if (bits != 4) return fail(ctx, IMQ_EUNSUPPORTED, "%s: bits %d (only 4 is provided)", fn, bits);
+  if (dtype != IMQ_BF16)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: dtype %d (bf16 is provided)", fn, (int)dtype);
+  if (k <= 0 || n <= 0 || m <= 0)
+    return fail(ctx, IMQ_EINVAL, "%s: non-positive shape K=%d N=%d M=%d", fn, k, n, m);
+  if (k % 64 != 0)
+    return fail(ctx, IMQ_EINVAL, "%s: K=%d is not a multiple of the group size 64", fn, k);
+  if (!aligned(w, 16) || !aligned(x, 16))
+    return fail(ctx, IMQ_EINVAL, "%s: w and x must be 16-byte aligned", fn);
+  if (!aligned(s, 2) || !aligned(b, 2) || !aligned(y, 2))
+    return fail(ctx, IMQ_EINVAL, "%s: scales, biases and y must be 2-byte aligned", fn);
+  return IMQ_OK;
+}
+
+enum class Regime { kAuto, kGemv, kGemm };
+
+int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, const void* s,
+            const void* b, const void* x, void* y, int k, int n, int m, int group_size, int bits,
+            imq_dtype dtype, imq_stream stream) {
+  int rc = check_qmm(ctx, fn, w, s, b, x, y, k, n, m, group_size, bits, dtype);
+  if (rc != IMQ_OK) return rc;
+  if (regime == Regime::kGemv && m > imq::kQgemvMaxM)
+    return fail(ctx, IMQ_EINVAL, "%s: M=%d exceeds the qGEMV limit %d", fn, m, imq::kQgemvMaxM);
+  if ((rc = bind_device(ctx)) != IMQ_OK) return rc;
+  const bool gemv = regime == Regime::kGemv || (regime == Regime::kAuto && m <= imq::kQgemvMaxM);
+  const auto* s16 = static_cast<const uint16_t*>(s);
+  const auto* b16 = static_cast<const uint16_t*>(b);
+  const auto* x16 = static_cast<const uint16_t*>(x);
+  auto* y16 = static_cast<uint16_t*>(y);
+  auto st = static_cast<hipStream_t>(stream);
+  const hipError_t e = gemv ? imq::launch_qgemv(w, s16, b16, x16, y16, k, n, m, st)
+                            : imq::launch_qgemm(w, s16, b16, x16, y16, k, n, m, st);
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int imq_abi_version(void) { return IMQ_ABI_VERSION; }
+
+const char* imq_status_string(int status) {
+  switch (status) {
+    case IMQ_OK: return "IMQ_OK";
+    case IMQ_EINVAL: return "IMQ_EINVAL";
+    case IMQ_EUNSUPPORTED: return "IMQ_EUNSUPPORTED";
+    case IMQ_EHIP: return "IMQ_EHIP";
+    case IMQ_ENOMEM: return "IMQ_ENOMEM";
+    default: return "IMQ_UNKNOWN";
+  }
+}
+
+int imq_create(int device, imq_ctx** out) {
+  if (!out) return fail(nullptr, IMQ_EINVAL, "imq_create: null output pointer");
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "imq_create: hipGetDeviceCount");
+  if (device < 0 || device >= count)
+    return fail(nullptr, IMQ_EINVAL, "imq_create: device %d out of range [0, %d)", device, count);
+  auto* c = new (std::nothrow) imq_ctx;
+  if (!c) return fail(nullptr, IMQ_ENOMEM, "imq_create: out of host memory");
+  c->device = device;
+  *out = c;
+  return IMQ_OK;
+}
+
+int imq_destroy(imq_ctx* ctx) {
+  delete ctx;
+  return IMQ_OK;
+}
+
+const char* imq_last_error(const imq_ctx* ctx) {
+  if (!ctx) return g_create_error.c_str();
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  return ctx->err.c_str();
+}
+
+int imq_stream_create(imq_ctx* ctx, imq_stream* out) {
+  if (!ctx || !out) return fail(ctx, IMQ_EINVAL, "imq_stream_create: null argument");
+  int rc = bind_device(ctx);
+  if (rc != IMQ_OK) return rc;
+  hipStream_t s = nullptr;
+  const hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e != hipSuccess) return hip_fail(ctx, e, "imq_stream_create");
+  *out = static_cast<imq_stream>(s);
+  return IMQ_OK;
+}
+
+int imq_stream_destroy(imq_ctx* ctx, imq_stream stream) {
+  if (!ctx) return fail(nullptr, IMQ_EINVAL, "imq_stream_destroy: null context");
+  if (!stream) return IMQ_OK;
+  const hipError_t e = hipStreamDestroy(static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, "imq_stream_destroy");
+}
+
+int imq_stream_sync(imq_ctx* ctx, imq_stream stream) {
+  if (!ctx) return fail(nullptr, IMQ_EINVAL, "imq_stream_sync: null context");
+  int rc = bind_device(ctx);
+  if (rc != IMQ_OK) return rc;
+  const hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, "imq_stream_sync");
+}
+
+int imq_malloc(imq_ctx* ctx, size_t bytes, void** out) {
+  if (!ctx || !out) return fail(ctx, IMQ_EINVAL, "imq_malloc: null argument");
+  *out = nullptr;
+  int rc = bind_device(ctx);
+  if (rc != IMQ_OK) return rc;
+  const hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+  if (e == hipErrorOutOfMemory)
+    return fail(ctx, IMQ_ENOMEM, "imq_malloc: %zu bytes: out of device memory", bytes);
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, "imq_malloc");
+}
+
+int imq_free(imq_ctx* ctx, void* ptr) {
+  if (!ctx) return fail(nullptr, IMQ_EINVAL, "imq_free: null context");
+  if (!ptr) return IMQ_OK;
+  int rc = bind_device(ctx);
+  if (rc != IMQ_OK) return rc;
+  const hipError_t e = hipFree(ptr);
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, "imq_free");
+}
+
+static int copy(imq_ctx* ctx, const char* fn, void* dst, const void* src, size_t bytes,
+                hipMemcpyKind kind, imq_stream stream) {
+  if (!ctx) return fail(nullptr, IMQ_EINVAL, "%s: null context", fn);
+  if (bytes == 0) return IMQ_OK;
+  if (!dst || !src) return fail(ctx, IMQ_EINVAL, "%s: null pointer", fn);
+  int rc = bind_device(ctx);
+  if (rc != IMQ_OK) return rc;
+  const hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
+}
+
+int imq_memcpy_h2d(imq_ctx* ctx, void* dst, const void* src, size_t bytes, imq_stream stream) {
+  return copy(ctx, "imq_memcpy_h2d", dst, src, bytes, hipMemcpyHostToDevice, stream);
+}
+
+int imq_memcpy_d2h(imq_ctx* ctx, void* dst, const void* src, size_t bytes, imq_stream stream) {
+  return copy(ctx, "imq_memcpy_d2h", dst, src, bytes, hipMemcpyDeviceToHost, stream);
+}
+
+int imq_dequantize(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                   void* out, int k, int n, int group_size, int bits, imq_dtype dtype,
+                   imq_stream stream) {
+  const char* fn = "imq_dequantize";
+  if (!ctx) return fail(nullptr, IMQ_EINVAL, "%s: null context", fn);
+  if (!w || !scales || !biases || !out)
+    return fail(ctx, IMQ_EINVAL, "%s: null device pointer", fn);
+  if (group_size != 64)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: group_size %d (only 64 is provided)", fn, group_size);
+  if (bits != 4) return fail(ctx, IMQ_EUNSUPPORTED, "%s: bits %d (only 4 is provided)", fn, bits);
+  if (dtype != IMQ_BF16 && dtype != IMQ_F16)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: dtype %d (bf16 and f16 are provided)", fn,
+                (int)dtype);
+  if (k <= 0 || n <= 0)
+    return fail(ctx, IMQ_EINVAL, "%s: non-positive shape K=%d N=%d", fn, k, n);
+  if (k % 64 != 0)
+    return fail(ctx, IMQ_EINVAL, "%s: K=%d is not a multiple of the group size 64", fn, k);
+  if (!aligned(w, 16) || !aligned(out, 16))
+    return fail(ctx, IMQ_EINVAL, "%s: w and out must be 16-byte aligned", fn);
+  if (!aligned(scales, 2) || !aligned(biases, 2))
+    return fail(ctx, IMQ_EINVAL, "%s: scales and biases must be 2-byte aligned", fn);
+  int rc = bind_device(ctx);
+  if (rc != IMQ_OK) return rc;
+  const hipError_t e = imq::launch_dequant(w, static_cast<const uint16_t*>(scales),
+                                           static_cast<const uint16_t*>(biases),
+                                           static_cast<uint16_t*>(out), k, n, dtype == IMQ_F16,
+                                           static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
+}
+
+int imq_qmm_t(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+              const void* x, void* y, int k, int n, int m, int group_size, int bits,
+              imq_dtype dtype, imq_stream stream) {
+  return run_qmm(ctx, "imq_qmm_t", Regime::kAuto, w, scales, biases, x, y, k, n, m, group_size,
+                 bits, dtype, stream);
+}
+
+int imq_qgemv(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+              const void* x, void* y, int k, int n, int m, int group_size, int bits,
+              imq_dtype dtype, imq_stream stream) {
+  return run_qmm(ctx, "imq_qgemv", Regime::kGemv, w, scales, biases, x, y, k, n, m, group_size,
+                 bits, dtype, stream);
+}
+
+int imq_qgemm(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+              const void* x, void* y, int k, int n, int m, int group_size, int bits,
+              imq_dtype dtype, imq_stream stream) {
+  return run_qmm(ctx, "imq_qgemm", Regime::kGemm, w, scales, biases, x, y, k, n, m, group_size,
+                 bits, dtype, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,78 @@
+// imq_device.hpp -- device helpers shared by the gfx950 kernels.
+//
+// Format: uint32 words of eight 4-bit codes, low nibble first; one bf16
+// (scale, bias) pair per 64 consecutive K elements of a row;
+// w = RNE_bf16(fl32(scale * q + bias))
+// (Sources/ImarelloDirect/DirectTEEncoder.swift:39-46,106-123).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace imq {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kGroup = 64;  // quantization group along K
+constexpr int kPack = 8;    // codes per uint32 word
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// RNE f32 -> bf16 by the integer formula of DirectTEEncoder.swift:39-43
+// (wrapping add, no NaN special case).  Used where results must be
+// bit-identical to that formula for every input pattern (the dequantize kernel).
+__device__ __forceinline__ uint32_t f32_to_bf16_int(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Hardware RNE pack of two floats into a bf16 pair (v_cvt_pk_bf16_f32):
+// identical to f32_to_bf16_int for every non-NaN input (finite, +-inf and
+// overflow-to-inf alike); NaN inputs become a quiet NaN instead of the
+// integer formula's wrapped pattern.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2_t p;
+  p[0] = (__bf16)lo;
+  p[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, p);
+}
+
+// A 16-bit lane of a dword holding a 4-bit code c at bit position 0 (or 4) is
+// the f16 subnormal c * 2^-24 (or c * 2^-20), exactly.  Decoding with a scale
+// pre-multiplied by 2^24 (or 2^20) gives fma(s', c * 2^-24, b) == fl32(s*c + b):
+// the power-of-two rescale is exact and the fma rounds once, like the
+// reference's `scale * q + bias` (s*q itself is exact in f32).  hipcc turns the
+// f16 -> f32 conversion + fma into one v_fma_mix_f32.
+__device__ __forceinline__ float f16_lo(uint32_t d) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(d & 0xFFFFu));
+}
+__device__ __forceinline__ float f16_hi(uint32_t d) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(d >> 16));
+}
+
+// Dequantize one packed word (codes k..k+7) to four bf16 pairs
+// out[p] = (w[2p], w[2p+1]) in k order.  s24 = scale * 2^24, s20 = scale * 2^20.
+__device__ __forceinline__ void dequant_word_bf16(uint32_t word, float s24, float s20, float b,
+                                                  uint32_t out[4]) {
+  const uint32_t d0 = word & 0x000F000Fu;   // codes 0 (lo) and 4 (hi), at bit 0
+  const uint32_t d1 = word & 0x00F000F0u;   // codes 1 and 5, at bit 4
+  const uint32_t w8 = word >> 8;
+  const uint32_t d2 = w8 & 0x000F000Fu;     // codes 2 and 6
+  const uint32_t d3 = w8 & 0x00F000F0u;     // codes 3 and 7
+  out[0] = pack_bf16x2(__builtin_fmaf(s24, f16_lo(d0), b), __builtin_fmaf(s20, f16_lo(d1), b));
+  out[1] = pack_bf16x2(__builtin_fmaf(s24, f16_lo(d2), b), __builtin_fmaf(s20, f16_lo(d3), b));
+  out[2] = pack_bf16x2(__builtin_fmaf(s24, f16_hi(d0), b), __builtin_fmaf(s20, f16_hi(d1), b));
+  out[3] = pack_bf16x2(__builtin_fmaf(s24, f16_hi(d2), b), __builtin_fmaf(s20, f16_hi(d3), b));
+}
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
+
+}  // namespace imq

@@ -1,0 +1,212 @@
+"""torch-facing mirror of the reference's quantized-linear operator surface.
+
+The reference reaches the path through MLX ops and its direct engine:
+
+* ``dequantized(w, scales:, biases:, groupSize: 64, bits: 4)``
+  (``Sources/ImarelloDirect/DirectTEEncoder.swift:129-134``)      -> ``dequantize``
+* ``quantizedMM(x, w, scales:, biases:, transpose: true, groupSize: 64, bits: 4)``
+  (``Sources/ImarelloDiT/AttentionUtils.swift:212-221``,
+  ``Sources/ImarelloDirect/DirectQmmSpike.swift:55-58``)          -> ``quantized_matmul``
+* ``QuantizedLinear`` built by ``quantize(model:groupSize:64,bits:4)``
+  (``Sources/ImarelloDiT/TransformerWeights.swift:20``)            -> ``QuantizedLinear``
+* ``DirectDiTStep.qmm(enc, q, x:, xOff:, y:, yOff:, m:)``
+  (``Sources/ImarelloDirect/DirectDiTStep.swift:374-406``)         -> ``qmm``
+
+Every call goes through the C ABI of ``libimq.so`` on torch's current HIP
+stream.  torch is used for device memory and streams only; there is no
+CPU or torch fallback for any computation.
+
+Tensors: packed weights are ``torch.int32`` (or ``torch.uint32``) ``[N, K/8]``
+holding the raw uint32 words; scales, biases, x and y share one dtype
+(bfloat16, or float16 for dequantize).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+GROUP_SIZE = 64
+BITS = 4
+
+_ctx_lock = threading.Lock()
+_ctxs: dict[int, ctypes.c_void_p] = {}
+
+_DTYPES = {torch.bfloat16: _lib.IMQ_BF16, torch.float16: _lib.IMQ_F16,
+           torch.float32: _lib.IMQ_F32}
+_WORD_DTYPES = (torch.int32,) + ((torch.uint32,) if hasattr(torch, "uint32") else ())
+
+
+def context(device: int | torch.device | None = None) -> ctypes.c_void_p:
+    """The library context of a HIP device (created once, kept for the process)."""
+    if device is None:
+        device = torch.cuda.current_device()
+    idx = torch.device("cuda", device).index if not isinstance(device, int) else device
+    if idx is None:
+        idx = torch.cuda.current_device()
+    with _ctx_lock:
+        ctx = _ctxs.get(idx)
+        if ctx is None:
+            L = _lib.load()
+            out = ctypes.c_void_p()
+            _lib.check(L.imq_create(idx, ctypes.byref(out)), None)
+            ctx = out
+            _ctxs[idx] = ctx
+        return ctx
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _check_weight(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                  group_size: int, bits: int) -> tuple[int, int]:
+    _require(w.is_cuda and scales.is_cuda and biases.is_cuda, "tensors must be on a HIP device")
+    _require(w.dtype in _WORD_DTYPES, f"packed weight must be int32/uint32 words, got {w.dtype}")
+    _require(w.dim() == 2 and scales.dim() == 2 and biases.dim() == 2,
+             "w, scales and biases must be 2-D")
+    _require(w.is_contiguous() and scales.is_contiguous() and biases.is_contiguous(),
+             "w, scales and biases must be contiguous")
+    _require(scales.dtype == biases.dtype, "scales and biases must share a dtype")
+    if group_size != GROUP_SIZE or bits != BITS:
+        # the same answer the C ABI gives (IMQ_EUNSUPPORTED)
+        raise _lib.ImqUnsupported(_lib.IMQ_EUNSUPPORTED,
+                                  f"group_size={group_size} bits={bits}: only 64 / 4 are provided")
+    n, k = w.shape[0], w.shape[1] * 8
+    _require(tuple(scales.shape) == (n, k // GROUP_SIZE) and scales.shape == biases.shape,
+             f"scales/biases must be [{n}, {k // GROUP_SIZE}] for w {tuple(w.shape)}, "
+             f"got {tuple(scales.shape)} / {tuple(biases.shape)}")
+    return n, k
+
+
+def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+               group_size: int = GROUP_SIZE, bits: int = BITS,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """deq(W) [N, K] in the scales' dtype: RNE(fl32(scale * q + bias)), bit-exact."""
+    n, k = _check_weight(w, scales, biases, group_size, bits)
+    if out is None:
+        out = torch.empty((n, k), dtype=scales.dtype, device=w.device)
+    _require(out.is_contiguous() and tuple(out.shape) == (n, k) and out.dtype == scales.dtype,
+             "out must be a contiguous [N, K] tensor of the scales' dtype")
+    dtype = _DTYPES.get(scales.dtype, -1)
+    ctx = context(w.device)
+    with torch.cuda.device(w.device):
+        st = _lib.load().imq_dequantize(ctx, _ptr(w), _ptr(scales), _ptr(biases), _ptr(out),
+                                        k, n, group_size, bits, dtype, _stream(w))
+    _lib.check(st, ctx)
+    return out
+
+
+def _qmm_call(entry: str, x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+              biases: torch.Tensor, group_size: int, bits: int,
+              out: torch.Tensor | None) -> torch.Tensor:
+    n, k = _check_weight(w, scales, biases, group_size, bits)
+    _require(x.is_cuda and x.device == w.device, "x must be on the weight's device")
+    _require(x.dim() >= 1 and x.shape[-1] == k, f"x's last dim must be K={k}, got {tuple(x.shape)}")
+    _require(x.dtype == scales.dtype, f"x ({x.dtype}) and scales ({scales.dtype}) must share T")
+    lead = tuple(x.shape[:-1])
+    m = 1
+    for d in lead:
+        m *= d
+    if not x.is_contiguous():
+        x = x.contiguous()
+    if out is None:
+        out = torch.empty(lead + (n,), dtype=x.dtype, device=x.device)
+    _require(out.is_contiguous() and tuple(out.shape) == lead + (n,) and out.dtype == x.dtype,
+             "out must be a contiguous [..., N] tensor of x's dtype")
+    if m == 0:
+        return out
+    dtype = _DTYPES.get(x.dtype, -1)
+    ctx = context(w.device)
+    with torch.cuda.device(w.device):
+        st = getattr(_lib.load(), entry)(ctx, _ptr(w), _ptr(scales), _ptr(biases), _ptr(x),
+                                         _ptr(out), k, n, m, group_size, bits, dtype, _stream(x))
+    _lib.check(st, ctx)
+    return out
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                     biases: torch.Tensor, transpose: bool = True,
+                     group_size: int = GROUP_SIZE, bits: int = BITS,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """y[..., N] = x[..., K] . deq(W)^T (MLX quantizedMM with transpose=true).
+
+    M <= 16 rows run the qGEMV kernel, larger M the MFMA qGEMM kernel."""
+    if not transpose:
+        raise NotImplementedError("only transpose=true (y = x . deq(w)^T) is on the path")
+    return _qmm_call("imq_qmm_t", x, w, scales, biases, group_size, bits, out)
+
+
+def qgemv(x, w, scales, biases, group_size: int = GROUP_SIZE, bits: int = BITS, out=None):
+    """The skinny-M kernel alone (1 <= M <= 16)."""
+    return _qmm_call("imq_qgemv", x, w, scales, biases, group_size, bits, out)
+
+
+def qgemm(x, w, scales, biases, group_size: int = GROUP_SIZE, bits: int = BITS, out=None):
+    """The MFMA kernel alone (any M)."""
+    return _qmm_call("imq_qgemm", x, w, scales, biases, group_size, bits, out)
+
+
+@dataclass
+class Q:
+    """A resident packed projection, the reference's ``Q(w:s:b:n:k:)``
+    (``Sources/ImarelloDirect/DirectDiTStep.swift:278-284``)."""
+
+    w: torch.Tensor
+    s: torch.Tensor
+    b: torch.Tensor
+    n: int
+    k: int
+
+
+def qmm(q: Q, x: torch.Tensor, x_off: int, y: torch.Tensor, y_off: int, m: int) -> None:
+    """``DirectDiTStep.qmm``: y rows [y_off, y_off + m) = x rows [x_off, x_off + m) . deq(W)^T.
+
+    The reference binds x and y with byte offsets (row halves,
+    ``DirectDiTStep.swift:573-580,597-611``); here offsets are in rows of the
+    2-D buffers x [*, K] and y [*, N]."""
+    _require(x.dim() == 2 and y.dim() == 2 and x.shape[1] == q.k and y.shape[1] == q.n,
+             "x must be [*, K] and y [*, N]")
+    _require(0 <= x_off and x_off + m <= x.shape[0] and 0 <= y_off and y_off + m <= y.shape[0],
+             "row range out of bounds")
+    quantized_matmul(x[x_off:x_off + m], q.w, q.s, q.b, out=y[y_off:y_off + m])
+
+
+class QuantizedLinear:
+    """Bias-free affine 4-bit Linear (every Linear on the path is bias-free,
+    ``Sources/ImarelloDiT/AttentionUtils.swift:223-228``); forward = quantized_matmul."""
+
+    def __init__(self, weight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                 group_size: int = GROUP_SIZE, bits: int = BITS):
+        _check_weight(weight, scales, biases, group_size, bits)
+        self.weight, self.scales, self.biases = weight, scales, biases
+        self.group_size, self.bits = group_size, bits
+
+    @property
+    def in_features(self) -> int:
+        return self.weight.shape[1] * 8
+
+    @property
+    def out_features(self) -> int:
+        return self.weight.shape[0]
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        return quantized_matmul(x, self.weight, self.scales, self.biases, True,
+                                self.group_size, self.bits)
+
+    def dequantized(self) -> torch.Tensor:
+        return dequantize(self.weight, self.scales, self.biases, self.group_size, self.bits)

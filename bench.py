@@ -1,0 +1,285 @@
+"""Benchmark of the affine 4-bit quantized linear path on one MI355X.
+
+Prints ONE JSON line.  The headline ("value") is the qGEMM throughput in
+TFLOP/s at M=4608, K=3072, N=18432 (the DiT MLP-in projection at 1024^2,
+bf16 activations, 4-bit group-64 weights); one "step" is one qGEMM launch
+over that synthetic batch, inputs resident in HBM.  The same line carries:
+
+* roofline   -- the qGEMM against the dense bf16 MFMA peak (2.5 PFLOP/s);
+* qgemv      -- M=1/4/16 on the text-encoder MLP shapes [9728x2560] and
+                [2560x9728], GB/s of algorithmic bytes against 8 TB/s, with the
+                weights rotated over enough copies to miss the 256 MB MALL;
+* dequant    -- the two projections of a DiT single-stream block, GB/s;
+* qgemm_shapes -- the other qGEMM shapes (PR1 1024x9216x3072, single-block
+                pair);
+* cpu_baseline -- the C oracle's f32-accumulating CPU quantized matmul
+                (MLX is not available) on a bounded sample of the same problem.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "4-bit qGEMM TFLOP/s (% MFMA peak) at M=4608; qGEMV GB/s (% HBM) at M=1"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+TARGET = (4608, 18432, 3072)  # M, N, K
+
+
+def qmm_bytes(m: int, n: int, k: int) -> int:
+    """Algorithmic bytes of one call: bf16 x and y, packed W, bf16 scales+biases."""
+    return 2 * m * k + n * k // 2 + 4 * n * k // 64 + 2 * m * n
+
+
+def dequant_bytes(n: int, k: int) -> int:
+    return n * k // 2 + 4 * n * k // 64 + 2 * n * k
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_events(fn, reps: int) -> float:
+    """Average milliseconds per fn() over reps back-to-back calls (HIP events on
+    torch's current stream, the stream the library launches on)."""
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def time_graph(launches, replays: int = 5) -> float:
+    """Average milliseconds per launch of a captured back-to-back sequence."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in launches:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in launches:
+            f()
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (replays * len(launches))
+
+
+def bench_qgemv(imq, synth, torch, copies: int = 48) -> dict:
+    out = {}
+    for (n, k) in ((9728, 2560), (2560, 9728)):
+        p = synth.make_problem(16, n, k, seed=0)
+        x, w, s, b = synth.to_device(p)
+        ws = [w.clone() for _ in range(copies)]
+        ss = [s.clone() for _ in range(copies)]
+        bs = [b.clone() for _ in range(copies)]
+        del w, s, b
+        for m in (1, 4, 16):
+            xm = x[:m].contiguous()
+            ys = [torch.empty((m, n), dtype=torch.bfloat16, device="cuda") for _ in range(copies)]
+            launches = [(lambda i=i: imq.qgemv(xm, ws[i], ss[i], bs[i], out=ys[i]))
+                        for i in range(copies)]
+            ms = time_graph(launches)
+            byts = qmm_bytes(m, n, k)
+            gbs = byts / (ms * 1e-3) / 1e9
+            out[f"M{m}_N{n}_K{k}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                                      "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts}
+            log(f"qgemv M={m} N={n} K={k}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
+        del ws, ss, bs
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_dequant(imq, synth, torch, copies: int = 6) -> dict:
+    out = {}
+    for (n, k) in ((27648, 3072), (3072, 12288)):
+        p = synth.make_problem(0, n, k, seed=1)
+        _, w, s, b = synth.to_device(p)
+        ws = [w.clone() for _ in range(copies)]
+        ss = [s.clone() for _ in range(copies)]
+        bs = [b.clone() for _ in range(copies)]
+        o = torch.empty((n, k), dtype=torch.bfloat16, device="cuda")
+        launches = [(lambda i=i: imq.dequantize(ws[i], ss[i], bs[i], out=o)) for i in range(copies)]
+        ms = time_graph(launches, replays=4)
+        byts = dequant_bytes(n, k)
+        gbs = byts / (ms * 1e-3) / 1e9
+        out[f"N{n}_K{k}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                             "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts}
+        log(f"dequant N={n} K={k}: {ms * 1e3:.1f} us  {gbs:.0f} GB/s")
+        del ws, ss, bs, o
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_qgemm_shape(imq, synth, torch, m, n, k, reps=10) -> dict:
+    p = synth.make_problem(m, n, k, seed=0)
+    x, w, s, b = synth.to_device(p)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    for _ in range(2):
+        imq.qgemm(x, w, s, b, out=y)
+    ms = time_events(lambda: imq.qgemm(x, w, s, b, out=y), reps)
+    tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    log(f"qgemm M={m} N={n} K={k}: {ms:.3f} ms  {tf:.1f} TFLOP/s")
+    return {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / PEAK_BF16_TFLOPS, 4)}
+
+
+def cpu_baseline(synth, seconds: float = 10.0) -> dict:
+    """The C oracle's f32-accumulating CPU quantized matmul on rows of the
+    target problem, repeated for about `seconds` (MLX is not available)."""
+    import numpy as np
+
+    from oracle import cref
+
+    m, n, k = TARGET
+    rows = 32
+    p = synth.make_problem(rows, n, k, seed=0)
+    threads = cref.max_threads()
+    cref.qmm_t_f32acc(p.x[:2], p.w[:256], p.scales[:256], p.biases[:256])  # warm
+    calls = 0
+    t0 = time.perf_counter()
+    while True:
+        cref.qmm_t_f32acc(p.x, p.w, p.scales, p.biases)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    flop = 2.0 * rows * n * k * calls
+    del np
+    return {"value": round(flop / el / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"MLX-equivalent CPU qmm (MLX unavailable): C oracle, on-the-fly bf16 dequant, "
+                      f"f32 accumulate, bf16 out; {rows} rows x N={n} x K={k} of the seed-0 "
+                      f"target problem, {calls} calls in {el:.1f} s on {threads} OpenMP threads"}
+
+
+def traffic_from_profiles():
+    path = os.path.join(ROOT, "profiles", "qgemm_target_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only-target", action="store_true",
+                    help="time the headline qGEMM only (for profiling runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} requested, but this path runs on one GPU "
+              "(no sharding, no collectives); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import aestrix_amd as imq
+    from aestrix_amd import synth
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+    imq._lib.load()
+    props = torch.cuda.get_device_properties(0)
+
+    m, n, k = TARGET
+    log(f"target qgemm M={m} N={n} K={k}")
+    p = synth.make_problem(m, n, k, seed=0)
+    x, w, s, b = synth.to_device(p)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    for _ in range(args.warmup):
+        imq.quantized_matmul(x, w, s, b, out=y)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        imq.quantized_matmul(x, w, s, b, out=y)
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end) / args.steps
+    flop = 2.0 * m * n * k
+    tflops = flop / (ms * 1e-3) / 1e12
+    log(f"target qgemm: {ms:.4f} ms/step  {tflops:.1f} TFLOP/s  (host wall {wall:.3f} s)")
+    del x, w, s, b, y
+    torch.cuda.empty_cache()
+
+    extra = {}
+    if not args.only_target:
+        extra["qgemv"] = bench_qgemv(imq, synth, torch)
+        extra["dequant"] = bench_dequant(imq, synth, torch)
+        extra["qgemm_shapes"] = {
+            "M1024_N9216_K3072": bench_qgemm_shape(imq, synth, torch, 1024, 9216, 3072),
+            "M4608_N27648_K3072": bench_qgemm_shape(imq, synth, torch, 4608, 27648, 3072),
+            "M4608_N3072_K9216": bench_qgemm_shape(imq, synth, torch, 4608, 3072, 9216),
+        }
+
+    result = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded PCG64: x~N(0,1) bf16, uniform 4-bit codes, "
+                "s=|N(0,0.02)|, b=-8s+N(0,0.002), group 64)",
+        "config": {"workload": "qgemm: y[4608x18432] = x[4608x3072] . deq(W[18432x3072])^T, "
+                               "affine 4-bit group 64, bf16 in/out, fp32 accumulate",
+                   "m": m, "n": n, "k": k, "group_size": 64, "bits": 4},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic_from_profiles()},
+        "device": {"name": props.name, "cus": props.multi_processor_count,
+                   "hip": torch.version.hip},
+    }
+    result.update(extra)
+    if qgemv := extra.get("qgemv"):
+        result["qgemv_headline"] = {"shape": "M=1 [9728x2560]",
+                                    **qgemv["M1_N9728_K2560"]}
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(synth)
+        log(f"cpu baseline: {result['cpu_baseline']['value']} TFLOP/s")
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,127 @@
+/*
+ * imq.h -- C ABI of the MI355X (gfx950) affine 4-bit quantized linear library.
+ *
+ * Drop-in boundary for the quantized-linear hot path of the reference's
+ * direct-dispatch engine (Sources/ImarelloDirect).  The reference binds MLX's
+ * compiled Metal kernel `affine_qmm_t_{T}_gs_64_b_4_alN_true_batch_0` with
+ * buffers w, scales, biases, x, y at indices 0-4 and int32 K, N, M at 5-7
+ * (Sources/ImarelloDirect/DirectQmmSpike.swift:113-128,
+ *  Sources/ImarelloDirect/DirectDiTStep.swift:393-405,
+ *  Sources/ImarelloDirect/DirectTELayer.swift:109-128,
+ *  Sources/ImarelloDirect/DirectConditioner.swift:96-117).
+ * The kernel entry points below keep that argument order and meaning.
+ *
+ * Data format (MLX affine quantization, bits = 4, group_size = 64):
+ *   w       uint32 [N, K/8]  eight 4-bit codes per word, low nibble first
+ *   scales  T      [N, K/64]
+ *   biases  T      [N, K/64]
+ *   deq(W)[n][k] = RNE_T( fl32( scales[n][k/64] * q[n][k] + biases[n][k/64] ) )
+ *   y[M, N]      = x[M, K] . deq(W)^T, accumulated in fp32, rounded to T.
+ * All tensors are row-major and contiguous; sub-tensors (row halves, the
+ * reference's setBuffer byte offsets, DirectDiTStep.swift:576-579) are passed
+ * as offset device pointers.  Every device pointer must be 16-byte aligned.
+ *
+ * Conventions:
+ *   - Every call returns an imq_status (0 = IMQ_OK).  No C++ exception crosses
+ *     the ABI.  The text of the last failure on a context is imq_last_error().
+ *   - Kernel calls are asynchronous on the given stream (NULL = the device's
+ *     null stream).  imq_stream_sync is the blocking wait, the counterpart of
+ *     waitUntilCompleted (DirectDiTStep.swift:968-970).
+ *   - Caller inputs are never written.  Kernels allocate nothing.
+ *   - A context belongs to one device.  Calls on one context from several
+ *     threads are safe; the last-error text is per context.
+ */
+#ifndef IMQ_H
+#define IMQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IMQ_ABI_VERSION 1
+
+typedef enum imq_status {
+    IMQ_OK = 0,
+    IMQ_EINVAL = 1,       /* null/misaligned pointer, bad shape (K % 64 != 0, M/N/K <= 0) */
+    IMQ_EUNSUPPORTED = 2, /* well-formed but not provided: bits != 4, group_size != 64, dtype */
+    IMQ_EHIP = 3,         /* HIP runtime failure; hipGetErrorString text in imq_last_error */
+    IMQ_ENOMEM = 4        /* device or host allocation failed */
+} imq_status;
+
+/* Element type T of x, scales, biases and y ("s and b share T",
+ * DirectQmmSpike.swift:84, DirectConditioner.swift:48-49). */
+typedef enum imq_dtype {
+    IMQ_BF16 = 0, /* the text encoder / context-embedder kernels (DirectTEEncoder.swift:69-72) */
+    IMQ_F16 = 1,  /* the DiT kernels (DirectDiTStep.swift:82-85) */
+    IMQ_F32 = 2   /* the M=1 conditioner kernels (DirectConditioner.swift:48) */
+} imq_dtype;
+
+typedef struct imq_ctx imq_ctx; /* opaque; owns the device binding and error text */
+typedef void* imq_stream;       /* a hipStream_t; NULL = null stream of the context's device */
+
+/* ---- library / context ------------------------------------------------ */
+
+int imq_abi_version(void);
+const char* imq_status_string(int status);
+
+/* Replaces the device/queue setup of DirectDiTStep.init (DirectDiTStep.swift:74-80). */
+int imq_create(int device, imq_ctx** out);
+int imq_destroy(imq_ctx* ctx);
+/* Text of the last failure on ctx ("" if none); valid until the next failing call. */
+const char* imq_last_error(const imq_ctx* ctx);
+
+/* ---- streams (MTLCommandQueue / command buffer counterpart) ------------ */
+
+int imq_stream_create(imq_ctx* ctx, imq_stream* out);
+int imq_stream_destroy(imq_ctx* ctx, imq_stream stream);
+int imq_stream_sync(imq_ctx* ctx, imq_stream stream);
+
+/* ---- memory (the reference's MTLBuffer upload/scratch,
+ *      DirectDiTStep.swift:135-153) ------------------------------------- */
+
+int imq_malloc(imq_ctx* ctx, size_t bytes, void** out);
+int imq_free(imq_ctx* ctx, void* ptr);
+int imq_memcpy_h2d(imq_ctx* ctx, void* dst, const void* src, size_t bytes, imq_stream stream);
+int imq_memcpy_d2h(imq_ctx* ctx, void* dst, const void* src, size_t bytes, imq_stream stream);
+
+/* ---- kernels ------------------------------------------------------------ */
+
+/* out[N, K] (T) = deq(W).  Replaces MLX `dequantized(w, scales:, biases:,
+ * groupSize: 64, bits: 4)` (DirectTEEncoder.swift:129-134) and the CPU
+ * embedding dequant DirectTEEncoder.embedRow (DirectTEEncoder.swift:106-123).
+ * Bit-exact: RNE_T(fl32(s*q + b)), RNE by the integer rounding of
+ * DirectTEEncoder.swift:39-43 for bf16. */
+int imq_dequantize(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                   void* out, int k, int n, int group_size, int bits, imq_dtype dtype,
+                   imq_stream stream);
+
+/* y[M, N] = x[M, K] . deq(W)^T -- the regime dispatcher.  Replaces the
+ * dispatch of `affine_qmm_t_{T}_gs_64_b_4_alN_true_batch_0` in
+ * DirectDiTStep.qmm (DirectDiTStep.swift:374-406), DirectTELayerSpike.encodeQmm
+ * (DirectTELayer.swift:109-128), DirectConditioner.qmm
+ * (DirectConditioner.swift:96-117) and MLX quantizedMM(transpose: true)
+ * (Sources/ImarelloDiT/AttentionUtils.swift:212-221).  M <= 16 runs the qGEMV
+ * kernel, larger M the MFMA qGEMM kernel. */
+int imq_qmm_t(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+              const void* x, void* y, int k, int n, int m, int group_size, int bits,
+              imq_dtype dtype, imq_stream stream);
+
+/* The skinny regime alone (1 <= M <= 16): register dequant, fp32 dot products,
+ * cross-lane reductions; no matrix cores.  Same contract as imq_qmm_t. */
+int imq_qgemv(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+              const void* x, void* y, int k, int n, int m, int group_size, int bits,
+              imq_dtype dtype, imq_stream stream);
+
+/* The dense regime alone (any M >= 1): dequant fused into bf16 MFMA tiles,
+ * fp32 accumulators.  Same contract as imq_qmm_t. */
+int imq_qgemm(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+              const void* x, void* y, int k, int n, int m, int group_size, int bits,
+              imq_dtype dtype, imq_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IMQ_H */

@@ -1,0 +1,113 @@
+"""numpy restatement of the affine 4-bit quantized linear path (test oracle).
+
+TEST INFRASTRUCTURE ONLY -- see the package docstring.  All bf16 values are
+carried as ``uint16`` bit patterns.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+GROUP_SIZE = 64
+BITS = 4
+PACK = 8  # codes per uint32 word
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    """bf16 bits -> float32 (``DirectTEEncoder.swift:44-46``: bits << 16)."""
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(v: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits, RNE by the integer formula of
+    ``DirectTEEncoder.swift:39-43`` (wrapping add, no NaN special case)."""
+    bits = np.asarray(v, dtype=np.float32).view(np.uint32)
+    rounded = bits + np.uint32(0x7FFF) + ((bits >> np.uint32(16)) & np.uint32(1))
+    return (rounded >> np.uint32(16)).astype(np.uint16)
+
+
+def f64_to_bf16(v: np.ndarray) -> np.ndarray:
+    """Correctly rounded float64 -> bf16 (RNE), via round-to-odd at float32."""
+    v = np.asarray(v, dtype=np.float64)
+    f = v.astype(np.float32)
+    bits = f.view(np.uint32).copy()
+    inexact = (f.astype(np.float64) != v) & np.isfinite(v)
+    away = np.abs(f.astype(np.float64)) > np.abs(v)
+    bits = np.where(inexact & away, bits - np.uint32(1), bits)
+    bits = np.where(inexact, bits | np.uint32(1), bits)
+    return f32_to_bf16(bits.view(np.float32))
+
+
+def unpack_codes(w: np.ndarray) -> np.ndarray:
+    """uint32 [N, K/8] -> uint8 codes [N, K]; code k = nibble k%8 of word k/8,
+    low nibble first (``DirectTEEncoder.swift:116-118``)."""
+    w = np.asarray(w, dtype=np.uint32)
+    shifts = (np.arange(PACK, dtype=np.uint32) * np.uint32(4))
+    codes = (w[..., None] >> shifts) & np.uint32(0xF)
+    return codes.reshape(*w.shape[:-1], w.shape[-1] * PACK).astype(np.uint8)
+
+
+def pack_codes(codes: np.ndarray) -> np.ndarray:
+    """uint8 codes [N, K] (values 0..15) -> uint32 [N, K/8], low nibble first."""
+    codes = np.asarray(codes, dtype=np.uint32)
+    n, k = codes.shape
+    assert k % PACK == 0
+    c = codes.reshape(n, k // PACK, PACK)
+    shifts = (np.arange(PACK, dtype=np.uint32) * np.uint32(4))
+    return np.bitwise_or.reduce(c << shifts, axis=-1).astype(np.uint32)
+
+
+def dequantize(w: np.ndarray, scales: np.ndarray, biases: np.ndarray) -> np.ndarray:
+    """bf16 bits [N, K] = RNE_bf16(fl32(s*q + b)) (``DirectTEEncoder.swift:106-123``).
+
+    Two float32 operations, like the reference's ``scale * q + bias`` on Float:
+    the product is exact unless it overflows (then +-inf), the sum rounds once."""
+    q = unpack_codes(w).astype(np.float32)
+    n, k = q.shape
+    assert k % GROUP_SIZE == 0
+    s = np.repeat(bf16_to_f32(scales), GROUP_SIZE, axis=-1).reshape(n, k)
+    b = np.repeat(bf16_to_f32(biases), GROUP_SIZE, axis=-1).reshape(n, k)
+    with np.errstate(over="ignore", invalid="ignore"):
+        return f32_to_bf16(s * q + b)
+
+
+def qmm_t_f64(x: np.ndarray, w: np.ndarray, scales: np.ndarray, biases: np.ndarray) -> np.ndarray:
+    """Unrounded float64 y = x . deq(w)^T with the bit-exact bf16 dequant."""
+    xd = bf16_to_f32(x).astype(np.float64)
+    wd = bf16_to_f32(dequantize(w, scales, biases)).astype(np.float64)
+    return xd @ wd.T
+
+
+def qmm_t(x: np.ndarray, w: np.ndarray, scales: np.ndarray, biases: np.ndarray) -> np.ndarray:
+    """bf16 bits y[M, N] = RNE_bf16(x . deq(w)^T) -- the parity oracle
+    (``DirectQmmSpike.swift:55-58``: quantizedMM with transpose=true)."""
+    return f64_to_bf16(qmm_t_f64(x, w, scales, biases))
+
+
+def qmm_t_f32_dequant_f64(x: np.ndarray, w: np.ndarray, scales: np.ndarray,
+                          biases: np.ndarray) -> np.ndarray:
+    """Unrounded float64 y with the dequant left unrounded (fl32(s*q+b)), for
+    reporting the literal 'fp32 dequant-then-matmul' reading of the tolerance."""
+    q = unpack_codes(w).astype(np.float32)
+    n, k = q.shape
+    s = np.repeat(bf16_to_f32(scales), GROUP_SIZE, axis=-1).reshape(n, k)
+    b = np.repeat(bf16_to_f32(biases), GROUP_SIZE, axis=-1).reshape(n, k)
+    wd = (s * q + b).astype(np.float64)
+    return bf16_to_f32(x).astype(np.float64) @ wd.T
+
+
+def error_stats(y_bits: np.ndarray, oracle_bits: np.ndarray) -> dict:
+    """Tolerance metrics: MAE, normwise max error, floored elementwise error."""
+    y = bf16_to_f32(y_bits).astype(np.float64)
+    o = bf16_to_f32(oracle_bits).astype(np.float64)
+    d = np.abs(y - o)
+    omax = float(np.max(np.abs(o))) if o.size else 0.0
+    rms = float(np.sqrt(np.mean(o * o))) if o.size else 0.0
+    floor = np.maximum(np.abs(o), 1e-3 * rms) if o.size else o
+    return {
+        "mae": float(np.mean(d)) if d.size else 0.0,
+        "max_abs": float(np.max(d)) if d.size else 0.0,
+        "max_rel_normwise": float(np.max(d) / omax) if d.size and omax > 0 else 0.0,
+        "max_rel_floored": float(np.max(d / np.where(floor > 0, floor, 1.0))) if d.size else 0.0,
+        "bit_exact_frac": float(np.mean(y_bits == oracle_bits)) if d.size else 1.0,
+    }

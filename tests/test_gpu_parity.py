@@ -1,0 +1,314 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bars (stated here, applied below):
+* dequantize: bit-exact against RNE_bf16(fl32(fl32(s*q) + b)).
+* qGEMV / qGEMM: against oracle = RNE_bf16(x . deq(W)^T accumulated in double)
+  with the bit-exact bf16 dequant: mean |y - oracle| <= MAE_TOL and
+  max |y - oracle| / max |oracle| <= NORMWISE_TOL.
+* one-hot activations make y a column of deq(W): that must be bit-exact in
+  both matmul kernels (it pins their fused in-register dequantization).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import aestrix_amd as imq
+from aestrix_amd import _lib, ops, synth
+from oracle import cref, ref
+
+pytestmark = pytest.mark.gpu
+
+MAE_TOL = 1e-3
+NORMWISE_TOL = 1e-2
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
+
+
+@pytest.fixture(autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+
+
+def note(msg: str) -> None:
+    print(msg, flush=True)
+
+
+def to_dev_words(w: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(w).view(np.int32)).cuda()
+
+
+def to_dev_bf16(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    torch.cuda.synchronize()
+    return synth.bf16_bits(t)
+
+
+def assert_close(y_bits: np.ndarray, oracle_bits: np.ndarray, what: str) -> dict:
+    st = ref.error_stats(y_bits, oracle_bits)
+    note(f"  {what}: mae={st['mae']:.3g} normwise={st['max_rel_normwise']:.3g} "
+         f"bit_exact={st['bit_exact_frac']:.4f}")
+    assert st["mae"] <= MAE_TOL, (what, st)
+    assert st["max_rel_normwise"] <= NORMWISE_TOL, (what, st)
+    return st
+
+
+# ------------------------------------------------------------------ dequant
+
+
+def test_dequant_golden_bit_exact():
+    d = np.load(GOLDEN)
+    for tag in ("deq", "kat"):
+        note(f"dequant golden {tag}")
+        out = imq.dequantize(to_dev_words(d[f"{tag}_w"]), to_dev_bf16(d[f"{tag}_s"]),
+                             to_dev_bf16(d[f"{tag}_b"]))
+        assert np.array_equal(bits(out), d[f"{tag}_out"])
+
+
+def test_dequant_exact_rational_grid():
+    import test_oracle as t
+
+    note("dequant exact-rational (scale, bias) grid")
+    _, _, w, s, b = t._grid_problem()
+    out = imq.dequantize(to_dev_words(w), to_dev_bf16(s), to_dev_bf16(b))
+    assert np.array_equal(bits(out), t.exact_grid())
+
+
+@pytest.mark.parametrize("n,k", [(27648, 3072), (3072, 12288), (1, 64), (7, 4160)])
+def test_dequant_block_shapes_bit_exact(n, k):
+    note(f"dequant N={n} K={k} seed=11")
+    p = synth.make_problem(0, n, k, seed=11)
+    out = imq.dequantize(to_dev_words(p.w), to_dev_bf16(p.scales), to_dev_bf16(p.biases))
+    got = bits(out)
+    want = cref.dequantize(p.w, p.scales, p.biases)
+    assert np.array_equal(got, want)
+
+
+def test_dequant_f16_bit_exact():
+    note("dequant f16 N=96 K=512")
+    p = synth.make_problem(0, 96, 512, seed=12)
+    s16 = ref.bf16_to_f32(p.scales).astype(np.float16)
+    b16 = ref.bf16_to_f32(p.biases).astype(np.float16)
+    q = ref.unpack_codes(p.w).astype(np.float32)
+    sf = np.repeat(s16.astype(np.float32), 64, axis=1)
+    bf = np.repeat(b16.astype(np.float32), 64, axis=1)
+    want = (sf * q + bf).astype(np.float16)
+    out = imq.dequantize(to_dev_words(p.w), torch.from_numpy(s16).cuda(),
+                         torch.from_numpy(b16).cuda())
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), want.view(np.uint16))
+
+
+# ------------------------------------------------------------ quantized matmul
+
+
+def test_qmm_golden_within_tolerance():
+    d = np.load(GOLDEN)
+    for i, (m, n, k, seed) in enumerate(d["qmm_cases"]):
+        note(f"qmm golden case {i}: M={m} N={n} K={k} seed={seed}")
+        x, w, s, b = (to_dev_bf16(d[f"qmm{i}_x"]), to_dev_words(d[f"qmm{i}_w"]),
+                      to_dev_bf16(d[f"qmm{i}_s"]), to_dev_bf16(d[f"qmm{i}_b"]))
+        for name, fn in (("qmm_t", imq.quantized_matmul), ("qgemm", imq.qgemm)):
+            assert_close(bits(fn(x, w, s, b)), d[f"qmm{i}_y"], f"{name} case {i}")
+        if m <= 16:
+            assert_close(bits(imq.qgemv(x, w, s, b)), d[f"qmm{i}_y"], f"qgemv case {i}")
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
+@pytest.mark.parametrize("n,k", [(9728, 2560), (2560, 9728), (100, 64), (33, 4160), (1000, 768)])
+def test_qgemv_shapes(m, n, k):
+    note(f"qgemv M={m} N={n} K={k} seed=13")
+    p = synth.make_problem(m, n, k, seed=13)
+    x, w, s, b = synth.to_device(p)
+    got = bits(imq.qgemv(x, w, s, b))
+    want = cref.qmm_t(p.x, p.w, p.scales, p.biases)
+    assert_close(got, want, f"qgemv M={m} N={n} K={k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(17, 32, 64), (64, 96, 128), (128, 256, 320), (129, 200, 192),
+                                   (300, 257, 3072), (1, 512, 256), (255, 1000, 640)])
+def test_qgemm_shapes(m, n, k):
+    note(f"qgemm M={m} N={n} K={k} seed=14")
+    p = synth.make_problem(m, n, k, seed=14)
+    x, w, s, b = synth.to_device(p)
+    got = bits(imq.qgemm(x, w, s, b))
+    want = cref.qmm_t(p.x, p.w, p.scales, p.biases)
+    assert_close(got, want, f"qgemm M={m} N={n} K={k}")
+
+
+def _sampled_rows_check(m, n, k, seed, rows=48):
+    note(f"qmm_t M={m} N={n} K={k} seed={seed} (oracle on {rows} sampled rows)")
+    p = synth.make_problem(m, n, k, seed=seed)
+    x, w, s, b = synth.to_device(p)
+    y = imq.quantized_matmul(x, w, s, b)
+    idx = np.unique(np.linspace(0, m - 1, rows).astype(np.int64))
+    got = bits(y)[idx]
+    want = cref.qmm_t(p.x[idx], p.w, p.scales, p.biases)
+    return assert_close(got, want, f"qmm_t M={m} N={n} K={k} rows={len(idx)}")
+
+
+def test_qmm_pr1_shape_sampled_rows():
+    _sampled_rows_check(1024, 9216, 3072, seed=0)
+
+
+def test_qmm_target_shape_sampled_rows():
+    _sampled_rows_check(4608, 18432, 3072, seed=0, rows=32)
+
+
+def test_qmm_single_block_shapes_sampled_rows():
+    _sampled_rows_check(4608, 27648, 3072, seed=1, rows=24)
+    _sampled_rows_check(4608, 3072, 9216, seed=2, rows=48)
+
+
+@pytest.mark.parametrize("fn_name,m,k", [("qgemm", 128, 128), ("qgemm", 40, 3072),
+                                         ("qgemv", 16, 3072), ("qgemv", 1, 2560)])
+def test_one_hot_rows_reproduce_dequant_bit_exact(fn_name, m, k):
+    """x rows are one-hot, so y[i, :] = deq(W)[:, k_i] exactly (products with
+    1.0 and 0.0 and their fp32 sums are exact)."""
+    n = 320
+    note(f"{fn_name} one-hot M={m} N={n} K={k}")
+    p = synth.make_problem(0, n, k, seed=15)
+    rng = np.random.default_rng(15)
+    cols = np.arange(m) if m == k else rng.choice(k, size=m, replace=False)
+    xh = np.zeros((m, k), dtype=np.uint16)
+    xh[np.arange(m), cols] = 0x3F80
+    x, w, s, b = to_dev_bf16(xh), to_dev_words(p.w), to_dev_bf16(p.scales), to_dev_bf16(p.biases)
+    y = bits(getattr(imq, fn_name)(x, w, s, b))
+    deq_gpu = bits(imq.dequantize(w, s, b))
+    assert np.array_equal(y, deq_gpu[:, cols].T)
+
+
+def test_dispatcher_routes_by_m():
+    p = synth.make_problem(17, 384, 512, seed=16)
+    x, w, s, b = synth.to_device(p)
+    for m in (16, 17):
+        note(f"dispatcher M={m}")
+        y = bits(imq.quantized_matmul(x[:m], w, s, b))
+        ref_kernel = imq.qgemv if m <= 16 else imq.qgemm
+        assert np.array_equal(y, bits(ref_kernel(x[:m], w, s, b)))
+
+
+# ----------------------------------------------------------- host interface
+
+
+def test_row_offsets_like_direct_engine():
+    note("qmm with row offsets (row halves)")
+    p = synth.make_problem(64, 256, 384, seed=17)
+    x, w, s, b = synth.to_device(p)
+    q = imq.Q(w=w, s=s, b=b, n=256, k=384)
+    y = torch.zeros((64, 256), dtype=torch.bfloat16, device="cuda")
+    imq.qmm(q, x, 0, y, 0, 32)
+    imq.qmm(q, x, 32, y, 32, 32)
+    want = cref.qmm_t(p.x, p.w, p.scales, p.biases)
+    assert_close(bits(y), want, "row halves")
+
+
+def test_quantized_linear_batched_input():
+    note("QuantizedLinear on [2, 40, K]")
+    p = synth.make_problem(80, 192, 256, seed=18)
+    x, w, s, b = synth.to_device(p)
+    lin = imq.QuantizedLinear(w, s, b)
+    assert lin.in_features == 256 and lin.out_features == 192
+    y = lin(x.view(2, 40, 256))
+    assert tuple(y.shape) == (2, 40, 192)
+    assert_close(bits(y).reshape(80, 192), cref.qmm_t(p.x, p.w, p.scales, p.biases), "3-D input")
+    assert np.array_equal(bits(lin.dequantized()), cref.dequantize(p.w, p.scales, p.biases))
+
+
+def test_runs_on_a_side_stream():
+    note("qgemm on a non-default torch stream")
+    p = synth.make_problem(200, 320, 512, seed=19)
+    x, w, s, b = synth.to_device(p)
+    base = bits(imq.qgemm(x, w, s, b))
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        y = imq.qgemm(x, w, s, b)
+    st.synchronize()
+    assert np.array_equal(bits(y), base)
+
+
+def test_argument_errors_are_reported():
+    p = synth.make_problem(4, 64, 128, seed=20)
+    x, w, s, b = synth.to_device(p)
+    note("error paths")
+    with pytest.raises(NotImplementedError):
+        imq.quantized_matmul(x, w, s, b, group_size=32)
+    with pytest.raises(NotImplementedError):
+        imq.quantized_matmul(x, w, s, b, bits=8)
+    with pytest.raises(NotImplementedError):
+        imq.quantized_matmul(x.float(), w, s.float(), b.float())
+    with pytest.raises(NotImplementedError):
+        imq.quantized_matmul(x, w, s, b, transpose=False)
+    with pytest.raises(ValueError):
+        imq.qgemv(torch.cat([x] * 5), w, s, b)  # M = 20 > 16
+    with pytest.raises(ValueError):
+        imq.quantized_matmul(x[:, :64], w, s, b)  # K mismatch
+    L = _lib.load()
+    ctx = ops.context()
+    y = torch.empty((4, 64), dtype=torch.bfloat16, device="cuda")
+    vp = ctypes.c_void_p
+    args = [vp(w.data_ptr()), vp(s.data_ptr()), vp(b.data_ptr()), vp(x.data_ptr()),
+            vp(y.data_ptr())]
+    st = L.imq_qmm_t(ctx, *args, 100, 64, 4, 64, 4, 0, None)  # K % 64 != 0
+    assert st == _lib.IMQ_EINVAL and b"multiple of the group size" in L.imq_last_error(ctx)
+    bad = list(args)
+    bad[3] = vp(x.data_ptr() + 2)  # misaligned x
+    assert L.imq_qmm_t(ctx, *bad, 128, 64, 4, 64, 4, 0, None) == _lib.IMQ_EINVAL
+    bad = list(args)
+    bad[0] = vp(0)
+    assert L.imq_qmm_t(ctx, *bad, 128, 64, 4, 64, 4, 0, None) == _lib.IMQ_EINVAL
+    assert L.imq_qmm_t(ctx, *args, 128, 64, 0, 64, 4, 0, None) == _lib.IMQ_EINVAL
+    assert L.imq_qmm_t(ctx, *args, 128, 64, 4, 64, 8, 0, None) == _lib.IMQ_EUNSUPPORTED
+    assert L.imq_qmm_t(ctx, *args, 128, 64, 4, 32, 4, 0, None) == _lib.IMQ_EUNSUPPORTED
+    assert L.imq_qgemv(ctx, *args, 128, 64, 17, 64, 4, 0, None) == _lib.IMQ_EINVAL
+    assert L.imq_dequantize(ctx, args[0], args[1], args[2], args[4], 128, 64, 64, 4, 2,
+                            None) == _lib.IMQ_EUNSUPPORTED
+    out = ctypes.c_void_p()
+    assert L.imq_create(10_000, ctypes.byref(out)) == _lib.IMQ_EINVAL
+
+
+def test_pure_c_abi_memory_stream_and_kernel():
+    """Everything through the C ABI: imq_malloc / memcpy / stream / dequant / qmm."""
+    note("pure C-ABI round trip")
+    L = _lib.load()
+    ctx = ops.context()
+    p = synth.make_problem(3, 128, 256, seed=21)
+    stream = ctypes.c_void_p()
+    _lib.check(L.imq_stream_create(ctx, ctypes.byref(stream)), ctx)
+    bufs = {}
+    host = {"w": p.w, "s": p.scales, "b": p.biases, "x": p.x}
+    for name, a in host.items():
+        ptr = ctypes.c_void_p()
+        _lib.check(L.imq_malloc(ctx, a.nbytes, ctypes.byref(ptr)), ctx)
+        _lib.check(L.imq_memcpy_h2d(ctx, ptr, a.ctypes.data_as(ctypes.c_void_p), a.nbytes,
+                                    stream), ctx)
+        bufs[name] = ptr
+    deq = ctypes.c_void_p()
+    y = ctypes.c_void_p()
+    _lib.check(L.imq_malloc(ctx, 128 * 256 * 2, ctypes.byref(deq)), ctx)
+    _lib.check(L.imq_malloc(ctx, 3 * 128 * 2, ctypes.byref(y)), ctx)
+    _lib.check(L.imq_dequantize(ctx, bufs["w"], bufs["s"], bufs["b"], deq, 256, 128, 64, 4,
+                                _lib.IMQ_BF16, stream), ctx)
+    _lib.check(L.imq_qmm_t(ctx, bufs["w"], bufs["s"], bufs["b"], bufs["x"], y, 256, 128, 3, 64,
+                           4, _lib.IMQ_BF16, stream), ctx)
+    deq_h = np.empty((128, 256), dtype=np.uint16)
+    y_h = np.empty((3, 128), dtype=np.uint16)
+    _lib.check(L.imq_memcpy_d2h(ctx, deq_h.ctypes.data_as(ctypes.c_void_p), deq, deq_h.nbytes,
+                                stream), ctx)
+    _lib.check(L.imq_memcpy_d2h(ctx, y_h.ctypes.data_as(ctypes.c_void_p), y, y_h.nbytes,
+                                stream), ctx)
+    _lib.check(L.imq_stream_sync(ctx, stream), ctx)
+    for ptr in list(bufs.values()) + [deq, y]:
+        _lib.check(L.imq_free(ctx, ptr), ctx)
+    _lib.check(L.imq_stream_destroy(ctx, stream), ctx)
+    assert np.array_equal(deq_h, cref.dequantize(p.w, p.scales, p.biases))
+    assert_close(y_h, cref.qmm_t(p.x, p.w, p.scales, p.biases), "pure C ABI qmm")

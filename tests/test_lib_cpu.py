@@ -1,0 +1,73 @@
+"""The C-ABI library loads and exports the header's entry points (no GPU needed).
+
+No kernel is launched here: only symbol lookup, status strings and argument
+checks that fail before any device work.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from aestrix_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "imq.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(imq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_is_built():
+    assert os.path.exists(_lib.LIB_PATH), "run `python -m aestrix_amd.build` first"
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    L = _lib.load()
+    declared = header_functions()
+    assert len(declared) >= 16
+    for name in declared:
+        assert hasattr(L, name), f"{name} declared in imq.h but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(declared)
+
+
+def test_status_strings_and_version():
+    L = _lib.load()
+    assert L.imq_abi_version() == 1
+    assert L.imq_status_string(0) == b"IMQ_OK"
+    assert L.imq_status_string(1) == b"IMQ_EINVAL"
+    assert L.imq_status_string(2) == b"IMQ_EUNSUPPORTED"
+    assert L.imq_status_string(3) == b"IMQ_EHIP"
+    assert L.imq_status_string(4) == b"IMQ_ENOMEM"
+    assert L.imq_status_string(99) == b"IMQ_UNKNOWN"
+
+
+def test_null_context_is_rejected_without_device_work():
+    L = _lib.load()
+    nul = ctypes.c_void_p()
+    for fn in ("imq_qmm_t", "imq_qgemv", "imq_qgemm"):
+        st = getattr(L, fn)(nul, nul, nul, nul, nul, nul, 64, 8, 1, 64, 4, 0, nul)
+        assert st == _lib.IMQ_EINVAL
+        assert b"null context" in L.imq_last_error(nul)
+    st = L.imq_dequantize(nul, nul, nul, nul, nul, 64, 8, 64, 4, 0, nul)
+    assert st == _lib.IMQ_EINVAL
+    assert L.imq_create(0, None) == _lib.IMQ_EINVAL
+    assert L.imq_stream_sync(nul, nul) == _lib.IMQ_EINVAL
+    assert L.imq_malloc(nul, 16, None) == _lib.IMQ_EINVAL
+
+
+def test_check_maps_status_to_exceptions():
+    L = _lib.load()
+    nul = ctypes.c_void_p()
+    L.imq_qmm_t(nul, nul, nul, nul, nul, nul, 64, 8, 1, 64, 4, 0, nul)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.IMQ_EINVAL, nul)
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.IMQ_EUNSUPPORTED, nul)
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.IMQ_EHIP, nul)

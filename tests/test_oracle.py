@@ -1,0 +1,390 @@
+"""Pins the CPU oracle (oracle/) against checks that do not restate it.
+
+The reference holds no golden vectors for this path (its only quantization
+test checks key presence, Tests/ImarelloDiTTests/TransformerStructureTests.swift:40-48)
+and its implementation (Swift + MLX + Metal) cannot run here.  The oracle is
+therefore pinned by:
+
+* exact rational arithmetic (fractions.Fraction) with an independent
+  round-to-nearest-even, over all 16 codes and a grid of (scale, bias) bf16
+  patterns (negative, zero, subnormal, huge, ties);
+* torch's own float32 arithmetic and bf16 conversion;
+* known-answer words and closed forms (q = 0 -> bias, scale = 0 -> bias,
+  all-equal codes -> rank-1 product);
+* brute-force exact dot products on tiny shapes, torch float64 matmul,
+  K-split additivity;
+* planted mutants (plausible mistakes) that must fail those same checks.
+"""
+
+from __future__ import annotations
+
+import struct
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from aestrix_amd import synth
+from oracle import cref, ref
+
+# ---------------------------------------------------------------- exact RNE
+
+
+def _rne(v: Fraction, p: int, emin: int = -126, emax: int = 127):
+    """Round a rational to the nearest p-bit binary float (ties to even),
+    with subnormals below 2^emin; returns a Fraction or +-inf (float)."""
+    if v == 0:
+        return Fraction(0)
+    sign = -1 if v < 0 else 1
+    a = -v if v < 0 else v
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    e = max(e, emin)
+    quantum = Fraction(2) ** (e - p + 1)
+    n = a / quantum
+    f = n.numerator // n.denominator
+    r = n - f
+    if r > Fraction(1, 2) or (r == Fraction(1, 2) and f % 2 == 1):
+        f += 1
+    res = f * quantum
+    if res >= Fraction(2) ** (emax + 1):
+        return sign * float("inf")
+    return sign * res
+
+
+def _bf16_bits_of(v) -> int:
+    """bf16 bits of a value that is exactly representable in bf16 (or +-inf)."""
+    f = float(v)
+    bits = struct.unpack("<I", struct.pack("<f", f))[0]
+    assert bits & 0xFFFF == 0, "not a bf16 value"
+    return bits >> 16
+
+
+def _bf16_value(bits: int) -> Fraction:
+    f = struct.unpack("<f", struct.pack("<I", (bits & 0xFFFF) << 16))[0]
+    return Fraction(f)
+
+
+def exact_dequant_bits(s_bits: int, b_bits: int, q: int) -> int:
+    """RNE_bf16(fl32(fl32(s*q) + b)) computed with exact rationals: the
+    reference's `scale * q + bias` on Float is two rounded operations
+    (DirectTEEncoder.swift:119).  The product is exact unless it overflows."""
+    prod = _rne(_bf16_value(s_bits) * q, 24)
+    if isinstance(prod, float):  # product overflowed to +-inf; a finite bias keeps it
+        return _bf16_bits_of(prod)
+    f32 = _rne(prod + _bf16_value(b_bits), 24)
+    if isinstance(f32, float):  # sum overflowed
+        return _bf16_bits_of(f32)
+    return _bf16_bits_of(_rne(f32, 8))
+
+
+# (scale, bias) bf16 bit patterns: ordinary, negative, zero, subnormal,
+# tiny normal, huge, and values whose sums land on bf16 ties.
+S_PATTERNS = [0x3F80, 0x3F00, 0x3EAB, 0x3CA4, 0x3B80, 0xBCA4, 0x0000, 0x0001, 0x0050, 0x0080,
+              0x00FF, 0x7E00, 0x7F00, 0x3D4D, 0x3F81, 0x4000, 0x3E4D, 0xC000]
+B_PATTERNS = [0x0000, 0x3F80, 0xBF80, 0xBE24, 0xC0A0, 0x3B00, 0x0001, 0x8080, 0x7F00, 0xFF00,
+              0xBD4D, 0x4100, 0x3C00, 0x2000]
+
+
+def _grid():
+    rows = []
+    for s in S_PATTERNS:
+        for b in B_PATTERNS:
+            rows.append((s, b))
+    return rows
+
+
+def _grid_problem():
+    """One weight row per (s, b) pair, each row holding codes 0..15 four times."""
+    grid = _grid()
+    n = len(grid)
+    codes = np.tile(np.arange(16, dtype=np.uint8), 4)[None, :].repeat(n, axis=0)  # [n, 64]
+    w = ref.pack_codes(codes)
+    s = np.array([[g[0]] for g in grid], dtype=np.uint16)
+    b = np.array([[g[1]] for g in grid], dtype=np.uint16)
+    return grid, codes, w, s, b
+
+
+def _exact_grid_expected():
+    grid, codes, w, s, b = _grid_problem()
+    exp = np.empty(codes.shape, dtype=np.uint16)
+    for i, (sb, bb) in enumerate(grid):
+        for k in range(codes.shape[1]):
+            exp[i, k] = exact_dequant_bits(sb, bb, int(codes[i, k]))
+    return exp
+
+
+_EXACT_CACHE: dict = {}
+
+
+def exact_grid():
+    if "v" not in _EXACT_CACHE:
+        _EXACT_CACHE["v"] = _exact_grid_expected()
+    return _EXACT_CACHE["v"]
+
+
+# ------------------------------------------------------------ bf16 rounding
+
+
+def test_f32_to_bf16_matches_torch_on_random_finite_patterns():
+    rng = np.random.default_rng(7)
+    bits = rng.integers(0, 1 << 32, size=200_000, dtype=np.uint64).astype(np.uint32)
+    f = bits.view(np.float32)
+    f = f[np.isfinite(f)]
+    ours = ref.f32_to_bf16(f)
+    theirs = torch.from_numpy(f.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, theirs)
+
+
+def test_f32_to_bf16_ties_and_overflow():
+    cases = {
+        0x3F808000: 0x3F80,  # tie, even stays
+        0x3F818000: 0x3F82,  # tie, odd rounds up
+        0x3F807FFF: 0x3F80,  # below tie
+        0x3F808001: 0x3F81,  # above tie
+        0x7F7FFFFF: 0x7F80,  # largest float rounds to inf
+        0x00008000: 0x0000,  # subnormal tie to even (zero)
+        0x00018000: 0x0002,  # subnormal tie to even (up)
+        0x80000000: 0x8000,  # negative zero
+    }
+    for fbits, want in cases.items():
+        v = np.array([fbits], dtype=np.uint32).view(np.float32)
+        assert int(ref.f32_to_bf16(v)[0]) == want, hex(fbits)
+        assert int(cref.lib().oracle_f32_to_bf16(float(v[0]))) == want, hex(fbits)
+
+
+def test_f64_to_bf16_is_correctly_rounded():
+    rng = np.random.default_rng(3)
+    vals = rng.standard_normal(20_000) * np.exp(rng.uniform(-20, 20, 20_000))
+    got = ref.f64_to_bf16(vals)
+    for v, g in zip(vals[:3000], got[:3000]):
+        want = _rne(Fraction(float(v)), 8)
+        assert int(g) == _bf16_bits_of(want)
+    # a double just above a bf16 tie must round up even when its float32 cast lands on the tie
+    tie = 1.0 + 2.0 ** -8          # exact midpoint between 1.0 and 1 + 2^-7
+    above = tie + 2.0 ** -40       # float32 cast rounds back to the tie
+    assert int(ref.f64_to_bf16(np.array([above]))[0]) == 0x3F81
+    assert int(ref.f64_to_bf16(np.array([tie]))[0]) == 0x3F80
+
+
+# --------------------------------------------------------------- dequantize
+
+
+def test_pack_unpack_round_trip():
+    rng = np.random.default_rng(11)
+    w = rng.integers(0, 1 << 32, size=(17, 24), dtype=np.uint32)
+    assert np.array_equal(ref.pack_codes(ref.unpack_codes(w)), w)
+    codes = rng.integers(0, 16, size=(5, 64), dtype=np.uint8)
+    assert np.array_equal(ref.unpack_codes(ref.pack_codes(codes)), codes)
+
+
+def test_known_answer_words_low_nibble_first():
+    w = np.array([[0x76543210, 0xFEDCBA98] * 4], dtype=np.uint32)
+    codes = ref.unpack_codes(w)[0]
+    assert list(codes[:16]) == list(range(16))
+    one = np.array([[0x3F80]], dtype=np.uint16)      # scale 1.0
+    zero = np.array([[0x0000]], dtype=np.uint16)     # bias 0
+    deq = ref.dequantize(w, one, zero)[0]
+    want = [_bf16_bits_of(float(v)) for v in range(16)] * 4
+    assert list(deq) == want
+    assert list(cref.dequantize(w, one, zero)[0]) == want
+    # scale 0.5, bias -4: 0.5 q - 4 is exact
+    half = np.array([[0x3F00]], dtype=np.uint16)
+    m4 = np.array([[0xC080]], dtype=np.uint16)
+    want2 = [_bf16_bits_of(0.5 * v - 4) for v in range(16)] * 4
+    assert list(ref.dequantize(w, half, m4)[0]) == want2
+
+
+def test_dequant_matches_exact_rational_grid():
+    _, _, w, s, b = _grid_problem()
+    exp = exact_grid()
+    assert np.array_equal(ref.dequantize(w, s, b), exp)
+    assert np.array_equal(cref.dequantize(w, s, b), exp)
+
+
+def test_dequant_matches_torch_arithmetic():
+    _, codes, w, s, b = _grid_problem()
+    sf = torch.from_numpy(ref.bf16_to_f32(s))
+    bf = torch.from_numpy(ref.bf16_to_f32(b))
+    q = torch.from_numpy(codes.astype(np.float32))
+    want = (sf * q + bf).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    finite = np.isfinite(ref.bf16_to_f32(want))
+    assert np.array_equal(ref.dequantize(w, s, b)[finite], want[finite])
+
+
+def test_dequant_special_cases():
+    rng = np.random.default_rng(5)
+    p = synth.make_problem(0, 8, 256, seed=9)
+    # q = 0 -> bias exactly
+    w0 = np.zeros_like(p.w)
+    d0 = ref.dequantize(w0, p.scales, p.biases)
+    assert np.array_equal(d0, np.repeat(p.biases, 64, axis=1))
+    # scale = 0 -> bias exactly
+    z = np.zeros_like(p.scales)
+    assert np.array_equal(ref.dequantize(p.w, z, p.biases), np.repeat(p.biases, 64, axis=1))
+    # group index is k // 64: changing group g's scale changes exactly columns [64g, 64g+64)
+    s2 = p.scales.copy()
+    s2[:, 2] = ref.f32_to_bf16(ref.bf16_to_f32(s2[:, 2]) * np.float32(2.0))
+    diff = ref.dequantize(p.w, s2, p.biases) != ref.dequantize(p.w, p.scales, p.biases)
+    cols = np.nonzero(diff.any(axis=0))[0]
+    assert cols.min() >= 128 and cols.max() < 192
+    del rng
+
+
+def test_c_and_numpy_dequant_agree_on_random_packs():
+    p = synth.make_problem(0, 300, 1024, seed=4)
+    assert np.array_equal(ref.dequantize(p.w, p.scales, p.biases),
+                          cref.dequantize(p.w, p.scales, p.biases))
+
+
+def test_dequant_rejects_bad_shapes():
+    w = np.zeros((4, 5), dtype=np.uint32)  # K = 40, not a multiple of 64
+    s = np.zeros((4, 1), dtype=np.uint16)
+    with pytest.raises(ValueError):
+        cref.dequantize(w, s, s)
+
+
+# ------------------------------------------------------- dequant-then-matmul
+
+
+def _exact_qmm_bits(x, w, s, b):
+    deq = ref.dequantize(w, s, b)
+    m, k = x.shape
+    n = w.shape[0]
+    out = np.empty((m, n), dtype=np.uint16)
+    for i in range(m):
+        for j in range(n):
+            acc = Fraction(0)
+            for t in range(k):
+                acc += _bf16_value(int(x[i, t])) * _bf16_value(int(deq[j, t]))
+            r = _rne(acc, 8)
+            out[i, j] = _bf16_bits_of(r)
+    return out
+
+
+def test_qmm_brute_force_exact_tiny():
+    p = synth.make_problem(3, 4, 128, seed=21)
+    want = _exact_qmm_bits(p.x, p.w, p.scales, p.biases)
+    assert np.array_equal(cref.qmm_t(p.x, p.w, p.scales, p.biases), want)
+    assert np.array_equal(ref.qmm_t(p.x, p.w, p.scales, p.biases), want)
+
+
+def test_qmm_matches_torch_float64():
+    p = synth.make_problem(33, 70, 320, seed=22)
+    deq = torch.from_numpy(ref.bf16_to_f32(ref.dequantize(p.w, p.scales, p.biases))).double()
+    x = torch.from_numpy(ref.bf16_to_f32(p.x)).double()
+    want = (x @ deq.T).numpy()
+    got = ref.qmm_t_f64(p.x, p.w, p.scales, p.biases)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    c = cref.qmm_t(p.x, p.w, p.scales, p.biases, threads=2)
+    assert np.array_equal(c, ref.f64_to_bf16(want))
+
+
+def test_qmm_rank1_known_answer():
+    """All codes equal c: deq(W) is one value per group, so
+    y[m, n] = sum_g w_g * sum_{k in g} x[m, k]."""
+    p = synth.make_problem(6, 5, 256, seed=23)
+    c = 11
+    word = 0
+    for i in range(8):
+        word |= c << (4 * i)
+    w = np.full_like(p.w, word)
+    wg = ref.bf16_to_f32(ref.f32_to_bf16(ref.bf16_to_f32(p.scales) * np.float32(c)
+                                         + ref.bf16_to_f32(p.biases))).astype(np.float64)
+    xs = ref.bf16_to_f32(p.x).astype(np.float64).reshape(6, 4, 64).sum(axis=2)  # [M, G]
+    want = xs @ wg.T
+    np.testing.assert_allclose(ref.qmm_t_f64(p.x, w, p.scales, p.biases), want,
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_qmm_k_split_additivity():
+    p = synth.make_problem(7, 9, 384, seed=24)
+    full = ref.qmm_t_f64(p.x, p.w, p.scales, p.biases)
+    k1 = 128
+    a = ref.qmm_t_f64(p.x[:, :k1], p.w[:, :k1 // 8], p.scales[:, :k1 // 64], p.biases[:, :k1 // 64])
+    b = ref.qmm_t_f64(p.x[:, k1:], p.w[:, k1 // 8:], p.scales[:, k1 // 64:], p.biases[:, k1 // 64:])
+    np.testing.assert_allclose(full, a + b, rtol=1e-12, atol=1e-12)
+
+
+def test_c_f32acc_baseline_within_tolerance_of_oracle():
+    p = synth.make_problem(16, 64, 1024, seed=25)
+    o = cref.qmm_t(p.x, p.w, p.scales, p.biases)
+    c = cref.qmm_t_f32acc(p.x, p.w, p.scales, p.biases)
+    st = ref.error_stats(c, o)
+    assert st["mae"] <= 1e-3 and st["max_rel_normwise"] <= 1e-2, st
+
+
+# ---------------------------------------------------------- planted mutants
+# Each plausible mistake in a restatement must fail a check above.
+
+
+def _deq_high_nibble_first(w, s, b):
+    codes = ref.unpack_codes(w).reshape(w.shape[0], -1, 8)[:, :, ::-1].reshape(w.shape[0], -1)
+    return _deq_from_codes(codes, s, b)
+
+
+def _deq_from_codes(codes, s, b, group=64):
+    q = codes.astype(np.float32)
+    n, k = q.shape
+    sf = np.repeat(ref.bf16_to_f32(s), group, axis=-1)[:, :k]
+    bf = np.repeat(ref.bf16_to_f32(b), group, axis=-1)[:, :k]
+    return ref.f32_to_bf16(sf * q + bf)
+
+
+def _deq_group32(w, s, b):
+    """Group index k // 32 into the row-major [N, K/64] tables (reads the next
+    groups, and past the row end into the next row)."""
+    codes = ref.unpack_codes(w)
+    n, k = codes.shape
+    g = k // 64
+    idx = (np.arange(n)[:, None] * g + np.arange(k)[None, :] // 32) % (n * g)
+    sf = ref.bf16_to_f32(s.reshape(-1)[idx])
+    bf = ref.bf16_to_f32(b.reshape(-1)[idx])
+    with np.errstate(over="ignore", invalid="ignore"):
+        return ref.f32_to_bf16(sf * codes.astype(np.float32) + bf)
+
+
+def _deq_per_op_rounding(w, s, b):
+    q = ref.unpack_codes(w).astype(np.float32)
+    n, k = q.shape
+    sf = np.repeat(ref.bf16_to_f32(s), 64, axis=-1)
+    bf = np.repeat(ref.bf16_to_f32(b), 64, axis=-1)
+    prod = ref.bf16_to_f32(ref.f32_to_bf16(sf * q))
+    return ref.f32_to_bf16(prod + bf)
+
+
+def _deq_truncating(w, s, b):
+    q = ref.unpack_codes(w).astype(np.float32)
+    sf = np.repeat(ref.bf16_to_f32(s), 64, axis=-1)
+    bf = np.repeat(ref.bf16_to_f32(b), 64, axis=-1)
+    return ((sf * q + bf).view(np.uint32) >> np.uint32(16)).astype(np.uint16)
+
+
+@pytest.mark.parametrize("mutant", [_deq_high_nibble_first, _deq_group32, _deq_per_op_rounding,
+                                    _deq_truncating])
+def test_dequant_checks_catch_mutants(mutant):
+    _, _, w, s, b = _grid_problem()
+    exact = exact_grid()
+    p = synth.make_problem(0, 64, 512, seed=31)
+    caught = (not np.array_equal(mutant(w, s, b), exact)
+              or not np.array_equal(mutant(p.w, p.scales, p.biases),
+                                    ref.dequantize(p.w, p.scales, p.biases)))
+    # the grid alone must already expose every mutant
+    assert not np.array_equal(mutant(w, s, b), exact)
+    assert caught
+
+
+def test_qmm_checks_catch_mutants():
+    p = synth.make_problem(3, 4, 128, seed=21)
+    want = _exact_qmm_bits(p.x, p.w, p.scales, p.biases)
+    deq = ref.bf16_to_f32(ref.dequantize(p.w, p.scales, p.biases)).astype(np.float64)
+    x = ref.bf16_to_f32(p.x).astype(np.float64)
+    # a dropped bias term, and the K order of one operand reversed
+    no_bias = ref.f64_to_bf16(x @ (deq - np.repeat(ref.bf16_to_f32(p.biases), 64, axis=1)).T)
+    wrong_order = ref.f64_to_bf16(x[:, ::-1] @ deq.T)
+    for mutant in (no_bias, wrong_order):
+        assert not np.array_equal(mutant, want)
