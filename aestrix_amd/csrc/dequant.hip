@@ -5,10 +5,15 @@
 // reference (Sources/ImarelloDirect/DirectTEEncoder.swift:106-134).
 //
 // HBM-bound: 0.5 B of codes + 4/64 B of scale/bias read and 2 B written per
-// element.  One lane owns 32 consecutive codes (a 16-byte load, half a group)
-// and writes 64 bytes of output; a wave therefore reads 1 KiB of packed codes
-// and writes 4 KiB of contiguous output.  The bf16 rounding uses the integer
-// formula so the result is bit-identical to it for every input pattern.
+// element.  Rows of W and of the output are contiguous, so a flat word index w
+// addresses everything: codes word w, group w / 8 (a row of K/8 words holds
+// K/64 groups of 8 words), output bytes [16 w, 16 w + 16).  A workgroup owns
+// 1024 consecutive words; lane t of it handles words t, t+256, t+512, t+768,
+// so every wave instruction loads 256 contiguous bytes of codes and stores
+// 1 KiB of contiguous output.  Rounding is v_cvt_pk_bf16_f32 (RNE), which
+// equals the integer formula of DirectTEEncoder.swift:39-43 for every non-NaN
+// value; a NaN result (possible only when a scale or bias is itself inf or
+// NaN) stays a quiet NaN.
 #include "imq_device.hpp"
 #include "imq_kernels.hpp"
 
@@ -16,23 +21,17 @@ namespace imq {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kWordsPerThread = 4;
+constexpr int kWordsPerBlock = kThreads * kWordsPerThread;
 
-template <typename T>
-struct DeqOut;
-
-template <>
-struct DeqOut<uint16_t> {  // bf16 bit patterns
-  static __device__ __forceinline__ float load(const uint16_t* p) { return bf16_to_f32(*p); }
-  static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
-    return f32_to_bf16_int(lo) | (f32_to_bf16_int(hi) << 16);
-  }
+struct Bf16Out {
+  static __device__ __forceinline__ float load(uint16_t h) { return bf16_to_f32(h); }
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_bf16x2(lo, hi); }
 };
 
-struct F16Tag {};
-template <>
-struct DeqOut<F16Tag> {  // f16 bit patterns
-  static __device__ __forceinline__ float load(const uint16_t* p) {
-    return (float)__builtin_bit_cast(_Float16, *p);
+struct F16Out {
+  static __device__ __forceinline__ float load(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
   }
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
     // v_cvt_f16_f32 rounds to nearest even (default round mode).
@@ -42,37 +41,51 @@ struct DeqOut<F16Tag> {  // f16 bit patterns
   }
 };
 
-template <typename Tag>
-__global__ __launch_bounds__(kThreads) void dequant_kernel(const u32x4_t* __restrict__ w,
+// out = s * q + b as two rounded operations, never contracted into an fma:
+// the product is exact unless it overflows, and then it must stay +-inf as in
+// the reference's `scale * q + bias` on Float.
+__device__ __forceinline__ float affine(float s, float q, float b) {
+#pragma clang fp contract(off)
+  const float p = s * q;
+  return p + b;
+}
+
+template <typename Out>
+__global__ __launch_bounds__(kThreads) void dequant_kernel(const uint32_t* __restrict__ w,
                                                            const uint16_t* __restrict__ scales,
                                                            const uint16_t* __restrict__ biases,
                                                            u32x4_t* __restrict__ out,
-                                                           uint32_t total_chunks,
-                                                           uint32_t chunks_per_row) {
-  const uint32_t c = blockIdx.x * kThreads + threadIdx.x;
-  if (c >= total_chunks) return;
-  const uint32_t row = c / chunks_per_row;
-  const uint32_t j = c - row * chunks_per_row;
-  const size_t gi = (size_t)row * (chunks_per_row >> 1) + (j >> 1);
-  const float s = DeqOut<Tag>::load(scales + gi);
-  const float b = DeqOut<Tag>::load(biases + gi);
-  const u32x4_t q = __builtin_nontemporal_load(w + c);
-  const uint32_t words[4] = {q.x, q.y, q.z, q.w};
-  u32x4_t* dst = out + (size_t)c * 4;
+                                                           uint32_t total_words) {
+  const uint32_t base = blockIdx.x * (uint32_t)kWordsPerBlock + threadIdx.x;
+  uint32_t words[kWordsPerThread];
+  uint16_t sb[kWordsPerThread][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t word = words[i];
+  for (int i = 0; i < kWordsPerThread; ++i) {
+    const uint32_t wi = base + (uint32_t)(i * kThreads);
+    if (wi < total_words) {
+      words[i] = __builtin_nontemporal_load(w + wi);
+      sb[i][0] = scales[wi >> 3];
+      sb[i][1] = biases[wi >> 3];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kWordsPerThread; ++i) {
+    const uint32_t wi = base + (uint32_t)(i * kThreads);
+    if (wi >= total_words) continue;
+    const float s = Out::load(sb[i][0]);
+    const float b = Out::load(sb[i][1]);
+    // Even codes sit in the low nibble of each byte, odd codes in the high
+    // nibble; each byte converts with one v_cvt_f32_ubyteN.
+    const uint32_t lo = words[i] & 0x0F0F0F0Fu;
+    const uint32_t hi = (words[i] >> 4) & 0x0F0F0F0Fu;
     uint32_t o[4];
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      const float q0 = (float)((word >> (8 * p)) & 0xFu);
-      const float q1 = (float)((word >> (8 * p + 4)) & 0xFu);
-      // Two rounded operations, never contracted into an fma: the product is
-      // exact unless it overflows, and then it must stay +-inf as in the
-      // reference's `scale * q + bias`.
-      o[p] = DeqOut<Tag>::pack(__fadd_rn(__fmul_rn(s, q0), b), __fadd_rn(__fmul_rn(s, q1), b));
+      const float q0 = (float)((lo >> (8 * p)) & 0xFFu);
+      const float q1 = (float)((hi >> (8 * p)) & 0xFFu);
+      o[p] = Out::pack(affine(s, q0, b), affine(s, q1, b));
     }
-    __builtin_nontemporal_store(u32x4_t{o[0], o[1], o[2], o[3]}, dst + i);
+    __builtin_nontemporal_store(u32x4_t{o[0], o[1], o[2], o[3]}, out + wi);
   }
 }
 
@@ -80,23 +93,19 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(const u32x4_t* __rest
 
 hipError_t launch_dequant(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                           uint16_t* out, int k, int n, bool f16, hipStream_t stream) {
-  const uint32_t chunks_per_row = (uint32_t)(k / 32);
-  // Keep each launch's flat chunk index inside 31 bits; split by rows.
-  const int64_t max_rows = (int64_t)0x7FFFFFFF / chunks_per_row;
-  for (int64_t r0 = 0; r0 < n; r0 += max_rows) {
-    const int64_t rows = (n - r0 < max_rows) ? (n - r0) : max_rows;
-    const uint32_t total = (uint32_t)(rows * chunks_per_row);
-    const u32x4_t* wp = reinterpret_cast<const u32x4_t*>(w + r0 * (k / 8));
-    const uint16_t* sp = scales + r0 * (k / 64);
-    const uint16_t* bp = biases + r0 * (k / 64);
-    u32x4_t* op = reinterpret_cast<u32x4_t*>(out + r0 * (int64_t)k);
-    const dim3 grid((total + kThreads - 1) / kThreads);
+  const int64_t total = (int64_t)n * (k / 8);
+  // Keep each launch's word index inside 31 bits; split at group boundaries.
+  const int64_t max_words = (int64_t)1 << 30;
+  for (int64_t w0 = 0; w0 < total; w0 += max_words) {
+    const uint32_t words = (uint32_t)((total - w0 < max_words) ? (total - w0) : max_words);
+    const dim3 grid((words + kWordsPerBlock - 1) / kWordsPerBlock);
+    u32x4_t* op = reinterpret_cast<u32x4_t*>(out) + w0;
     if (f16)
-      hipLaunchKernelGGL(dequant_kernel<F16Tag>, grid, dim3(kThreads), 0, stream, wp, sp, bp, op,
-                         total, chunks_per_row);
+      hipLaunchKernelGGL(dequant_kernel<F16Out>, grid, dim3(kThreads), 0, stream, w + w0,
+                         scales + w0 / 8, biases + w0 / 8, op, words);
     else
-      hipLaunchKernelGGL(dequant_kernel<uint16_t>, grid, dim3(kThreads), 0, stream, wp, sp, bp,
-                         op, total, chunks_per_row);
+      hipLaunchKernelGGL(dequant_kernel<Bf16Out>, grid, dim3(kThreads), 0, stream, w + w0,
+                         scales + w0 / 8, biases + w0 / 8, op, words);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

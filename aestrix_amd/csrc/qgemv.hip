@@ -23,26 +23,57 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kUnroll = 8;              // 16-byte chunks in flight per lane
-constexpr int kLdsBytesMax = 64 * 1024; // x tile budget per workgroup
+constexpr int kMaxU = 8;                 // 16-byte chunks in flight per lane
+constexpr int kLdsBytesMax = 64 * 1024;  // x tile budget per workgroup
 
-template <int MR, int G>
+// LDS position of x piece p (16 bytes) of chunk j (32 elements) is
+// 4 j + (p ^ ((j >> 2) & 3)).  The lanes of a row group read chunks j, j+1, ...
+// in the same instruction; the swizzle spreads their 16-byte reads over all
+// bank groups while the piece index p stays a compile-time constant.
+__device__ __forceinline__ int xs_swizzle(int slot) {
+  const int j = slot >> 2;
+  return (j << 2) | ((slot & 3) ^ ((j >> 2) & 3));
+}
+
+// x staging slot idx of a tile: row idx / vpr, 16-byte piece idx % vpr.  The
+// load is clamped into the tile (never predicated), the store is guarded.
+__device__ __forceinline__ u32x4_t load_x_slot(const uint16_t* x, int K, int k0, int vpr,
+                                               int total, int idx) {
+  const int i = min(idx, total - 1);
+  const int m = i / vpr;
+  return *reinterpret_cast<const u32x4_t*>(x + (size_t)m * K + k0 + (i - m * vpr) * 8);
+}
+
+__device__ __forceinline__ void store_x_slot(u32x4_t* xs, int stride, int vpr, int total, int idx,
+                                             u32x4_t v) {
+  if (idx < total) {
+    const int m = idx / vpr;
+    xs[m * stride + xs_swizzle(idx - m * vpr)] = v;
+  }
+}
+
+// Loads are never predicated: an index past the end is clamped to the last
+// valid chunk (a harmless duplicate read).  Predicated loads make the compiler
+// merge the register array through a phi and wait on each load in turn.
+template <int MR, int G, int U>
 __global__ __launch_bounds__(kThreads) void qgemv_kernel(const uint32_t* __restrict__ w,
                                                          const uint16_t* __restrict__ scales,
                                                          const uint16_t* __restrict__ biases,
                                                          const uint16_t* __restrict__ x,
                                                          uint16_t* __restrict__ y, int K, int N,
-                                                         int kt) {
-  extern __shared__ u32x4_t xs[];  // [MR][kt / 8] u32x4_t (bf16 x tile)
-  constexpr int RPW = 64 / G;    // rows per wave
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+                                                         int M, int kt) {
+  extern __shared__ u32x4_t xs[];  // [MR][kt / 8] bf16 x tile
+  constexpr int RPW = 64 / G;      // rows per wave
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int gl = lane & (G - 1);
   const int row = (blockIdx.x * kWaves + wave) * RPW + lane / G;
   const bool row_ok = row < N;
   const int wpr = K >> 3;
   const int gpr = K >> 6;
   const int xs_stride = kt >> 3;  // u32x4_t per x row in LDS
+  // Lanes past the last row read row 0 (in bounds) and never store.
   const size_t rsafe = row_ok ? (size_t)row : 0;
   const u32x4_t* wrow = reinterpret_cast<const u32x4_t*>(w + rsafe * wpr);
   const uint16_t* srow = scales + rsafe * gpr;
@@ -54,50 +85,70 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(const uint32_t* __restr
 
   for (int k0 = 0; k0 < K; k0 += kt) {
     const int ktc = (K - k0 < kt) ? (K - k0) : kt;
-    if (k0 > 0) __syncthreads();
-    const int vpr = ktc >> 3;  // u32x4_t of x per row in this tile
-    for (int i = threadIdx.x; i < MR * vpr; i += kThreads) {
-      const int m = i / vpr;
-      const int v = i - m * vpr;
-      xs[m * xs_stride + v] = *reinterpret_cast<const u32x4_t*>(x + (size_t)m * K + k0 + v * 8);
-    }
-    __syncthreads();
-    if (row_ok) {
-      const int nch = ktc >> 5;  // 16-byte chunks of this row inside the tile
-      const int c0 = k0 >> 5;
-      for (int jb = gl; jb < nch; jb += G * kUnroll) {
-        u32x4_t q[kUnroll];
-        uint32_t sb[kUnroll][2];
+    const int nch = ktc >> 5;  // 16-byte chunks of a row inside this tile
+    const int c0 = k0 >> 5;
+    const int batches = (nch + G * U - 1) / (G * U);  // the same for every lane
+    const int vpr = ktc >> 3;       // u32x4_t of x per row in this tile
+    const int xtotal = M * vpr;     // u32x4_t of x in this tile (<= 4 rounds of 1024)
+    for (int it = 0; it < batches; ++it) {
+      const int jb = gl + it * G * U;
+      // x loads of the first staging round go out first: the LDS writes that
+      // need them then do not wait for the weight loads issued after them.
+      u32x4_t xv[4];
+      if (it == 0) {
+        if (k0 > 0) __syncthreads();  // every wave is done with the previous tile
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const int j = jb + u * G;
-          if (j < nch) {
-            q[u] = __builtin_nontemporal_load(wrow + c0 + j);
-            const int g = (c0 + j) >> 1;
-            sb[u][0] = srow[g];
-            sb[u][1] = brow[g];
+        for (int i = 0; i < 4; ++i) xv[i] = load_x_slot(x, K, k0, vpr, xtotal, tid + i * kThreads);
+      }
+      u32x4_t q[U];
+      uint32_t sv[U], bv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int j = min(jb + u * G, nch - 1);
+        q[u] = __builtin_nontemporal_load(wrow + c0 + j);
+        const int g = (c0 + j) >> 1;
+        sv[u] = srow[g];
+        bv[u] = brow[g];
+      }
+      if (it == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_x_slot(xs, xs_stride, vpr, xtotal, tid + i * kThreads, xv[i]);
+        // Further rounds (M * tile > 1024 chunks of x): unrolled, no loop back edge.
+#pragma unroll
+        for (int r = 1; r < 4; ++r) {
+          if (r * 4 * kThreads < xtotal) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              xv[i] = load_x_slot(x, K, k0, vpr, xtotal, tid + (4 * r + i) * kThreads);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              store_x_slot(xs, xs_stride, vpr, xtotal, tid + (4 * r + i) * kThreads, xv[i]);
           }
         }
+        __syncthreads();
+      }
+      if (row_ok) {
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
           const int j = jb + u * G;
           if (j < nch) {
-            const float s = bf16_to_f32(sb[u][0]);
-            const float b = bf16_to_f32(sb[u][1]);
-            const float s24 = s * 0x1p24f;
-            const float s20 = s * 0x1p20f;
+            const float sc = bf16_to_f32(sv[u]);
+            const float bi = bf16_to_f32(bv[u]);
+            const float s24 = sc * 0x1p24f;
+            const float s20 = sc * 0x1p20f;
+            const int swz = (j >> 2) & 3;
             uint32_t wp[16];
-            dequant_word_bf16(q[u].x, s24, s20, b, wp + 0);
-            dequant_word_bf16(q[u].y, s24, s20, b, wp + 4);
-            dequant_word_bf16(q[u].z, s24, s20, b, wp + 8);
-            dequant_word_bf16(q[u].w, s24, s20, b, wp + 12);
+            dequant_word_bf16(q[u].x, s24, s20, bi, wp + 0);
+            dequant_word_bf16(q[u].y, s24, s20, bi, wp + 4);
+            dequant_word_bf16(q[u].z, s24, s20, bi, wp + 8);
+            dequant_word_bf16(q[u].w, s24, s20, bi, wp + 12);
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
               const u32x4_t* xv = xs + m * xs_stride + j * 4;
               float a = acc[m];
 #pragma unroll
               for (int v = 0; v < 4; ++v) {
-                const u32x4_t xx = xv[v];
+                const u32x4_t xx = xv[v ^ swz];
                 a = dot2_bf16(wp[4 * v + 0], xx.x, a);
                 a = dot2_bf16(wp[4 * v + 1], xx.y, a);
                 a = dot2_bf16(wp[4 * v + 2], xx.z, a);
@@ -118,38 +169,164 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(const uint32_t* __restr
   }
   if (row_ok && gl == 0) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m) y[(size_t)m * N + row] = (uint16_t)f32_to_bf16_int(acc[m]);
+    for (int m = 0; m < MR; ++m)
+      if (m < M) y[(size_t)m * N + row] = (uint16_t)f32_to_bf16_int(acc[m]);
   }
+}
+
+// Straight-line variant for the common case: x[0:M][0:K] fits the LDS tile
+// and one batch of U chunks per lane covers a row (K <= 32 * G * U).  There is
+// no loop, so nothing makes the compiler wait on loads it does not need yet:
+// x loads, then weight loads, then the x LDS writes (waiting on x only), one
+// barrier, then the dequant + dot products (waiting on the weights).
+template <int MR, int G, int U>
+__global__ __launch_bounds__(kThreads) void qgemv_single_kernel(
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
+    const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+    int K, int N, int M) {
+  extern __shared__ u32x4_t xs[];  // [MR][K / 8] bf16 x
+  constexpr int RPW = 64 / G;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int gl = lane & (G - 1);
+  const int row = (blockIdx.x * kWaves + wave) * RPW + lane / G;
+  const bool row_ok = row < N;
+  const int gpr = K >> 6;
+  const int nch = K >> 5;
+  const int vpr = K >> 3;
+  const int xtotal = M * vpr;
+  const size_t rsafe = row_ok ? (size_t)row : 0;
+  const u32x4_t* wrow = reinterpret_cast<const u32x4_t*>(w + rsafe * (K >> 3));
+  const uint16_t* srow = scales + rsafe * gpr;
+  const uint16_t* brow = biases + rsafe * gpr;
+
+  u32x4_t xv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xv[i] = load_x_slot(x, K, 0, vpr, xtotal, tid + i * kThreads);
+  // Keep the issue order x, then weights: the x LDS writes then wait for the x
+  // loads only, and the compute of chunk u waits only for chunk u's loads.
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4_t q[U];
+  uint32_t sv[U], bv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int j = min(gl + u * G, nch - 1);
+    q[u] = __builtin_nontemporal_load(wrow + j);
+    sv[u] = srow[j >> 1];
+    bv[u] = brow[j >> 1];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) store_x_slot(xs, vpr, vpr, xtotal, tid + i * kThreads, xv[i]);
+#pragma unroll
+  for (int r = 1; r < 4; ++r) {
+    if (r * 4 * kThreads < xtotal) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xv[i] = load_x_slot(x, K, 0, vpr, xtotal, tid + (4 * r + i) * kThreads);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        store_x_slot(xs, vpr, vpr, xtotal, tid + (4 * r + i) * kThreads, xv[i]);
+    }
+  }
+  __syncthreads();
+
+  float acc[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int j = gl + u * G;
+    if (j < nch) {
+      const float sc = bf16_to_f32(sv[u]);
+      const float bi = bf16_to_f32(bv[u]);
+      const float s24 = sc * 0x1p24f;
+      const float s20 = sc * 0x1p20f;
+      const int swz = (j >> 2) & 3;
+      uint32_t wp[16];
+      dequant_word_bf16(q[u].x, s24, s20, bi, wp + 0);
+      dequant_word_bf16(q[u].y, s24, s20, bi, wp + 4);
+      dequant_word_bf16(q[u].z, s24, s20, bi, wp + 8);
+      dequant_word_bf16(q[u].w, s24, s20, bi, wp + 12);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const u32x4_t* xp = xs + m * vpr + j * 4;
+        float a = acc[m];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const u32x4_t xx = xp[v ^ swz];
+          a = dot2_bf16(wp[4 * v + 0], xx.x, a);
+          a = dot2_bf16(wp[4 * v + 1], xx.y, a);
+          a = dot2_bf16(wp[4 * v + 2], xx.z, a);
+          a = dot2_bf16(wp[4 * v + 3], xx.w, a);
+        }
+        acc[m] = a;
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+#pragma unroll
+    for (int off = G >> 1; off > 0; off >>= 1) acc[m] += __shfl_xor(acc[m], off, 64);
+  }
+  if (row_ok && gl == 0) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      if (m < M) y[(size_t)m * N + row] = (uint16_t)f32_to_bf16_int(acc[m]);
+  }
+}
+
+template <int MR, int G, int U>
+hipError_t launch_u(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
+                    uint16_t* y, int k, int n, int m, int kt, hipStream_t stream) {
+  const int rows_per_block = kWaves * (64 / G);
+  const dim3 grid((n + rows_per_block - 1) / rows_per_block);
+  if (kt == k && k / 32 <= G * U) {
+    const size_t lds = (size_t)MR * k * 2;
+    hipLaunchKernelGGL((qgemv_single_kernel<MR, G, U>), grid, dim3(kThreads), lds, stream, w, s,
+                       b, x, y, k, n, m);
+  } else {
+    const size_t lds = (size_t)MR * kt * 2;
+    hipLaunchKernelGGL((qgemv_kernel<MR, G, U>), grid, dim3(kThreads), lds, stream, w, s, b, x, y,
+                       k, n, m, kt);
+  }
+  return hipGetLastError();
 }
 
 template <int MR, int G>
 hipError_t launch_g(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
-                    uint16_t* y, int k, int n, hipStream_t stream) {
+                    uint16_t* y, int k, int n, int m, hipStream_t stream) {
   int kt = (kLdsBytesMax / (2 * MR)) / 64 * 64;
   if (kt > k) kt = k;
-  const int rows_per_block = kWaves * (64 / G);
-  const dim3 grid((n + rows_per_block - 1) / rows_per_block);
-  const size_t lds = (size_t)MR * kt * 2;
-  hipLaunchKernelGGL((qgemv_kernel<MR, G>), grid, dim3(kThreads), lds, stream, w, s, b, x, y, k,
-                     n, kt);
-  return hipGetLastError();
+  int u = (kt / 32 + G - 1) / G;  // chunks per lane for one batch covering the tile
+  if (u > kMaxU) u = kMaxU;
+  switch (u) {
+    case 1: return launch_u<MR, G, 1>(w, s, b, x, y, k, n, m, kt, stream);
+    case 2: return launch_u<MR, G, 2>(w, s, b, x, y, k, n, m, kt, stream);
+    case 3: return launch_u<MR, G, 3>(w, s, b, x, y, k, n, m, kt, stream);
+    case 4: return launch_u<MR, G, 4>(w, s, b, x, y, k, n, m, kt, stream);
+    case 5: return launch_u<MR, G, 5>(w, s, b, x, y, k, n, m, kt, stream);
+    case 6: return launch_u<MR, G, 6>(w, s, b, x, y, k, n, m, kt, stream);
+    case 7: return launch_u<MR, G, 7>(w, s, b, x, y, k, n, m, kt, stream);
+    default: return launch_u<MR, G, 8>(w, s, b, x, y, k, n, m, kt, stream);
+  }
 }
 
 template <int MR>
 hipError_t launch_m(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
-                    uint16_t* y, int k, int n, hipStream_t stream) {
-  // Lanes per row: enough waves to cover the chip (about 2048 waves), but no
-  // more lanes than the row has 16-byte chunks.
-  const int chunks = k / 32;
+                    uint16_t* y, int k, int n, int m, hipStream_t stream) {
+  // Lanes per row: enough waves to cover the chip (about 2048), but no more
+  // lanes than the row has 16-byte chunks when that can be avoided.
   int g = 16;
   if ((int64_t)n * 16 / 64 < 2048) g = 32;
   if ((int64_t)n * 32 / 64 < 2048) g = 64;
-  while (g > 8 && g > chunks) g >>= 1;
+  const int chunks = k / 32;
+  while (g > 16 && g > chunks) g >>= 1;
   switch (g) {
-    case 8: return launch_g<MR, 8>(w, s, b, x, y, k, n, stream);
-    case 16: return launch_g<MR, 16>(w, s, b, x, y, k, n, stream);
-    case 32: return launch_g<MR, 32>(w, s, b, x, y, k, n, stream);
-    default: return launch_g<MR, 64>(w, s, b, x, y, k, n, stream);
+    case 16: return launch_g<MR, 16>(w, s, b, x, y, k, n, m, stream);
+    case 32: return launch_g<MR, 32>(w, s, b, x, y, k, n, m, stream);
+    default: return launch_g<MR, 64>(w, s, b, x, y, k, n, m, stream);
   }
 }
 
@@ -157,16 +334,14 @@ hipError_t launch_m(const uint32_t* w, const uint16_t* s, const uint16_t* b, con
 
 hipError_t launch_qgemv(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                         const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
-  switch (m) {
-#define IMQ_QGEMV_CASE(MR) \
-  case MR: return launch_m<MR>(w, scales, biases, x, y, k, n, stream);
-    IMQ_QGEMV_CASE(1) IMQ_QGEMV_CASE(2) IMQ_QGEMV_CASE(3) IMQ_QGEMV_CASE(4)
-    IMQ_QGEMV_CASE(5) IMQ_QGEMV_CASE(6) IMQ_QGEMV_CASE(7) IMQ_QGEMV_CASE(8)
-    IMQ_QGEMV_CASE(9) IMQ_QGEMV_CASE(10) IMQ_QGEMV_CASE(11) IMQ_QGEMV_CASE(12)
-    IMQ_QGEMV_CASE(13) IMQ_QGEMV_CASE(14) IMQ_QGEMV_CASE(15) IMQ_QGEMV_CASE(16)
-#undef IMQ_QGEMV_CASE
-    default: return hipErrorInvalidValue;
-  }
+  // M is rounded up to a power of two for the register tile; rows >= M are
+  // neither read from x nor stored.
+  if (m <= 1) return launch_m<1>(w, scales, biases, x, y, k, n, m, stream);
+  if (m <= 2) return launch_m<2>(w, scales, biases, x, y, k, n, m, stream);
+  if (m <= 4) return launch_m<4>(w, scales, biases, x, y, k, n, m, stream);
+  if (m <= 8) return launch_m<8>(w, scales, biases, x, y, k, n, m, stream);
+  if (m <= 16) return launch_m<16>(w, scales, biases, x, y, k, n, m, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace imq

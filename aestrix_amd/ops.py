@@ -42,13 +42,21 @@ _DTYPES = {torch.bfloat16: _lib.IMQ_BF16, torch.float16: _lib.IMQ_F16,
 _WORD_DTYPES = (torch.int32,) + ((torch.uint32,) if hasattr(torch, "uint32") else ())
 
 
-def context(device: int | torch.device | None = None) -> ctypes.c_void_p:
-    """The library context of a HIP device (created once, kept for the process)."""
+def device_index(device: int | str | torch.device | None) -> int:
+    """Ordinal of a HIP device given as an int, a string or a torch.device."""
     if device is None:
-        device = torch.cuda.current_device()
-    idx = torch.device("cuda", device).index if not isinstance(device, int) else device
-    if idx is None:
-        idx = torch.cuda.current_device()
+        return torch.cuda.current_device()
+    if isinstance(device, int):
+        return device
+    d = torch.device(device)
+    if d.type != "cuda":
+        raise ValueError(f"not a HIP device: {d}")
+    return d.index if d.index is not None else torch.cuda.current_device()
+
+
+def context(device: int | str | torch.device | None = None) -> ctypes.c_void_p:
+    """The library context of a HIP device (created once, kept for the process)."""
+    idx = device_index(device)
     with _ctx_lock:
         ctx = _ctxs.get(idx)
         if ctx is None:

@@ -71,3 +71,15 @@ def test_check_maps_status_to_exceptions():
         _lib.check(_lib.IMQ_EUNSUPPORTED, nul)
     with pytest.raises(RuntimeError):
         _lib.check(_lib.IMQ_EHIP, nul)
+
+
+def test_device_index_normalisation():
+    import torch
+
+    from aestrix_amd import ops
+
+    assert ops.device_index(3) == 3
+    assert ops.device_index("cuda:2") == 2
+    assert ops.device_index(torch.device("cuda", 1)) == 1
+    with pytest.raises(ValueError):
+        ops.device_index("cpu")
