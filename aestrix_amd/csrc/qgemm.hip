@@ -26,15 +26,13 @@
 #include "imq_device.hpp"
 #include "imq_kernels.hpp"
 
+#include <cstdlib>
+
 namespace imq {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int BM = 128;           // workgroup tile rows (M)
-constexpr int BN = 256;           // workgroup tile cols (N)
-constexpr int MT = BM / 32;       // MFMA row tiles per wave
-constexpr int NT = BN / 4 / 32;   // MFMA col tiles per wave
-constexpr int kGroupM = 8;        // M tiles per raster group
+constexpr int kGroupM = 8;  // M tiles per raster group
 constexpr int kXcds = 8;
 
 __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -53,13 +51,25 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
   tn = in / gsz;
 }
 
-__global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(const uint32_t* __restrict__ w,
-                                                            const uint16_t* __restrict__ scales,
-                                                            const uint16_t* __restrict__ biases,
-                                                            const uint16_t* __restrict__ x,
-                                                            uint16_t* __restrict__ y, int M, int N,
-                                                            int K, int tiles_m, int tiles_n) {
-  __shared__ uint4 a_lds[2][BM * 8];  // [buffer][row * 8 + (chunk ^ (row & 7))]
+// LDS slot of 16-byte chunk c (0..7) of activation-tile row r.  Conflict-free
+// for the MFMA operand reads (16 lanes = 16 consecutive rows, one chunk) with
+// 64 banks, and for 8-lane groups with 32 banks.
+__device__ __forceinline__ int a_slot(int r, int c) {
+  return r * 8 + (c ^ ((r & 7) ^ ((r >> 3) & 1)));
+}
+
+// One workgroup = 4 waves along N; a wave owns MT x NT MFMA tiles of 32x32,
+// i.e. a (32 MT) x (32 NT) sub-tile; the workgroup tile is (32 MT) x (128 NT).
+template <int MT, int NT>
+__global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_kernel(
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
+    const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+    int M, int N, int K, int tiles_m, int tiles_n) {
+  constexpr int BM = 32 * MT;
+  constexpr int BN = 128 * NT;
+  constexpr int A_CHUNKS = BM * 8;                 // 16-byte chunks per activation tile
+  constexpr int A_PER_THREAD = A_CHUNKS / kThreads;
+  __shared__ uint4 a_lds[2][A_CHUNKS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -87,17 +97,15 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(const uint32_t* __re
     bbrow[nt] = biases + nn * gpr;
   }
 
-  // Activation rows this thread stages: idx = tid + 256 * i -> row idx/8, chunk idx%8.
-  const uint4* arow[4];
-  bool aok[4];
+  // Activation chunks this thread stages: idx = tid + 256 i -> row idx/8, chunk idx%8.
+  // Rows past M are clamped to the last row (read, never stored).
+  const uint4* arow[A_PER_THREAD];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < A_PER_THREAD; ++i) {
     const int idx = tid + kThreads * i;
-    const int row = idx >> 3;
-    const int ch = idx & 7;
-    aok[i] = (m0 + row) < M;
-    const size_t rr = aok[i] ? (size_t)(m0 + row) : 0;
-    arow[i] = reinterpret_cast<const uint4*>(x + rr * K) + ch;
+    const int row = m0 + (idx >> 3);
+    const size_t rr = (row < M) ? (size_t)row : (size_t)(M - 1);
+    arow[i] = reinterpret_cast<const uint4*>(x + rr * K) + (idx & 7);
   }
 
   f32x16_t acc[MT][NT];
@@ -109,11 +117,11 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(const uint32_t* __re
       for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.f;
 
   // Prologue: K-step 0.
-  uint4 a_reg[4];
+  uint4 a_reg[A_PER_THREAD];
   uint4 b_reg[NT];
   uint32_t s_reg[NT], bi_reg[NT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) a_reg[i] = aok[i] ? arow[i][0] : make_uint4(0, 0, 0, 0);
+  for (int i = 0; i < A_PER_THREAD; ++i) a_reg[i] = arow[i][0];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     b_reg[nt] = brow[nt][0];
@@ -121,45 +129,42 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(const uint32_t* __re
     bi_reg[nt] = bbrow[nt][0];
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < A_PER_THREAD; ++i) {
     const int idx = tid + kThreads * i;
-    const int row = idx >> 3;
-    const int ch = idx & 7;
-    a_lds[0][row * 8 + (ch ^ (row & 7))] = a_reg[i];
+    a_lds[0][a_slot(idx >> 3, idx & 7)] = a_reg[i];
   }
   __syncthreads();
 
   for (int g = 0; g < gpr; ++g) {
     const int cur = g & 1;
     const bool more = (g + 1) < gpr;
-    uint4 a_nxt[4];
+    // Loads of step g+1 (clamped to the last step: a harmless re-read).
+    const int gn = more ? g + 1 : g;
+    uint4 a_nxt[A_PER_THREAD];
     uint4 b_nxt[NT];
     uint32_t s_nxt[NT], bi_nxt[NT];
-    if (more) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        a_nxt[i] = aok[i] ? arow[i][(g + 1) * 8] : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < A_PER_THREAD; ++i) a_nxt[i] = arow[i][gn * 8];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        b_nxt[nt] = brow[nt][(g + 1) * 2];
-        s_nxt[nt] = srow[nt][g + 1];
-        bi_nxt[nt] = bbrow[nt][g + 1];
-      }
+    for (int nt = 0; nt < NT; ++nt) {
+      b_nxt[nt] = brow[nt][gn * 2];
+      s_nxt[nt] = srow[nt][gn];
+      bi_nxt[nt] = bbrow[nt][gn];
     }
 
     // Dequantize this lane's 32 codes per column tile into 4 MFMA operands.
     bf16x8_t bfrag[NT][4];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const float s = bf16_to_f32(s_reg[nt]);
-      const float b = bf16_to_f32(bi_reg[nt]);
-      const float s24 = s * 0x1p24f;
-      const float s20 = s * 0x1p20f;
+      const float sc = bf16_to_f32(s_reg[nt]);
+      const float bi = bf16_to_f32(bi_reg[nt]);
+      const float s24 = sc * 0x1p24f;
+      const float s20 = sc * 0x1p20f;
       const uint32_t words[4] = {b_reg[nt].x, b_reg[nt].y, b_reg[nt].z, b_reg[nt].w};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         uint32_t p[4];
-        dequant_word_bf16(words[kk], s24, s20, b, p);
+        dequant_word_bf16(words[kk], s24, s20, bi, p);
         u32x4_t v = {p[0], p[1], p[2], p[3]};
         bfrag[nt][kk] = __builtin_bit_cast(bf16x8_t, v);
       }
@@ -171,11 +176,8 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(const uint32_t* __re
     for (int kk = 0; kk < 4; ++kk) {
       bf16x8_t afrag[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int row = mt * 32 + r32;
-        const int ch = 4 * h + kk;
-        afrag[mt] = __builtin_bit_cast(bf16x8_t, a_lds[cur][row * 8 + (ch ^ (row & 7))]);
-      }
+      for (int mt = 0; mt < MT; ++mt)
+        afrag[mt] = __builtin_bit_cast(bf16x8_t, a_lds[cur][a_slot(mt * 32 + r32, 4 * h + kk)]);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -184,20 +186,16 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(const uint32_t* __re
                                                                  acc[mt][nt], 0, 0, 0);
     }
 
-    if (more) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int idx = tid + kThreads * i;
-        const int row = idx >> 3;
-        const int ch = idx & 7;
-        a_lds[cur ^ 1][row * 8 + (ch ^ (row & 7))] = a_nxt[i];
-      }
+    for (int i = 0; i < A_PER_THREAD; ++i) {
+      const int idx = tid + kThreads * i;
+      a_lds[cur ^ 1][a_slot(idx >> 3, idx & 7)] = a_nxt[i];
+    }
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        b_reg[nt] = b_nxt[nt];
-        s_reg[nt] = s_nxt[nt];
-        bi_reg[nt] = bi_nxt[nt];
-      }
+    for (int nt = 0; nt < NT; ++nt) {
+      b_reg[nt] = b_nxt[nt];
+      s_reg[nt] = s_nxt[nt];
+      bi_reg[nt] = bi_nxt[nt];
     }
     __syncthreads();
   }
@@ -218,16 +216,267 @@ __global__ __launch_bounds__(kThreads, 2) void qgemm_kernel(const uint32_t* __re
   }
 }
 
+// ---------------------------------------------------------------------------
+// Large-M kernel: a 256 x 256 workgroup tile, one wave per SIMD (each wave a
+// 256 x 64 sub-tile, 8 x 2 MFMA tiles, 256 fp32 accumulators in AGPRs).
+//
+// Activations and packed weights are staged by direct global->LDS loads
+// (global_load_lds_dwordx4: lane L writes LDS base + 16 L, no VGPRs) into a
+// 3-stage LDS ring, issued two K-steps ahead.  Every step issues the same
+// number of vector-memory instructions (4 scale/bias loads, 2 weight and 8
+// activation direct loads; steps past the end re-load the last step into the
+// free stage), so one fixed `s_waitcnt vmcnt(10)` at the top of step g
+// guarantees that this wave's loads of step g have landed, and a raw
+// s_barrier (no fence, which would wait for every outstanding load) makes the
+// other waves' parts visible and frees the stage that step g+2 overwrites.
+// Within a step, the A fragments of kk+1 are read from LDS and the weight
+// words of kk+1 dequantized while the 16 MFMAs of kk run.
+// ---------------------------------------------------------------------------
+constexpr int kBigBM = 256;
+constexpr int kBigBN = 256;
+constexpr int kStages = 3;
+constexpr int kAStageSlots = kBigBM * 8;  // 16-byte slots of one activation stage
+constexpr int kWStageSlots = kBigBN * 2;  // 16-byte slots of one weight stage
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glob_void_t;
+
+__device__ __forceinline__ void load_lds16(const void* gptr, uint4* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((glob_void_t*)gptr, (lds_void_t*)lds_wave_base, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) leaving expcnt and lgkmcnt unconstrained (gfx9 encoding).
+#define IMQ_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+struct BigRing {
+  uint4* a[kStages];
+  uint4* w[kStages];
+};
+
+// One K-step (one quantization group) of the large-M kernel.  S = g % 3 is a
+// compile-time constant: the stage arrays it reads and the ones its direct
+// loads fill are distinct LDS objects, so the compiler can prove that the
+// in-flight loads into stages S+1 and S+2 do not alias the reads of stage S
+// and does not wait for them.
+template <int S>
+__device__ __forceinline__ void big_step(int g, int gpr, const BigRing& ring,
+                                         const uint16_t* const (&a_src)[8],
+                                         const uint32_t* const (&w_src)[2],
+                                         const uint16_t* const (&s_src)[2],
+                                         const uint16_t* const (&b_src)[2],
+                                         uint32_t (&sc)[kStages][2], uint32_t (&bs)[kStages][2],
+                                         f32x16_t (&acc)[8][2], int wave, int r32, int h) {
+  constexpr int MT = 8, NT = 2;
+  constexpr int S1 = (S + 1) % kStages;
+  constexpr int S2 = (S + 2) % kStages;
+  IMQ_WAIT_VMCNT(10);  // this wave's loads up to step g are done
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Next step's scales (registers), then the tiles of step g+2 (LDS stage S2).
+  const int g1 = min(g + 1, gpr - 1);
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    sc[S1][nt] = s_src[nt][g1];
+    bs[S1][nt] = b_src[nt][g1];
+  }
+  const int g2 = min(g + 2, gpr - 1);
+  {
+    uint4* ab = ring.a[S2] + wave * 64;
+    uint4* wb = ring.w[S2] + wave * 64;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) load_lds16(w_src[i] + (size_t)g2 * 8, wb + i * kThreads);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) load_lds16(a_src[i] + (size_t)g2 * 64, ab + i * kThreads);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // the loads go out before this step's compute
+
+  const uint4* at = ring.a[S];
+  const uint4* wt = ring.w[S];
+  uint4 wraw[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) wraw[nt] = wt[(wave * 64 + nt * 32 + r32) * 2 + h];
+  float s24[NT], s20[NT], bb[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const float sv = bf16_to_f32(sc[S][nt]);
+    s24[nt] = sv * 0x1p24f;
+    s20[nt] = sv * 0x1p20f;
+    bb[nt] = bf16_to_f32(bs[S][nt]);
+  }
+
+  bf16x8_t afrag[2][MT];
+  bf16x8_t bfrag[2][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    afrag[0][mt] = __builtin_bit_cast(bf16x8_t, at[a_slot(mt * 32 + r32, 4 * h)]);
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    uint32_t p[4];
+    dequant_word_bf16(wraw[nt].x, s24[nt], s20[nt], bb[nt], p);
+    bfrag[0][nt] = __builtin_bit_cast(bf16x8_t, u32x4_t{p[0], p[1], p[2], p[3]});
+  }
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    const int cb = kk & 1;
+    if (kk < 3) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        afrag[cb ^ 1][mt] =
+            __builtin_bit_cast(bf16x8_t, at[a_slot(mt * 32 + r32, 4 * h + kk + 1)]);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t word = (kk == 0) ? wraw[nt].y : (kk == 1) ? wraw[nt].z : wraw[nt].w;
+        uint32_t p[4];
+        dequant_word_bf16(word, s24[nt], s20[nt], bb[nt], p);
+        bfrag[cb ^ 1][nt] = __builtin_bit_cast(bf16x8_t, u32x4_t{p[0], p[1], p[2], p[3]});
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afrag[cb][mt], bfrag[cb][nt],
+                                                               acc[mt][nt], 0, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
+    const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+    int M, int N, int K, int tiles_m, int tiles_n) {
+  constexpr int MT = kBigBM / 32;  // 8
+  constexpr int NT = 2;            // 64 columns per wave
+  __shared__ uint4 a_st0[kAStageSlots], a_st1[kAStageSlots], a_st2[kAStageSlots];
+  __shared__ uint4 w_st0[kWStageSlots], w_st1[kWStageSlots], w_st2[kWStageSlots];
+  const BigRing ring = {{a_st0, a_st1, a_st2}, {w_st0, w_st1, w_st2}};
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int r32 = lane & 31;
+  const int h = lane >> 5;
+  int tm, tn;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * kBigBM;
+  const int n0 = tn * kBigBN;
+  const int wpr = K >> 3;
+  const int gpr = K >> 6;
+
+  // Direct-load sources.  Activation slot s = i*256 + tid holds row s/8,
+  // physical chunk s%8, i.e. logical chunk (s%8) ^ f(row) of that row.
+  const uint16_t* a_src[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int slot = i * kThreads + tid;
+    const int row = slot >> 3;
+    const int c = (slot & 7) ^ ((row & 7) ^ ((row >> 3) & 1));
+    const int gr = min(m0 + row, M - 1);
+    a_src[i] = x + (size_t)gr * K + c * 8;
+  }
+  // Weight slot s = i*256 + tid holds row s/2 of the tile, half s%2 of the group.
+  const uint32_t* w_src[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int slot = i * kThreads + tid;
+    const int gr = min(n0 + (slot >> 1), N - 1);
+    w_src[i] = w + (size_t)gr * wpr + (slot & 1) * 4;
+  }
+  // Scale/bias rows of this lane's two MFMA column tiles.
+  const uint16_t* s_src[NT];
+  const uint16_t* b_src[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int gr = min(n0 + wave * 64 + nt * 32 + r32, N - 1);
+    s_src[nt] = scales + (size_t)gr * gpr;
+    b_src[nt] = biases + (size_t)gr * gpr;
+  }
+
+  f32x16_t acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.f;
+
+  // Prologue: scales of step 0, tiles of steps 0 and 1 (clamped), in the same
+  // per-step issue order as big_step (4 scale loads, then 10 tile loads).
+  uint32_t sc[kStages][NT], bs[kStages][NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    sc[0][nt] = s_src[nt][0];
+    bs[0][nt] = b_src[nt][0];
+  }
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    const int gg = min(st, gpr - 1);
+    uint4* ab = ring.a[st] + wave * 64;
+    uint4* wb = ring.w[st] + wave * 64;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) load_lds16(w_src[i] + (size_t)gg * 8, wb + i * kThreads);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) load_lds16(a_src[i] + (size_t)gg * 64, ab + i * kThreads);
+  }
+
+  int g = 0;
+  for (; g + 3 <= gpr; g += 3) {
+    big_step<0>(g, gpr, ring, a_src, w_src, s_src, b_src, sc, bs, acc, wave, r32, h);
+    big_step<1>(g + 1, gpr, ring, a_src, w_src, s_src, b_src, sc, bs, acc, wave, r32, h);
+    big_step<2>(g + 2, gpr, ring, a_src, w_src, s_src, b_src, sc, bs, acc, wave, r32, h);
+  }
+  if (g < gpr) big_step<0>(g, gpr, ring, a_src, w_src, s_src, b_src, sc, bs, acc, wave, r32, h);
+  if (g + 1 < gpr)
+    big_step<1>(g + 1, gpr, ring, a_src, w_src, s_src, b_src, sc, bs, acc, wave, r32, h);
+  IMQ_WAIT_VMCNT(0);  // drain the clamped tail loads before the workgroup ends
+
+  const int nw0 = n0 + wave * 64;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int col = nw0 + nt * 32 + r32;
+      if (col >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (row < M) y[(size_t)row * N + col] = (uint16_t)f32_to_bf16_int(acc[mt][nt][r]);
+      }
+    }
+  }
+}
+
+hipError_t launch_big(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                      const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
+  const int tiles_m = (m + kBigBM - 1) / kBigBM;
+  const int tiles_n = (n + kBigBN - 1) / kBigBN;
+  const dim3 grid((unsigned)tiles_m * (unsigned)tiles_n);
+  hipLaunchKernelGGL(qgemm_big_kernel, grid, dim3(kThreads), 0, stream, w, scales, biases, x, y,
+                     m, n, k, tiles_m, tiles_n);
+  return hipGetLastError();
+}
+
+template <int MT, int NT>
+hipError_t launch_tile(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                       const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
+  const int tiles_m = (m + 32 * MT - 1) / (32 * MT);
+  const int tiles_n = (n + 128 * NT - 1) / (128 * NT);
+  const dim3 grid((unsigned)tiles_m * (unsigned)tiles_n);
+  hipLaunchKernelGGL((qgemm_kernel<MT, NT>), grid, dim3(kThreads), 0, stream, w, scales, biases,
+                     x, y, m, n, k, tiles_m, tiles_n);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_qgemm(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                         const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
-  const int tiles_m = (m + BM - 1) / BM;
-  const int tiles_n = (n + BN - 1) / BN;
-  const dim3 grid((unsigned)tiles_m * (unsigned)tiles_n);
-  hipLaunchKernelGGL(qgemm_kernel, grid, dim3(kThreads), 0, stream, w, scales, biases, x, y, m,
-                     n, k, tiles_m, tiles_n);
-  return hipGetLastError();
+  const char* env = getenv("IMQ_QGEMM_TILE");
+  const int tile = env ? atoi(env) : 0;
+  if (tile == 4) return launch_tile<4, 2>(w, scales, biases, x, y, k, n, m, stream);
+  if (tile == 8) return launch_tile<8, 2>(w, scales, biases, x, y, k, n, m, stream);
+  return launch_big(w, scales, biases, x, y, k, n, m, stream);
 }
 
 }  // namespace imq
