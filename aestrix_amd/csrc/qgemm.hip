@@ -217,40 +217,56 @@ __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_
 }
 
 // ---------------------------------------------------------------------------
-// Large-M kernel: a 256 x 256 workgroup tile, one wave per SIMD (each wave a
-// 256 x 64 sub-tile, 8 x 2 MFMA tiles, 256 fp32 accumulators in AGPRs).
+// Large-M kernel: a (32 MT) x 256 workgroup tile, one wave per SIMD (each wave
+// a (32 MT) x 64 sub-tile, MT x 2 MFMA tiles, up to 256 fp32 accumulators per
+// lane in AGPRs).
 //
-// Activations and packed weights are staged by direct global->LDS loads
-// (global_load_lds_dwordx4: lane L writes LDS base + 16 L, no VGPRs) into a
-// 3-stage LDS ring, issued two K-steps ahead.  Every step issues the same
-// number of vector-memory instructions (4 scale/bias loads, 2 weight and 8
-// activation direct loads; steps past the end re-load the last step into the
-// free stage), so one fixed `s_waitcnt vmcnt(10)` at the top of step g
+// Activations and packed weights are staged by direct buffer->LDS loads
+// (buffer_load_dwordx4 ... lds: lane L writes LDS base + 16 L, no VGPRs; the
+// per-lane byte offset is fixed for the whole K loop and the K-step advance
+// is a scalar offset, so a load costs no vector ALU work) into a 3-stage LDS
+// ring, issued two K-steps ahead.  Every step issues the same number of
+// vector-memory instructions (4 scale/bias loads, then 2 weight and MT
+// activation loads; steps past the end re-load the last step into the free
+// stage), so one fixed `s_waitcnt vmcnt(2 + MT)` at the top of step g
 // guarantees that this wave's loads of step g have landed, and a raw
 // s_barrier (no fence, which would wait for every outstanding load) makes the
 // other waves' parts visible and frees the stage that step g+2 overwrites.
-// Within a step, the A fragments of kk+1 are read from LDS and the weight
-// words of kk+1 dequantized while the 16 MFMAs of kk run.
+// Within a step, the A fragments of k-slice kk+1 are read from LDS and the
+// weight words of kk+1 dequantized while the MFMAs of kk run.
 // ---------------------------------------------------------------------------
-constexpr int kBigBM = 256;
 constexpr int kBigBN = 256;
 constexpr int kStages = 3;
-constexpr int kAStageSlots = kBigBM * 8;  // 16-byte slots of one activation stage
 constexpr int kWStageSlots = kBigBN * 2;  // 16-byte slots of one weight stage
 
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glob_void_t;
 
-__device__ __forceinline__ void load_lds16(const void* gptr, uint4* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((glob_void_t*)gptr, (lds_void_t*)lds_wave_base, 16, 0, 0);
+// Raw buffer resource over [base, base + bytes) (gfx9 word 3: 32-bit data format).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff,
+                                           uint4* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds_wave_base, 16, voff, soff, 0, 0);
 }
 
 // s_waitcnt vmcnt(n) leaving expcnt and lgkmcnt unconstrained (gfx9 encoding).
 #define IMQ_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 
+template <int MT>
 struct BigRing {
   uint4* a[kStages];
   uint4* w[kStages];
+};
+
+template <int MT>
+struct BigSrc {
+  __amdgpu_buffer_rsrc_t xr, wr;
+  uint32_t a_off[MT];  // byte offsets of this thread's activation slots
+  uint32_t w_off[2];   // byte offsets of this thread's weight slots
+  const uint16_t* s_src[2];
+  const uint16_t* b_src[2];
 };
 
 // One K-step (one quantization group) of the large-M kernel.  S = g % 3 is a
@@ -258,18 +274,15 @@ struct BigRing {
 // loads fill are distinct LDS objects, so the compiler can prove that the
 // in-flight loads into stages S+1 and S+2 do not alias the reads of stage S
 // and does not wait for them.
-template <int S>
-__device__ __forceinline__ void big_step(int g, int gpr, const BigRing& ring,
-                                         const uint16_t* const (&a_src)[8],
-                                         const uint32_t* const (&w_src)[2],
-                                         const uint16_t* const (&s_src)[2],
-                                         const uint16_t* const (&b_src)[2],
-                                         uint32_t (&sc)[kStages][2], uint32_t (&bs)[kStages][2],
-                                         f32x16_t (&acc)[8][2], int wave, int r32, int h) {
-  constexpr int MT = 8, NT = 2;
+template <int MT, int S>
+__device__ __forceinline__ void big_step(int g, int gpr, const BigRing<MT>& ring,
+                                         const BigSrc<MT>& src, uint32_t (&sc)[kStages][2],
+                                         uint32_t (&bs)[kStages][2], f32x16_t (&acc)[MT][2],
+                                         int wave, int r32, int h) {
+  constexpr int NT = 2;
   constexpr int S1 = (S + 1) % kStages;
   constexpr int S2 = (S + 2) % kStages;
-  IMQ_WAIT_VMCNT(10);  // this wave's loads up to step g are done
+  IMQ_WAIT_VMCNT(2 + MT);  // this wave's loads up to step g are done
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
@@ -278,17 +291,17 @@ __device__ __forceinline__ void big_step(int g, int gpr, const BigRing& ring,
   const int g1 = min(g + 1, gpr - 1);
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    sc[S1][nt] = s_src[nt][g1];
-    bs[S1][nt] = b_src[nt][g1];
+    sc[S1][nt] = src.s_src[nt][g1];
+    bs[S1][nt] = src.b_src[nt][g1];
   }
-  const int g2 = min(g + 2, gpr - 1);
+  const uint32_t g2 = (uint32_t)min(g + 2, gpr - 1);
   {
     uint4* ab = ring.a[S2] + wave * 64;
     uint4* wb = ring.w[S2] + wave * 64;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) load_lds16(w_src[i] + (size_t)g2 * 8, wb + i * kThreads);
+    for (int i = 0; i < 2; ++i) load_lds16(src.wr, src.w_off[i], g2 * 32u, wb + i * kThreads);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) load_lds16(a_src[i] + (size_t)g2 * 64, ab + i * kThreads);
+    for (int i = 0; i < MT; ++i) load_lds16(src.xr, src.a_off[i], g2 * 128u, ab + i * kThreads);
   }
   __builtin_amdgcn_sched_barrier(0);  // the loads go out before this step's compute
 
@@ -342,55 +355,54 @@ __device__ __forceinline__ void big_step(int g, int gpr, const BigRing& ring,
   }
 }
 
+template <int MT>
 __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
     int M, int N, int K, int tiles_m, int tiles_n) {
-  constexpr int MT = kBigBM / 32;  // 8
-  constexpr int NT = 2;            // 64 columns per wave
-  __shared__ uint4 a_st0[kAStageSlots], a_st1[kAStageSlots], a_st2[kAStageSlots];
+  constexpr int BM = 32 * MT;
+  constexpr int NT = 2;  // 64 columns per wave
+  constexpr int A_SLOTS = BM * 8;
+  __shared__ uint4 a_st0[A_SLOTS], a_st1[A_SLOTS], a_st2[A_SLOTS];
   __shared__ uint4 w_st0[kWStageSlots], w_st1[kWStageSlots], w_st2[kWStageSlots];
-  const BigRing ring = {{a_st0, a_st1, a_st2}, {w_st0, w_st1, w_st2}};
+  const BigRing<MT> ring = {{a_st0, a_st1, a_st2}, {w_st0, w_st1, w_st2}};
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31;
   const int h = lane >> 5;
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * kBigBM;
+  const int m0 = tm * BM;
   const int n0 = tn * kBigBN;
-  const int wpr = K >> 3;
   const int gpr = K >> 6;
 
-  // Direct-load sources.  Activation slot s = i*256 + tid holds row s/8,
-  // physical chunk s%8, i.e. logical chunk (s%8) ^ f(row) of that row.
-  const uint16_t* a_src[8];
+  BigSrc<MT> src;
+  src.xr = make_rsrc(x, (uint32_t)((size_t)M * K * 2));
+  src.wr = make_rsrc(w, (uint32_t)((size_t)N * K / 2));
+  // Activation slot s = i*256 + tid holds tile row s/8, physical chunk s%8,
+  // i.e. logical chunk (s%8) ^ f(row) of that row.  Rows past M are clamped.
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < MT; ++i) {
     const int slot = i * kThreads + tid;
     const int row = slot >> 3;
     const int c = (slot & 7) ^ ((row & 7) ^ ((row >> 3) & 1));
-    const int gr = min(m0 + row, M - 1);
-    a_src[i] = x + (size_t)gr * K + c * 8;
+    const uint32_t gr = (uint32_t)min(m0 + row, M - 1);
+    src.a_off[i] = (gr * (uint32_t)K + (uint32_t)c * 8u) * 2u;
   }
-  // Weight slot s = i*256 + tid holds row s/2 of the tile, half s%2 of the group.
-  const uint32_t* w_src[2];
+  // Weight slot s = i*256 + tid holds tile row s/2, half s%2 of the group.
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int slot = i * kThreads + tid;
-    const int gr = min(n0 + (slot >> 1), N - 1);
-    w_src[i] = w + (size_t)gr * wpr + (slot & 1) * 4;
+    const uint32_t gr = (uint32_t)min(n0 + (slot >> 1), N - 1);
+    src.w_off[i] = gr * (uint32_t)(K / 2) + (uint32_t)(slot & 1) * 16u;
   }
-  // Scale/bias rows of this lane's two MFMA column tiles.
-  const uint16_t* s_src[NT];
-  const uint16_t* b_src[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int gr = min(n0 + wave * 64 + nt * 32 + r32, N - 1);
-    s_src[nt] = scales + (size_t)gr * gpr;
-    b_src[nt] = biases + (size_t)gr * gpr;
+    src.s_src[nt] = scales + (size_t)gr * gpr;
+    src.b_src[nt] = biases + (size_t)gr * gpr;
   }
 
   f32x16_t acc[MT][NT];
@@ -402,33 +414,32 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
       for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.f;
 
   // Prologue: scales of step 0, tiles of steps 0 and 1 (clamped), in the same
-  // per-step issue order as big_step (4 scale loads, then 10 tile loads).
+  // per-step issue order as big_step.
   uint32_t sc[kStages][NT], bs[kStages][NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    sc[0][nt] = s_src[nt][0];
-    bs[0][nt] = b_src[nt][0];
+    sc[0][nt] = src.s_src[nt][0];
+    bs[0][nt] = src.b_src[nt][0];
   }
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
-    const int gg = min(st, gpr - 1);
+    const uint32_t gg = (uint32_t)min(st, gpr - 1);
     uint4* ab = ring.a[st] + wave * 64;
     uint4* wb = ring.w[st] + wave * 64;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) load_lds16(w_src[i] + (size_t)gg * 8, wb + i * kThreads);
+    for (int i = 0; i < 2; ++i) load_lds16(src.wr, src.w_off[i], gg * 32u, wb + i * kThreads);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) load_lds16(a_src[i] + (size_t)gg * 64, ab + i * kThreads);
+    for (int i = 0; i < MT; ++i) load_lds16(src.xr, src.a_off[i], gg * 128u, ab + i * kThreads);
   }
 
   int g = 0;
   for (; g + 3 <= gpr; g += 3) {
-    big_step<0>(g, gpr, ring, a_src, w_src, s_src, b_src, sc, bs, acc, wave, r32, h);
-    big_step<1>(g + 1, gpr, ring, a_src, w_src, s_src, b_src, sc, bs, acc, wave, r32, h);
-    big_step<2>(g + 2, gpr, ring, a_src, w_src, s_src, b_src, sc, bs, acc, wave, r32, h);
+    big_step<MT, 0>(g, gpr, ring, src, sc, bs, acc, wave, r32, h);
+    big_step<MT, 1>(g + 1, gpr, ring, src, sc, bs, acc, wave, r32, h);
+    big_step<MT, 2>(g + 2, gpr, ring, src, sc, bs, acc, wave, r32, h);
   }
-  if (g < gpr) big_step<0>(g, gpr, ring, a_src, w_src, s_src, b_src, sc, bs, acc, wave, r32, h);
-  if (g + 1 < gpr)
-    big_step<1>(g + 1, gpr, ring, a_src, w_src, s_src, b_src, sc, bs, acc, wave, r32, h);
+  if (g < gpr) big_step<MT, 0>(g, gpr, ring, src, sc, bs, acc, wave, r32, h);
+  if (g + 1 < gpr) big_step<MT, 1>(g + 1, gpr, ring, src, sc, bs, acc, wave, r32, h);
   IMQ_WAIT_VMCNT(0);  // drain the clamped tail loads before the workgroup ends
 
   const int nw0 = n0 + wave * 64;
@@ -447,14 +458,34 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   }
 }
 
+template <int MT>
 hipError_t launch_big(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                       const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
-  const int tiles_m = (m + kBigBM - 1) / kBigBM;
+  const int tiles_m = (m + 32 * MT - 1) / (32 * MT);
   const int tiles_n = (n + kBigBN - 1) / kBigBN;
   const dim3 grid((unsigned)tiles_m * (unsigned)tiles_n);
-  hipLaunchKernelGGL(qgemm_big_kernel, grid, dim3(kThreads), 0, stream, w, scales, biases, x, y,
-                     m, n, k, tiles_m, tiles_n);
+  hipLaunchKernelGGL((qgemm_big_kernel<MT>), grid, dim3(kThreads), 0, stream, w, scales, biases,
+                     x, y, m, n, k, tiles_m, tiles_n);
   return hipGetLastError();
+}
+
+// Tile height for the large-M kernel: fewest estimated tile-rounds over the
+// chip, each round costing about (MT + 1.5) units (MFMA work plus per-tile
+// dequant, prologue and epilogue).
+int pick_big_mt(int m, int n, int cus) {
+  const int tiles_n = (n + kBigBN - 1) / kBigBN;
+  int best = 8;
+  double best_cost = 1e30;
+  for (int mt : {8, 6, 4}) {
+    const long tiles = (long)((m + 32 * mt - 1) / (32 * mt)) * tiles_n;
+    const long rounds = (tiles + cus - 1) / cus;
+    const double cost = (double)rounds * (mt + 1.5);
+    if (cost < best_cost - 1e-9) {
+      best_cost = cost;
+      best = mt;
+    }
+  }
+  return best;
 }
 
 template <int MT, int NT>
@@ -472,11 +503,29 @@ hipError_t launch_tile(const uint32_t* w, const uint16_t* scales, const uint16_t
 
 hipError_t launch_qgemm(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                         const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
+  // The buffer-load kernel addresses x and w with 32-bit byte offsets.
+  const bool fits32 = (size_t)m * k * 2 < ((size_t)1 << 31) && (size_t)n * k / 2 < ((size_t)1 << 31);
   const char* env = getenv("IMQ_QGEMM_TILE");
   const int tile = env ? atoi(env) : 0;
-  if (tile == 4) return launch_tile<4, 2>(w, scales, biases, x, y, k, n, m, stream);
-  if (tile == 8) return launch_tile<8, 2>(w, scales, biases, x, y, k, n, m, stream);
-  return launch_big(w, scales, biases, x, y, k, n, m, stream);
+  if (tile == 4 || !fits32) return launch_tile<4, 2>(w, scales, biases, x, y, k, n, m, stream);
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      cus = v;
+    else
+      cus = 256;
+  }
+  int mt = pick_big_mt(m, n, cus);
+  if (tile == 16) mt = 4;
+  if (tile == 24) mt = 6;
+  if (tile == 32) mt = 8;
+  switch (mt) {
+    case 4: return launch_big<4>(w, scales, biases, x, y, k, n, m, stream);
+    case 6: return launch_big<6>(w, scales, biases, x, y, k, n, m, stream);
+    default: return launch_big<8>(w, scales, biases, x, y, k, n, m, stream);
+  }
 }
 
 }  // namespace imq
