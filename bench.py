@@ -15,7 +15,10 @@ over that synthetic batch, inputs resident in HBM.  The same line carries:
 * cpu_baseline -- the C oracle's f32-accumulating CPU quantized matmul
                 (MLX is not available) on a bounded sample of the same problem.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 100] [--no-cpu-baseline]
+
+The default warm-up (about 60 ms of qGEMM work) is past the clock transient
+that the first ~15 ms of sustained MFMA load shows on this GPU.
 """
 
 from __future__ import annotations
@@ -178,6 +181,24 @@ def cpu_baseline(synth, seconds: float = 10.0) -> dict:
                       f"target problem, {calls} calls in {el:.1f} s on {threads} OpenMP threads"}
 
 
+def floors(torch) -> int:
+    """Reference kernels for reading kernel durations under rocprofv3: a
+    one-element fill (the launch floor) and a full-tensor sum over each of 48
+    distinct 12.45 MB buffers (the streaming-read floor at the qGEMV weight
+    size, past the 256 MB MALL)."""
+    t = torch.empty(1, dtype=torch.float32, device="cuda")
+    for _ in range(200):
+        t.zero_()
+    bufs = [torch.ones(9728 * 2560 // 8, dtype=torch.int32, device="cuda") for _ in range(48)]
+    out = torch.empty((), dtype=torch.int64, device="cuda")
+    for _ in range(5):
+        for b in bufs:
+            torch.sum(b, dim=0, out=out)
+    torch.cuda.synchronize()
+    log("floors: 200 one-element fills; 240 sums over 12451840-byte int32 buffers")
+    return 0
+
+
 def traffic_from_profiles():
     path = os.path.join(ROOT, "profiles", "qgemm_target_traffic.json")
     if not os.path.exists(path):
@@ -189,11 +210,13 @@ def traffic_from_profiles():
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-target", action="store_true",
                     help="time the headline qGEMM only (for profiling runs)")
+    ap.add_argument("--floors", action="store_true",
+                    help="run the launch and streaming-read floor kernels only (for profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} requested, but this path runs on one GPU "
@@ -209,6 +232,8 @@ def main() -> int:
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
     torch.cuda.set_device(0)
+    if args.floors:
+        return floors(torch)
     imq._lib.load()
     props = torch.cuda.get_device_properties(0)
 

@@ -19,7 +19,9 @@
  *   y[M, N]      = x[M, K] . deq(W)^T, accumulated in fp32, rounded to T.
  * All tensors are row-major and contiguous; sub-tensors (row halves, the
  * reference's setBuffer byte offsets, DirectDiTStep.swift:576-579) are passed
- * as offset device pointers.  Every device pointer must be 16-byte aligned.
+ * as offset device pointers.  w, x and the dequantize output must be 16-byte
+ * aligned (any whole number of rows of a K % 64 == 0 matrix keeps that);
+ * scales, biases and y must be 2-byte aligned.
  *
  * Conventions:
  *   - Every call returns an imq_status (0 = IMQ_OK).  No C++ exception crosses
@@ -92,8 +94,9 @@ int imq_memcpy_d2h(imq_ctx* ctx, void* dst, const void* src, size_t bytes, imq_s
 /* out[N, K] (T) = deq(W).  Replaces MLX `dequantized(w, scales:, biases:,
  * groupSize: 64, bits: 4)` (DirectTEEncoder.swift:129-134) and the CPU
  * embedding dequant DirectTEEncoder.embedRow (DirectTEEncoder.swift:106-123).
- * Bit-exact: RNE_T(fl32(s*q + b)), RNE by the integer rounding of
- * DirectTEEncoder.swift:39-43 for bf16. */
+ * Bit-exact: RNE_T(fl32(fl32(s*q) + b)), the rounding of
+ * DirectTEEncoder.swift:39-43 for every non-NaN value (a NaN result, possible
+ * only when a scale or bias is inf or NaN, stays a quiet NaN). */
 int imq_dequantize(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
                    void* out, int k, int n, int group_size, int bits, imq_dtype dtype,
                    imq_stream stream);
