@@ -221,11 +221,13 @@ __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_
 // a (32 MT) x 64 sub-tile, MT x 2 MFMA tiles, up to 256 fp32 accumulators per
 // lane in AGPRs).
 //
-// Activations and packed weights are staged by direct buffer->LDS loads
-// (buffer_load_dwordx4 ... lds: lane L writes LDS base + 16 L, no VGPRs; the
-// per-lane byte offset is fixed for the whole K loop and the K-step advance
-// is a scalar offset, so a load costs no vector ALU work) into a 3-stage LDS
-// ring, issued two K-steps ahead.  Every step issues the same number of
+// Activations are staged by direct buffer->LDS loads (buffer_load_dwordx4 ...
+// lds: lane L writes LDS base + 16 L, no VGPRs; the per-lane byte offset is
+// fixed for the whole K loop and the K-step advance is a scalar offset, so a
+// load costs no vector ALU work) into a 3-stage LDS ring, issued two K-steps
+// ahead.  Packed weights need no sharing between waves (each wave owns its
+// columns), so they are loaded straight into registers, also two steps ahead,
+// keeping their bytes off the LDS port that the activation reads saturate.  Every step issues the same number of
 // vector-memory instructions (4 scale/bias loads, then 2 weight and MT
 // activation loads; steps past the end re-load the last step into the free
 // stage), so one fixed `s_waitcnt vmcnt(2 + MT)` at the top of step g
@@ -237,7 +239,6 @@ __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_
 // ---------------------------------------------------------------------------
 constexpr int kBigBN = 256;
 constexpr int kStages = 3;
-constexpr int kWStageSlots = kBigBN * 2;  // 16-byte slots of one weight stage
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -251,22 +252,36 @@ __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t rs, uint32_t v
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds_wave_base, 16, voff, soff, 0, 0);
 }
 
+// 16 bytes of packed weights straight into registers (buffer_load_dwordx4).
+__device__ __forceinline__ u32x4_t load_w16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0));
+}
+
 // s_waitcnt vmcnt(n) leaving expcnt and lgkmcnt unconstrained (gfx9 encoding).
 #define IMQ_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 
-template <int MT>
-struct BigRing {
-  uint4* a[kStages];
-  uint4* w[kStages];
+// Tile geometry: WM x WN = 4 waves; a wave owns MTW x NTW MFMA tiles of 32x32
+// (a (32 MTW) x (32 NTW) sub-tile); the workgroup tile is
+// (32 MTW WM) x (32 NTW WN) with WN * 32 * NTW = 256 columns.
+template <int MTW, int NTW, int WM>
+struct BigCfg {
+  static constexpr int kWN = 4 / WM;
+  static constexpr int kBM = 32 * MTW * WM;
+  static constexpr int kA = kBM * 8 / kThreads;  // activation slots per thread per step
+  static_assert(32 * NTW * kWN == kBigBN, "workgroup tile must be 256 columns wide");
 };
 
-template <int MT>
+struct BigRing {
+  uint4* a[kStages];
+};
+
+template <int MTW, int NTW, int WM>
 struct BigSrc {
   __amdgpu_buffer_rsrc_t xr, wr;
-  uint32_t a_off[MT];  // byte offsets of this thread's activation slots
-  uint32_t w_off[2];   // byte offsets of this thread's weight slots
-  const uint16_t* s_src[2];
-  const uint16_t* b_src[2];
+  uint32_t a_off[BigCfg<MTW, NTW, WM>::kA];  // byte offsets of this thread's activation slots
+  uint32_t w_off[NTW];  // byte offsets of this lane's 16 weight bytes, per column tile
+  const uint16_t* s_src[NTW];
+  const uint16_t* b_src[NTW];
 };
 
 // One K-step (one quantization group) of the large-M kernel.  S = g % 3 is a
@@ -274,58 +289,58 @@ struct BigSrc {
 // loads fill are distinct LDS objects, so the compiler can prove that the
 // in-flight loads into stages S+1 and S+2 do not alias the reads of stage S
 // and does not wait for them.
-template <int MT, int S>
-__device__ __forceinline__ void big_step(int g, int gpr, const BigRing<MT>& ring,
-                                         const BigSrc<MT>& src, uint32_t (&sc)[kStages][2],
-                                         uint32_t (&bs)[kStages][2], f32x16_t (&acc)[MT][2],
-                                         int wave, int r32, int h) {
-  constexpr int NT = 2;
+template <int MTW, int NTW, int WM, int S>
+__device__ __forceinline__ void big_step(int g, int gpr, const BigRing& ring,
+                                         const BigSrc<MTW, NTW, WM>& src,
+                                         uint32_t (&sc)[kStages][NTW], uint32_t (&bs)[kStages][NTW],
+                                         u32x4_t (&wr)[kStages][NTW], f32x16_t (&acc)[MTW][NTW],
+                                         int wave, int arow0, int r32, int h) {
+  using C = BigCfg<MTW, NTW, WM>;
   constexpr int S1 = (S + 1) % kStages;
   constexpr int S2 = (S + 2) % kStages;
-  IMQ_WAIT_VMCNT(2 + MT);  // this wave's loads up to step g are done
+  IMQ_WAIT_VMCNT(NTW + C::kA);  // this wave's loads up to step g are done
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
-  // Next step's scales (registers), then the tiles of step g+2 (LDS stage S2).
+  // Next step's scales, then the weights (registers) and activations (LDS
+  // stage S2) of step g+2.
   const int g1 = min(g + 1, gpr - 1);
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
+  for (int nt = 0; nt < NTW; ++nt) {
     sc[S1][nt] = src.s_src[nt][g1];
     bs[S1][nt] = src.b_src[nt][g1];
   }
   const uint32_t g2 = (uint32_t)min(g + 2, gpr - 1);
+#pragma unroll
+  for (int nt = 0; nt < NTW; ++nt) wr[S2][nt] = load_w16(src.wr, src.w_off[nt], g2 * 32u);
   {
     uint4* ab = ring.a[S2] + wave * 64;
-    uint4* wb = ring.w[S2] + wave * 64;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) load_lds16(src.wr, src.w_off[i], g2 * 32u, wb + i * kThreads);
-#pragma unroll
-    for (int i = 0; i < MT; ++i) load_lds16(src.xr, src.a_off[i], g2 * 128u, ab + i * kThreads);
+    for (int i = 0; i < C::kA; ++i) load_lds16(src.xr, src.a_off[i], g2 * 128u, ab + i * kThreads);
   }
   __builtin_amdgcn_sched_barrier(0);  // the loads go out before this step's compute
 
   const uint4* at = ring.a[S];
-  const uint4* wt = ring.w[S];
-  uint4 wraw[NT];
+  u32x4_t wraw[NTW];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) wraw[nt] = wt[(wave * 64 + nt * 32 + r32) * 2 + h];
-  float s24[NT], s20[NT], bb[NT];
+  for (int nt = 0; nt < NTW; ++nt) wraw[nt] = wr[S][nt];
+  float s24[NTW], s20[NTW], bb[NTW];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
+  for (int nt = 0; nt < NTW; ++nt) {
     const float sv = bf16_to_f32(sc[S][nt]);
     s24[nt] = sv * 0x1p24f;
     s20[nt] = sv * 0x1p20f;
     bb[nt] = bf16_to_f32(bs[S][nt]);
   }
 
-  bf16x8_t afrag[2][MT];
-  bf16x8_t bfrag[2][NT];
+  bf16x8_t afrag[2][MTW];
+  bf16x8_t bfrag[2][NTW];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-    afrag[0][mt] = __builtin_bit_cast(bf16x8_t, at[a_slot(mt * 32 + r32, 4 * h)]);
+  for (int mt = 0; mt < MTW; ++mt)
+    afrag[0][mt] = __builtin_bit_cast(bf16x8_t, at[a_slot(arow0 + mt * 32 + r32, 4 * h)]);
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
+  for (int nt = 0; nt < NTW; ++nt) {
     uint32_t p[4];
     dequant_word_bf16(wraw[nt].x, s24[nt], s20[nt], bb[nt], p);
     bfrag[0][nt] = __builtin_bit_cast(bf16x8_t, u32x4_t{p[0], p[1], p[2], p[3]});
@@ -333,13 +348,14 @@ __device__ __forceinline__ void big_step(int g, int gpr, const BigRing<MT>& ring
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
     const int cb = kk & 1;
+    __builtin_amdgcn_sched_barrier(0);
     if (kk < 3) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MTW; ++mt)
         afrag[cb ^ 1][mt] =
-            __builtin_bit_cast(bf16x8_t, at[a_slot(mt * 32 + r32, 4 * h + kk + 1)]);
+            __builtin_bit_cast(bf16x8_t, at[a_slot(arow0 + mt * 32 + r32, 4 * h + kk + 1)]);
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
+      for (int nt = 0; nt < NTW; ++nt) {
         const uint32_t word = (kk == 0) ? wraw[nt].y : (kk == 1) ? wraw[nt].z : wraw[nt].w;
         uint32_t p[4];
         dequant_word_bf16(word, s24[nt], s20[nt], bb[nt], p);
@@ -347,77 +363,89 @@ __device__ __forceinline__ void big_step(int g, int gpr, const BigRing<MT>& ring
       }
     }
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
+      for (int nt = 0; nt < NTW; ++nt)
         acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afrag[cb][mt], bfrag[cb][nt],
                                                                acc[mt][nt], 0, 0, 0);
+    if (kk < 3) {
+      // Interleave: every MFMA of this k-slice is followed by a share of the
+      // next slice's dequant VALU work and, for the first MTW, one LDS read,
+      // so a single wave keeps the matrix core fed while it dequantizes.
+      constexpr int kMfma = MTW * NTW;
+      constexpr int kValuPer = (NTW * 17 + kMfma - 1) / kMfma;
+#pragma unroll
+      for (int i = 0; i < kMfma; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        if (i < MTW) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);  // VALU
+      }
+    }
   }
 }
 
-template <int MT>
+template <int MTW, int NTW, int WM>
 __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
     int M, int N, int K, int tiles_m, int tiles_n) {
-  constexpr int BM = 32 * MT;
-  constexpr int NT = 2;  // 64 columns per wave
-  constexpr int A_SLOTS = BM * 8;
+  using C = BigCfg<MTW, NTW, WM>;
+  constexpr int A_SLOTS = C::kBM * 8;
   __shared__ uint4 a_st0[A_SLOTS], a_st1[A_SLOTS], a_st2[A_SLOTS];
-  __shared__ uint4 w_st0[kWStageSlots], w_st1[kWStageSlots], w_st2[kWStageSlots];
-  const BigRing<MT> ring = {{a_st0, a_st1, a_st2}, {w_st0, w_st1, w_st2}};
+  const BigRing ring = {{a_st0, a_st1, a_st2}};
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / C::kWN;
+  const int wn = wave - wm * C::kWN;
   const int r32 = lane & 31;
   const int h = lane >> 5;
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * BM;
+  const int m0 = tm * C::kBM;
   const int n0 = tn * kBigBN;
+  const int arow0 = wm * 32 * MTW;        // this wave's first row inside the tile
+  const int ncol0 = n0 + wn * 32 * NTW;   // this wave's first output column
   const int gpr = K >> 6;
 
-  BigSrc<MT> src;
+  BigSrc<MTW, NTW, WM> src;
   src.xr = make_rsrc(x, (uint32_t)((size_t)M * K * 2));
   src.wr = make_rsrc(w, (uint32_t)((size_t)N * K / 2));
   // Activation slot s = i*256 + tid holds tile row s/8, physical chunk s%8,
   // i.e. logical chunk (s%8) ^ f(row) of that row.  Rows past M are clamped.
 #pragma unroll
-  for (int i = 0; i < MT; ++i) {
+  for (int i = 0; i < C::kA; ++i) {
     const int slot = i * kThreads + tid;
     const int row = slot >> 3;
     const int c = (slot & 7) ^ ((row & 7) ^ ((row >> 3) & 1));
     const uint32_t gr = (uint32_t)min(m0 + row, M - 1);
     src.a_off[i] = (gr * (uint32_t)K + (uint32_t)c * 8u) * 2u;
   }
-  // Weight slot s = i*256 + tid holds tile row s/2, half s%2 of the group.
+  // In MFMA operand layout lane (r32, h) of column tile nt owns weight row
+  // ncol0 + 32 nt + r32 and bytes [16 h, 16 h + 16) of each group.
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int slot = i * kThreads + tid;
-    const uint32_t gr = (uint32_t)min(n0 + (slot >> 1), N - 1);
-    src.w_off[i] = gr * (uint32_t)(K / 2) + (uint32_t)(slot & 1) * 16u;
-  }
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int gr = min(n0 + wave * 64 + nt * 32 + r32, N - 1);
+  for (int nt = 0; nt < NTW; ++nt) {
+    const int gr = min(ncol0 + nt * 32 + r32, N - 1);
+    src.w_off[nt] = (uint32_t)gr * (uint32_t)(K / 2) + (uint32_t)h * 16u;
     src.s_src[nt] = scales + (size_t)gr * gpr;
     src.b_src[nt] = biases + (size_t)gr * gpr;
   }
 
-  f32x16_t acc[MT][NT];
+  f32x16_t acc[MTW][NTW];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
+    for (int nt = 0; nt < NTW; ++nt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.f;
 
-  // Prologue: scales of step 0, tiles of steps 0 and 1 (clamped), in the same
-  // per-step issue order as big_step.
-  uint32_t sc[kStages][NT], bs[kStages][NT];
+  // Prologue: scales of step 0, weights and activations of steps 0 and 1
+  // (clamped), in the same per-step issue order as big_step.
+  uint32_t sc[kStages][NTW], bs[kStages][NTW];
+  u32x4_t wr[kStages][NTW];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
+  for (int nt = 0; nt < NTW; ++nt) {
     sc[0][nt] = src.s_src[nt][0];
     bs[0][nt] = src.b_src[nt][0];
   }
@@ -425,47 +453,47 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   for (int st = 0; st < 2; ++st) {
     const uint32_t gg = (uint32_t)min(st, gpr - 1);
     uint4* ab = ring.a[st] + wave * 64;
-    uint4* wb = ring.w[st] + wave * 64;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) load_lds16(src.wr, src.w_off[i], gg * 32u, wb + i * kThreads);
+    for (int nt = 0; nt < NTW; ++nt) wr[st][nt] = load_w16(src.wr, src.w_off[nt], gg * 32u);
 #pragma unroll
-    for (int i = 0; i < MT; ++i) load_lds16(src.xr, src.a_off[i], gg * 128u, ab + i * kThreads);
+    for (int i = 0; i < C::kA; ++i) load_lds16(src.xr, src.a_off[i], gg * 128u, ab + i * kThreads);
   }
 
   int g = 0;
   for (; g + 3 <= gpr; g += 3) {
-    big_step<MT, 0>(g, gpr, ring, src, sc, bs, acc, wave, r32, h);
-    big_step<MT, 1>(g + 1, gpr, ring, src, sc, bs, acc, wave, r32, h);
-    big_step<MT, 2>(g + 2, gpr, ring, src, sc, bs, acc, wave, r32, h);
+    big_step<MTW, NTW, WM, 0>(g, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
+    big_step<MTW, NTW, WM, 1>(g + 1, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
+    big_step<MTW, NTW, WM, 2>(g + 2, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
   }
-  if (g < gpr) big_step<MT, 0>(g, gpr, ring, src, sc, bs, acc, wave, r32, h);
-  if (g + 1 < gpr) big_step<MT, 1>(g + 1, gpr, ring, src, sc, bs, acc, wave, r32, h);
+  if (g < gpr) big_step<MTW, NTW, WM, 0>(g, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
+  if (g + 1 < gpr)
+    big_step<MTW, NTW, WM, 1>(g + 1, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
   IMQ_WAIT_VMCNT(0);  // drain the clamped tail loads before the workgroup ends
 
-  const int nw0 = n0 + wave * 64;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
+  for (int mt = 0; mt < MTW; ++mt) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int col = nw0 + nt * 32 + r32;
+    for (int nt = 0; nt < NTW; ++nt) {
+      const int col = ncol0 + nt * 32 + r32;
       if (col >= N) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int row = m0 + arow0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
         if (row < M) y[(size_t)row * N + col] = (uint16_t)f32_to_bf16_int(acc[mt][nt][r]);
       }
     }
   }
 }
 
-template <int MT>
+template <int MTW, int NTW, int WM>
 hipError_t launch_big(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                       const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
-  const int tiles_m = (m + 32 * MT - 1) / (32 * MT);
+  constexpr int BM = BigCfg<MTW, NTW, WM>::kBM;
+  const int tiles_m = (m + BM - 1) / BM;
   const int tiles_n = (n + kBigBN - 1) / kBigBN;
   const dim3 grid((unsigned)tiles_m * (unsigned)tiles_n);
-  hipLaunchKernelGGL((qgemm_big_kernel<MT>), grid, dim3(kThreads), 0, stream, w, scales, biases,
-                     x, y, m, n, k, tiles_m, tiles_n);
+  hipLaunchKernelGGL((qgemm_big_kernel<MTW, NTW, WM>), grid, dim3(kThreads), 0, stream, w, scales,
+                     biases, x, y, m, n, k, tiles_m, tiles_n);
   return hipGetLastError();
 }
 
@@ -521,10 +549,13 @@ hipError_t launch_qgemm(const uint32_t* w, const uint16_t* scales, const uint16_
   if (tile == 16) mt = 4;
   if (tile == 24) mt = 6;
   if (tile == 32) mt = 8;
+  if (tile == 96) return launch_big<3, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
+  if (tile == 128) return launch_big<4, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
+  if (tile == 64) return launch_big<2, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
   switch (mt) {
-    case 4: return launch_big<4>(w, scales, biases, x, y, k, n, m, stream);
-    case 6: return launch_big<6>(w, scales, biases, x, y, k, n, m, stream);
-    default: return launch_big<8>(w, scales, biases, x, y, k, n, m, stream);
+    case 4: return launch_big<4, 2, 1>(w, scales, biases, x, y, k, n, m, stream);
+    case 6: return launch_big<6, 2, 1>(w, scales, biases, x, y, k, n, m, stream);
+    default: return launch_big<8, 2, 1>(w, scales, biases, x, y, k, n, m, stream);
   }
 }
 
