@@ -70,6 +70,30 @@ __device__ __forceinline__ void dequant_word_bf16(uint32_t word, float s24, floa
   out[3] = pack_bf16x2(__builtin_fmaf(s24, f16_hi(d2), b), __builtin_fmaf(s20, f16_hi(d3), b));
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Raw buffer resource over [base, base + bytes) (gfx9 word 3: 32-bit data
+// format).  Buffer loads take a per-lane 32-bit byte offset plus a scalar one.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+// Direct buffer -> LDS load of 16 bytes per lane: lane L writes
+// lds_wave_base + 16 L (lds_wave_base must be uniform across the wave).
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff,
+                                           void* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds_wave_base, 16, voff, soff, 0, 0);
+}
+
+// 16 bytes straight into registers (buffer_load_dwordx4).
+__device__ __forceinline__ u32x4_t load_b128(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0));
+}
+
+// s_waitcnt vmcnt(n) leaving expcnt and lgkmcnt unconstrained (gfx9 encoding).
+#define IMQ_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
                                          __builtin_bit_cast(bf16x2_t, b), acc, false);

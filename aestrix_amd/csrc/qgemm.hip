@@ -240,25 +240,9 @@ __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_
 constexpr int kBigBN = 256;
 constexpr int kStages = 3;
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// Raw buffer resource over [base, base + bytes) (gfx9 word 3: 32-bit data format).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
-
-__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff,
-                                           uint4* lds_wave_base) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds_wave_base, 16, voff, soff, 0, 0);
-}
-
-// 16 bytes of packed weights straight into registers (buffer_load_dwordx4).
 __device__ __forceinline__ u32x4_t load_w16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0));
+  return load_b128(rs, voff, soff);
 }
-
-// s_waitcnt vmcnt(n) leaving expcnt and lgkmcnt unconstrained (gfx9 encoding).
-#define IMQ_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 
 // Tile geometry: WM x WN = 4 waves; a wave owns MTW x NTW MFMA tiles of 32x32
 // (a (32 MTW) x (32 NTW) sub-tile); the workgroup tile is

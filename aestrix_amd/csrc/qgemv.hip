@@ -18,6 +18,9 @@
 #include "imq_device.hpp"
 #include "imq_kernels.hpp"
 
+#include <algorithm>
+#include <cstdlib>
+
 namespace imq {
 namespace {
 
@@ -175,20 +178,22 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(const uint32_t* __restr
 }
 
 // Straight-line variant for the common case: x[0:M][0:K] fits the LDS tile
-// and one batch of U chunks per lane covers a row (K <= 32 * G * U).  There is
-// no loop, so nothing makes the compiler wait on loads it does not need yet:
-// x loads, then weight loads, then the x LDS writes (waiting on x only), one
-// barrier, then the dequant + dot products (waiting on the weights).
+// and one batch of U chunks per lane covers a row (K <= 32 * G * U).  x is
+// staged first, by direct buffer->LDS loads (no registers, so the compiler
+// inserts no waits for them); then the weight/scale loads go out; one
+// `s_waitcnt vmcnt(3U)` (the x loads are the older ones) and a raw barrier
+// make x visible while the weights are still in flight, and the dot products
+// of chunk u wait only for chunk u's own loads.
 template <int MR, int G, int U>
 __global__ __launch_bounds__(kThreads) void qgemv_single_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
     int K, int N, int M) {
-  extern __shared__ u32x4_t xs[];  // [MR][K / 8] bf16 x
+  extern __shared__ u32x4_t xs[];  // [MR][K / 8] bf16 x, swizzled; rounded up to 256 slots
   constexpr int RPW = 64 / G;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int gl = lane & (G - 1);
   const int row = (blockIdx.x * kWaves + wave) * RPW + lane / G;
   const bool row_ok = row < N;
@@ -201,12 +206,23 @@ __global__ __launch_bounds__(kThreads) void qgemv_single_kernel(
   const uint16_t* srow = scales + rsafe * gpr;
   const uint16_t* brow = biases + rsafe * gpr;
 
-  u32x4_t xv[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) xv[i] = load_x_slot(x, K, 0, vpr, xtotal, tid + i * kThreads);
-  // Keep the issue order x, then weights: the x LDS writes then wait for the x
-  // loads only, and the compute of chunk u waits only for chunk u's loads.
+  // 1. x -> LDS.  LDS slot s holds x piece (m, idx) = (s / vpr, s % vpr) with
+  //    idx the swizzled position xs_swizzle(4 j + p); slots past the end load
+  //    a clamped duplicate into the padding.
+  {
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)((size_t)M * K * 2));
+    for (int base = 0; base < xtotal; base += kThreads) {
+      const int sl = min(base + tid, xtotal - 1);
+      const int m = sl / vpr;
+      const int idx = sl - m * vpr;
+      const int j = idx >> 2;
+      const int pc = (idx & 3) ^ ((j >> 2) & 3);
+      const uint32_t off = (uint32_t)((m * K + j * 32 + pc * 8) * 2);
+      load_lds16(xr, off, 0u, xs + base + wave * 64);
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
+  // 2. weight chunks and their scales/biases.
   u32x4_t q[U];
   uint32_t sv[U], bv[U];
 #pragma unroll
@@ -217,52 +233,46 @@ __global__ __launch_bounds__(kThreads) void qgemv_single_kernel(
     bv[u] = brow[j >> 1];
   }
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) store_x_slot(xs, vpr, vpr, xtotal, tid + i * kThreads, xv[i]);
-#pragma unroll
-  for (int r = 1; r < 4; ++r) {
-    if (r * 4 * kThreads < xtotal) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        xv[i] = load_x_slot(x, K, 0, vpr, xtotal, tid + (4 * r + i) * kThreads);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        store_x_slot(xs, vpr, vpr, xtotal, tid + (4 * r + i) * kThreads, xv[i]);
-    }
-  }
-  __syncthreads();
+  // 3. x visible; the weight loads may still be in flight.
+  IMQ_WAIT_VMCNT(3 * U);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
 
   float acc[MR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+  // Chunks past the row end (possible only in the last batch) were loaded
+  // from a clamped index; their sums are computed and dropped by a select, so
+  // every load is consumed in straight-line code (a branch would let the
+  // compiler sink the loads behind the barrier and break the vmcnt count).
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int j = gl + u * G;
-    if (j < nch) {
-      const float sc = bf16_to_f32(sv[u]);
-      const float bi = bf16_to_f32(bv[u]);
-      const float s24 = sc * 0x1p24f;
-      const float s20 = sc * 0x1p20f;
-      const int swz = (j >> 2) & 3;
-      uint32_t wp[16];
-      dequant_word_bf16(q[u].x, s24, s20, bi, wp + 0);
-      dequant_word_bf16(q[u].y, s24, s20, bi, wp + 4);
-      dequant_word_bf16(q[u].z, s24, s20, bi, wp + 8);
-      dequant_word_bf16(q[u].w, s24, s20, bi, wp + 12);
+    const int j = min(gl + u * G, nch - 1);
+    const bool ok = gl + u * G < nch;
+    const float sc = bf16_to_f32(sv[u]);
+    const float bi = bf16_to_f32(bv[u]);
+    const float s24 = sc * 0x1p24f;
+    const float s20 = sc * 0x1p20f;
+    const int swz = (j >> 2) & 3;
+    uint32_t wp[16];
+    dequant_word_bf16(q[u].x, s24, s20, bi, wp + 0);
+    dequant_word_bf16(q[u].y, s24, s20, bi, wp + 4);
+    dequant_word_bf16(q[u].z, s24, s20, bi, wp + 8);
+    dequant_word_bf16(q[u].w, s24, s20, bi, wp + 12);
+    // Rows m >= M (M rounded up to MR) repeat row M - 1 and are not stored.
 #pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        const u32x4_t* xp = xs + m * vpr + j * 4;
-        float a = acc[m];
+    for (int m = 0; m < MR; ++m) {
+      const u32x4_t* xp = xs + min(m, M - 1) * vpr + j * 4;
+      float a = acc[m];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const u32x4_t xx = xp[v ^ swz];
-          a = dot2_bf16(wp[4 * v + 0], xx.x, a);
-          a = dot2_bf16(wp[4 * v + 1], xx.y, a);
-          a = dot2_bf16(wp[4 * v + 2], xx.z, a);
-          a = dot2_bf16(wp[4 * v + 3], xx.w, a);
-        }
-        acc[m] = a;
+      for (int v = 0; v < 4; ++v) {
+        const u32x4_t xx = xp[v ^ swz];
+        a = dot2_bf16(wp[4 * v + 0], xx.x, a);
+        a = dot2_bf16(wp[4 * v + 1], xx.y, a);
+        a = dot2_bf16(wp[4 * v + 2], xx.z, a);
+        a = dot2_bf16(wp[4 * v + 3], xx.w, a);
       }
+      acc[m] = ok ? a : acc[m];
     }
   }
 #pragma unroll
@@ -283,7 +293,9 @@ hipError_t launch_u(const uint32_t* w, const uint16_t* s, const uint16_t* b, con
   const int rows_per_block = kWaves * (64 / G);
   const dim3 grid((n + rows_per_block - 1) / rows_per_block);
   if (kt == k && k / 32 <= G * U) {
-    const size_t lds = (size_t)MR * k * 2;
+    // x slots rounded up to whole 256-slot rounds (the DMA padding).
+    const size_t slots = ((size_t)m * (k / 8) + kThreads - 1) / kThreads * kThreads;
+    const size_t lds = slots * 16;
     hipLaunchKernelGGL((qgemv_single_kernel<MR, G, U>), grid, dim3(kThreads), lds, stream, w, s,
                        b, x, y, k, n, m);
   } else {
@@ -313,17 +325,39 @@ hipError_t launch_g(const uint32_t* w, const uint16_t* s, const uint16_t* b, con
   }
 }
 
+// Lanes per row.  Each candidate G in {16, 32, 64} gives n * G / 64 waves
+// and uses nch / (G * U) of its lanes' chunk slots (U = ceil(nch / G));
+// pick the one with the most useful waves, counting at most 4096 waves (two
+// per SIMD at 64 VGPRs is where more waves stopped helping on the two
+// shapes measured: 9728 x 2560 and 2560 x 9728), and prefer G values whose
+// U fits the straight-line kernel.  IMQ_QGEMV_LANES=16|32|64 overrides.
+int pick_lanes(int k, int n) {
+  static const int forced = [] {
+    const char* e = getenv("IMQ_QGEMV_LANES");
+    const int v = e ? atoi(e) : 0;
+    return (v == 16 || v == 32 || v == 64) ? v : 0;
+  }();
+  if (forced) return forced;
+  const int nch = k / 32;
+  int best = 16;
+  double best_score = -1.0;
+  for (int g = 16; g <= 64; g *= 2) {
+    const int u = (nch + g - 1) / g;
+    const double waves = std::min((double)n * g / 64.0, 4096.0);
+    double score = waves * nch / (double)(g * u);
+    if (u > kMaxU) score *= 0.5;  // looped kernel
+    if (score > best_score * 1.02) {
+      best = g;
+      best_score = score;
+    }
+  }
+  return best;
+}
+
 template <int MR>
 hipError_t launch_m(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
                     uint16_t* y, int k, int n, int m, hipStream_t stream) {
-  // Lanes per row: enough waves to cover the chip (about 2048), but no more
-  // lanes than the row has 16-byte chunks when that can be avoided.
-  int g = 16;
-  if ((int64_t)n * 16 / 64 < 2048) g = 32;
-  if ((int64_t)n * 32 / 64 < 2048) g = 64;
-  const int chunks = k / 32;
-  while (g > 16 && g > chunks) g >>= 1;
-  switch (g) {
+  switch (pick_lanes(k, n)) {
     case 16: return launch_g<MR, 16>(w, s, b, x, y, k, n, m, stream);
     case 32: return launch_g<MR, 32>(w, s, b, x, y, k, n, m, stream);
     default: return launch_g<MR, 64>(w, s, b, x, y, k, n, m, stream);
@@ -335,7 +369,7 @@ hipError_t launch_m(const uint32_t* w, const uint16_t* s, const uint16_t* b, con
 hipError_t launch_qgemv(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                         const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
   // M is rounded up to a power of two for the register tile; rows >= M are
-  // neither read from x nor stored.
+  // not stored.
   if (m <= 1) return launch_m<1>(w, scales, biases, x, y, k, n, m, stream);
   if (m <= 2) return launch_m<2>(w, scales, biases, x, y, k, n, m, stream);
   if (m <= 4) return launch_m<4>(w, scales, biases, x, y, k, n, m, stream);

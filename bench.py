@@ -183,19 +183,20 @@ def cpu_baseline(synth, seconds: float = 10.0) -> dict:
 
 def floors(torch) -> int:
     """Reference kernels for reading kernel durations under rocprofv3: a
-    one-element fill (the launch floor) and a full-tensor sum over each of 48
-    distinct 12.45 MB buffers (the streaming-read floor at the qGEMV weight
-    size, past the 256 MB MALL)."""
+    one-element fill (the launch floor) and device-to-device copies of
+    6225920 bytes between 48 distinct buffer pairs (12.45 MB of HBM traffic
+    per launch, the qGEMV weight size, past the 256 MB MALL)."""
     t = torch.empty(1, dtype=torch.float32, device="cuda")
     for _ in range(200):
         t.zero_()
-    bufs = [torch.ones(9728 * 2560 // 8, dtype=torch.int32, device="cuda") for _ in range(48)]
-    out = torch.empty((), dtype=torch.int64, device="cuda")
+    words = 9728 * 2560 // 16
+    src = [torch.ones(words, dtype=torch.int32, device="cuda") for _ in range(48)]
+    dst = [torch.empty(words, dtype=torch.int32, device="cuda") for _ in range(48)]
     for _ in range(5):
-        for b in bufs:
-            torch.sum(b, dim=0, out=out)
+        for a, b in zip(src, dst):
+            b.copy_(a)
     torch.cuda.synchronize()
-    log("floors: 200 one-element fills; 240 sums over 12451840-byte int32 buffers")
+    log(f"floors: 200 one-element fills; 240 copies of {words * 4} bytes")
     return 0
 
 
