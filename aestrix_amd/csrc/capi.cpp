@@ -6,6 +6,7 @@
 // buffer error after the wait, Sources/ImarelloDirect/DirectDiTStep.swift:968-970).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
@@ -46,6 +47,8 @@ int hip_fail(imq_ctx* ctx, hipError_t e, const char* what) {
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+size_t elem_size(imq_dtype dtype) { return dtype == IMQ_F32 ? 4 : 2; }
+
 int bind_device(imq_ctx* ctx) {
   const hipError_t e = hipSetDevice(ctx->device);
   return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, "hipSetDevice");
@@ -62,16 +65,18 @@ int check_qmm(imq_ctx* ctx, const char* fn, const uint32_t* w, const void* s, co
   if (group_size != 64)
     return fail(ctx, IMQ_EUNSUPPORTED, "%s: group_size %d (only 64 is provided)", fn, group_size);
   if (bits != 4) return fail(ctx, IMQ_EUNSUPPORTED, "%s: bits %d (only 4 is provided)", fn, bits);
-  if (dtype != IMQ_BF16)
-    return fail(ctx, IMQ_EUNSUPPORTED, "%s: dtype %d (bf16 is provided)", fn, (int)dtype);
+  if (dtype != IMQ_BF16 && dtype != IMQ_F16 && dtype != IMQ_F32)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: dtype %d (bf16, f16 and f32 are provided)", fn,
+                (int)dtype);
   if (k <= 0 || n <= 0 || m <= 0)
     return fail(ctx, IMQ_EINVAL, "%s: non-positive shape K=%d N=%d M=%d", fn, k, n, m);
   if (k % 64 != 0)
     return fail(ctx, IMQ_EINVAL, "%s: K=%d is not a multiple of the group size 64", fn, k);
   if (!aligned(w, 16) || !aligned(x, 16))
     return fail(ctx, IMQ_EINVAL, "%s: w and x must be 16-byte aligned", fn);
-  if (!aligned(s, 2) || !aligned(b, 2) || !aligned(y, 2))
-    return fail(ctx, IMQ_EINVAL, "%s: scales, biases and y must be 2-byte aligned", fn);
+  const size_t es = elem_size(dtype);
+  if (!aligned(s, es) || !aligned(b, es) || !aligned(y, es))
+    return fail(ctx, IMQ_EINVAL, "%s: scales, biases and y must be %zu-byte aligned", fn, es);
   return IMQ_OK;
 }
 
@@ -84,15 +89,30 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
   if (rc != IMQ_OK) return rc;
   if (regime == Regime::kGemv && m > imq::kQgemvMaxM)
     return fail(ctx, IMQ_EINVAL, "%s: M=%d exceeds the qGEMV limit %d", fn, m, imq::kQgemvMaxM);
+  if (regime == Regime::kGemm && dtype == IMQ_F32)
+    return fail(ctx, IMQ_EUNSUPPORTED,
+                "%s: f32 has no MFMA kernel (imq_qmm_t runs f32 at any M on the qGEMV kernel)", fn);
+  const size_t es = elem_size(dtype);
+  // The qGEMV kernel addresses one 16-row block of x with 32-bit byte offsets.
+  if (regime != Regime::kGemm && (size_t)std::min(m, imq::kQgemvMaxM) * k * es >= ((size_t)1 << 31))
+    return fail(ctx, IMQ_EINVAL, "%s: K=%d too long for the qGEMV kernel", fn, k);
   if ((rc = bind_device(ctx)) != IMQ_OK) return rc;
-  const bool gemv = regime == Regime::kGemv || (regime == Regime::kAuto && m <= imq::kQgemvMaxM);
-  const auto* s16 = static_cast<const uint16_t*>(s);
-  const auto* b16 = static_cast<const uint16_t*>(b);
-  const auto* x16 = static_cast<const uint16_t*>(x);
-  auto* y16 = static_cast<uint16_t*>(y);
+  const bool gemv = regime == Regime::kGemv ||
+                    (regime == Regime::kAuto && (m <= imq::kQgemvMaxM || dtype == IMQ_F32));
   auto st = static_cast<hipStream_t>(stream);
-  const hipError_t e = gemv ? imq::launch_qgemv(w, s16, b16, x16, y16, k, n, m, st)
-                            : imq::launch_qgemm(w, s16, b16, x16, y16, k, n, m, st);
+  hipError_t e = hipSuccess;
+  if (!gemv) {
+    e = imq::launch_qgemm(w, s, b, x, y, k, n, m, (int)dtype, st);
+  } else {
+    // f32 beyond 16 rows (the conditioner's multi-row calls): blocks of 16 rows.
+    const auto* xb = static_cast<const char*>(x);
+    auto* yb = static_cast<char*>(y);
+    for (int m0 = 0; m0 < m && e == hipSuccess; m0 += imq::kQgemvMaxM) {
+      const int mb = std::min(imq::kQgemvMaxM, m - m0);
+      e = imq::launch_qgemv(w, s, b, xb + (size_t)m0 * k * es, yb + (size_t)m0 * n * es, k, n, mb,
+                            (int)dtype, st);
+    }
+  }
   return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
 }
 
@@ -214,8 +234,8 @@ int imq_dequantize(imq_ctx* ctx, const uint32_t* w, const void* scales, const vo
   if (group_size != 64)
     return fail(ctx, IMQ_EUNSUPPORTED, "%s: group_size %d (only 64 is provided)", fn, group_size);
   if (bits != 4) return fail(ctx, IMQ_EUNSUPPORTED, "%s: bits %d (only 4 is provided)", fn, bits);
-  if (dtype != IMQ_BF16 && dtype != IMQ_F16)
-    return fail(ctx, IMQ_EUNSUPPORTED, "%s: dtype %d (bf16 and f16 are provided)", fn,
+  if (dtype != IMQ_BF16 && dtype != IMQ_F16 && dtype != IMQ_F32)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: dtype %d (bf16, f16 and f32 are provided)", fn,
                 (int)dtype);
   if (k <= 0 || n <= 0)
     return fail(ctx, IMQ_EINVAL, "%s: non-positive shape K=%d N=%d", fn, k, n);
@@ -223,13 +243,12 @@ int imq_dequantize(imq_ctx* ctx, const uint32_t* w, const void* scales, const vo
     return fail(ctx, IMQ_EINVAL, "%s: K=%d is not a multiple of the group size 64", fn, k);
   if (!aligned(w, 16) || !aligned(out, 16))
     return fail(ctx, IMQ_EINVAL, "%s: w and out must be 16-byte aligned", fn);
-  if (!aligned(scales, 2) || !aligned(biases, 2))
-    return fail(ctx, IMQ_EINVAL, "%s: scales and biases must be 2-byte aligned", fn);
+  const size_t es = elem_size(dtype);
+  if (!aligned(scales, es) || !aligned(biases, es))
+    return fail(ctx, IMQ_EINVAL, "%s: scales and biases must be %zu-byte aligned", fn, es);
   int rc = bind_device(ctx);
   if (rc != IMQ_OK) return rc;
-  const hipError_t e = imq::launch_dequant(w, static_cast<const uint16_t*>(scales),
-                                           static_cast<const uint16_t*>(biases),
-                                           static_cast<uint16_t*>(out), k, n, dtype == IMQ_F16,
+  const hipError_t e = imq::launch_dequant(w, scales, biases, out, k, n, (int)dtype,
                                            static_cast<hipStream_t>(stream));
   return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
 }

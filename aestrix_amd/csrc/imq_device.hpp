@@ -46,7 +46,8 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // the f16 subnormal c * 2^-24 (or c * 2^-20), exactly.  Decoding with a scale
 // pre-multiplied by 2^24 (or 2^20) gives fma(s', c * 2^-24, b) == fl32(s*c + b):
 // the power-of-two rescale is exact and the fma rounds once, like the
-// reference's `scale * q + bias` (s*q itself is exact in f32).  hipcc turns the
+// reference's `scale * q + bias` (for bf16 and f16 scales s*q is exact in f32,
+// so one rounding and two agree).  hipcc turns the
 // f16 -> f32 conversion + fma into one v_fma_mix_f32.
 __device__ __forceinline__ float f16_lo(uint32_t d) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(d & 0xFFFFu));
@@ -69,6 +70,90 @@ __device__ __forceinline__ void dequant_word_bf16(uint32_t word, float s24, floa
   out[2] = pack_bf16x2(__builtin_fmaf(s24, f16_hi(d0), b), __builtin_fmaf(s20, f16_hi(d1), b));
   out[3] = pack_bf16x2(__builtin_fmaf(s24, f16_hi(d2), b), __builtin_fmaf(s20, f16_hi(d3), b));
 }
+
+// Pack two floats into an f16 pair, each rounded to nearest even
+// (v_cvt_f16_f32 in the default round mode).
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  const uint32_t a = __builtin_bit_cast(uint16_t, (_Float16)lo);
+  const uint32_t b = __builtin_bit_cast(uint16_t, (_Float16)hi);
+  return a | (b << 16);
+}
+
+// dequant_word_bf16 with f16 results: out[p] = (w[2p], w[2p+1]) as RNE_f16(fl32(s*q + b)).
+__device__ __forceinline__ void dequant_word_f16(uint32_t word, float s24, float s20, float b,
+                                                 uint32_t out[4]) {
+  const uint32_t d0 = word & 0x000F000Fu;
+  const uint32_t d1 = word & 0x00F000F0u;
+  const uint32_t w8 = word >> 8;
+  const uint32_t d2 = w8 & 0x000F000Fu;
+  const uint32_t d3 = w8 & 0x00F000F0u;
+  out[0] = pack_f16x2(__builtin_fmaf(s24, f16_lo(d0), b), __builtin_fmaf(s20, f16_lo(d1), b));
+  out[1] = pack_f16x2(__builtin_fmaf(s24, f16_lo(d2), b), __builtin_fmaf(s20, f16_lo(d3), b));
+  out[2] = pack_f16x2(__builtin_fmaf(s24, f16_hi(d0), b), __builtin_fmaf(s20, f16_hi(d1), b));
+  out[3] = pack_f16x2(__builtin_fmaf(s24, f16_hi(d2), b), __builtin_fmaf(s20, f16_hi(d3), b));
+}
+
+// The eight codes of a word as f32 weights fl32(fl32(s*q) + b), in k order:
+// two rounded operations, like the reference's `scale * q + bias` on Float.
+// With f32 scales (24-bit significands) s*q is not exact in f32, so an fma
+// would round differently; s24 = s * 2^24 and s20 = s * 2^20 are exact.
+__device__ __forceinline__ void dequant_word_f32(uint32_t word, float s24, float s20, float b,
+                                                 float out[8]) {
+#pragma clang fp contract(off)
+  const uint32_t d0 = word & 0x000F000Fu;
+  const uint32_t d1 = word & 0x00F000F0u;
+  const uint32_t w8 = word >> 8;
+  const uint32_t d2 = w8 & 0x000F000Fu;
+  const uint32_t d3 = w8 & 0x00F000F0u;
+  out[0] = s24 * f16_lo(d0) + b;
+  out[1] = s20 * f16_lo(d1) + b;
+  out[2] = s24 * f16_lo(d2) + b;
+  out[3] = s20 * f16_lo(d3) + b;
+  out[4] = s24 * f16_hi(d0) + b;
+  out[5] = s20 * f16_hi(d1) + b;
+  out[6] = s24 * f16_hi(d2) + b;
+  out[7] = s20 * f16_hi(d3) + b;
+}
+
+// Element type T of x, scales, biases and y (the values of imq_dtype).
+enum Dtype : int { kBf16 = 0, kF16 = 1, kF32 = 2 };
+
+template <int T>
+struct Elem;
+
+template <>
+struct Elem<kBf16> {
+  using S = uint16_t;
+  static constexpr int kBytes = 2;
+  static __device__ __forceinline__ float param(S v) { return bf16_to_f32(v); }
+  static __device__ __forceinline__ S out(float v) { return (S)f32_to_bf16_int(v); }
+  static __device__ __forceinline__ void dequant(uint32_t word, float s24, float s20, float b,
+                                                 uint32_t o[4]) {
+    dequant_word_bf16(word, s24, s20, b, o);
+  }
+};
+
+template <>
+struct Elem<kF16> {
+  using S = uint16_t;
+  static constexpr int kBytes = 2;
+  static __device__ __forceinline__ float param(S v) {
+    return (float)__builtin_bit_cast(_Float16, v);
+  }
+  static __device__ __forceinline__ S out(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+  static __device__ __forceinline__ void dequant(uint32_t word, float s24, float s20, float b,
+                                                 uint32_t o[4]) {
+    dequant_word_f16(word, s24, s20, b, o);
+  }
+};
+
+template <>
+struct Elem<kF32> {
+  using S = float;
+  static constexpr int kBytes = 4;
+  static __device__ __forceinline__ float param(S v) { return v; }
+  static __device__ __forceinline__ S out(float v) { return v; }
+};
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -97,6 +182,12 @@ __device__ __forceinline__ u32x4_t load_b128(__amdgpu_buffer_rsrc_t rs, uint32_t
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
                                          __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
+
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b),
+                                acc, false);
 }
 
 }  // namespace imq

@@ -1,6 +1,7 @@
-// qgemm.hip -- dense quantized matmul for gfx950 on bf16 MFMA.
+// qgemm.hip -- dense quantized matmul for gfx950 on bf16 / f16 MFMA.
 //
-// y[M][N] = x[M][K] . deq(W)^T, fp32 accumulation, bf16 output: the prefill /
+// y[M][N] = x[M][K] . deq(W)^T, fp32 accumulation, output in T (bf16, or f16
+// for the reference's DiT kernels, DirectDiTStep.swift:82-85): the prefill /
 // DiT regime of MLX quantizedMM(transpose: true, groupSize: 64, bits: 4),
 // i.e. the `affine_qmm_t_*` dispatches of the reference's direct engine
 // (Sources/ImarelloDirect/DirectDiTStep.swift:374-406,
@@ -26,7 +27,6 @@
 #include "imq_device.hpp"
 #include "imq_kernels.hpp"
 
-#include <cstdlib>
 
 namespace imq {
 namespace {
@@ -58,9 +58,20 @@ __device__ __forceinline__ int a_slot(int r, int c) {
   return r * 8 + (c ^ ((r & 7) ^ ((r >> 3) & 1)));
 }
 
+// One 32x32x16 MFMA on 16-bit operands held as raw dwords (8 elements per lane).
+template <int T>
+__device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+  if constexpr (T == kBf16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
 // One workgroup = 4 waves along N; a wave owns MT x NT MFMA tiles of 32x32,
 // i.e. a (32 MT) x (32 NT) sub-tile; the workgroup tile is (32 MT) x (128 NT).
-template <int MT, int NT>
+template <int T, int MT, int NT>
 __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
@@ -153,20 +164,19 @@ __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_
     }
 
     // Dequantize this lane's 32 codes per column tile into 4 MFMA operands.
-    bf16x8_t bfrag[NT][4];
+    u32x4_t bfrag[NT][4];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const float sc = bf16_to_f32(s_reg[nt]);
-      const float bi = bf16_to_f32(bi_reg[nt]);
+      const float sc = Elem<T>::param(s_reg[nt]);
+      const float bi = Elem<T>::param(bi_reg[nt]);
       const float s24 = sc * 0x1p24f;
       const float s20 = sc * 0x1p20f;
       const uint32_t words[4] = {b_reg[nt].x, b_reg[nt].y, b_reg[nt].z, b_reg[nt].w};
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         uint32_t p[4];
-        dequant_word_bf16(words[kk], s24, s20, bi, p);
-        u32x4_t v = {p[0], p[1], p[2], p[3]};
-        bfrag[nt][kk] = __builtin_bit_cast(bf16x8_t, v);
+        Elem<T>::dequant(words[kk], s24, s20, bi, p);
+        bfrag[nt][kk] = u32x4_t{p[0], p[1], p[2], p[3]};
       }
     }
 
@@ -174,16 +184,15 @@ __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_
     // for both operands.
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      bf16x8_t afrag[MT];
+      u32x4_t afrag[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-        afrag[mt] = __builtin_bit_cast(bf16x8_t, a_lds[cur][a_slot(mt * 32 + r32, 4 * h + kk)]);
+        afrag[mt] = __builtin_bit_cast(u32x4_t, a_lds[cur][a_slot(mt * 32 + r32, 4 * h + kk)]);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afrag[mt], bfrag[nt][kk],
-                                                                 acc[mt][nt], 0, 0, 0);
+          acc[mt][nt] = mfma32<T>(afrag[mt], bfrag[nt][kk], acc[mt][nt]);
     }
 
 #pragma unroll
@@ -210,7 +219,7 @@ __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (row < M) y[(size_t)row * N + col] = (uint16_t)f32_to_bf16_int(acc[mt][nt][r]);
+        if (row < M) y[(size_t)row * N + col] = Elem<T>::out(acc[mt][nt][r]);
       }
     }
   }
@@ -273,7 +282,7 @@ struct BigSrc {
 // loads fill are distinct LDS objects, so the compiler can prove that the
 // in-flight loads into stages S+1 and S+2 do not alias the reads of stage S
 // and does not wait for them.
-template <int MTW, int NTW, int WM, int S>
+template <int T, int MTW, int NTW, int WM, int S>
 __device__ __forceinline__ void big_step(int g, int gpr, const BigRing& ring,
                                          const BigSrc<MTW, NTW, WM>& src,
                                          uint32_t (&sc)[kStages][NTW], uint32_t (&bs)[kStages][NTW],
@@ -312,22 +321,22 @@ __device__ __forceinline__ void big_step(int g, int gpr, const BigRing& ring,
   float s24[NTW], s20[NTW], bb[NTW];
 #pragma unroll
   for (int nt = 0; nt < NTW; ++nt) {
-    const float sv = bf16_to_f32(sc[S][nt]);
+    const float sv = Elem<T>::param(sc[S][nt]);
     s24[nt] = sv * 0x1p24f;
     s20[nt] = sv * 0x1p20f;
-    bb[nt] = bf16_to_f32(bs[S][nt]);
+    bb[nt] = Elem<T>::param(bs[S][nt]);
   }
 
-  bf16x8_t afrag[2][MTW];
-  bf16x8_t bfrag[2][NTW];
+  u32x4_t afrag[2][MTW];
+  u32x4_t bfrag[2][NTW];
 #pragma unroll
   for (int mt = 0; mt < MTW; ++mt)
-    afrag[0][mt] = __builtin_bit_cast(bf16x8_t, at[a_slot(arow0 + mt * 32 + r32, 4 * h)]);
+    afrag[0][mt] = __builtin_bit_cast(u32x4_t, at[a_slot(arow0 + mt * 32 + r32, 4 * h)]);
 #pragma unroll
   for (int nt = 0; nt < NTW; ++nt) {
     uint32_t p[4];
-    dequant_word_bf16(wraw[nt].x, s24[nt], s20[nt], bb[nt], p);
-    bfrag[0][nt] = __builtin_bit_cast(bf16x8_t, u32x4_t{p[0], p[1], p[2], p[3]});
+    Elem<T>::dequant(wraw[nt].x, s24[nt], s20[nt], bb[nt], p);
+    bfrag[0][nt] = u32x4_t{p[0], p[1], p[2], p[3]};
   }
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
@@ -337,21 +346,20 @@ __device__ __forceinline__ void big_step(int g, int gpr, const BigRing& ring,
 #pragma unroll
       for (int mt = 0; mt < MTW; ++mt)
         afrag[cb ^ 1][mt] =
-            __builtin_bit_cast(bf16x8_t, at[a_slot(arow0 + mt * 32 + r32, 4 * h + kk + 1)]);
+            __builtin_bit_cast(u32x4_t, at[a_slot(arow0 + mt * 32 + r32, 4 * h + kk + 1)]);
 #pragma unroll
       for (int nt = 0; nt < NTW; ++nt) {
         const uint32_t word = (kk == 0) ? wraw[nt].y : (kk == 1) ? wraw[nt].z : wraw[nt].w;
         uint32_t p[4];
-        dequant_word_bf16(word, s24[nt], s20[nt], bb[nt], p);
-        bfrag[cb ^ 1][nt] = __builtin_bit_cast(bf16x8_t, u32x4_t{p[0], p[1], p[2], p[3]});
+        Elem<T>::dequant(word, s24[nt], s20[nt], bb[nt], p);
+        bfrag[cb ^ 1][nt] = u32x4_t{p[0], p[1], p[2], p[3]};
       }
     }
 #pragma unroll
     for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
       for (int nt = 0; nt < NTW; ++nt)
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afrag[cb][mt], bfrag[cb][nt],
-                                                               acc[mt][nt], 0, 0, 0);
+        acc[mt][nt] = mfma32<T>(afrag[cb][mt], bfrag[cb][nt], acc[mt][nt]);
     if (kk < 3) {
       // Interleave: every MFMA of this k-slice is followed by a share of the
       // next slice's dequant VALU work and, for the first MTW, one LDS read,
@@ -368,7 +376,7 @@ __device__ __forceinline__ void big_step(int g, int gpr, const BigRing& ring,
   }
 }
 
-template <int MTW, int NTW, int WM>
+template <int T, int MTW, int NTW, int WM>
 __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
@@ -445,13 +453,14 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
 
   int g = 0;
   for (; g + 3 <= gpr; g += 3) {
-    big_step<MTW, NTW, WM, 0>(g, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
-    big_step<MTW, NTW, WM, 1>(g + 1, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
-    big_step<MTW, NTW, WM, 2>(g + 2, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
+    big_step<T, MTW, NTW, WM, 0>(g, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
+    big_step<T, MTW, NTW, WM, 1>(g + 1, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
+    big_step<T, MTW, NTW, WM, 2>(g + 2, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
   }
-  if (g < gpr) big_step<MTW, NTW, WM, 0>(g, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
+  if (g < gpr)
+    big_step<T, MTW, NTW, WM, 0>(g, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
   if (g + 1 < gpr)
-    big_step<MTW, NTW, WM, 1>(g + 1, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
+    big_step<T, MTW, NTW, WM, 1>(g + 1, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
   IMQ_WAIT_VMCNT(0);  // drain the clamped tail loads before the workgroup ends
 
 #pragma unroll
@@ -463,20 +472,20 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + arow0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (row < M) y[(size_t)row * N + col] = (uint16_t)f32_to_bf16_int(acc[mt][nt][r]);
+        if (row < M) y[(size_t)row * N + col] = Elem<T>::out(acc[mt][nt][r]);
       }
     }
   }
 }
 
-template <int MTW, int NTW, int WM>
+template <int T, int MTW, int NTW, int WM>
 hipError_t launch_big(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                       const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
   constexpr int BM = BigCfg<MTW, NTW, WM>::kBM;
   const int tiles_m = (m + BM - 1) / BM;
   const int tiles_n = (n + kBigBN - 1) / kBigBN;
   const dim3 grid((unsigned)tiles_m * (unsigned)tiles_n);
-  hipLaunchKernelGGL((qgemm_big_kernel<MTW, NTW, WM>), grid, dim3(kThreads), 0, stream, w, scales,
+  hipLaunchKernelGGL((qgemm_big_kernel<T, MTW, NTW, WM>), grid, dim3(kThreads), 0, stream, w, scales,
                      biases, x, y, m, n, k, tiles_m, tiles_n);
   return hipGetLastError();
 }
@@ -500,46 +509,49 @@ int pick_big_mt(int m, int n, int cus) {
   return best;
 }
 
-template <int MT, int NT>
+template <int T, int MT, int NT>
 hipError_t launch_tile(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                        const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
   const int tiles_m = (m + 32 * MT - 1) / (32 * MT);
   const int tiles_n = (n + 128 * NT - 1) / (128 * NT);
   const dim3 grid((unsigned)tiles_m * (unsigned)tiles_n);
-  hipLaunchKernelGGL((qgemm_kernel<MT, NT>), grid, dim3(kThreads), 0, stream, w, scales, biases,
+  hipLaunchKernelGGL((qgemm_kernel<T, MT, NT>), grid, dim3(kThreads), 0, stream, w, scales, biases,
                      x, y, m, n, k, tiles_m, tiles_n);
   return hipGetLastError();
 }
 
-}  // namespace
-
-hipError_t launch_qgemm(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
-                        const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
+template <int T>
+hipError_t launch_t(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                    const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
   // The buffer-load kernel addresses x and w with 32-bit byte offsets.
   const bool fits32 = (size_t)m * k * 2 < ((size_t)1 << 31) && (size_t)n * k / 2 < ((size_t)1 << 31);
-  const char* env = getenv("IMQ_QGEMM_TILE");
-  const int tile = env ? atoi(env) : 0;
-  if (tile == 4 || !fits32) return launch_tile<4, 2>(w, scales, biases, x, y, k, n, m, stream);
-  static int cus = 0;
-  if (cus == 0) {
+  if (!fits32) return launch_tile<T, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
+  static const int cus = [] {
     int dev = 0, v = 0;
     if (hipGetDevice(&dev) == hipSuccess &&
         hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      cus = v;
-    else
-      cus = 256;
+      return v;
+    return 256;
+  }();
+  switch (pick_big_mt(m, n, cus)) {
+    case 4: return launch_big<T, 4, 2, 1>(w, scales, biases, x, y, k, n, m, stream);
+    case 6: return launch_big<T, 6, 2, 1>(w, scales, biases, x, y, k, n, m, stream);
+    default: return launch_big<T, 8, 2, 1>(w, scales, biases, x, y, k, n, m, stream);
   }
-  int mt = pick_big_mt(m, n, cus);
-  if (tile == 16) mt = 4;
-  if (tile == 24) mt = 6;
-  if (tile == 32) mt = 8;
-  if (tile == 96) return launch_big<3, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
-  if (tile == 128) return launch_big<4, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
-  if (tile == 64) return launch_big<2, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
-  switch (mt) {
-    case 4: return launch_big<4, 2, 1>(w, scales, biases, x, y, k, n, m, stream);
-    case 6: return launch_big<6, 2, 1>(w, scales, biases, x, y, k, n, m, stream);
-    default: return launch_big<8, 2, 1>(w, scales, biases, x, y, k, n, m, stream);
+}
+
+}  // namespace
+
+hipError_t launch_qgemm(const uint32_t* w, const void* scales, const void* biases, const void* x,
+                        void* y, int k, int n, int m, int dtype, hipStream_t stream) {
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* b = static_cast<const uint16_t*>(biases);
+  const auto* xx = static_cast<const uint16_t*>(x);
+  auto* yy = static_cast<uint16_t*>(y);
+  switch (dtype) {
+    case kBf16: return launch_t<kBf16>(w, s, b, xx, yy, k, n, m, stream);
+    case kF16: return launch_t<kF16>(w, s, b, xx, yy, k, n, m, stream);
+    default: return hipErrorInvalidValue;
   }
 }
 

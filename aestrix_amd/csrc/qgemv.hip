@@ -1,9 +1,11 @@
 // qgemv.hip -- skinny quantized matmul (1 <= M <= 16) for gfx950, no MFMA.
 //
-// y[m][n] = sum_k x[m][k] * deq(W)[n][k], fp32 accumulation, bf16 output:
+// y[m][n] = sum_k x[m][k] * deq(W)[n][k], fp32 accumulation, output in T:
 // the M <= 16 regime of MLX quantizedMM(transpose: true, groupSize: 64,
 // bits: 4) (Sources/ImarelloDiT/AttentionUtils.swift:212-221) and of the
-// reference's M=1 conditioner qmm (Sources/ImarelloDirect/DirectConditioner.swift:168-213).
+// reference's M=1 conditioner qmm with f32 x, scales, biases and y
+// (Sources/ImarelloDirect/DirectConditioner.swift:48,75-84,168-213).
+// T in {bf16, f16, f32}; x, scales, biases and y share T.
 //
 // Bandwidth-bound on the packed weight (0.5 B/element) at small M; the fp32
 // dot products (0.5 v_dot2 per element and row of x) take over towards M = 16.
@@ -13,11 +15,12 @@
 //    chunks l, l+G, l+2G, ... of each of its rows (32 codes, half a
 //    quantization group each), so one wave instruction reads 64/G contiguous
 //    row segments of G*16 bytes;
-//  * x[M][K-tile] is staged per workgroup in LDS by direct buffer->LDS loads
-//    and read as bf16 pairs; each x read feeds all R rows of the lane;
-//  * codes are dequantized in registers to bf16 (the same rounding as the
-//    dequantize kernel: RNE_bf16(fl32(s*q + b))) and multiplied with
-//    v_dot2_f32_bf16 into fp32 accumulators;
+//  * x[M][K-tile] is staged per workgroup in LDS by direct buffer->LDS loads;
+//    each x read feeds all R rows of the lane;
+//  * codes are dequantized in registers to T (the dequantize kernel's
+//    rounding, RNE_T(fl32(s*q + b)); for f32 the weight is fl32(s*q + b)) and
+//    multiplied into fp32 accumulators with v_dot2_f32_bf16 / v_dot2_f32_f16
+//    (16-bit T) or fma (f32);
 //  * the G partial sums of a row are combined with cross-lane shuffles.
 #include "imq_device.hpp"
 #include "imq_kernels.hpp"
@@ -36,10 +39,12 @@ constexpr int kLdsBudget = 64 * 1024;  // x tile bytes per workgroup
 constexpr int rows_per_lane(int mr) { return mr >= 8 ? 2 : 1; }
 constexpr int max_chunks(int mr) { return mr >= 8 ? 4 : 8; }
 
-// One K tile of x in LDS: row m, 16-byte piece p of chunk j (32 elements) sits
-// at slot m * vpr + 4 j + (p ^ ((j >> 2) & 3)), vpr = tile length / 8.  The
-// lanes of a row group read chunks j, j+1, ... in the same instruction; the
-// swizzle spreads their 16-byte reads over all bank groups while p stays a
+// One K tile of x in LDS, in 16-byte pieces (EPP = 16 / sizeof(T) elements;
+// P = 32 / EPP pieces per chunk of 32 elements): row m, piece p of chunk j
+// sits at slot m * vpr + P j + (p ^ f(j)), vpr = tile length / EPP, with
+// f(j) = (j >> 2) & 3 for 16-bit T and (j >> 1) & 7 for f32.  The lanes of a
+// row group read chunks j, j+1, ... in the same instruction; the swizzle
+// spreads their 16-byte reads over all bank groups while p stays a
 // compile-time constant in the reader.
 //
 // Per tile: x goes first, by buffer->LDS loads (no registers, so the compiler
@@ -49,13 +54,22 @@ constexpr int max_chunks(int mr) { return mr >= 8 ? 4 : 8; }
 // chunk u wait only for chunk u's own loads.  Loads are never predicated: an
 // index past the end is clamped (a duplicate read) and its sum dropped by a
 // select, so every load is consumed in straight-line code.
-template <int MR, int G, int U, int R>
-__global__ __launch_bounds__(kThreads) void qgemv_kernel(const uint32_t* __restrict__ w,
-                                                         const uint16_t* __restrict__ scales,
-                                                         const uint16_t* __restrict__ biases,
-                                                         const uint16_t* __restrict__ x,
-                                                         uint16_t* __restrict__ y, int K, int N,
-                                                         int M, int kt) {
+template <int T>
+struct XTile {
+  static constexpr int kEpp = 16 / Elem<T>::kBytes;  // elements per 16-byte piece
+  static constexpr int kP = 32 / kEpp;               // pieces per chunk
+  static constexpr int kSh = (kP == 4) ? 2 : 1;
+  static __device__ __forceinline__ int swz(int j) { return (j >> kSh) & (kP - 1); }
+};
+
+template <int T, int MR, int G, int U, int R>
+__global__ __launch_bounds__(kThreads) void qgemv_kernel(
+    const uint32_t* __restrict__ w, const typename Elem<T>::S* __restrict__ scales,
+    const typename Elem<T>::S* __restrict__ biases, const typename Elem<T>::S* __restrict__ x,
+    typename Elem<T>::S* __restrict__ y, int K, int N, int M, int kt) {
+  using E = Elem<T>;
+  using X = XTile<T>;
+  constexpr int P = X::kP;
   extern __shared__ u32x4_t xs[];  // x tile, padded to whole 256-slot rounds
   constexpr int RPW = 64 / G * R;  // rows per wave
   const int tid = threadIdx.x;
@@ -66,8 +80,8 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(const uint32_t* __restr
   const int gpr = K >> 6;
 
   const u32x4_t* wrow[R];
-  const uint16_t* srow[R];
-  const uint16_t* brow[R];
+  const typename E::S* srow[R];
+  const typename E::S* brow[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const size_t rr = (size_t)min(row0 + r, N - 1);
@@ -75,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(const uint32_t* __restr
     srow[r] = scales + rr * gpr;
     brow[r] = biases + rr * gpr;
   }
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)((size_t)M * K * 2));
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)((size_t)M * K * E::kBytes));
 
   float acc[R][MR];
 #pragma unroll
@@ -85,7 +99,7 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(const uint32_t* __restr
 
   for (int k0 = 0; k0 < K; k0 += kt) {
     const int kl = min(kt, K - k0);  // tile length
-    const int vpr = kl >> 3;
+    const int vpr = kl / X::kEpp;
     const int tch = kl >> 5;         // chunks in the tile
     const int c0 = k0 >> 5;
     const int xtotal = M * vpr;
@@ -98,15 +112,15 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(const uint32_t* __restr
       const int sl = min(base + tid, xtotal - 1);
       const int m = sl / vpr;
       const int idx = sl - m * vpr;
-      const int j = idx >> 2;
-      const int pc = (idx & 3) ^ ((j >> 2) & 3);
-      const uint32_t off = (uint32_t)((m * K + k0 + j * 32 + pc * 8) * 2);
+      const int j = idx / P;
+      const int pc = (idx & (P - 1)) ^ X::swz(j);
+      const uint32_t off = (uint32_t)((m * K + k0 + j * 32 + pc * X::kEpp) * E::kBytes);
       load_lds16(xr, off, 0u, xs + base + wave * 64);
     }
     __builtin_amdgcn_sched_barrier(0);
     // 2. weight chunks and their scales/biases.
     u32x4_t q[R][U];
-    uint32_t sv[R][U], bv[R][U];
+    typename E::S sv[R][U], bv[R][U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = c0 + min(gl + u * G, tch - 1);
@@ -127,39 +141,79 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(const uint32_t* __restr
     for (int u = 0; u < U; ++u) {
       const int j = min(gl + u * G, tch - 1);
       const bool ok = gl + u * G < tch;
-      const int swz = (j >> 2) & 3;
-      uint32_t wp[R][16];
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float sc = bf16_to_f32(sv[r][u]);
-        const float bi = bf16_to_f32(bv[r][u]);
-        const float s24 = sc * 0x1p24f;
-        const float s20 = sc * 0x1p20f;
-        dequant_word_bf16(q[r][u].x, s24, s20, bi, wp[r] + 0);
-        dequant_word_bf16(q[r][u].y, s24, s20, bi, wp[r] + 4);
-        dequant_word_bf16(q[r][u].z, s24, s20, bi, wp[r] + 8);
-        dequant_word_bf16(q[r][u].w, s24, s20, bi, wp[r] + 12);
-      }
+      const int swz = X::swz(j);
       // Rows m >= M (M rounded up to MR) repeat row M - 1 and are not stored.
+      if constexpr (T == kF32) {
+        float wf[R][32];
 #pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        const u32x4_t* xp = xs + min(m, M - 1) * vpr + j * 4;
-        float a[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) a[r] = acc[r][m];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const u32x4_t xx = xp[v ^ swz];
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-            a[r] = dot2_bf16(wp[r][4 * v + 0], xx.x, a[r]);
-            a[r] = dot2_bf16(wp[r][4 * v + 1], xx.y, a[r]);
-            a[r] = dot2_bf16(wp[r][4 * v + 2], xx.z, a[r]);
-            a[r] = dot2_bf16(wp[r][4 * v + 3], xx.w, a[r]);
-          }
+        for (int r = 0; r < R; ++r) {
+          const float sc = E::param(sv[r][u]);
+          const float bi = E::param(bv[r][u]);
+          dequant_word_f32(q[r][u].x, sc * 0x1p24f, sc * 0x1p20f, bi, wf[r] + 0);
+          dequant_word_f32(q[r][u].y, sc * 0x1p24f, sc * 0x1p20f, bi, wf[r] + 8);
+          dequant_word_f32(q[r][u].z, sc * 0x1p24f, sc * 0x1p20f, bi, wf[r] + 16);
+          dequant_word_f32(q[r][u].w, sc * 0x1p24f, sc * 0x1p20f, bi, wf[r] + 24);
         }
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r][m] = ok ? a[r] : acc[r][m];
+        for (int m = 0; m < MR; ++m) {
+          const u32x4_t* xp = xs + min(m, M - 1) * vpr + j * P;
+          float a[R];
+#pragma unroll
+          for (int r = 0; r < R; ++r) a[r] = acc[r][m];
+#pragma unroll
+          for (int v = 0; v < P; ++v) {
+            const u32x4_t xx = xp[v ^ swz];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              a[r] = __builtin_fmaf(wf[r][4 * v + 0], __uint_as_float(xx.x), a[r]);
+              a[r] = __builtin_fmaf(wf[r][4 * v + 1], __uint_as_float(xx.y), a[r]);
+              a[r] = __builtin_fmaf(wf[r][4 * v + 2], __uint_as_float(xx.z), a[r]);
+              a[r] = __builtin_fmaf(wf[r][4 * v + 3], __uint_as_float(xx.w), a[r]);
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < R; ++r) acc[r][m] = ok ? a[r] : acc[r][m];
+        }
+      } else {
+        uint32_t wp[R][16];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const float sc = E::param(sv[r][u]);
+          const float bi = E::param(bv[r][u]);
+          const float s24 = sc * 0x1p24f;
+          const float s20 = sc * 0x1p20f;
+          E::dequant(q[r][u].x, s24, s20, bi, wp[r] + 0);
+          E::dequant(q[r][u].y, s24, s20, bi, wp[r] + 4);
+          E::dequant(q[r][u].z, s24, s20, bi, wp[r] + 8);
+          E::dequant(q[r][u].w, s24, s20, bi, wp[r] + 12);
+        }
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          const u32x4_t* xp = xs + min(m, M - 1) * vpr + j * P;
+          float a[R];
+#pragma unroll
+          for (int r = 0; r < R; ++r) a[r] = acc[r][m];
+#pragma unroll
+          for (int v = 0; v < P; ++v) {
+            const u32x4_t xx = xp[v ^ swz];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              if constexpr (T == kBf16) {
+                a[r] = dot2_bf16(wp[r][4 * v + 0], xx.x, a[r]);
+                a[r] = dot2_bf16(wp[r][4 * v + 1], xx.y, a[r]);
+                a[r] = dot2_bf16(wp[r][4 * v + 2], xx.z, a[r]);
+                a[r] = dot2_bf16(wp[r][4 * v + 3], xx.w, a[r]);
+              } else {
+                a[r] = dot2_f16(wp[r][4 * v + 0], xx.x, a[r]);
+                a[r] = dot2_f16(wp[r][4 * v + 1], xx.y, a[r]);
+                a[r] = dot2_f16(wp[r][4 * v + 2], xx.z, a[r]);
+                a[r] = dot2_f16(wp[r][4 * v + 3], xx.w, a[r]);
+              }
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < R; ++r) acc[r][m] = ok ? a[r] : acc[r][m];
+        }
       }
     }
   }
@@ -175,7 +229,7 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(const uint32_t* __restr
       if (row0 + r < N) {
 #pragma unroll
         for (int m = 0; m < MR; ++m)
-          if (m < M) y[(size_t)m * N + row0 + r] = (uint16_t)f32_to_bf16_int(acc[r][m]);
+          if (m < M) y[(size_t)m * N + row0 + r] = E::out(acc[r][m]);
       }
     }
   }
@@ -188,8 +242,8 @@ struct Plan {
 
 // K tiles: as long as the LDS budget and U <= max_chunks allow, then evened
 // out so the last tile is not a sliver.
-int tile_len(int k, int mr, int g) {
-  const int by_lds = (kLdsBudget / (2 * mr)) / 64 * 64;
+int tile_len(int k, int mr, int g, int eb) {
+  const int by_lds = (kLdsBudget / (eb * mr)) / 64 * 64;
   const int by_u = 32 * g * max_chunks(mr);
   const int cap = std::min(by_lds, by_u);
   const int tiles = (k + cap - 1) / cap;
@@ -202,7 +256,7 @@ int tile_len(int k, int mr, int g) {
 // counting at most 2048 (where more waves stopped paying for idle lanes on
 // the shapes measured, 9728 x 2560 and 2560 x 9728 at M = 1 ... 16).
 // IMQ_QGEMV_LANES=16|32|64 overrides.
-Plan make_plan(int k, int n, int mr) {
+Plan make_plan(int k, int n, int mr, int eb) {
   static const int forced = [] {
     const char* e = getenv("IMQ_QGEMV_LANES");
     const int v = e ? atoi(e) : 0;
@@ -213,7 +267,7 @@ Plan make_plan(int k, int n, int mr) {
   double best_score = -1.0;
   for (int g = 16; g <= 64; g *= 2) {
     if (forced && g != forced) continue;
-    const int kt = tile_len(k, mr, g);
+    const int kt = tile_len(k, mr, g, eb);
     const int tch = kt / 32;
     const int u = (tch + g - 1) / g;
     const double waves = std::min((double)n * g / (64.0 * r), 2048.0);
@@ -226,66 +280,80 @@ Plan make_plan(int k, int n, int mr) {
   return best;
 }
 
-template <int MR, int G, int U>
-hipError_t launch_u(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
-                    uint16_t* y, int k, int n, int m, int kt, hipStream_t stream) {
+template <int T, int MR, int G, int U>
+hipError_t launch_u(const uint32_t* w, const void* s, const void* b, const void* x, void* y, int k,
+                    int n, int m, int kt, hipStream_t stream) {
+  using ST = typename Elem<T>::S;
   constexpr int R = rows_per_lane(MR);
   constexpr int rows_per_block = kWaves * (64 / G) * R;
   const dim3 grid((n + rows_per_block - 1) / rows_per_block);
   // x slots of the longest tile, rounded up to whole 256-slot rounds.
-  const size_t slots = ((size_t)m * (kt / 8) + kThreads - 1) / kThreads * kThreads;
-  hipLaunchKernelGGL((qgemv_kernel<MR, G, U, R>), grid, dim3(kThreads), slots * 16, stream, w, s,
-                     b, x, y, k, n, m, kt);
+  const size_t pieces = (size_t)m * kt / XTile<T>::kEpp;
+  const size_t slots = (pieces + kThreads - 1) / kThreads * kThreads;
+  hipLaunchKernelGGL((qgemv_kernel<T, MR, G, U, R>), grid, dim3(kThreads), slots * 16, stream, w,
+                     static_cast<const ST*>(s), static_cast<const ST*>(b),
+                     static_cast<const ST*>(x), static_cast<ST*>(y), k, n, m, kt);
   return hipGetLastError();
 }
 
-template <int MR, int G>
-hipError_t launch_g(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
-                    uint16_t* y, int k, int n, int m, const Plan& p, hipStream_t stream) {
+template <int T, int MR, int G>
+hipError_t launch_g(const uint32_t* w, const void* s, const void* b, const void* x, void* y, int k,
+                    int n, int m, const Plan& p, hipStream_t stream) {
   if constexpr (max_chunks(MR) == 8) {
     switch (p.u) {
-      case 1: return launch_u<MR, G, 1>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 2: return launch_u<MR, G, 2>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 3: return launch_u<MR, G, 3>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 4: return launch_u<MR, G, 4>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 5: return launch_u<MR, G, 5>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 6: return launch_u<MR, G, 6>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 7: return launch_u<MR, G, 7>(w, s, b, x, y, k, n, m, p.kt, stream);
-      default: return launch_u<MR, G, 8>(w, s, b, x, y, k, n, m, p.kt, stream);
+      case 1: return launch_u<T, MR, G, 1>(w, s, b, x, y, k, n, m, p.kt, stream);
+      case 2: return launch_u<T, MR, G, 2>(w, s, b, x, y, k, n, m, p.kt, stream);
+      case 3: return launch_u<T, MR, G, 3>(w, s, b, x, y, k, n, m, p.kt, stream);
+      case 4: return launch_u<T, MR, G, 4>(w, s, b, x, y, k, n, m, p.kt, stream);
+      case 5: return launch_u<T, MR, G, 5>(w, s, b, x, y, k, n, m, p.kt, stream);
+      case 6: return launch_u<T, MR, G, 6>(w, s, b, x, y, k, n, m, p.kt, stream);
+      case 7: return launch_u<T, MR, G, 7>(w, s, b, x, y, k, n, m, p.kt, stream);
+      default: return launch_u<T, MR, G, 8>(w, s, b, x, y, k, n, m, p.kt, stream);
     }
   } else {
     switch (p.u) {
-      case 1: return launch_u<MR, G, 1>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 2: return launch_u<MR, G, 2>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 3: return launch_u<MR, G, 3>(w, s, b, x, y, k, n, m, p.kt, stream);
-      default: return launch_u<MR, G, 4>(w, s, b, x, y, k, n, m, p.kt, stream);
+      case 1: return launch_u<T, MR, G, 1>(w, s, b, x, y, k, n, m, p.kt, stream);
+      case 2: return launch_u<T, MR, G, 2>(w, s, b, x, y, k, n, m, p.kt, stream);
+      case 3: return launch_u<T, MR, G, 3>(w, s, b, x, y, k, n, m, p.kt, stream);
+      default: return launch_u<T, MR, G, 4>(w, s, b, x, y, k, n, m, p.kt, stream);
     }
   }
 }
 
-template <int MR>
-hipError_t launch_m(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
-                    uint16_t* y, int k, int n, int m, hipStream_t stream) {
-  const Plan p = make_plan(k, n, MR);
+template <int T, int MR>
+hipError_t launch_m(const uint32_t* w, const void* s, const void* b, const void* x, void* y, int k,
+                    int n, int m, hipStream_t stream) {
+  const Plan p = make_plan(k, n, MR, Elem<T>::kBytes);
   switch (p.g) {
-    case 16: return launch_g<MR, 16>(w, s, b, x, y, k, n, m, p, stream);
-    case 32: return launch_g<MR, 32>(w, s, b, x, y, k, n, m, p, stream);
-    default: return launch_g<MR, 64>(w, s, b, x, y, k, n, m, p, stream);
+    case 16: return launch_g<T, MR, 16>(w, s, b, x, y, k, n, m, p, stream);
+    case 32: return launch_g<T, MR, 32>(w, s, b, x, y, k, n, m, p, stream);
+    default: return launch_g<T, MR, 64>(w, s, b, x, y, k, n, m, p, stream);
   }
+}
+
+template <int T>
+hipError_t launch_t(const uint32_t* w, const void* s, const void* b, const void* x, void* y, int k,
+                    int n, int m, hipStream_t stream) {
+  // M is rounded up to a power of two for the register tile; rows >= M are
+  // not stored.
+  if (m <= 1) return launch_m<T, 1>(w, s, b, x, y, k, n, m, stream);
+  if (m <= 2) return launch_m<T, 2>(w, s, b, x, y, k, n, m, stream);
+  if (m <= 4) return launch_m<T, 4>(w, s, b, x, y, k, n, m, stream);
+  if (m <= 8) return launch_m<T, 8>(w, s, b, x, y, k, n, m, stream);
+  if (m <= 16) return launch_m<T, 16>(w, s, b, x, y, k, n, m, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-hipError_t launch_qgemv(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
-                        const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
-  // M is rounded up to a power of two for the register tile; rows >= M are
-  // not stored.
-  if (m <= 1) return launch_m<1>(w, scales, biases, x, y, k, n, m, stream);
-  if (m <= 2) return launch_m<2>(w, scales, biases, x, y, k, n, m, stream);
-  if (m <= 4) return launch_m<4>(w, scales, biases, x, y, k, n, m, stream);
-  if (m <= 8) return launch_m<8>(w, scales, biases, x, y, k, n, m, stream);
-  if (m <= 16) return launch_m<16>(w, scales, biases, x, y, k, n, m, stream);
-  return hipErrorInvalidValue;
+hipError_t launch_qgemv(const uint32_t* w, const void* scales, const void* biases, const void* x,
+                        void* y, int k, int n, int m, int dtype, hipStream_t stream) {
+  switch (dtype) {
+    case kBf16: return launch_t<kBf16>(w, scales, biases, x, y, k, n, m, stream);
+    case kF16: return launch_t<kF16>(w, scales, biases, x, y, k, n, m, stream);
+    case kF32: return launch_t<kF32>(w, scales, biases, x, y, k, n, m, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace imq

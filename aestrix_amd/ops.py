@@ -17,8 +17,11 @@ stream.  torch is used for device memory and streams only; there is no
 CPU or torch fallback for any computation.
 
 Tensors: packed weights are ``torch.int32`` (or ``torch.uint32``) ``[N, K/8]``
-holding the raw uint32 words; scales, biases, x and y share one dtype
-(bfloat16, or float16 for dequantize).
+holding the raw uint32 words; scales, biases, x and y share one element type
+T: bfloat16 (the text encoder), float16 (the reference's DiT kernels,
+``DirectDiTStep.swift:82-85``) or float32 (its M=1 conditioner kernels,
+``DirectConditioner.swift:48``; no MFMA kernel, so ``qgemm`` rejects it and
+``quantized_matmul`` runs any M on the qGEMV kernel).
 """
 
 from __future__ import annotations

@@ -15,13 +15,14 @@
  *   w       uint32 [N, K/8]  eight 4-bit codes per word, low nibble first
  *   scales  T      [N, K/64]
  *   biases  T      [N, K/64]
- *   deq(W)[n][k] = RNE_T( fl32( scales[n][k/64] * q[n][k] + biases[n][k/64] ) )
+ *   deq(W)[n][k] = RNE_T( fl32( fl32(scales[n][k/64] * q[n][k]) + biases[n][k/64] ) )
+ *                  (for bf16 and f16 scales the product is exact)
  *   y[M, N]      = x[M, K] . deq(W)^T, accumulated in fp32, rounded to T.
  * All tensors are row-major and contiguous; sub-tensors (row halves, the
  * reference's setBuffer byte offsets, DirectDiTStep.swift:576-579) are passed
  * as offset device pointers.  w, x and the dequantize output must be 16-byte
  * aligned (any whole number of rows of a K % 64 == 0 matrix keeps that);
- * scales, biases and y must be 2-byte aligned.
+ * scales, biases and y must be aligned to sizeof(T).
  *
  * Conventions:
  *   - Every call returns an imq_status (0 = IMQ_OK).  No C++ exception crosses
@@ -54,7 +55,9 @@ typedef enum imq_status {
 } imq_status;
 
 /* Element type T of x, scales, biases and y ("s and b share T",
- * DirectQmmSpike.swift:84, DirectConditioner.swift:48-49). */
+ * DirectQmmSpike.swift:84, DirectConditioner.swift:48-49).  All three are
+ * provided by imq_dequantize, imq_qmm_t and imq_qgemv; imq_qgemm (MFMA) takes
+ * bf16 and f16, and imq_qmm_t runs f32 at any M on the qGEMV kernel. */
 typedef enum imq_dtype {
     IMQ_BF16 = 0, /* the text encoder / context-embedder kernels (DirectTEEncoder.swift:69-72) */
     IMQ_F16 = 1,  /* the DiT kernels (DirectDiTStep.swift:82-85) */
@@ -107,7 +110,8 @@ int imq_dequantize(imq_ctx* ctx, const uint32_t* w, const void* scales, const vo
  * (DirectTELayer.swift:109-128), DirectConditioner.qmm
  * (DirectConditioner.swift:96-117) and MLX quantizedMM(transpose: true)
  * (Sources/ImarelloDiT/AttentionUtils.swift:212-221).  M <= 16 runs the qGEMV
- * kernel, larger M the MFMA qGEMM kernel. */
+ * kernel, larger M the MFMA qGEMM kernel (f32: the qGEMV kernel, 16 rows at a
+ * time). */
 int imq_qmm_t(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
               const void* x, void* y, int k, int n, int m, int group_size, int bits,
               imq_dtype dtype, imq_stream stream);
@@ -118,8 +122,9 @@ int imq_qgemv(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* b
               const void* x, void* y, int k, int n, int m, int group_size, int bits,
               imq_dtype dtype, imq_stream stream);
 
-/* The dense regime alone (any M >= 1): dequant fused into bf16 MFMA tiles,
- * fp32 accumulators.  Same contract as imq_qmm_t. */
+/* The dense regime alone (any M >= 1): dequant fused into bf16 / f16 MFMA
+ * tiles, fp32 accumulators.  Same contract as imq_qmm_t; f32 returns
+ * IMQ_EUNSUPPORTED. */
 int imq_qgemm(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
               const void* x, void* y, int k, int n, int m, int group_size, int bits,
               imq_dtype dtype, imq_stream stream);

@@ -1,7 +1,8 @@
 """numpy restatement of the affine 4-bit quantized linear path (test oracle).
 
 TEST INFRASTRUCTURE ONLY -- see the package docstring.  All bf16 values are
-carried as ``uint16`` bit patterns.
+carried as ``uint16`` bit patterns; f16 and f32 values as numpy float16 /
+float32 arrays (the ``*_as`` functions).
 """
 
 from __future__ import annotations
@@ -96,10 +97,57 @@ def qmm_t_f32_dequant_f64(x: np.ndarray, w: np.ndarray, scales: np.ndarray,
     return bf16_to_f32(x).astype(np.float64) @ wd.T
 
 
+def dequantize_as(w: np.ndarray, scales: np.ndarray, biases: np.ndarray,
+                  dtype) -> np.ndarray:
+    """deq(W) [N, K] in T = float16 or float32, with scales and biases given in T:
+    RNE_T(fl32(fl32(s*q) + b)); for float32 the weight is fl32(fl32(s*q) + b)
+    itself.  Two rounded float32 operations, as in ``dequantize``; with f16
+    scales the product is exact, with f32 scales it is not.
+
+    The element type of the reference's DiT kernels (``affine_qmm_t_float16_t``,
+    ``DirectDiTStep.swift:82-85``, scales precast to f16 by
+    ``TransformerWeights.swift:40-54``) and of its conditioner kernels
+    (``affine_qmm_t_float``, f32 scales, ``DirectConditioner.swift:48,75-84``).
+    numpy's float32 -> float16 cast rounds to nearest even."""
+    dtype = np.dtype(dtype)
+    assert dtype in (np.float16, np.float32)
+    q = unpack_codes(w).astype(np.float32)
+    n, k = q.shape
+    assert k % GROUP_SIZE == 0
+    s = np.repeat(np.asarray(scales).astype(np.float32), GROUP_SIZE, axis=-1).reshape(n, k)
+    b = np.repeat(np.asarray(biases).astype(np.float32), GROUP_SIZE, axis=-1).reshape(n, k)
+    with np.errstate(over="ignore", invalid="ignore"):
+        return (s * q + b).astype(dtype)
+
+
+def qmm_t_as(x: np.ndarray, w: np.ndarray, scales: np.ndarray, biases: np.ndarray,
+             dtype) -> np.ndarray:
+    """y[M, N] = RNE_T(x . deq_T(w)^T accumulated in float64), T = float16 or
+    float32 (numpy's float64 -> float16 / float32 casts round once, to nearest
+    even)."""
+    dtype = np.dtype(dtype)
+    xd = np.asarray(x).astype(np.float64)
+    wd = dequantize_as(w, scales, biases, dtype).astype(np.float64)
+    return (xd @ wd.T).astype(dtype)
+
+
+def error_stats_values(y: np.ndarray, o: np.ndarray) -> dict:
+    """error_stats for float16 / float32 outputs (values, not bit patterns)."""
+    stats = _stats(np.asarray(y).astype(np.float64), np.asarray(o).astype(np.float64))
+    stats["bit_exact_frac"] = float(np.mean(np.asarray(y) == np.asarray(o))) if o.size else 1.0
+    return stats
+
+
 def error_stats(y_bits: np.ndarray, oracle_bits: np.ndarray) -> dict:
     """Tolerance metrics: MAE, normwise max error, floored elementwise error."""
     y = bf16_to_f32(y_bits).astype(np.float64)
     o = bf16_to_f32(oracle_bits).astype(np.float64)
+    stats = _stats(y, o)
+    stats["bit_exact_frac"] = float(np.mean(y_bits == oracle_bits)) if o.size else 1.0
+    return stats
+
+
+def _stats(y: np.ndarray, o: np.ndarray) -> dict:
     d = np.abs(y - o)
     omax = float(np.max(np.abs(o))) if o.size else 0.0
     rms = float(np.sqrt(np.mean(o * o))) if o.size else 0.0
@@ -109,5 +157,4 @@ def error_stats(y_bits: np.ndarray, oracle_bits: np.ndarray) -> dict:
         "max_abs": float(np.max(d)) if d.size else 0.0,
         "max_rel_normwise": float(np.max(d) / omax) if d.size and omax > 0 else 0.0,
         "max_rel_floored": float(np.max(d / np.where(floor > 0, floor, 1.0))) if d.size else 0.0,
-        "bit_exact_frac": float(np.mean(y_bits == oracle_bits)) if d.size else 1.0,
     }

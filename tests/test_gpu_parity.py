@@ -245,7 +245,7 @@ def test_argument_errors_are_reported():
     with pytest.raises(NotImplementedError):
         imq.quantized_matmul(x, w, s, b, bits=8)
     with pytest.raises(NotImplementedError):
-        imq.quantized_matmul(x.float(), w, s.float(), b.float())
+        imq.quantized_matmul(x.double(), w, s.double(), b.double())  # no f64 element type
     with pytest.raises(NotImplementedError):
         imq.quantized_matmul(x, w, s, b, transpose=False)
     with pytest.raises(ValueError):
@@ -270,8 +270,8 @@ def test_argument_errors_are_reported():
     assert L.imq_qmm_t(ctx, *args, 128, 64, 4, 64, 8, 0, None) == _lib.IMQ_EUNSUPPORTED
     assert L.imq_qmm_t(ctx, *args, 128, 64, 4, 32, 4, 0, None) == _lib.IMQ_EUNSUPPORTED
     assert L.imq_qgemv(ctx, *args, 128, 64, 17, 64, 4, 0, None) == _lib.IMQ_EINVAL
-    assert L.imq_dequantize(ctx, args[0], args[1], args[2], args[4], 128, 64, 64, 4, 2,
-                            None) == _lib.IMQ_EUNSUPPORTED
+    assert L.imq_dequantize(ctx, args[0], args[1], args[2], args[4], 128, 64, 64, 4, 7,
+                            None) == _lib.IMQ_EUNSUPPORTED  # no such dtype
     out = ctypes.c_void_p()
     assert L.imq_create(10_000, ctypes.byref(out)) == _lib.IMQ_EINVAL
 

@@ -388,3 +388,128 @@ def test_qmm_checks_catch_mutants():
     wrong_order = ref.f64_to_bf16(x[:, ::-1] @ deq.T)
     for mutant in (no_bias, wrong_order):
         assert not np.array_equal(mutant, want)
+
+
+# ------------------------------------------- f16 / f32 element types (DiT, conditioner)
+# The reference's DiT kernels run in f16 (DirectDiTStep.swift:82-85) and its
+# conditioner kernels in f32 (DirectConditioner.swift:48,75-84).  The oracle's
+# *_as functions are pinned here by the same exact-rational rounding.
+
+F16 = dict(p=11, emin=-14, emax=15)
+F32 = dict(p=24, emin=-126, emax=127)
+
+
+def _f16_param_values() -> np.ndarray:
+    vals = [0.0, -0.0, 1.0, -1.0, 0.02, -0.0175, 3.0517578125e-05, 6.1035156e-05, 5.96e-08,
+            -5.96e-08, 1.5e-05, 0.333, 1000.0, -4096.0, 65504.0, 0.5 + 2 ** -11, 2 ** -14]
+    return np.array(vals, dtype=np.float16)
+
+
+def _exact_deq(s: float, b: float, q: int, fmt: dict):
+    prod = _rne(Fraction(float(s)) * q, 24)
+    if isinstance(prod, float):
+        return prod
+    f32 = _rne(prod + Fraction(float(b)), 24)
+    if isinstance(f32, float):
+        return f32
+    return _rne(f32, **fmt)
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_dequant_as_matches_exact_rational_grid(dtype):
+    vals = _f16_param_values().astype(dtype)
+    if dtype == np.float32:
+        vals = np.concatenate([vals, np.array([3.4e38, -1e-40, 7.0e-39, 1.0000001], np.float32)])
+    fmt = F16 if dtype == np.float16 else F32
+    s = np.repeat(vals, len(vals)).reshape(-1, 1)
+    b = np.tile(vals, len(vals)).reshape(-1, 1)
+    n = s.shape[0]
+    codes = np.tile(np.arange(16, dtype=np.uint8), (n, 4))  # K = 64: every code 4 times
+    w = ref.pack_codes(codes)
+    got = ref.dequantize_as(w, s, b, dtype)
+    for i in range(n):
+        for c in range(16):
+            want = _exact_deq(s[i, 0], b[i, 0], c, fmt)
+            g = got[i, c]
+            if isinstance(want, float):
+                assert np.isinf(g) and np.sign(g) == np.sign(want), (s[i, 0], b[i, 0], c)
+            else:
+                assert Fraction(float(g)) == want, (s[i, 0], b[i, 0], c, g, want)
+
+
+def test_f64_to_f16_and_f32_casts_round_once():
+    rng = np.random.default_rng(7)
+    v = np.concatenate([rng.standard_normal(3000) * 10.0 ** rng.integers(-9, 5, 3000),
+                        # f16 halfway points nudged by less than an f32 ulp: a cast through
+                        # float32 would round these twice
+                        (1 + (2 * rng.integers(0, 1024, 500) + 1) * 2.0 ** -11) * (1 + 2.0 ** -40),
+                        (1 + (2 * rng.integers(0, 1024, 500) + 1) * 2.0 ** -11) * (1 - 2.0 ** -40)])
+    for dtype, fmt in ((np.float16, F16), (np.float32, F32)):
+        got = v.astype(dtype)
+        for a, g in zip(v, got):
+            want = _rne(Fraction(float(a)), **fmt)
+            if isinstance(want, float):
+                assert np.isinf(g)
+            else:
+                assert Fraction(float(g)) == want, (dtype, a, g)
+
+
+def _exact_qmm_as(x, w, s, b, dtype, fmt):
+    deq = ref.dequantize_as(w, s, b, dtype)
+    m, n = x.shape[0], w.shape[0]
+    y = np.empty((m, n), dtype=dtype)
+    for i in range(m):
+        for j in range(n):
+            acc = sum(Fraction(float(a)) * Fraction(float(c)) for a, c in zip(x[i], deq[j]))
+            r = _rne(acc, **fmt)
+            y[i, j] = float(r)
+    return y
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_qmm_as_brute_force_exact_tiny(dtype):
+    fmt = F16 if dtype == np.float16 else F32
+    p = synth.make_problem(3, 5, 128, seed=21)
+    x = ref.bf16_to_f32(p.x).astype(dtype)
+    s = ref.bf16_to_f32(p.scales).astype(dtype)
+    b = ref.bf16_to_f32(p.biases).astype(dtype)
+    got = ref.qmm_t_as(x, p.w, s, b, dtype)
+    want = _exact_qmm_as(x, p.w, s, b, dtype, fmt)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_qmm_as_rank1_known_answer(dtype):
+    """All codes equal c: deq is constant per group, y = sum_g w_g * sum_{k in g} x_k."""
+    n, k, c = 4, 192, 11
+    codes = np.full((n, k), c, dtype=np.uint8)
+    w = ref.pack_codes(codes)
+    s = np.array([[0.02, 0.5, -0.25]] * n, dtype=dtype)
+    b = np.array([[-0.16, 1.0, 2.0]] * n, dtype=dtype)
+    x = np.linspace(-1, 1, 2 * k).reshape(2, k).astype(dtype)
+    wg = [float(np.float32(np.float32(s[0, g]) * c) + np.float32(b[0, g])) for g in range(3)]
+    wg = [float(np.asarray(v, np.float32).astype(dtype)) for v in wg]
+    for i in range(2):
+        exact = sum(Fraction(wg[g]) * sum(Fraction(float(v)) for v in x[i, 64 * g:64 * g + 64])
+                    for g in range(3))
+        want = float(_rne(exact, **(F16 if dtype == np.float16 else F32)))
+        got = ref.qmm_t_as(x, w, s, b, dtype)
+        assert np.all(got[i] == np.asarray(want, dtype=dtype))
+
+
+def test_f16_checks_catch_unrounded_dequant_mutant():
+    """Skipping the f16 rounding of deq(W) (keeping fl32(s*q+b)) must fail the
+    brute-force check on a small case.  Scales and biases carry full 11-bit
+    significands here: bf16-derived ones (8 bits) make s*q + b exact in f16,
+    which is why the reference's f16 precast of the bf16 pack loses nothing
+    (TransformerWeights.swift:40-54)."""
+    rng = np.random.default_rng(5)
+    p = synth.make_problem(4, 16, 256, seed=21)
+    x = ref.bf16_to_f32(p.x).astype(np.float16)
+    s = (rng.random((16, 4)) * 0.05 + 0.01).astype(np.float16)
+    b = (-8 * s.astype(np.float64) + rng.standard_normal((16, 4)) * 0.01).astype(np.float16)
+    want = _exact_qmm_as(x, p.w, s, b, np.float16, F16)
+    assert np.array_equal(ref.qmm_t_as(x, p.w, s, b, np.float16), want)
+    deq32 = ref.dequantize_as(p.w, s, b, np.float32).astype(np.float64)
+    mutant = (x.astype(np.float64) @ deq32.T).astype(np.float16)
+    assert not np.array_equal(mutant, want)
