@@ -1,4 +1,5 @@
-"""ctypes binding of the C ABI in ``include/imq.h`` (``aestrix_amd/libimq.so``).
+"""ctypes binding of the C ABI in ``include/imq.h`` and ``include/imq_weights.h``
+(``aestrix_amd/libimq.so``).
 
 The library is built in-tree by ``aestrix_amd/build.py``.  Loading never
 builds and never falls back: a missing library raises ``ImqLibraryMissing``.
@@ -22,10 +23,32 @@ IMQ_BF16 = 0
 IMQ_F16 = 1
 IMQ_F32 = 2
 
-# Every entry point the header declares, with its ctypes signature.
+IMQ_ST_MAX_DIMS = 8
+# safetensors dtype strings in imq_st_dtype order, with element sizes.
+ST_DTYPES = ["BOOL", "U8", "I8", "U16", "I16", "F16", "BF16", "U32", "I32", "F32", "U64", "I64",
+             "F64", "F8_E4M3", "F8_E5M2"]
+ST_SIZES = [1, 1, 1, 2, 2, 2, 2, 4, 4, 4, 8, 8, 8, 1, 1]
+
+
+class StInfo(ctypes.Structure):
+    """imq_st_info."""
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_int), ("ndim", ctypes.c_int),
+                ("shape", ctypes.c_int64 * IMQ_ST_MAX_DIMS), ("data", ctypes.c_void_p),
+                ("bytes", ctypes.c_size_t), ("shard", ctypes.c_int)]
+
+
+class QWeight(ctypes.Structure):
+    """imq_qweight."""
+    _fields_ = [("w", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("biases", ctypes.c_void_p),
+                ("n", ctypes.c_int), ("k", ctypes.c_int), ("dtype", ctypes.c_int),
+                ("base", ctypes.c_void_p)]
+
+
+# Every entry point the headers declare, with its ctypes signature.
 _p = ctypes.c_void_p
 _i = ctypes.c_int
 _sz = ctypes.c_size_t
+_s = ctypes.c_char_p
 _QMM = [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]
 SIGNATURES = {
     "imq_abi_version": ([], _i),
@@ -44,6 +67,21 @@ SIGNATURES = {
     "imq_qmm_t": (_QMM, _i),
     "imq_qgemv": (_QMM, _i),
     "imq_qgemm": (_QMM, _i),
+    # imq_weights.h
+    "imq_st_open": ([ctypes.POINTER(_s), _i, ctypes.POINTER(_p)], _i),
+    "imq_st_open_dir": ([_s, ctypes.POINTER(_p)], _i),
+    "imq_st_close": ([_p], _i),
+    "imq_st_last_error": ([_p], _s),
+    "imq_st_shard_count": ([_p], _i),
+    "imq_st_shard_path": ([_p, _i], _s),
+    "imq_st_metadata": ([_p, _i, _s], _s),
+    "imq_st_count": ([_p], _i),
+    "imq_st_info_at": ([_p, _i, ctypes.POINTER(StInfo)], _i),
+    "imq_st_find": ([_p, _s, ctypes.POINTER(StInfo)], _i),
+    "imq_upload": ([_p, _p, _p, _sz, _p], _i),
+    "imq_st_upload": ([_p, _p, _s, _i, _p, _sz, _p], _i),
+    "imq_load_qlinear": ([_p, _p, _s, _i, ctypes.POINTER(QWeight), _p], _i),
+    "imq_qweight_free": ([_p, ctypes.POINTER(QWeight)], _i),
 }
 
 

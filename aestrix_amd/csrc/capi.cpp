@@ -13,16 +13,19 @@
 #include <new>
 #include <string>
 
+#include "ctx.hpp"
 #include "imq.h"
 #include "imq_kernels.hpp"
 
-struct imq_ctx {
-  int device = 0;
-  mutable std::mutex mu;
-  std::string err;
-};
+imq_ctx::~imq_ctx() {
+  for (int i = 0; i < kStagingBuffers; ++i) {
+    if (staging_done[i]) (void)hipEventDestroy(staging_done[i]);
+    if (staging[i]) (void)hipHostFree(staging[i]);
+  }
+}
 
-namespace {
+namespace imq {
+namespace detail {
 
 thread_local std::string g_create_error;  // failures before a context exists
 
@@ -53,6 +56,13 @@ int bind_device(imq_ctx* ctx) {
   const hipError_t e = hipSetDevice(ctx->device);
   return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, "hipSetDevice");
 }
+
+}  // namespace detail
+}  // namespace imq
+
+using namespace imq::detail;
+
+namespace {
 
 // Shared validation of the quantized-matmul entry points.
 int check_qmm(imq_ctx* ctx, const char* fn, const uint32_t* w, const void* s, const void* b,

@@ -5,6 +5,7 @@ checks that fail before any device work.
 """
 
 import ctypes
+import glob
 import os
 import re
 
@@ -13,13 +14,15 @@ import pytest
 from aestrix_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "imq.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
 
 
 def header_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(imq_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(imq_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_is_built():
@@ -31,7 +34,7 @@ def test_every_declared_symbol_is_exported_and_bound():
     declared = header_functions()
     assert len(declared) >= 16
     for name in declared:
-        assert hasattr(L, name), f"{name} declared in imq.h but not exported"
+        assert hasattr(L, name), f"{name} declared in include/ but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
     assert set(_lib.SIGNATURES) == set(declared)
 
