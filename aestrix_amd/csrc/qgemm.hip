@@ -233,25 +233,36 @@ __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_
 // Activations are staged by direct buffer->LDS loads (buffer_load_dwordx4 ...
 // lds: lane L writes LDS base + 16 L, no VGPRs; the per-lane byte offset is
 // fixed for the whole K loop and the K-step advance is a scalar offset, so a
-// load costs no vector ALU work) into a 3-stage LDS ring, issued two K-steps
+// load costs no vector ALU work) into a 4-stage LDS ring, issued two K-steps
 // ahead.  Packed weights need no sharing between waves (each wave owns its
 // columns), so they are loaded straight into registers, also two steps ahead,
-// keeping their bytes off the LDS port that the activation reads saturate.  Every step issues the same number of
-// vector-memory instructions (4 scale/bias loads, then 2 weight and MT
-// activation loads; steps past the end re-load the last step into the free
-// stage), so one fixed `s_waitcnt vmcnt(2 + MT)` at the top of step g
+// keeping their bytes off the LDS port that the activation reads saturate.
+//
+// Scales and biases are loaded four groups at a time (8 bytes of a row per
+// load, one block ahead): a lane's per-step 2-byte loads touch one cache line
+// per row each, and at four such loads per step they cost more memory-pipeline
+// time than the weights and activations together.  The K loop is unrolled by
+// four so that the ring stage, the register slot and the group's position in
+// its scale block (and the block's register slot, over a two-block unroll of
+// eight steps) are all compile-time constants.
+//
+// Step g issues NTW weight and kA activation loads (for step g+2), plus at
+// steps g % 4 == 0 the 2 NTW scale-block loads of the next block (for steps
+// g+4 .. g+7); steps past the end re-load the last step into the free stage.
+// At the top of step g, `s_waitcnt vmcnt(<loads issued by step g-1>)`
 // guarantees that this wave's loads of step g have landed, and a raw
 // s_barrier (no fence, which would wait for every outstanding load) makes the
-// other waves' parts visible and frees the stage that step g+2 overwrites.
-// Within a step, the A fragments of k-slice kk+1 are read from LDS and the
-// weight words of kk+1 dequantized while the MFMAs of kk run.
+// other waves' parts visible and frees the stage that step g+2 overwrites
+// (stage (g+2) % 4 was last read in step g-2).  Within a step, the A fragments
+// of k-slice kk+1 are read from LDS and the weight words of kk+1 dequantized
+// while the MFMAs of kk run.
+//
+// Requires K % 256 == 0 (whole scale blocks); other K take the
+// register-staged kernel.  An odd number of blocks ends with one 4-step block
+// in slot 0.
 // ---------------------------------------------------------------------------
 constexpr int kBigBN = 256;
-constexpr int kStages = 3;
-
-__device__ __forceinline__ u32x4_t load_w16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
-  return load_b128(rs, voff, soff);
-}
+constexpr int kStages = 4;
 
 // Tile geometry: WM x WN = 4 waves; a wave owns MTW x NTW MFMA tiles of 32x32
 // (a (32 MTW) x (32 NTW) sub-tile); the workgroup tile is
@@ -270,43 +281,63 @@ struct BigRing {
 
 template <int MTW, int NTW, int WM>
 struct BigSrc {
-  __amdgpu_buffer_rsrc_t xr, wr;
+  __amdgpu_buffer_rsrc_t xr, wr, sr, br;
   uint32_t a_off[BigCfg<MTW, NTW, WM>::kA];  // byte offsets of this thread's activation slots
   uint32_t w_off[NTW];  // byte offsets of this lane's 16 weight bytes, per column tile
-  const uint16_t* s_src[NTW];
-  const uint16_t* b_src[NTW];
+  uint32_t p_off[NTW];  // byte offsets of this lane's scale / bias row, per column tile
 };
 
-// One K-step (one quantization group) of the large-M kernel.  S = g % 3 is a
-// compile-time constant: the stage arrays it reads and the ones its direct
+// Four consecutive scales (or biases) of a row, groups 4b .. 4b+3.
+__device__ __forceinline__ uint2 load_param_block(__amdgpu_buffer_rsrc_t rs, uint32_t voff,
+                                                  uint32_t b) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, b * 8u, 0);
+  return __builtin_bit_cast(uint2, v);
+}
+
+// Scale or bias of position j (0..3) of a block.
+__device__ __forceinline__ uint32_t param_at(uint2 blk, int j) {
+  const uint32_t w = (j < 2) ? blk.x : blk.y;
+  return (j & 1) ? (w >> 16) : (w & 0xFFFFu);
+}
+
+// One K-step (one quantization group) of the large-M kernel.  S = g % 8 is a
+// compile-time constant: the LDS stage S % 4 it reads and the ones its direct
 // loads fill are distinct LDS objects, so the compiler can prove that the
-// in-flight loads into stages S+1 and S+2 do not alias the reads of stage S
-// and does not wait for them.
+// in-flight loads into other stages do not alias the reads of stage S % 4 and
+// does not wait for them; its scale block sits in register slot S / 4 while
+// the next block loads into the other slot.
 template <int T, int MTW, int NTW, int WM, int S>
 __device__ __forceinline__ void big_step(int g, int gpr, const BigRing& ring,
                                          const BigSrc<MTW, NTW, WM>& src,
-                                         uint32_t (&sc)[kStages][NTW], uint32_t (&bs)[kStages][NTW],
+                                         uint2 (&sblk)[2][NTW], uint2 (&bblk)[2][NTW],
                                          u32x4_t (&wr)[kStages][NTW], f32x16_t (&acc)[MTW][NTW],
                                          int wave, int arow0, int r32, int h) {
   using C = BigCfg<MTW, NTW, WM>;
-  constexpr int S1 = (S + 1) % kStages;
+  constexpr int ST = S % kStages;
   constexpr int S2 = (S + 2) % kStages;
-  IMQ_WAIT_VMCNT(NTW + C::kA);  // this wave's loads up to step g are done
+  constexpr int SLOT = S / 4;
+  constexpr int J = S % 4;  // position in the scale block
+  // Loads issued by step g-1: its weights and activations, and a scale block
+  // when g-1 started a block.
+  constexpr int kPrev = NTW + C::kA + (((S + 7) % 4) == 0 ? 2 * NTW : 0);
+  IMQ_WAIT_VMCNT(kPrev);  // this wave's loads up to step g are done
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
-  // Next step's scales, then the weights (registers) and activations (LDS
-  // stage S2) of step g+2.
-  const int g1 = min(g + 1, gpr - 1);
+  // At a block start the next block goes to the other slot.
+  if constexpr (J == 0) {
+    const uint32_t nb = (uint32_t)min((g >> 2) + 1, (gpr >> 2) - 1);
 #pragma unroll
-  for (int nt = 0; nt < NTW; ++nt) {
-    sc[S1][nt] = src.s_src[nt][g1];
-    bs[S1][nt] = src.b_src[nt][g1];
+    for (int nt = 0; nt < NTW; ++nt) {
+      sblk[SLOT ^ 1][nt] = load_param_block(src.sr, src.p_off[nt], nb);
+      bblk[SLOT ^ 1][nt] = load_param_block(src.br, src.p_off[nt], nb);
+    }
   }
+  // Weights (registers) and activations (LDS stage S2) of step g+2.
   const uint32_t g2 = (uint32_t)min(g + 2, gpr - 1);
 #pragma unroll
-  for (int nt = 0; nt < NTW; ++nt) wr[S2][nt] = load_w16(src.wr, src.w_off[nt], g2 * 32u);
+  for (int nt = 0; nt < NTW; ++nt) wr[S2][nt] = load_b128(src.wr, src.w_off[nt], g2 * 32u);
   {
     uint4* ab = ring.a[S2] + wave * 64;
 #pragma unroll
@@ -314,17 +345,17 @@ __device__ __forceinline__ void big_step(int g, int gpr, const BigRing& ring,
   }
   __builtin_amdgcn_sched_barrier(0);  // the loads go out before this step's compute
 
-  const uint4* at = ring.a[S];
+  const uint4* at = ring.a[ST];
   u32x4_t wraw[NTW];
 #pragma unroll
-  for (int nt = 0; nt < NTW; ++nt) wraw[nt] = wr[S][nt];
+  for (int nt = 0; nt < NTW; ++nt) wraw[nt] = wr[ST][nt];
   float s24[NTW], s20[NTW], bb[NTW];
 #pragma unroll
   for (int nt = 0; nt < NTW; ++nt) {
-    const float sv = Elem<T>::param(sc[S][nt]);
+    const float sv = Elem<T>::param((typename Elem<T>::S)param_at(sblk[SLOT][nt], J));
     s24[nt] = sv * 0x1p24f;
     s20[nt] = sv * 0x1p20f;
-    bb[nt] = Elem<T>::param(bs[S][nt]);
+    bb[nt] = Elem<T>::param((typename Elem<T>::S)param_at(bblk[SLOT][nt], J));
   }
 
   u32x4_t afrag[2][MTW];
@@ -383,8 +414,8 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     int M, int N, int K, int tiles_m, int tiles_n) {
   using C = BigCfg<MTW, NTW, WM>;
   constexpr int A_SLOTS = C::kBM * 8;
-  __shared__ uint4 a_st0[A_SLOTS], a_st1[A_SLOTS], a_st2[A_SLOTS];
-  const BigRing ring = {{a_st0, a_st1, a_st2}};
+  __shared__ uint4 a_st0[A_SLOTS], a_st1[A_SLOTS], a_st2[A_SLOTS], a_st3[A_SLOTS];
+  const BigRing ring = {{a_st0, a_st1, a_st2, a_st3}};
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -404,6 +435,8 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   BigSrc<MTW, NTW, WM> src;
   src.xr = make_rsrc(x, (uint32_t)((size_t)M * K * 2));
   src.wr = make_rsrc(w, (uint32_t)((size_t)N * K / 2));
+  src.sr = make_rsrc(scales, (uint32_t)((size_t)N * gpr * 2));
+  src.br = make_rsrc(biases, (uint32_t)((size_t)N * gpr * 2));
   // Activation slot s = i*256 + tid holds tile row s/8, physical chunk s%8,
   // i.e. logical chunk (s%8) ^ f(row) of that row.  Rows past M are clamped.
 #pragma unroll
@@ -420,8 +453,7 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   for (int nt = 0; nt < NTW; ++nt) {
     const int gr = min(ncol0 + nt * 32 + r32, N - 1);
     src.w_off[nt] = (uint32_t)gr * (uint32_t)(K / 2) + (uint32_t)h * 16u;
-    src.s_src[nt] = scales + (size_t)gr * gpr;
-    src.b_src[nt] = biases + (size_t)gr * gpr;
+    src.p_off[nt] = (uint32_t)gr * (uint32_t)gpr * 2u;
   }
 
   f32x16_t acc[MTW][NTW];
@@ -432,35 +464,43 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.f;
 
-  // Prologue: scales of step 0, weights and activations of steps 0 and 1
-  // (clamped), in the same per-step issue order as big_step.
-  uint32_t sc[kStages][NTW], bs[kStages][NTW];
+  // Prologue: the scale block of steps 0..3, then weights and activations of
+  // steps 0 and 1 (clamped) in the loop's per-step order.
+  uint2 sblk[2][NTW], bblk[2][NTW];
   u32x4_t wr[kStages][NTW];
 #pragma unroll
   for (int nt = 0; nt < NTW; ++nt) {
-    sc[0][nt] = src.s_src[nt][0];
-    bs[0][nt] = src.b_src[nt][0];
+    sblk[0][nt] = load_param_block(src.sr, src.p_off[nt], 0u);
+    bblk[0][nt] = load_param_block(src.br, src.p_off[nt], 0u);
   }
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
     const uint32_t gg = (uint32_t)min(st, gpr - 1);
     uint4* ab = ring.a[st] + wave * 64;
 #pragma unroll
-    for (int nt = 0; nt < NTW; ++nt) wr[st][nt] = load_w16(src.wr, src.w_off[nt], gg * 32u);
+    for (int nt = 0; nt < NTW; ++nt) wr[st][nt] = load_b128(src.wr, src.w_off[nt], gg * 32u);
 #pragma unroll
     for (int i = 0; i < C::kA; ++i) load_lds16(src.xr, src.a_off[i], gg * 128u, ab + i * kThreads);
   }
 
+  // gpr is a multiple of 4: pairs of blocks, then possibly one block.
   int g = 0;
-  for (; g + 3 <= gpr; g += 3) {
-    big_step<T, MTW, NTW, WM, 0>(g, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
-    big_step<T, MTW, NTW, WM, 1>(g + 1, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
-    big_step<T, MTW, NTW, WM, 2>(g + 2, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
+  for (; g + 8 <= gpr; g += 8) {
+    big_step<T, MTW, NTW, WM, 0>(g, gpr, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
+    big_step<T, MTW, NTW, WM, 1>(g + 1, gpr, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
+    big_step<T, MTW, NTW, WM, 2>(g + 2, gpr, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
+    big_step<T, MTW, NTW, WM, 3>(g + 3, gpr, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
+    big_step<T, MTW, NTW, WM, 4>(g + 4, gpr, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
+    big_step<T, MTW, NTW, WM, 5>(g + 5, gpr, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
+    big_step<T, MTW, NTW, WM, 6>(g + 6, gpr, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
+    big_step<T, MTW, NTW, WM, 7>(g + 7, gpr, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
   }
-  if (g < gpr)
-    big_step<T, MTW, NTW, WM, 0>(g, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
-  if (g + 1 < gpr)
-    big_step<T, MTW, NTW, WM, 1>(g + 1, gpr, ring, src, sc, bs, wr, acc, wave, arow0, r32, h);
+  if (g < gpr) {
+    big_step<T, MTW, NTW, WM, 0>(g, gpr, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
+    big_step<T, MTW, NTW, WM, 1>(g + 1, gpr, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
+    big_step<T, MTW, NTW, WM, 2>(g + 2, gpr, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
+    big_step<T, MTW, NTW, WM, 3>(g + 3, gpr, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
+  }
   IMQ_WAIT_VMCNT(0);  // drain the clamped tail loads before the workgroup ends
 
 #pragma unroll
@@ -523,9 +563,10 @@ hipError_t launch_tile(const uint32_t* w, const uint16_t* scales, const uint16_t
 template <int T>
 hipError_t launch_t(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                     const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
-  // The buffer-load kernel addresses x and w with 32-bit byte offsets.
+  // The buffer-load kernel addresses x and w with 32-bit byte offsets and
+  // loads scales in blocks of four groups.
   const bool fits32 = (size_t)m * k * 2 < ((size_t)1 << 31) && (size_t)n * k / 2 < ((size_t)1 << 31);
-  if (!fits32) return launch_tile<T, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
+  if (!fits32 || k % 256 != 0) return launch_tile<T, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
   static const int cus = [] {
     int dev = 0, v = 0;
     if (hipGetDevice(&dev) == hipSuccess &&
