@@ -9,7 +9,9 @@ the C ABI of ``include/imq.h`` (``aestrix_amd/libimq.so``):
 * ``qgemv``             -- M <= 16, register dequant, no MFMA, HBM-bound
 * ``qgemm``             -- dense M, dequant fused into bf16 MFMA tiles
 
-``quantized_matmul`` dispatches between the two matmul regimes.
+``quantized_matmul`` dispatches between the two matmul regimes;
+``qmm_postscale`` / ``qmm_gate_add`` / ``qmm_swiglu`` fold the reference's
+post-qmm glue kernels into the MFMA kernel's epilogue.
 """
 
 from ._lib import ImqError, ImqInvalid, ImqLibraryMissing, ImqUnsupported  # noqa: F401
@@ -23,5 +25,8 @@ from .ops import (  # noqa: F401
     qgemm,
     qgemv,
     qmm,
+    qmm_gate_add,
+    qmm_postscale,
+    qmm_swiglu,
     quantized_matmul,
 )

@@ -67,6 +67,11 @@ SIGNATURES = {
     "imq_qmm_t": (_QMM, _i),
     "imq_qgemv": (_QMM, _i),
     "imq_qgemm": (_QMM, _i),
+    "imq_qmm_postscale": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, ctypes.c_float, _i, _i, _i, _p], _i),
+    "imq_qmm_gate_add": ([_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, ctypes.c_float, _i, _i, _i,
+                          _p], _i),
+    "imq_qmm_swiglu": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float,
+                        ctypes.c_float, _i, _i, _i, _p], _i),
     # imq_weights.h
     "imq_st_open": ([ctypes.POINTER(_s), _i, ctypes.POINTER(_p)], _i),
     "imq_st_open_dir": ([_s, ctypes.POINTER(_p)], _i),

@@ -128,6 +128,27 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
 
 }  // namespace
 
+namespace {
+
+// Shared checks of the fused-epilogue entry points: the qmm checks, then T in
+// {bf16, f16} and the MFMA kernel's shape condition.
+int check_epilogue(imq_ctx* ctx, const char* fn, const uint32_t* w, const void* s, const void* b,
+                   const void* x, const void* y, int k, int n, int m, int group_size, int bits,
+                   imq_dtype dtype) {
+  int rc = check_qmm(ctx, fn, w, s, b, x, const_cast<void*>(y), k, n, m, group_size, bits, dtype);
+  if (rc != IMQ_OK) return rc;
+  if (dtype == IMQ_F32)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: f32 has no MFMA kernel (bf16 and f16 are provided)",
+                fn);
+  if (!imq::qgemm_big_supported(k, n, m))
+    return fail(ctx, IMQ_EUNSUPPORTED,
+                "%s: K=%d must be a multiple of 256 (and x, w under 2 GiB) for fused epilogues",
+                fn, k);
+  return bind_device(ctx);
+}
+
+}  // namespace
+
 extern "C" {
 
 int imq_abi_version(void) { return IMQ_ABI_VERSION; }
@@ -282,6 +303,54 @@ int imq_qgemm(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* b
               imq_dtype dtype, imq_stream stream) {
   return run_qmm(ctx, "imq_qgemm", Regime::kGemm, w, scales, biases, x, y, k, n, m, group_size,
                  bits, dtype, stream);
+}
+
+
+int imq_qmm_postscale(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                      const void* x, float* y, int k, int n, int m, float scale, int group_size,
+                      int bits, imq_dtype dtype, imq_stream stream) {
+  const char* fn = "imq_qmm_postscale";
+  int rc = check_epilogue(ctx, fn, w, scales, biases, x, y, k, n, m, group_size, bits, dtype);
+  if (rc != IMQ_OK) return rc;
+  if (!aligned(y, 4)) return fail(ctx, IMQ_EINVAL, "%s: y must be 4-byte aligned", fn);
+  const hipError_t e = imq::launch_qgemm_postscale(w, scales, biases, x, y, k, n, m, scale,
+                                                   (int)dtype, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
+}
+
+int imq_qmm_gate_add(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                     const void* x, const float* residual, const float* gate, float* y, int k,
+                     int n, int m, float scale, int group_size, int bits, imq_dtype dtype,
+                     imq_stream stream) {
+  const char* fn = "imq_qmm_gate_add";
+  int rc = check_epilogue(ctx, fn, w, scales, biases, x, y, k, n, m, group_size, bits, dtype);
+  if (rc != IMQ_OK) return rc;
+  if (!residual || !gate) return fail(ctx, IMQ_EINVAL, "%s: null residual or gate", fn);
+  if (!aligned(y, 4) || !aligned(residual, 4) || !aligned(gate, 4))
+    return fail(ctx, IMQ_EINVAL, "%s: y, residual and gate must be 4-byte aligned", fn);
+  const hipError_t e = imq::launch_qgemm_gate_add(w, scales, biases, x, residual, gate, y, k, n,
+                                                  m, scale, (int)dtype,
+                                                  static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
+}
+
+int imq_qmm_swiglu(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                   const void* x, void* y, int ldy, int k, int n, int m, int width, int gate_row,
+                   int up_row, float in_scale, float out_scale, int group_size, int bits,
+                   imq_dtype dtype, imq_stream stream) {
+  const char* fn = "imq_qmm_swiglu";
+  int rc = check_epilogue(ctx, fn, w, scales, biases, x, y, k, n, m, group_size, bits, dtype);
+  if (rc != IMQ_OK) return rc;
+  if (width <= 0 || gate_row < 0 || up_row < 0 || (int64_t)gate_row + width > n ||
+      (int64_t)up_row + width > n || ldy < width)
+    return fail(ctx, IMQ_EINVAL,
+                "%s: sections gate [%d, +%d) / up [%d, +%d) must lie in the %d weight rows and "
+                "ldy (%d) >= width",
+                fn, gate_row, width, up_row, width, n, ldy);
+  const hipError_t e = imq::launch_qgemm_swiglu(w, scales, biases, x, y, ldy, k, n, m, width,
+                                                gate_row, up_row, in_scale, out_scale, (int)dtype,
+                                                static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
 }
 
 }  // extern "C"

@@ -21,6 +21,28 @@ hipError_t launch_qgemv(const uint32_t* w, const void* scales, const void* biase
 hipError_t launch_qgemm(const uint32_t* w, const void* scales, const void* biases, const void* x,
                         void* y, int k, int n, int m, int dtype, hipStream_t stream);
 
+// Whether the buffer-load MFMA kernel (and so the fused epilogues) takes
+// these shapes: K % 256 == 0 and x, w addressable with 32-bit byte offsets.
+bool qgemm_big_supported(int k, int n, int m);
+
+// Fused output stages on the MFMA kernel (T in {bf16, f16}; the shapes must
+// satisfy qgemm_big_supported).  They equal the qmm followed by the
+// reference's glue kernel on its T output:
+//   postscale: y[m][n] (f32) = float(T(acc)) * scale
+//   gate_add:  y[m][n] (f32) = residual[m][n] + gate[n] * float(T(acc)) * scale
+//   swiglu:    y[m][j] (T, row pitch ldy) = T(g * sigmoid(g) * u * out_scale), j < width,
+//              g = float(T(x . W[gate_row + j])) * in_scale, u likewise with up_row.
+hipError_t launch_qgemm_postscale(const uint32_t* w, const void* scales, const void* biases,
+                                  const void* x, float* y, int k, int n, int m, float scale,
+                                  int dtype, hipStream_t stream);
+hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const void* biases,
+                                 const void* x, const float* residual, const float* gate, float* y,
+                                 int k, int n, int m, float scale, int dtype, hipStream_t stream);
+hipError_t launch_qgemm_swiglu(const uint32_t* w, const void* scales, const void* biases,
+                               const void* x, void* y, int ldy, int k, int n, int m, int width,
+                               int gate_row, int up_row, float in_scale, float out_scale, int dtype,
+                               hipStream_t stream);
+
 // Largest M routed to the qGEMV kernel by the regime dispatcher.
 constexpr int kQgemvMaxM = 16;
 

@@ -24,6 +24,7 @@
 //  * Workgroup ids are remapped so that each XCD (ids are dealt round-robin to
 //    the 8 XCDs) walks a contiguous, M-grouped stretch of tiles, keeping the
 //    shared x and W panels in that XCD's L2.
+#include "epilogue.hpp"
 #include "imq_device.hpp"
 #include "imq_kernels.hpp"
 
@@ -448,11 +449,16 @@ __device__ __forceinline__ void big_step(
   }
 }
 
-template <int T, int MTW, int NTW, int WM, int KG>
+// EP is the output stage (epilogue.hpp).  With EP::kPair (SwiGLU) the
+// workgroup's 256 weight rows are 128 gate rows and the 128 matching up rows:
+// a wave's column tile 0 holds gate rows, tile 1 the up rows of the same 32
+// output columns, so each lane has both accumulators of an output.
+template <int T, int MTW, int NTW, int WM, int KG, class EP>
 __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
-    const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, const EP ep,
     int M, int N, int K, int tiles_m, int tiles_n) {
+  static_assert(!EP::kPair || NTW == 2, "paired epilogue needs two column tiles per wave");
   using C = BigCfg<MTW, NTW, WM, KG>;
   constexpr int A_SLOTS = C::kBM * 8 * KG;
   __shared__ uint4 a_st0[A_SLOTS], a_st1[A_SLOTS], a_st2[C::kStages > 2 ? A_SLOTS : 1],
@@ -472,6 +478,7 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   const int n0 = tn * kBigBN;
   const int arow0 = wm * 32 * MTW;        // this wave's first row inside the tile
   const int ncol0 = n0 + wn * 32 * NTW;   // this wave's first output column
+  const int pcol0 = tn * (kBigBN / 2) + wn * 32;  // paired epilogue: first output column
   const int gpr = K >> 6;
   const int steps = gpr / KG;
 
@@ -495,7 +502,9 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   // ncol0 + 32 nt + r32 and bytes [16 h, 16 h + 16) of each group.
 #pragma unroll
   for (int nt = 0; nt < NTW; ++nt) {
-    const int gr = min(ncol0 + nt * 32 + r32, N - 1);
+    int wrow = ncol0 + nt * 32 + r32;
+    if constexpr (EP::kPair) wrow = (nt == 0 ? ep.gate_row : ep.up_row) + min(pcol0 + r32, ep.width - 1);
+    const int gr = min(wrow, N - 1);
     src.w_off[nt] = (uint32_t)gr * (uint32_t)(K / 2) + (uint32_t)h * 16u;
     src.p_off[nt] = (uint32_t)gr * (uint32_t)gpr * 2u;
   }
@@ -547,30 +556,46 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   }
   IMQ_WAIT_VMCNT(0);  // drain the clamped tail loads before the workgroup ends
 
+  // Accumulator r of a 32x32 tile holds row 8*(r/4) + 4*h + r%4, column r32.
+  if constexpr (EP::kPair) {
+    const int j = pcol0 + r32;
+    if (j < ep.width) {
 #pragma unroll
-  for (int mt = 0; mt < MTW; ++mt) {
+      for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < NTW; ++nt) {
-      const int col = ncol0 + nt * 32 + r32;
-      if (col >= N) continue;
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + arow0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (row < M) ep.store2(row, j, acc[mt][0][r], acc[mt][1][r]);
+        }
+    }
+  } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + arow0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (row < M) y[(size_t)row * N + col] = Elem<T>::out(acc[mt][nt][r]);
+    for (int mt = 0; mt < MTW; ++mt) {
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) {
+        const int col = ncol0 + nt * 32 + r32;
+        if (col >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + arow0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (row < M) ep.store(row, col, acc[mt][nt][r]);
+        }
       }
     }
   }
 }
 
-template <int T, int MTW, int NTW, int WM, int KG>
+template <int T, int MTW, int NTW, int WM, int KG, class EP>
 hipError_t launch_big(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
-                      const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
+                      const uint16_t* x, const EP& ep, int k, int n, int m, hipStream_t stream) {
   constexpr int BM = BigCfg<MTW, NTW, WM, KG>::kBM;
   const int tiles_m = (m + BM - 1) / BM;
-  const int tiles_n = (n + kBigBN - 1) / kBigBN;
+  int cols = n;  // weight rows the workgroups cover
+  if constexpr (EP::kPair) cols = 2 * ep.width;
+  const int tiles_n = (cols + kBigBN - 1) / kBigBN;
   const dim3 grid((unsigned)tiles_m * (unsigned)tiles_n);
-  hipLaunchKernelGGL((qgemm_big_kernel<T, MTW, NTW, WM, KG>), grid, dim3(kThreads), 0, stream, w,
-                     scales, biases, x, y, m, n, k, tiles_m, tiles_n);
+  hipLaunchKernelGGL((qgemm_big_kernel<T, MTW, NTW, WM, KG, EP>), grid, dim3(kThreads), 0, stream,
+                     w, scales, biases, x, ep, m, n, k, tiles_m, tiles_n);
   return hipGetLastError();
 }
 
@@ -604,13 +629,7 @@ hipError_t launch_tile(const uint32_t* w, const uint16_t* scales, const uint16_t
   return hipGetLastError();
 }
 
-template <int T>
-hipError_t launch_t(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
-                    const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
-  // The buffer-load kernel addresses x and w with 32-bit byte offsets and
-  // loads scales in blocks of four groups.
-  const bool fits32 = (size_t)m * k * 2 < ((size_t)1 << 31) && (size_t)n * k / 2 < ((size_t)1 << 31);
-  if (!fits32 || k % 256 != 0) return launch_tile<T, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
+int device_cus() {
   static const int cus = [] {
     int dev = 0, v = 0;
     if (hipGetDevice(&dev) == hipSuccess &&
@@ -618,16 +637,39 @@ hipError_t launch_t(const uint32_t* w, const uint16_t* scales, const uint16_t* b
       return v;
     return 256;
   }();
-  // Two groups per K-step (2-stage ring): half the barriers and waits of one
-  // group per step (4-stage ring), measured 3.5% faster at M=4608 K=3072 N=18432.
-  switch (pick_big_mt(m, n, cus)) {
-    case 4: return launch_big<T, 4, 2, 1, 2>(w, scales, biases, x, y, k, n, m, stream);
-    case 6: return launch_big<T, 6, 2, 1, 2>(w, scales, biases, x, y, k, n, m, stream);
-    default: return launch_big<T, 8, 2, 1, 2>(w, scales, biases, x, y, k, n, m, stream);
+  return cus;
+}
+
+// The large-M kernel with output stage ep.  Two groups per K-step (2-stage
+// ring): half the barriers and waits of one group per step (4-stage ring),
+// measured 3.5% faster at M=4608 K=3072 N=18432.
+template <int T, class EP>
+hipError_t launch_big_ep(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                         const uint16_t* x, const EP& ep, int k, int n, int m, hipStream_t stream) {
+  int cols = n;
+  if constexpr (EP::kPair) cols = 2 * ep.width;
+  switch (pick_big_mt(m, cols, device_cus())) {
+    case 4: return launch_big<T, 4, 2, 1, 2>(w, scales, biases, x, ep, k, n, m, stream);
+    case 6: return launch_big<T, 6, 2, 1, 2>(w, scales, biases, x, ep, k, n, m, stream);
+    default: return launch_big<T, 8, 2, 1, 2>(w, scales, biases, x, ep, k, n, m, stream);
   }
 }
 
+template <int T>
+hipError_t launch_t(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                    const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
+  if (!qgemm_big_supported(k, n, m)) return launch_tile<T, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
+  return launch_big_ep<T>(w, scales, biases, x, EpStore<T>{y, n}, k, n, m, stream);
+}
+
 }  // namespace
+
+bool qgemm_big_supported(int k, int n, int m) {
+  // The buffer-load kernel addresses x and w with 32-bit byte offsets and
+  // loads scales in blocks of four groups.
+  return (size_t)m * k * 2 < ((size_t)1 << 31) && (size_t)n * k / 2 < ((size_t)1 << 31) &&
+         k % 256 == 0;
+}
 
 hipError_t launch_qgemm(const uint32_t* w, const void* scales, const void* biases, const void* x,
                         void* y, int k, int n, int m, int dtype, hipStream_t stream) {
@@ -638,6 +680,57 @@ hipError_t launch_qgemm(const uint32_t* w, const void* scales, const void* biase
   switch (dtype) {
     case kBf16: return launch_t<kBf16>(w, s, b, xx, yy, k, n, m, stream);
     case kF16: return launch_t<kF16>(w, s, b, xx, yy, k, n, m, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_qgemm_postscale(const uint32_t* w, const void* scales, const void* biases,
+                                  const void* x, float* y, int k, int n, int m, float scale,
+                                  int dtype, hipStream_t stream) {
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* b = static_cast<const uint16_t*>(biases);
+  const auto* xx = static_cast<const uint16_t*>(x);
+  switch (dtype) {
+    case kBf16: return launch_big_ep<kBf16>(w, s, b, xx, EpPostscale<kBf16>{y, n, scale}, k, n, m, stream);
+    case kF16: return launch_big_ep<kF16>(w, s, b, xx, EpPostscale<kF16>{y, n, scale}, k, n, m, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const void* biases,
+                                 const void* x, const float* residual, const float* gate, float* y,
+                                 int k, int n, int m, float scale, int dtype, hipStream_t stream) {
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* b = static_cast<const uint16_t*>(biases);
+  const auto* xx = static_cast<const uint16_t*>(x);
+  switch (dtype) {
+    case kBf16:
+      return launch_big_ep<kBf16>(w, s, b, xx, EpGateAdd<kBf16>{y, residual, gate, n, scale}, k, n, m,
+                                  stream);
+    case kF16:
+      return launch_big_ep<kF16>(w, s, b, xx, EpGateAdd<kF16>{y, residual, gate, n, scale}, k, n, m,
+                                 stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_qgemm_swiglu(const uint32_t* w, const void* scales, const void* biases,
+                               const void* x, void* y, int ldy, int k, int n, int m, int width,
+                               int gate_row, int up_row, float in_scale, float out_scale, int dtype,
+                               hipStream_t stream) {
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* b = static_cast<const uint16_t*>(biases);
+  const auto* xx = static_cast<const uint16_t*>(x);
+  auto* yy = static_cast<uint16_t*>(y);
+  switch (dtype) {
+    case kBf16:
+      return launch_big_ep<kBf16>(
+          w, s, b, xx, EpSwiGLU<kBf16>{yy, ldy, width, gate_row, up_row, in_scale, out_scale}, k, n,
+          m, stream);
+    case kF16:
+      return launch_big_ep<kF16>(
+          w, s, b, xx, EpSwiGLU<kF16>{yy, ldy, width, gate_row, up_row, in_scale, out_scale}, k, n,
+          m, stream);
     default: return hipErrorInvalidValue;
   }
 }

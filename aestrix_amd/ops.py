@@ -172,6 +172,92 @@ def qgemm(x, w, scales, biases, group_size: int = GROUP_SIZE, bits: int = BITS, 
     return _qmm_call("imq_qgemm", x, w, scales, biases, group_size, bits, out)
 
 
+def _epi_args(x, w, scales, biases, group_size, bits):
+    n, k = _check_weight(w, scales, biases, group_size, bits)
+    _require(x.is_cuda and x.device == w.device, "x must be on the weight's device")
+    _require(x.dim() >= 1 and x.shape[-1] == k, f"x's last dim must be K={k}, got {tuple(x.shape)}")
+    _require(x.dtype == scales.dtype, f"x ({x.dtype}) and scales ({scales.dtype}) must share T")
+    lead = tuple(x.shape[:-1])
+    m = 1
+    for d in lead:
+        m *= d
+    return n, k, m, lead, (x if x.is_contiguous() else x.contiguous())
+
+
+def _f32_out(out, shape, device, what):
+    if out is None:
+        return torch.empty(shape, dtype=torch.float32, device=device)
+    _require(out.dtype == torch.float32 and out.is_contiguous() and tuple(out.shape) == shape,
+             f"{what} must be a contiguous float32 tensor of shape {shape}")
+    return out
+
+
+def qmm_postscale(x, w, scales, biases, scale: float, group_size: int = GROUP_SIZE,
+                  bits: int = BITS, out=None) -> torch.Tensor:
+    """float32 y = float(T(x . deq(W)^T)) * scale in one kernel (the reference's
+    qmm + dd_cast_postscale, ``DirectDiTKernels.swift:199-209``)."""
+    n, k, m, lead, x = _epi_args(x, w, scales, biases, group_size, bits)
+    out = _f32_out(out, lead + (n,), x.device, "out")
+    dtype = _DTYPES.get(x.dtype, -1)
+    ctx = context(w.device)
+    with torch.cuda.device(w.device):
+        st = _lib.load().imq_qmm_postscale(ctx, _ptr(w), _ptr(scales), _ptr(biases), _ptr(x),
+                                           _ptr(out), k, n, m, float(scale), group_size, bits,
+                                           dtype, _stream(x))
+    _lib.check(st, ctx)
+    return out
+
+
+def qmm_gate_add(x, w, scales, biases, residual: torch.Tensor, gate: torch.Tensor, scale: float,
+                 group_size: int = GROUP_SIZE, bits: int = BITS, out=None) -> torch.Tensor:
+    """float32 y = residual + gate * float(T(x . deq(W)^T)) * scale in one kernel
+    (qmm + dd_gate_add, ``DirectDiTKernels.swift:211-224``); ``out=residual``
+    updates the residual stream in place."""
+    n, k, m, lead, x = _epi_args(x, w, scales, biases, group_size, bits)
+    _require(residual.dtype == torch.float32 and residual.is_contiguous()
+             and tuple(residual.shape) == lead + (n,), "residual must be float32 [..., N]")
+    _require(gate.dtype == torch.float32 and gate.is_contiguous() and tuple(gate.shape) == (n,),
+             "gate must be float32 [N]")
+    out = _f32_out(out, lead + (n,), x.device, "out")
+    dtype = _DTYPES.get(x.dtype, -1)
+    ctx = context(w.device)
+    with torch.cuda.device(w.device):
+        st = _lib.load().imq_qmm_gate_add(ctx, _ptr(w), _ptr(scales), _ptr(biases), _ptr(x),
+                                          _ptr(residual), _ptr(gate), _ptr(out), k, n, m,
+                                          float(scale), group_size, bits, dtype, _stream(x))
+    _lib.check(st, ctx)
+    return out
+
+
+def qmm_swiglu(x, w, scales, biases, width: int, gate_row: int, up_row: int,
+               in_scale: float = 1.0, out_scale: float = 1.0, group_size: int = GROUP_SIZE,
+               bits: int = BITS, out=None) -> torch.Tensor:
+    """y[..., j] = T(g * sigmoid(g) * u * out_scale) for j < width, with g and u
+    the T-rounded products of x with weight rows gate_row + j and up_row + j
+    times in_scale (qmm + dd_swiglu_pitched, ``DirectDiTKernels.swift:137-157``).
+    ``out`` may be a column slice of a wider 2-D buffer (unit column stride)."""
+    n, k, m, lead, x = _epi_args(x, w, scales, biases, group_size, bits)
+    if out is None:
+        out = torch.empty(lead + (width,), dtype=x.dtype, device=x.device)
+    _require(out.dtype == x.dtype and tuple(out.shape) == lead + (width,) and out.stride(-1) == 1,
+             "out must be [..., width] of x's dtype with unit column stride")
+    if out.dim() >= 2:
+        ldy = out.stride(-2)
+        _require(all(out.stride(i) == out.stride(i + 1) * out.shape[i + 1]
+                     for i in range(out.dim() - 2)), "out's leading dims must be packed")
+    else:
+        ldy = width
+    dtype = _DTYPES.get(x.dtype, -1)
+    ctx = context(w.device)
+    with torch.cuda.device(w.device):
+        st = _lib.load().imq_qmm_swiglu(ctx, _ptr(w), _ptr(scales), _ptr(biases), _ptr(x),
+                                        _ptr(out), ldy, k, n, m, width, gate_row, up_row,
+                                        float(in_scale), float(out_scale), group_size, bits,
+                                        dtype, _stream(x))
+    _lib.check(st, ctx)
+    return out
+
+
 @dataclass
 class Q:
     """A resident packed projection, the reference's ``Q(w:s:b:n:k:)``

@@ -129,6 +129,40 @@ int imq_qgemm(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* b
               const void* x, void* y, int k, int n, int m, int group_size, int bits,
               imq_dtype dtype, imq_stream stream);
 
+/* ---- fused output stages ------------------------------------------------
+ * The MFMA kernel with the reference's post-qmm glue kernel folded into its
+ * epilogue (Sources/ImarelloDirect/DirectDiTKernels.swift).  Each equals the
+ * qmm (T output) followed by that glue kernel: the accumulator is rounded to T
+ * first, then the glue arithmetic runs in fp32.  T is bf16 or f16 (f32:
+ * IMQ_EUNSUPPORTED); K % 256 == 0 (else IMQ_EUNSUPPORTED); any M >= 1.  Other
+ * arguments as imq_qmm_t; fp32 arrays must be 4-byte aligned. */
+
+/* y[M, N] (fp32) = float(T(x . deq(W)^T)) * scale: dd_cast_postscale
+ * (DirectDiTKernels.swift:199-209), the x16 after a /16 pre-scaled qmm. */
+int imq_qmm_postscale(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                      const void* x, float* y, int k, int n, int m, float scale, int group_size,
+                      int bits, imq_dtype dtype, imq_stream stream);
+
+/* y[M, N] (fp32) = residual + gate[n] * float(T(x . deq(W)^T)) * scale: the
+ * gated residual dd_gate_add (DirectDiTKernels.swift:211-224).  y may equal
+ * residual (in place). */
+int imq_qmm_gate_add(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                     const void* x, const float* residual, const float* gate, float* y, int k,
+                     int n, int m, float scale, int group_size, int bits, imq_dtype dtype,
+                     imq_stream stream);
+
+/* SwiGLU over the gate and up sections of one projection W [n, K/8]:
+ * y[i][j] (T, row pitch ldy elements) = T(g * sigmoid(g) * u * out_scale) for
+ * j < width, g = float(T(x_i . deq(W)[gate_row + j])) * in_scale, u the same
+ * with up_row: dd_swiglu_pitched (DirectDiTKernels.swift:137-157) fused into
+ * the projection that feeds it (the single block's to_qkv_mlp_proj,
+ * DirectDiTStep.swift:328-333).  Requires gate_row + width <= n,
+ * up_row + width <= n, ldy >= width. */
+int imq_qmm_swiglu(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                   const void* x, void* y, int ldy, int k, int n, int m, int width, int gate_row,
+                   int up_row, float in_scale, float out_scale, int group_size, int bits,
+                   imq_dtype dtype, imq_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

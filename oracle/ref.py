@@ -158,3 +158,29 @@ def _stats(y: np.ndarray, o: np.ndarray) -> dict:
         "max_rel_normwise": float(np.max(d) / omax) if d.size and omax > 0 else 0.0,
         "max_rel_floored": float(np.max(d / np.where(floor > 0, floor, 1.0))) if d.size else 0.0,
     }
+
+
+# ------------------------------------------------------------- glue stages
+# The reference's post-qmm glue kernels (Sources/ImarelloDirect/DirectDiTKernels.swift)
+# on the T output of a qmm, in fp32 (the Metal kernels compute in float).
+# `y_t` is the qmm output as float32 values of T.
+
+def glue_postscale(y_t: np.ndarray, scale: float) -> np.ndarray:
+    """dd_cast_postscale (DirectDiTKernels.swift:199-209): float(y) * s."""
+    return (np.asarray(y_t, dtype=np.float32) * np.float32(scale)).astype(np.float32)
+
+
+def glue_gate_add(y_t: np.ndarray, residual: np.ndarray, gate: np.ndarray,
+                  scale: float) -> np.ndarray:
+    """dd_gate_add (DirectDiTKernels.swift:211-224): fma(gate[j], float(v) * s, x)."""
+    v = (np.asarray(y_t, dtype=np.float32) * np.float32(scale)).astype(np.float64)
+    exact = np.asarray(gate, np.float64)[None, :] * v + np.asarray(residual, np.float64)
+    return exact.astype(np.float32)
+
+
+def glue_swiglu(g_t: np.ndarray, u_t: np.ndarray, in_scale: float, out_scale: float) -> np.ndarray:
+    """dd_swiglu_pitched (DirectDiTKernels.swift:137-157): g, u = float(.) * inScale;
+    g * sigmoid(g) * u * outScale, as float64 (to be rounded to T by the caller)."""
+    g = np.asarray(g_t, np.float64) * np.float32(in_scale)
+    u = np.asarray(u_t, np.float64) * np.float32(in_scale)
+    return g / (1.0 + np.exp(-g)) * u * np.float32(out_scale)

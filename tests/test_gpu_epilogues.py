@@ -1,0 +1,141 @@
+"""Fused output stages of the MFMA kernel against qmm + glue.
+
+Known answers: the CPU oracle's qmm (RNE_T of the double-accumulated product
+with the bit-exact dequant) followed by the reference's glue arithmetic
+(oracle/ref.py glue_*, restating Sources/ImarelloDirect/DirectDiTKernels.swift);
+and the library's own unfused qmm output followed by the same glue, which the
+fused kernels must match (postscale bit-exactly: same accumulator, same
+rounding; the others to one unit in the last place / the stated tolerance).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import aestrix_amd as imq
+from aestrix_amd import synth
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+MAE_TOL = 1e-3
+NORMWISE_TOL = 1e-2
+TORCH = {np.float16: torch.float16}
+
+
+@pytest.fixture(autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+
+
+def note(msg: str) -> None:
+    print(msg, flush=True)
+
+
+def problem(m, n, k, dtype, seed):
+    """bf16: the synthetic generator; f16: the same values cast (bf16 values of
+    these magnitudes are exact in f16)."""
+    p = synth.make_problem(m, n, k, seed=seed)
+    x, w, s, b = synth.to_device(p)
+    if dtype == "f16":
+        x, s, b = x.half(), s.half(), b.half()
+    return p, x, w, s, b
+
+
+def oracle_qmm(p, x, s, b, dtype, rows=None):
+    """float32 values of the T-rounded oracle product x . deq(W[rows])^T."""
+    w = p.w if rows is None else p.w[rows]
+    if dtype == "bf16":
+        sb = p.scales if rows is None else p.scales[rows]
+        bb = p.biases if rows is None else p.biases[rows]
+        return ref.bf16_to_f32(ref.qmm_t(p.x, w, sb, bb))
+    sh = s.cpu().numpy() if rows is None else s.cpu().numpy()[rows]
+    bh = b.cpu().numpy() if rows is None else b.cpu().numpy()[rows]
+    return ref.qmm_t_as(x.cpu().numpy(), w, sh, bh, np.float16).astype(np.float32)
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy()
+
+
+def assert_close(y: np.ndarray, want: np.ndarray, what: str) -> None:
+    st = ref.error_stats_values(y.astype(np.float64), want.astype(np.float64))
+    note(f"  {what}: mae={st['mae']:.3g} normwise={st['max_rel_normwise']:.3g} "
+         f"bit_exact={st['bit_exact_frac']:.4f}")
+    assert st["mae"] <= MAE_TOL and st["max_rel_normwise"] <= NORMWISE_TOL, (what, st)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("m,n,k", [(300, 512, 768), (17, 96, 256), (1, 64, 512)])
+def test_postscale(dtype, m, n, k):
+    note(f"qmm_postscale {dtype} M={m} N={n} K={k}")
+    p, x, w, s, b = problem(m, n, k, dtype, seed=50)
+    y = imq.qmm_postscale(x, w, s, b, 16.0)
+    assert y.dtype == torch.float32
+    unfused = to_np(imq.qgemm(x, w, s, b)) * np.float32(16.0)
+    assert np.array_equal(to_np(y), unfused)
+    assert_close(to_np(y), ref.glue_postscale(oracle_qmm(p, x, s, b, dtype), 16.0), "postscale")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("inplace", [False, True])
+def test_gate_add(dtype, inplace):
+    m, n, k = 260, 384, 1024
+    note(f"qmm_gate_add {dtype} M={m} N={n} K={k} inplace={inplace}")
+    p, x, w, s, b = problem(m, n, k, dtype, seed=51)
+    rng = np.random.default_rng(51)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    gate = rng.standard_normal(n).astype(np.float32)
+    r_dev = torch.from_numpy(res).cuda()
+    g_dev = torch.from_numpy(gate).cuda()
+    y = imq.qmm_gate_add(x, w, s, b, r_dev, g_dev, 1.0 / 16, out=r_dev if inplace else None)
+    got = to_np(y)
+    unfused = ref.glue_gate_add(to_np(imq.qgemm(x, w, s, b)), res, gate, 1.0 / 16)
+    assert np.max(np.abs(got - unfused) / np.maximum(np.abs(unfused), 1e-30)) <= 2.0 ** -23
+    assert_close(got, ref.glue_gate_add(oracle_qmm(p, x, s, b, dtype), res, gate, 1.0 / 16),
+                 "gate_add")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("m,width", [(300, 300), (33, 128), (2, 70)])
+def test_swiglu_into_a_pitched_buffer(dtype, m, width):
+    """gate and up sections of one projection (N=1024 rows), SwiGLU written into
+    columns [40, 40 + width) of a wider buffer; the other columns stay as they were."""
+    n, k, gate_row, up_row = 1024, 512, 256, 600
+    note(f"qmm_swiglu {dtype} M={m} width={width}")
+    p, x, w, s, b = problem(m, n, k, dtype, seed=52)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    buf = torch.full((m, width + 100), 7.0, dtype=tdt, device="cuda")
+    out = buf[:, 40:40 + width]
+    imq.qmm_swiglu(x, w, s, b, width, gate_row, up_row, in_scale=16.0, out_scale=1.0 / 16, out=out)
+    got = to_np(buf)
+    assert np.all(got[:, :40] == 7.0) and np.all(got[:, 40 + width:] == 7.0)
+    ys = got[:, 40:40 + width]
+    full = to_np(imq.qgemm(x, w, s, b))
+    unfused = ref.glue_swiglu(full[:, gate_row:gate_row + width], full[:, up_row:up_row + width],
+                              16.0, 1.0 / 16)
+    want = ref.glue_swiglu(oracle_qmm(p, x, s, b, dtype, np.arange(gate_row, gate_row + width)),
+                           oracle_qmm(p, x, s, b, dtype, np.arange(up_row, up_row + width)),
+                           16.0, 1.0 / 16)
+
+    def round_t(v):
+        t = torch.from_numpy(v.astype(np.float32)).to(tdt).float().numpy()
+        return t
+
+    assert_close(ys, round_t(unfused), "swiglu vs unfused")
+    assert_close(ys, round_t(want), "swiglu vs oracle")
+
+
+def test_epilogue_argument_checks():
+    p, x, w, s, b = problem(8, 128, 256, "bf16", seed=53)
+    with pytest.raises(ValueError):
+        imq.qmm_swiglu(x, w, s, b, 100, 0, 64)  # up section past N
+    with pytest.raises(NotImplementedError):
+        imq.qmm_postscale(x.float(), w, s.float(), b.float(), 1.0)  # f32: no MFMA kernel
+    p2, x2, w2, s2, b2 = problem(8, 128, 192, "bf16", seed=53)
+    with pytest.raises(NotImplementedError):
+        imq.qmm_postscale(x2, w2, s2, b2, 1.0)  # K % 256 != 0
