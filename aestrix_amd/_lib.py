@@ -44,6 +44,12 @@ class QWeight(ctypes.Structure):
                 ("base", ctypes.c_void_p)]
 
 
+class DitDims(ctypes.Structure):
+    """imq_dit_dims."""
+    _fields_ = [("l_img", ctypes.c_int), ("l_txt", ctypes.c_int), ("dim", ctypes.c_int),
+                ("ff_inner", ctypes.c_int), ("n_double", ctypes.c_int), ("n_single", ctypes.c_int)]
+
+
 # Every entry point the headers declare, with its ctypes signature.
 _p = ctypes.c_void_p
 _i = ctypes.c_int
@@ -87,6 +93,13 @@ SIGNATURES = {
     "imq_st_upload": ([_p, _p, _s, _i, _p, _sz, _p], _i),
     "imq_load_qlinear": ([_p, _p, _s, _i, ctypes.POINTER(QWeight), _p], _i),
     "imq_qweight_free": ([_p, ctypes.POINTER(QWeight)], _i),
+    # imq_step.h
+    "imq_dit_step_create": ([_p, ctypes.POINTER(DitDims), ctypes.POINTER(QWeight), _i, _i,
+                             ctypes.POINTER(_p)], _i),
+    "imq_dit_step_set_conditioning": ([_p, _p, _p, _p], _i),
+    "imq_dit_step_run": ([_p, _p, _p, _p, _i, _p], _i),
+    "imq_dit_step_launches": ([_p], _i),
+    "imq_dit_step_destroy": ([_p], _i),
 }
 
 

@@ -253,8 +253,9 @@ int tile_len(int k, int mr, int g, int eb) {
 
 // Each candidate G gives n * G / (64 R) waves and uses tch / (G U) of its
 // lanes' chunk slots per tile; pick the one with the most useful waves,
-// counting at most 2048 (where more waves stopped paying for idle lanes on
-// the shapes measured, 9728 x 2560 and 2560 x 9728 at M = 1 ... 16).
+// counting at most 4096 for M <= 2 and 2048 above (where more waves stopped
+// paying for idle lanes on the shapes measured, 9728 x 2560 and 2560 x 9728
+// at M = 1 ... 16).
 // IMQ_QGEMV_LANES=16|32|64 overrides.
 Plan make_plan(int k, int n, int mr, int eb) {
   static const int forced = [] {
@@ -270,7 +271,7 @@ Plan make_plan(int k, int n, int mr, int eb) {
     const int kt = tile_len(k, mr, g, eb);
     const int tch = kt / 32;
     const int u = (tch + g - 1) / g;
-    const double waves = std::min((double)n * g / (64.0 * r), 2048.0);
+    const double waves = std::min((double)n * g / (64.0 * r), mr <= 2 ? 4096.0 : 2048.0);
     const double score = waves * tch / (double)(g * u);
     if (score > best_score * 1.02) {
       best = Plan{g, kt, u};

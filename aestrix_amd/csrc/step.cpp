@@ -1,0 +1,293 @@
+// step.cpp -- whole-step replay of a DiT step's quantized linear layers as a
+// HIP graph: the C ABI of include/imq_step.h.
+//
+// Mirrors DirectDiTStep (Sources/ImarelloDirect/DirectDiTStep.swift): scratch
+// allocated once in one arena (allocateScratch, :155-274), the blocks encoded
+// in the reference's order (encodeBlocks / encodeDouble / encodeSingle,
+// :545-685), inputs copied into the internal residual so the step re-runs on
+// pristine inputs (:644-654).  Where the reference encodes ~25 command
+// encoders per step, the step here is one graph launch.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "ctx.hpp"
+#include "imq.h"
+#include "imq_kernels.hpp"
+#include "imq_step.h"
+
+using namespace imq::detail;
+
+struct imq_dit_step {
+  imq_ctx* ctx = nullptr;
+  imq_dit_dims d{};
+  imq_dtype dtype = IMQ_BF16;
+  std::vector<imq_qweight> w;
+  void* arena = nullptr;
+  float* X = nullptr;       // fp32 [J, dim] residual, text rows first
+  char* nX = nullptr;       // T [J, dim]
+  char* Q = nullptr;        // T [J, dim]
+  char* K = nullptr;
+  char* V = nullptr;
+  char* SW = nullptr;       // T [J, ff_inner]
+  char* QKV = nullptr;      // T [J, 3 dim]
+  char* C = nullptr;        // T [J, dim + ff_inner]
+  float* norm_w = nullptr;  // fp32 [dim]
+  float* gates = nullptr;   // fp32 [4 n_double + n_single][dim]
+  hipStream_t cap = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  int launches = 0;
+};
+
+namespace {
+
+constexpr float kEps = 1e-5f;  // DirectDiTStep.swift:416
+
+size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+// Launch every kernel of one step on stream s.
+hipError_t encode(imq_dit_step* st, hipStream_t s) {
+  const imq_dit_dims& d = st->d;
+  const int J = d.l_txt + d.l_img;
+  const int dim = d.dim, ffi = d.ff_inner;
+  const int T = (int)st->dtype;
+  const size_t es = 2;
+  st->launches = 0;
+  hipError_t e = hipSuccess;
+  auto ok = [&](hipError_t r) {
+    ++st->launches;
+    if (e == hipSuccess) e = r;
+  };
+  auto rows = [&](char* base, int row0, int width) { return base + (size_t)row0 * width * es; };
+  float* Xt = st->X;
+  float* Xi = st->X + (size_t)d.l_txt * dim;
+  for (int b = 0; b < d.n_double; ++b) {
+    const imq_qweight* W = &st->w[(size_t)12 * b];
+    const float* g = st->gates + (size_t)4 * b * dim;
+    ok(imq::launch_rmsnorm(st->X, st->norm_w, st->nX, J, dim, kEps, T, s));
+    char* nXt = rows(st->nX, 0, dim);
+    char* nXi = rows(st->nX, d.l_txt, dim);
+    char* outs[3] = {st->Q, st->K, st->V};
+    for (int q = 0; q < 3; ++q) {
+      ok(imq::launch_qgemm(W[q].w, W[q].scales, W[q].biases, nXi, rows(outs[q], d.l_txt, dim), dim,
+                           dim, d.l_img, T, s));
+      ok(imq::launch_qgemm(W[3 + q].w, W[3 + q].scales, W[3 + q].biases, nXt, rows(outs[q], 0, dim),
+                           dim, dim, d.l_txt, T, s));
+    }
+    // to_out / to_add_out on the V rows (the attention output's stand-in).
+    ok(imq::launch_qgemm_gate_add(W[6].w, W[6].scales, W[6].biases, rows(st->V, d.l_txt, dim), Xi,
+                                  g, Xi, dim, dim, d.l_img, 1.0f, T, s));
+    ok(imq::launch_qgemm_gate_add(W[7].w, W[7].scales, W[7].biases, rows(st->V, 0, dim), Xt,
+                                  g + dim, Xt, dim, dim, d.l_txt, 1.0f, T, s));
+    ok(imq::launch_rmsnorm(st->X, st->norm_w, st->nX, J, dim, kEps, T, s));
+    ok(imq::launch_qgemm_swiglu(W[8].w, W[8].scales, W[8].biases, nXi, rows(st->SW, d.l_txt, ffi),
+                                ffi, dim, 2 * ffi, d.l_img, ffi, 0, ffi, 1.0f, 1.0f, T, s));
+    ok(imq::launch_qgemm_gate_add(W[9].w, W[9].scales, W[9].biases, rows(st->SW, d.l_txt, ffi), Xi,
+                                  g + 2 * dim, Xi, ffi, dim, d.l_img, 1.0f, T, s));
+    ok(imq::launch_qgemm_swiglu(W[10].w, W[10].scales, W[10].biases, nXt, rows(st->SW, 0, ffi), ffi,
+                                dim, 2 * ffi, d.l_txt, ffi, 0, ffi, 1.0f, 1.0f, T, s));
+    ok(imq::launch_qgemm_gate_add(W[11].w, W[11].scales, W[11].biases, rows(st->SW, 0, ffi), Xt,
+                                  g + 3 * dim, Xt, ffi, dim, d.l_txt, 1.0f, T, s));
+  }
+  const int cw = dim + ffi;
+  for (int b = 0; b < d.n_single; ++b) {
+    const imq_qweight* W = &st->w[(size_t)12 * d.n_double + 2 * b];
+    const float* g = st->gates + ((size_t)4 * d.n_double + b) * dim;
+    ok(imq::launch_rmsnorm(st->X, st->norm_w, st->nX, J, dim, kEps, T, s));
+    ok(imq::launch_qgemm(W[0].w, W[0].scales, W[0].biases, st->nX, st->QKV, dim, 3 * dim, J, T, s));
+    ok(imq::launch_qgemm_swiglu(W[0].w, W[0].scales, W[0].biases, st->nX, st->C + (size_t)dim * es,
+                                cw, dim, 3 * dim + 2 * ffi, J, ffi, 3 * dim, 3 * dim + ffi, 1.0f,
+                                1.0f, T, s));
+    ok(imq::launch_qgemm_gate_add(W[1].w, W[1].scales, W[1].biases, st->C, st->X, g, st->X, cw, dim,
+                                  J, 1.0f, T, s));
+  }
+  return e;
+}
+
+void release(imq_dit_step* st) {
+  if (st->exec) (void)hipGraphExecDestroy(st->exec);
+  if (st->graph) (void)hipGraphDestroy(st->graph);
+  if (st->cap) (void)hipStreamDestroy(st->cap);
+  if (st->arena) (void)hipFree(st->arena);
+}
+
+// Expected [N, K] of projection i of the plan.
+void expected_shape(const imq_dit_dims& d, int i, int& n, int& k) {
+  const int dim = d.dim, ffi = d.ff_inner;
+  if (i < 12 * d.n_double) {
+    switch (i % 12) {
+      case 8: case 10: n = 2 * ffi; k = dim; return;
+      case 9: case 11: n = dim; k = ffi; return;
+      default: n = dim; k = dim; return;
+    }
+  }
+  const int j = (i - 12 * d.n_double) % 2;
+  if (j == 0) {
+    n = 3 * dim + 2 * ffi;
+    k = dim;
+  } else {
+    n = dim;
+    k = dim + ffi;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int imq_dit_step_create(imq_ctx* ctx, const imq_dit_dims* dims, const imq_qweight* weights,
+                        int n_weights, imq_dtype dtype, imq_dit_step** out) {
+  const char* fn = "imq_dit_step_create";
+  if (!ctx) return fail(nullptr, IMQ_EINVAL, "%s: null context", fn);
+  if (!dims || !out || (n_weights > 0 && !weights)) return fail(ctx, IMQ_EINVAL, "%s: null argument", fn);
+  *out = nullptr;
+  const imq_dit_dims d = *dims;
+  if (d.l_img <= 0 || d.l_txt <= 0 || d.dim <= 0 || d.ff_inner <= 0 || d.n_double < 0 ||
+      d.n_single < 0)
+    return fail(ctx, IMQ_EINVAL, "%s: non-positive dimension", fn);
+  if (d.dim % 256 != 0 || d.ff_inner % 256 != 0)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: dim and ff_inner must be multiples of 256", fn);
+  if (dtype != IMQ_BF16 && dtype != IMQ_F16)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: dtype %d (bf16 and f16 are provided)", fn, (int)dtype);
+  const int need = 12 * d.n_double + 2 * d.n_single;
+  if (n_weights != need)
+    return fail(ctx, IMQ_EINVAL, "%s: %d projections given, the plan needs %d", fn, n_weights, need);
+  for (int i = 0; i < n_weights; ++i) {
+    int n = 0, k = 0;
+    expected_shape(d, i, n, k);
+    const imq_qweight& q = weights[i];
+    if (!q.w || !q.scales || !q.biases || q.n != n || q.k != k || q.dtype != dtype)
+      return fail(ctx, IMQ_EINVAL, "%s: projection %d is [%d, %d] dtype %d, expected [%d, %d] dtype %d",
+                  fn, i, q.n, q.k, (int)q.dtype, n, k, (int)dtype);
+  }
+  int rc = bind_device(ctx);
+  if (rc != IMQ_OK) return rc;
+  auto* st = new (std::nothrow) imq_dit_step;
+  if (!st) return fail(ctx, IMQ_ENOMEM, "%s: out of host memory", fn);
+  st->ctx = ctx;
+  st->d = d;
+  st->dtype = dtype;
+  st->w.assign(weights, weights + n_weights);
+  const size_t J = (size_t)d.l_txt + d.l_img;
+  const size_t es = 2;
+  const size_t sizes[] = {J * d.dim * 4,
+                          J * d.dim * es,
+                          J * d.dim * es,
+                          J * d.dim * es,
+                          J * d.dim * es,
+                          J * d.ff_inner * es,
+                          J * 3 * d.dim * es,
+                          J * (d.dim + d.ff_inner) * es,
+                          (size_t)d.dim * 4,
+                          ((size_t)4 * d.n_double + d.n_single) * d.dim * 4};
+  size_t off[10], total = 0;
+  for (int i = 0; i < 10; ++i) {
+    off[i] = total;
+    total += align256(sizes[i]);
+  }
+  hipError_t e = hipMalloc(&st->arena, total);
+  if (e != hipSuccess) {
+    st->arena = nullptr;
+    release(st);
+    delete st;
+    return e == hipErrorOutOfMemory
+               ? fail(ctx, IMQ_ENOMEM, "%s: %zu bytes of scratch: out of device memory", fn, total)
+               : hip_fail(ctx, e, fn);
+  }
+  char* a = static_cast<char*>(st->arena);
+  st->X = reinterpret_cast<float*>(a + off[0]);
+  st->nX = a + off[1];
+  st->Q = a + off[2];
+  st->K = a + off[3];
+  st->V = a + off[4];
+  st->SW = a + off[5];
+  st->QKV = a + off[6];
+  st->C = a + off[7];
+  st->norm_w = reinterpret_cast<float*>(a + off[8]);
+  st->gates = reinterpret_cast<float*>(a + off[9]);
+  // Zero everything (the attention half of C stays zero), ones for the
+  // conditioning vectors.  Plain (uncaptured) memsets at set-up.
+  e = hipMemset(st->arena, 0, total);
+  if (e == hipSuccess) e = hipMemsetD32(st->norm_w, 0x3F800000u, (size_t)d.dim);
+  if (e == hipSuccess)
+    e = hipMemsetD32(st->gates, 0x3F800000u, ((size_t)4 * d.n_double + d.n_single) * d.dim);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&st->cap, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    release(st);
+    delete st;
+    return hip_fail(ctx, e, fn);
+  }
+  *out = st;
+  return IMQ_OK;
+}
+
+int imq_dit_step_set_conditioning(imq_dit_step* st, const float* norm_weight, const float* gates,
+                                  imq_stream stream) {
+  if (!st) return fail(nullptr, IMQ_EINVAL, "imq_dit_step_set_conditioning: null step");
+  int rc = bind_device(st->ctx);
+  if (rc != IMQ_OK) return rc;
+  auto s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipSuccess;
+  if (norm_weight)
+    e = hipMemcpyAsync(st->norm_w, norm_weight, (size_t)st->d.dim * 4, hipMemcpyDefault, s);
+  if (e == hipSuccess && gates)
+    e = hipMemcpyAsync(st->gates, gates,
+                       ((size_t)4 * st->d.n_double + st->d.n_single) * st->d.dim * 4,
+                       hipMemcpyDefault, s);
+  return e == hipSuccess ? IMQ_OK : hip_fail(st->ctx, e, "imq_dit_step_set_conditioning");
+}
+
+int imq_dit_step_run(imq_dit_step* st, const float* h_in, const float* e_in, float* x_out,
+                     int use_graph, imq_stream stream) {
+  const char* fn = "imq_dit_step_run";
+  if (!st) return fail(nullptr, IMQ_EINVAL, "%s: null step", fn);
+  if (!h_in || !e_in || !x_out) return fail(st->ctx, IMQ_EINVAL, "%s: null buffer", fn);
+  int rc = bind_device(st->ctx);
+  if (rc != IMQ_OK) return rc;
+  const imq_dit_dims& d = st->d;
+  auto s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipSuccess;
+  if (use_graph && !st->exec) {
+    // First graph run: one eager step on the plan's own stream does the
+    // launches' first-use set-up (device queries) outside the capture, then
+    // the step is captured there once.  The eager step only writes scratch
+    // that every run rewrites, and runs before the inputs are copied in.
+    e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = encode(st, st->cap);
+    if (e == hipSuccess) e = hipStreamSynchronize(st->cap);
+    if (e == hipSuccess) e = hipStreamBeginCapture(st->cap, hipStreamCaptureModeRelaxed);
+    if (e == hipSuccess) {
+      const hipError_t enc = encode(st, st->cap);
+      e = hipStreamEndCapture(st->cap, &st->graph);
+      if (e == hipSuccess) e = enc;
+    }
+    if (e == hipSuccess) e = hipGraphInstantiate(&st->exec, st->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) return hip_fail(st->ctx, e, "imq_dit_step_run: graph capture");
+  }
+  const size_t row = (size_t)d.dim * 4;
+  e = hipMemcpyAsync(st->X, e_in, (size_t)d.l_txt * row, hipMemcpyDefault, s);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(st->X + (size_t)d.l_txt * d.dim, h_in, (size_t)d.l_img * row,
+                       hipMemcpyDefault, s);
+  if (e == hipSuccess) e = use_graph ? hipGraphLaunch(st->exec, s) : encode(st, s);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(x_out, st->X, (size_t)(d.l_txt + d.l_img) * row, hipMemcpyDefault, s);
+  return e == hipSuccess ? IMQ_OK : hip_fail(st->ctx, e, fn);
+}
+
+int imq_dit_step_launches(const imq_dit_step* st) { return st ? st->launches : 0; }
+
+int imq_dit_step_destroy(imq_dit_step* st) {
+  if (!st) return IMQ_OK;
+  (void)hipSetDevice(st->ctx->device);
+  (void)hipDeviceSynchronize();
+  release(st);
+  delete st;
+  return IMQ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,152 @@
+"""Whole-step replay of a DiT step's quantized linear layers (include/imq_step.h).
+
+``DitStep`` mirrors the reference's ``DirectDiTStep`` call surface
+(``Sources/ImarelloDirect/DirectDiTStep.swift``): created once over resident
+projections (``loadBlocks``), per-step conditioning (``setStepConditioning``),
+and ``run`` = ``encodeStep`` (one graph launch instead of ~25 encoders).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .ops import Q, _DTYPES, context, device_index
+from .weights import dit_double_linears, dit_single_linears
+
+
+@dataclass(frozen=True)
+class DitDims:
+    l_img: int = 4096
+    l_txt: int = 512
+    dim: int = 3072
+    ff_inner: int = 9216
+    n_double: int = 5
+    n_single: int = 20
+
+    @property
+    def joint(self) -> int:
+        return self.l_img + self.l_txt
+
+    def projection_shapes(self) -> list[tuple[str, int, int]]:
+        """(name, N, K) of every projection in the plan's order."""
+        out = []
+        for i in range(self.n_double):
+            for name, n, k in dit_double_linears(self.dim, self.ff_inner, 2 * self.ff_inner):
+                out.append((f"transformer_blocks.{i}.{name}", n, k))
+        for i in range(self.n_single):
+            for name, n, k in dit_single_linears(self.dim, 3 * self.dim + 2 * self.ff_inner,
+                                                 self.dim + self.ff_inner):
+                out.append((f"single_transformer_blocks.{i}.{name}", n, k))
+        return out
+
+    def rows_of(self, name: str) -> int:
+        """M of a projection: image rows, text rows (double-block add_* /
+        to_add_out / ff_context.*) or all joint rows (single blocks)."""
+        if name.startswith("single_transformer_blocks."):
+            return self.joint
+        txt = (".add_", ".to_add_out", ".ff_context.")
+        return self.l_txt if any(t in name for t in txt) else self.l_img
+
+    def step_flops(self) -> float:
+        """2 M N K summed over the step's projections (the SwiGLU-fused
+        projections count their full 2 ff_inner rows; the single blocks'
+        to_qkv_mlp_proj its full width)."""
+        return sum(2.0 * self.rows_of(name) * n * k for name, n, k in self.projection_shapes())
+
+
+def random_projections(dims: DitDims, dtype: torch.dtype = torch.float16, seed: int = 0,
+                       device=None) -> list[Q]:
+    """Synthetic resident projections of the plan's shapes (random packed words,
+    scale = |N(0, 0.02)|, bias = -8 scale + N(0, 0.002)), generated on the device."""
+    dev = torch.device("cuda", device_index(device))
+    g = torch.Generator(device=dev).manual_seed(seed)
+    out = []
+    for _, n, k in dims.projection_shapes():
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k // 8), dtype=torch.int32, device=dev,
+                          generator=g)
+        s = (torch.randn((n, k // 64), device=dev, generator=g).abs() * 0.02)
+        b = -8.0 * s + torch.randn((n, k // 64), device=dev, generator=g) * 0.002
+        out.append(Q(w=w, s=s.to(dtype), b=b.to(dtype), n=n, k=k))
+    return out
+
+
+class DitStep:
+    """A created step plan over resident projections (kept alive here)."""
+
+    def __init__(self, dims: DitDims, projections: list[Q], device=None):
+        self.dims = dims
+        self.projections = projections
+        self.device = torch.device("cuda", device_index(device))
+        dt = projections[0].s.dtype
+        self.dtype = dt
+        L = _lib.load()
+        self._L = L
+        self._ctx = context(self.device)
+        arr = (_lib.QWeight * len(projections))()
+        for i, q in enumerate(projections):
+            arr[i].w = q.w.data_ptr()
+            arr[i].scales = q.s.data_ptr()
+            arr[i].biases = q.b.data_ptr()
+            arr[i].n = q.n
+            arr[i].k = q.k
+            arr[i].dtype = _DTYPES.get(q.s.dtype, -1)
+            arr[i].base = None
+        d = _lib.DitDims(dims.l_img, dims.l_txt, dims.dim, dims.ff_inner, dims.n_double,
+                         dims.n_single)
+        out = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            _lib.check(L.imq_dit_step_create(self._ctx, ctypes.byref(d), arr, len(projections),
+                                             _DTYPES.get(dt, -1), ctypes.byref(out)), self._ctx)
+        self._h = out
+
+    def close(self) -> None:
+        if self._h:
+            self._L.imq_dit_step_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_conditioning(self, norm_weight: torch.Tensor | None = None,
+                         gates: torch.Tensor | None = None) -> None:
+        d = self.dims
+        if norm_weight is not None:
+            assert norm_weight.dtype == torch.float32 and norm_weight.numel() == d.dim
+            assert norm_weight.is_contiguous()
+        if gates is not None:
+            assert gates.dtype == torch.float32 and gates.is_contiguous()
+            assert gates.numel() == (4 * d.n_double + d.n_single) * d.dim
+        st = torch.cuda.current_stream(self.device).cuda_stream
+        with torch.cuda.device(self.device):
+            _lib.check(self._L.imq_dit_step_set_conditioning(
+                self._h, ctypes.c_void_p(norm_weight.data_ptr() if norm_weight is not None else 0),
+                ctypes.c_void_p(gates.data_ptr() if gates is not None else 0),
+                ctypes.c_void_p(st)), self._ctx)
+
+    def run(self, h: torch.Tensor, e: torch.Tensor, out: torch.Tensor | None = None,
+            use_graph: bool = True) -> torch.Tensor:
+        """x_out [l_txt + l_img, dim] fp32 (text rows first) from h [l_img, dim]
+        and e [l_txt, dim] fp32."""
+        d = self.dims
+        assert h.dtype == torch.float32 and tuple(h.shape) == (d.l_img, d.dim) and h.is_contiguous()
+        assert e.dtype == torch.float32 and tuple(e.shape) == (d.l_txt, d.dim) and e.is_contiguous()
+        if out is None:
+            out = torch.empty((d.joint, d.dim), dtype=torch.float32, device=self.device)
+        st = torch.cuda.current_stream(self.device).cuda_stream
+        with torch.cuda.device(self.device):
+            _lib.check(self._L.imq_dit_step_run(self._h, ctypes.c_void_p(h.data_ptr()),
+                                                ctypes.c_void_p(e.data_ptr()),
+                                                ctypes.c_void_p(out.data_ptr()), int(use_graph),
+                                                ctypes.c_void_p(st)), self._ctx)
+        return out
+
+    @property
+    def launches(self) -> int:
+        return self._L.imq_dit_step_launches(self._h)

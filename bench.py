@@ -12,6 +12,12 @@ over that synthetic batch, inputs resident in HBM.  The same line carries:
 * dequant    -- the two projections of a DiT single-stream block, GB/s;
 * qgemm_shapes -- the other qGEMM shapes (PR1 1024x9216x3072, single-block
                 pair);
+* dit_single_block -- one DiT single-stream block's projections at 1024^2
+                (f16): to_qkv_mlp_proj with the SwiGLU fused into its epilogue,
+                to_out with the gated residual add fused;
+* dit_step     -- a whole DiT step's quantized linear layers (5 double + 20
+                single blocks, l_img 4096 + l_txt 512, f16, random-init packed
+                weights of the model's shapes) replayed as one HIP graph;
 * cpu_baseline -- the C oracle's f32-accumulating CPU quantized matmul
                 (MLX is not available) on a bounded sample of the same problem.
 
@@ -144,9 +150,11 @@ def bench_qgemm_shape(imq, synth, torch, m, n, k, reps=10) -> dict:
     p = synth.make_problem(m, n, k, seed=0)
     x, w, s, b = synth.to_device(p)
     y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-    for _ in range(2):
+    # Warm up for about 60 ms of MFMA work (past the clock transient).
+    warm = max(2, int(60e-3 * 1e15 / (2.0 * m * n * k)))
+    for _ in range(warm):
         imq.qgemm(x, w, s, b, out=y)
-    ms = time_events(lambda: imq.qgemm(x, w, s, b, out=y), reps)
+    ms = time_events(lambda: imq.qgemm(x, w, s, b, out=y), max(reps, 20))
     tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     log(f"qgemm M={m} N={n} K={k}: {ms:.3f} ms  {tf:.1f} TFLOP/s")
     return {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / PEAK_BF16_TFLOPS, 4)}
@@ -198,6 +206,80 @@ def floors(torch) -> int:
     torch.cuda.synchronize()
     log(f"floors: 200 one-element fills; 240 copies of {words * 4} bytes")
     return 0
+
+
+def bench_dit_single_block(imq, torch) -> dict:
+    """Single-stream block projections at J=4608 (f16): QKV part of
+    to_qkv_mlp_proj (9216 rows), its MLP part with SwiGLU fused (2 x 9216 rows
+    -> 9216 outputs), to_out (K=12288) with the gated residual fused."""
+    from aestrix_amd.step import random_projections, DitDims
+    d = DitDims(n_double=0, n_single=1)
+    proj, out_w = random_projections(d, torch.float16, seed=3)
+    J, dim, ffi = d.joint, d.dim, d.ff_inner
+    nx = torch.randn((J, dim), device="cuda").half()
+    qkv = torch.empty((J, 3 * dim), dtype=torch.float16, device="cuda")
+    concat = torch.zeros((J, dim + ffi), dtype=torch.float16, device="cuda")
+    x = torch.randn((J, dim), device="cuda")
+    gate = torch.ones(dim, device="cuda")
+    w3, s3, b3 = proj.w[:3 * dim], proj.s[:3 * dim], proj.b[:3 * dim]
+
+    def block():
+        imq.quantized_matmul(nx, w3, s3, b3, out=qkv)
+        imq.qmm_swiglu(nx, proj.w, proj.s, proj.b, ffi, 3 * dim, 3 * dim + ffi,
+                       out=concat[:, dim:])
+        imq.qmm_gate_add(concat, out_w.w, out_w.s, out_w.b, x, gate, 1.0, out=x)
+
+    for _ in range(5):
+        block()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        block()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 20
+    flop = 2.0 * J * dim * (3 * dim + 2 * ffi) + 2.0 * J * (dim + ffi) * dim
+    log(f"dit single block (f16, fused SwiGLU + gated residual): {ms:.3f} ms "
+        f"{flop / ms / 1e9:.1f} TFLOP/s")
+    return {"ms": round(ms, 4), "TFLOP/s": round(flop / ms / 1e9, 1),
+            "frac_mfma": round(flop / ms / 1e9 / PEAK_BF16_TFLOPS, 4), "gflop": round(flop / 1e9, 2)}
+
+
+def bench_dit_step(torch) -> dict:
+    """A whole step (5 double + 20 single blocks) as one graph launch."""
+    from aestrix_amd.step import DitDims, DitStep, random_projections
+    d = DitDims()
+    projs = random_projections(d, torch.float16, seed=4)
+    step = DitStep(d, projs)
+    h = torch.randn((d.l_img, d.dim), device="cuda")
+    e = torch.randn((d.l_txt, d.dim), device="cuda")
+    out = torch.empty((d.joint, d.dim), device="cuda")
+    for _ in range(3):
+        step.run(h, e, out)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        step.run(h, e, out)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 10
+    flop = d.step_flops()
+    wbytes = sum(q.w.numel() * 4 + 2 * q.s.numel() * 2 for q in projs)
+    log(f"dit step (graph, {step.launches} launches): {ms:.2f} ms {flop / ms / 1e9:.1f} TFLOP/s")
+    res = {"ms": round(ms, 3), "TFLOP/s": round(flop / ms / 1e9, 1),
+           "frac_mfma": round(flop / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+           "tflop_per_step": round(flop / 1e12, 3), "launches": step.launches,
+           "packed_weight_bytes": wbytes,
+           "config": "5 double + 20 single blocks, l_img 4096 + l_txt 512, dim 3072, "
+                     "ff_inner 9216, f16, RMSNorm before each block's projections"}
+    step.close()
+    del projs
+    torch.cuda.empty_cache()
+    return res
 
 
 def traffic_from_profiles():
@@ -280,6 +362,8 @@ def main() -> int:
             "M4608_N27648_K3072": bench_qgemm_shape(imq, synth, torch, 4608, 27648, 3072),
             "M4608_N3072_K9216": bench_qgemm_shape(imq, synth, torch, 4608, 3072, 9216),
         }
+        extra["dit_single_block"] = bench_dit_single_block(imq, torch)
+        extra["dit_step"] = bench_dit_step(torch)
 
     result = {
         "metric": METRIC,

@@ -1,0 +1,91 @@
+/*
+ * imq_step.h -- whole-step replay of the quantized linear layers of a FLUX.2
+ * klein DiT step as one HIP graph.
+ *
+ * Mirrors the reference's DirectDiTStep: a static scratch plan allocated once
+ * (DirectDiTStep.allocateScratch, Sources/ImarelloDirect/DirectDiTStep.swift:155-274),
+ * the 5 double + 20 single blocks encoded in order (encodeBlocks / encodeDouble /
+ * encodeSingle, :545-685) and run per denoise step with one blocking wait
+ * (encodeStep, :636-649).  The graph holds every quantized projection of the
+ * step at its real shape, with the glue the reference runs right after them
+ * folded into the projection's epilogue (SwiGLU, gated residual add), and an
+ * RMSNorm of the fp32 residual stream before each block's projections.
+ *
+ * Not in the graph (outside the quantized-linear path): attention, RoPE, the
+ * per-head Q/K norms and the LayerNorm modulation.  Where the reference feeds
+ * the attention output into to_out / to_add_out, the step feeds the V
+ * projection of the same rows; in single blocks the attention half of the
+ * concat buffer keeps the values it was created with (zeros).
+ *
+ * Data flow per double block (img rows = the l_img rows after the l_txt text
+ * rows of the joint residual X, fp32 [l_txt + l_img, dim]):
+ *   nX = RMSNorm(X)
+ *   Q, K, V [rows] = nX[rows] . {to_q, to_k, to_v}^T (img) / {add_q, add_k, add_v}^T (txt)
+ *   X[img] += gate[0] * (V[img] . to_out^T);   X[txt] += gate[1] * (V[txt] . to_add_out^T)
+ *   nX = RMSNorm(X)
+ *   SW[img] = SwiGLU(nX[img] . ff.linear_in^T);  X[img] += gate[2] * (SW[img] . ff.linear_out^T)
+ *   SW[txt] = SwiGLU(nX[txt] . ff_context.linear_in^T);  X[txt] += gate[3] * (...linear_out^T)
+ * and per single block (all J = l_txt + l_img rows):
+ *   nX = RMSNorm(X)
+ *   QKV = nX . to_qkv_mlp_proj[0 : 3 dim]^T
+ *   C[:, dim : dim + ff_inner] = SwiGLU over to_qkv_mlp_proj rows [3 dim, 3 dim + 2 ff_inner)
+ *   X += gate * (C . to_out^T)             (C = [attention | mlp], dim + ff_inner wide)
+ * SwiGLU pairs gate row j with up row ff_inner + j of its section.
+ */
+#ifndef IMQ_STEP_H
+#define IMQ_STEP_H
+
+#include "imq.h"
+#include "imq_weights.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct imq_dit_dims {
+    int l_img;     /* image tokens (4096 at 1024x1024) */
+    int l_txt;     /* text tokens (512) */
+    int dim;       /* model width (3072) */
+    int ff_inner;  /* MLP hidden width (9216) */
+    int n_double;  /* double-stream blocks (5) */
+    int n_single;  /* single-stream blocks (20) */
+} imq_dit_dims;
+
+typedef struct imq_dit_step imq_dit_step; /* opaque */
+
+/* weights: n_double * 12 + n_single * 2 resident projections, per double
+ * block in the reference's DoubleWeights order (DirectDiTStep.swift:310-323):
+ * to_q, to_k, to_v, add_q, add_k, add_v, to_out, to_add_out, ff.linear_in,
+ * ff.linear_out, ff_context.linear_in, ff_context.linear_out; per single block
+ * (:328-333): to_qkv_mlp_proj, to_out.  Shapes [N, K] must be the model's
+ * (ff.linear_in is [2 ff_inner, dim], to_qkv_mlp_proj [3 dim + 2 ff_inner,
+ * dim], single to_out [dim, dim + ff_inner]), K % 256 == 0, and every
+ * projection's dtype (its scales' element type) must be dtype, bf16 or f16.
+ * The plan allocates its scratch once; the weights must outlive it. */
+int imq_dit_step_create(imq_ctx* ctx, const imq_dit_dims* dims, const imq_qweight* weights,
+                        int n_weights, imq_dtype dtype, imq_dit_step** out);
+
+/* Per-step conditioning, fp32, each may be NULL to keep the current values
+ * (initially all ones): the RMSNorm weight [dim], and the gate vectors
+ * [n_double * 4 + n_single][dim] (double: img attention, txt attention, img
+ * MLP, txt MLP; single: one).  Asynchronous on stream. */
+int imq_dit_step_set_conditioning(imq_dit_step* step, const float* norm_weight,
+                                  const float* gates, imq_stream stream);
+
+/* One step: X = [e_in; h_in] (h_in fp32 [l_img, dim], e_in fp32 [l_txt, dim],
+ * copied in, never written), the blocks, and x_out (fp32 [l_txt + l_img, dim],
+ * text rows first) = the final X.  use_graph != 0 replays the captured graph
+ * (captured on the first such call), 0 launches the same kernels one by one.
+ * Asynchronous on stream. */
+int imq_dit_step_run(imq_dit_step* step, const float* h_in, const float* e_in, float* x_out,
+                     int use_graph, imq_stream stream);
+
+/* Kernel launches in one step (graph nodes). */
+int imq_dit_step_launches(const imq_dit_step* step);
+
+int imq_dit_step_destroy(imq_dit_step* step);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IMQ_STEP_H */
