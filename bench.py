@@ -100,7 +100,7 @@ def time_graph(launches, replays: int = 5) -> float:
     return start.elapsed_time(end) / (replays * len(launches))
 
 
-def bench_qgemv(imq, synth, torch, copies: int = 48) -> dict:
+def bench_qgemv(imq, synth, torch, copies: int = 48, ms_list=(1, 4, 16)) -> dict:
     out = {}
     for (n, k) in ((9728, 2560), (2560, 9728)):
         p = synth.make_problem(16, n, k, seed=0)
@@ -109,7 +109,7 @@ def bench_qgemv(imq, synth, torch, copies: int = 48) -> dict:
         ss = [s.clone() for _ in range(copies)]
         bs = [b.clone() for _ in range(copies)]
         del w, s, b
-        for m in (1, 4, 16):
+        for m in ms_list:
             xm = x[:m].contiguous()
             ys = [torch.empty((m, n), dtype=torch.bfloat16, device="cuda") for _ in range(copies)]
             launches = [(lambda i=i: imq.qgemv(xm, ws[i], ss[i], bs[i], out=ys[i]))
@@ -133,15 +133,16 @@ def bench_dequant(imq, synth, torch, copies: int = 6) -> dict:
         ws = [w.clone() for _ in range(copies)]
         ss = [s.clone() for _ in range(copies)]
         bs = [b.clone() for _ in range(copies)]
-        o = torch.empty((n, k), dtype=torch.bfloat16, device="cuda")
-        launches = [(lambda i=i: imq.dequantize(ws[i], ss[i], bs[i], out=o)) for i in range(copies)]
+        os_ = [torch.empty((n, k), dtype=torch.bfloat16, device="cuda") for _ in range(copies)]
+        launches = [(lambda i=i: imq.dequantize(ws[i], ss[i], bs[i], out=os_[i]))
+                    for i in range(copies)]
         ms = time_graph(launches, replays=4)
         byts = dequant_bytes(n, k)
         gbs = byts / (ms * 1e-3) / 1e9
         out[f"N{n}_K{k}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                              "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts}
         log(f"dequant N={n} K={k}: {ms * 1e3:.1f} us  {gbs:.0f} GB/s")
-        del ws, ss, bs, o
+        del ws, ss, bs, os_
         torch.cuda.empty_cache()
     return out
 
@@ -298,6 +299,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-target", action="store_true",
                     help="time the headline qGEMM only (for profiling runs)")
+    ap.add_argument("--only-hbm", action="store_true",
+                    help="run the M=1 qGEMV and dequantize benchmarks and a calibration copy only "
+                         "(for counter runs)")
     ap.add_argument("--floors", action="store_true",
                     help="run the launch and streaming-read floor kernels only (for profiling runs)")
     args = ap.parse_args()
@@ -319,6 +323,15 @@ def main() -> int:
         return floors(torch)
     imq._lib.load()
     props = torch.cuda.get_device_properties(0)
+    if args.only_hbm:
+        bench_qgemv(imq, synth, torch, ms_list=(1,))
+        bench_dequant(imq, synth, torch)
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calibration copy: 268435456 bytes read and written")
+        return 0
 
     m, n, k = TARGET
     log(f"target qgemm M={m} N={n} K={k}")
