@@ -18,6 +18,7 @@ over that synthetic batch, inputs resident in HBM.  The same line carries:
 * dit_step     -- a whole DiT step's quantized linear layers (5 double + 20
                 single blocks, l_img 4096 + l_txt 512, f16, random-init packed
                 weights of the model's shapes) replayed as one HIP graph;
+* upload       -- the loader's host -> device path (pinned double buffer) in GB/s;
 * cpu_baseline -- the C oracle's f32-accumulating CPU quantized matmul
                 (MLX is not available) on a bounded sample of the same problem.
 
@@ -283,6 +284,48 @@ def bench_dit_step(torch) -> dict:
     return res
 
 
+def bench_upload(torch) -> dict:
+    """Loader path: host -> device through the library's pinned double buffer
+    (imq_upload, what the safetensors loader uses for mapped shards) from a
+    pageable 1 GiB host buffer, beside a plain pageable torch copy."""
+    import ctypes
+
+    import numpy as np
+
+    from aestrix_amd import _lib, ops
+
+    n = 1 << 30
+    host = np.ones(n, dtype=np.uint8)
+    dev = torch.empty(n, dtype=torch.uint8, device="cuda")
+    L = _lib.load()
+    ctx = ops.context()
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def staged():
+        _lib.check(L.imq_upload(ctx, ctypes.c_void_p(dev.data_ptr()),
+                                host.ctypes.data_as(ctypes.c_void_p), n, st), ctx)
+
+    staged()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        staged()
+    torch.cuda.synchronize()
+    staged_s = (time.perf_counter() - t0) / 3
+    src = torch.from_numpy(host)
+    dev.copy_(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        dev.copy_(src)
+    torch.cuda.synchronize()
+    plain_s = (time.perf_counter() - t0) / 3
+    log(f"upload 1 GiB: staged {n / staged_s / 1e9:.1f} GB/s, plain pageable copy "
+        f"{n / plain_s / 1e9:.1f} GB/s")
+    return {"bytes": n, "staged_GB/s": round(n / staged_s / 1e9, 2),
+            "pageable_copy_GB/s": round(n / plain_s / 1e9, 2)}
+
+
 def traffic_from_profiles():
     path = os.path.join(ROOT, "profiles", "qgemm_target_traffic.json")
     if not os.path.exists(path):
@@ -377,6 +420,7 @@ def main() -> int:
         }
         extra["dit_single_block"] = bench_dit_single_block(imq, torch)
         extra["dit_step"] = bench_dit_step(torch)
+        extra["upload"] = bench_upload(torch)
 
     result = {
         "metric": METRIC,

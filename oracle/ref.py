@@ -184,3 +184,12 @@ def glue_swiglu(g_t: np.ndarray, u_t: np.ndarray, in_scale: float, out_scale: fl
     g = np.asarray(g_t, np.float64) * np.float32(in_scale)
     u = np.asarray(u_t, np.float64) * np.float32(in_scale)
     return g / (1.0 + np.exp(-g)) * u * np.float32(out_scale)
+
+
+def rmsnorm_rows(x: np.ndarray, w: np.ndarray, eps: float = 1e-5) -> np.ndarray:
+    """Row RMSNorm in float64: x * 1/sqrt(mean(x^2) + eps) * w (the shape of the
+    reference's dd_rmsnorm_pitched, DirectDiTKernels.swift:61-99, eps 1e-5 at
+    DirectDiTStep.swift:416); the caller rounds to T."""
+    x = np.asarray(x, np.float64)
+    inv = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    return x * inv * np.asarray(w, np.float64)

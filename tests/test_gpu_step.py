@@ -64,9 +64,7 @@ def oracle_step(d: DitDims, projs, norm_w, gates, h, e, tdt):
     dim, ffi = d.dim, d.ff_inner
 
     def rms(X):
-        x = X.astype(np.float64)
-        inv = 1.0 / np.sqrt(np.mean(x * x, axis=1, keepdims=True) + 1e-5)
-        return to_t(x * inv * norm_w[None, :].astype(np.float64), tdt)
+        return to_t(ref.rmsnorm_rows(X, norm_w), tdt)
 
     def swiglu(x_t, q, gate_row, up_row):
         g = qmm_t(x_t, sub(q, slice(gate_row, gate_row + ffi)), tdt)

@@ -513,3 +513,35 @@ def test_f16_checks_catch_unrounded_dequant_mutant():
     deq32 = ref.dequantize_as(p.w, s, b, np.float32).astype(np.float64)
     mutant = (x.astype(np.float64) @ deq32.T).astype(np.float16)
     assert not np.array_equal(mutant, want)
+
+
+# ------------------------------------------------ glue stages and RMSNorm
+# Pinned against torch's own functions and closed forms (not restatements).
+
+def test_glue_swiglu_matches_torch_silu():
+    rng = np.random.default_rng(3)
+    g = rng.standard_normal((7, 33)).astype(np.float32) * 4
+    u = rng.standard_normal((7, 33)).astype(np.float32)
+    want = (torch.nn.functional.silu(torch.from_numpy(g).double() * 16)
+            * torch.from_numpy(u).double() * 16 / 8).numpy()
+    assert np.allclose(ref.glue_swiglu(g, u, 16.0, 1.0 / 8), want, rtol=1e-12, atol=1e-12)
+    assert np.all(ref.glue_swiglu(np.zeros(3, np.float32), np.ones(3, np.float32), 1, 1) == 0)
+
+
+def test_glue_gate_add_and_postscale_closed_forms():
+    rng = np.random.default_rng(4)
+    y = rng.standard_normal((5, 8)).astype(np.float32)
+    x = rng.standard_normal((5, 8)).astype(np.float32)
+    assert np.array_equal(ref.glue_gate_add(y, x, np.zeros(8, np.float32), 3.0), x)
+    one = ref.glue_gate_add(y, x, np.ones(8, np.float32), 1.0)
+    assert np.array_equal(one, (x.astype(np.float64) + y).astype(np.float32))
+    assert np.array_equal(ref.glue_postscale(y, 16.0), y * np.float32(16))
+
+
+def test_rmsnorm_rows_matches_torch():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((9, 300))
+    w = rng.standard_normal(300)
+    want = torch.nn.functional.rms_norm(torch.from_numpy(x), (300,), torch.from_numpy(w),
+                                        eps=1e-5).numpy()
+    assert np.allclose(ref.rmsnorm_rows(x, w), want, rtol=1e-12, atol=1e-12)
