@@ -178,6 +178,9 @@ __device__ __forceinline__ u32x4_t load_b128(__amdgpu_buffer_rsrc_t rs, uint32_t
 // s_waitcnt vmcnt(n) leaving expcnt and lgkmcnt unconstrained (gfx9 encoding).
 #define IMQ_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+// s_waitcnt vmcnt(0) lgkmcnt(0): every load of this wave, to registers or LDS,
+// and every LDS read has completed.
+#define IMQ_WAIT_VM_LGKM_0() __builtin_amdgcn_s_waitcnt(7 << 4)
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),

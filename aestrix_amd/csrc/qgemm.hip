@@ -245,70 +245,73 @@ __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_
 }
 
 // ---------------------------------------------------------------------------
-// Large-M kernel: a (32 MT) x 256 workgroup tile, one wave per SIMD (each wave
-// a (32 MT) x 64 sub-tile, MT x 2 MFMA tiles, up to 256 fp32 accumulators per
-// lane in AGPRs).
+// Large-M kernel: a (32 MT) x 256 workgroup tile, one wave per SIMD, the four
+// waves side by side along N (each a (32 MT) x 64 sub-tile: MT x 2 MFMA tiles,
+// up to 256 fp32 accumulators per lane in AGPRs).  Each code is dequantized
+// once per workgroup.  A K-step covers two quantization groups: 128 K, eight
+// k-slices of 16.
 //
 // Activations are staged by direct buffer->LDS loads (buffer_load_dwordx4 ...
 // lds: lane L writes LDS base + 16 L, no VGPRs; the per-lane byte offset is
 // fixed for the whole K loop and the K-step advance is a scalar offset, so a
-// load costs no vector ALU work) into an LDS ring (see BigCfg for the depth).  Packed weights need no sharing between waves (each wave owns its
-// columns), so they are loaded straight into registers, also two steps ahead,
-// keeping their bytes off the LDS port that the activation reads saturate.
+// load costs no vector ALU work) into a 2-stage LDS ring.  Packed weights need
+// no sharing between waves (each wave owns its columns), so they are loaded
+// straight into registers.  Both are loaded one step ahead.  Scales and biases
+// are loaded four groups at a time (8 bytes of a row per load, one block of
+// two steps ahead): a lane's per-group 2-byte loads touch one cache line per
+// row each and cost more memory-pipeline time than the weights and
+// activations together.  The K loop is unrolled by four steps so that the
+// ring stage, the weight registers, the scale-block slot and the group's
+// position in its block are compile-time constants: the compiler can prove
+// that loads in flight into the other stage do not alias this stage's reads
+// and emits no waits of its own in the loop.
 //
-// Scales and biases are loaded four groups at a time (8 bytes of a row per
-// load, one block ahead): a lane's per-step 2-byte loads touch one cache line
-// per row each, and at four such loads per step they cost more memory-pipeline
-// time than the weights and activations together.  The K loop is unrolled by
-// four so that the ring stage, the register slot and the group's position in
-// its scale block (and the block's register slot, over a two-block unroll of
-// eight steps) are all compile-time constants.
-//
-// Step g issues NTW weight and kA activation loads (for step g+2), plus at
-// steps g % 4 == 0 the 2 NTW scale-block loads of the next block (for steps
-// g+4 .. g+7); steps past the end re-load the last step into the free stage.
-// At the top of step g, `s_waitcnt vmcnt(<loads issued by step g-1>)`
-// guarantees that this wave's loads of step g have landed, and a raw
-// s_barrier (no fence, which would wait for every outstanding load) makes the
-// other waves' parts visible and frees the stage that step g+2 overwrites
-// (stage (g+2) % 4 was last read in step g-2).  Within a step, the A fragments
-// of k-slice kk+1 are read from LDS and the weight words of kk+1 dequantized
-// while the MFMAs of kk run.
+// Step g (stage g % 2):
+//  * s_waitcnt vmcnt(0) lgkmcnt(0) and a raw s_barrier (no fence, which would
+//    wait for every outstanding load): this wave's loads of step g have
+//    landed, and once every wave has passed, all of them have; every wave's
+//    LDS reads of the other stage (step g-1) have returned, so it may be
+//    refilled.
+//  * The LDS reads and the weight dequant of k-slice 0, then the MFMAs of step
+//    g-1's last k-slice with the loads of step g+1 (and, every other step, the
+//    next scale block) issued between them.
+//  * k-slices 0 .. 6: the MFMAs of slice i with the LDS reads and dequant of
+//    slice i+1 interleaved; the MFMAs of slice 7 wait for the top of step g+1.
+// Deferring the last slice keeps the matrix core busy through the barrier,
+// the issue of the next step's loads and the LDS latency of the first slice.
 //
 // Requires K % 256 == 0 (whole scale blocks); other K take the
-// register-staged kernel.  An odd number of blocks ends with one 4-step block
-// in slot 0.
+// register-staged kernel.
 // ---------------------------------------------------------------------------
 constexpr int kBigBN = 256;
+constexpr int kBigKG = 2;                // quantization groups per K-step
+constexpr int kBigSlices = 4 * kBigKG;   // k-slices of 16 per K-step
+constexpr int kBigUnroll = 4;            // K-steps per loop iteration (two scale blocks)
 
-// Tile geometry: WM x WN = 4 waves; a wave owns MTW x NTW MFMA tiles of 32x32
-// (a (32 MTW) x (32 NTW) sub-tile); the workgroup tile is
-// (32 MTW WM) x (32 NTW WN) with WN * 32 * NTW = 256 columns.  A K-step holds
-// KG quantization groups: KG = 1 runs a 4-stage ring with loads two steps
-// ahead, KG = 2 a 2-stage ring with loads one (twice as long) step ahead.
-template <int MTW, int NTW, int WM, int KG>
+template <int MT>
 struct BigCfg {
-  static constexpr int kWN = 4 / WM;
-  static constexpr int kBM = 32 * MTW * WM;
-  static constexpr int kA = kBM * 8 * KG / kThreads;  // activation slots per thread per step
-  static constexpr int kStages = KG == 1 ? 4 : 2;
-  static constexpr int kAhead = KG == 1 ? 2 : 1;      // steps between a load and its use
-  static constexpr int kSpb = 4 / KG;                 // steps per 4-group scale block
-  static constexpr int kUnroll = 2 * kSpb;            // two scale blocks
-  static_assert(32 * NTW * kWN == kBigBN, "workgroup tile must be 256 columns wide");
+  static constexpr int kBM = 32 * MT;
+  static constexpr int kSlots = kBM * 8 * kBigKG;     // 16-byte LDS slots per stage
+  static constexpr int kA = kSlots / kThreads;        // activation slots per thread per step
 };
 
-constexpr int kMaxStages = 4;
 struct BigRing {
-  uint4* a[kMaxStages];
+  uint4* a[2];
 };
 
-template <int MTW, int NTW, int WM, int KG>
+template <int MT>
 struct BigSrc {
   __amdgpu_buffer_rsrc_t xr, wr, sr, br;
-  uint32_t a_off[BigCfg<MTW, NTW, WM, KG>::kA];  // byte offsets of this thread's activation slots
-  uint32_t w_off[NTW];  // byte offsets of this lane's 16 weight bytes, per column tile
-  uint32_t p_off[NTW];  // byte offsets of this lane's scale / bias row, per column tile
+  uint32_t a_off[BigCfg<MT>::kA];  // byte offsets of this thread's activation slots
+  uint32_t w_off[2];  // byte offsets of this lane's 16 weight bytes, per column tile
+  uint32_t p_off[2];  // byte offsets of this lane's scale / bias row, per column tile
+};
+
+// MFMA operands of two consecutive k-slices (buffer = slice parity).
+template <int MT>
+struct BigFrags {
+  u32x4_t a[2][MT];
+  u32x4_t b[2][2];
 };
 
 // Four consecutive scales (or biases) of a row, groups 4b .. 4b+3.
@@ -324,184 +327,196 @@ __device__ __forceinline__ uint32_t param_at(uint2 blk, int j) {
   return (j & 1) ? (w >> 16) : (w & 0xFFFFu);
 }
 
-// Issue the weight and activation loads of step gl (clamped into range) into
-// ring stage ST: KG groups, weights to registers, activations to LDS.
-template <int MTW, int NTW, int WM, int KG, int ST>
-__device__ __forceinline__ void big_issue(int gl, int steps, const BigRing& ring,
-                                          const BigSrc<MTW, NTW, WM, KG>& src,
-                                          u32x4_t (&wr)[BigCfg<MTW, NTW, WM, KG>::kStages][NTW][KG],
-                                          int wave) {
-  using C = BigCfg<MTW, NTW, WM, KG>;
-  const uint32_t gs = (uint32_t)min(gl, steps - 1);
+// Dequant parameters of one group for the two column tiles: s * 2^24 and
+// s * 2^20 (the fma_mix nibble trick) and the bias.
+struct GroupParams {
+  float s24[2], s20[2], b[2];
+};
+
+template <int T>
+__device__ __forceinline__ GroupParams group_params(const uint2 (&sblk)[2], const uint2 (&bblk)[2],
+                                                    int j) {
+  GroupParams p;
 #pragma unroll
-  for (int q = 0; q < KG; ++q)
-#pragma unroll
-    for (int nt = 0; nt < NTW; ++nt)
-      wr[ST][nt][q] = load_b128(src.wr, src.w_off[nt], (gs * KG + q) * 32u);
-  uint4* ab = ring.a[ST] + wave * 64;
-#pragma unroll
-  for (int i = 0; i < C::kA; ++i)
-    load_lds16(src.xr, src.a_off[i], gs * (128u * KG), ab + i * kThreads);
+  for (int nt = 0; nt < 2; ++nt) {
+    const float sv = Elem<T>::param((typename Elem<T>::S)param_at(sblk[nt], j));
+    p.s24[nt] = sv * 0x1p24f;
+    p.s20[nt] = sv * 0x1p20f;
+    p.b[nt] = Elem<T>::param((typename Elem<T>::S)param_at(bblk[nt], j));
+  }
+  return p;
 }
 
-// One K-step of the large-M kernel.  S = g % kUnroll is a compile-time
-// constant: the LDS stage S % kStages it reads and the ones its direct loads
-// fill are distinct LDS objects, so the compiler can prove that the in-flight
-// loads into other stages do not alias the reads of this stage and does not
-// wait for them; its scale block sits in register slot S / kSpb while the
-// next block loads into the other slot.
-template <int T, int MTW, int NTW, int WM, int KG, int S>
-__device__ __forceinline__ void big_step(
-    int g, int steps, const BigRing& ring, const BigSrc<MTW, NTW, WM, KG>& src,
-    uint2 (&sblk)[2][NTW], uint2 (&bblk)[2][NTW],
-    u32x4_t (&wr)[BigCfg<MTW, NTW, WM, KG>::kStages][NTW][KG], f32x16_t (&acc)[MTW][NTW], int wave,
-    int arow0, int r32, int h) {
-  using C = BigCfg<MTW, NTW, WM, KG>;
-  constexpr int ST = S % C::kStages;
-  constexpr int SA = (S + C::kAhead) % C::kStages;
-  constexpr int SLOT = S / C::kSpb;
-  constexpr int J0 = (S % C::kSpb) * KG;  // position of the step's first group in its block
-  // Loads that may stay in flight: those issued by steps after the one that
-  // loaded this step's data (with loads one step ahead, none).
-  constexpr int kPrev =
-      C::kAhead == 2 ? NTW + C::kA + (((S + C::kUnroll - 1) % C::kSpb) == 0 ? 2 * NTW : 0) : 0;
-  IMQ_WAIT_VMCNT(kPrev);  // this wave's loads of step g are done
+// Issue the weight and activation loads of step gl (clamped into range) into
+// ring stage ST: weights to registers, activations to LDS.
+template <int MT, int ST>
+__device__ __forceinline__ void big_issue(int gl, int steps, const BigRing& ring,
+                                          const BigSrc<MT>& src, u32x4_t (&wr)[2][2][kBigKG],
+                                          int wave) {
+  const uint32_t gs = (uint32_t)min(gl, steps - 1);
+#pragma unroll
+  for (int q = 0; q < kBigKG; ++q)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+      wr[ST][nt][q] = load_b128(src.wr, src.w_off[nt], (gs * kBigKG + q) * 32u);
+  uint4* ab = ring.a[ST] + wave * 64;
+#pragma unroll
+  for (int i = 0; i < BigCfg<MT>::kA; ++i)
+    load_lds16(src.xr, src.a_off[i], gs * (128u * kBigKG), ab + i * kThreads);
+}
+
+// LDS reads and weight dequant of k-slice t of a step into buffer B.  In
+// group q = t / 4, slice kk = t % 4, lane (r32, h) holds k = 64 q + 32 h +
+// 8 kk .. +8 of its activation row and of its weight row (word kk of its 16
+// bytes of the group), so the two operands agree.
+template <int T, int MT, int B>
+__device__ __forceinline__ void big_operands(int t, const uint4* at, const u32x4_t (&wr)[2][kBigKG],
+                                             const GroupParams& gp, BigFrags<MT>& f, int arow0,
+                                             int r32, int h) {
+  const int q = t >> 2, kk = t & 3;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    f.a[B][mt] = __builtin_bit_cast(
+        u32x4_t, at[a_slot_kg<kBigKG>(arow0 + mt * 32 + r32, 8 * q + 4 * h + kk)]);
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const u32x4_t wv = wr[nt][q];
+    const uint32_t word = (kk == 0) ? wv.x : (kk == 1) ? wv.y : (kk == 2) ? wv.z : wv.w;
+    uint32_t p[4];
+    Elem<T>::dequant(word, gp.s24[nt], gp.s20[nt], gp.b[nt], p);
+    f.b[B][nt] = u32x4_t{p[0], p[1], p[2], p[3]};
+  }
+}
+
+template <int T, int MT, int B>
+__device__ __forceinline__ void big_mfmas(const BigFrags<MT>& f, f32x16_t (&acc)[MT][2]) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma32<T>(f.a[B][mt], f.b[B][nt], acc[mt][nt]);
+}
+
+// One K-step.  S = g % kBigUnroll: stage and weight registers S % 2, scale
+// block slot S / 2, first group at position 2 (S % 2) of its block.
+template <int T, int MT, int S>
+__device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
+                                         const BigSrc<MT>& src, uint2 (&sblk)[2][2],
+                                         uint2 (&bblk)[2][2], u32x4_t (&wr)[2][2][kBigKG],
+                                         BigFrags<MT>& f, f32x16_t (&acc)[MT][2], int wave,
+                                         int arow0, int r32, int h) {
+  constexpr int ST = S % 2;
+  constexpr int SLOT = S / 2;
+  constexpr int J0 = (S % 2) * kBigKG;
+  constexpr int kMfma = 2 * MT;
+  IMQ_WAIT_VM_LGKM_0();
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
-  // At a block start the next block goes to the other slot.
-  if constexpr (S % C::kSpb == 0) {
-    const int steps_blocks = steps * KG / 4;
-    const uint32_t nb = (uint32_t)min(g * KG / 4 + 1, steps_blocks - 1);
+  const uint4* at = ring.a[ST];
+  GroupParams gp = group_params<T>(sblk[SLOT], bblk[SLOT], J0);
+  big_operands<T, MT, 0>(0, at, wr[ST], gp, f, arow0, r32, h);
+  if constexpr (S % 2 == 0) {
+    // The next block (steps g+2, g+3) goes to the other slot.
+    const int blocks = steps * kBigKG / 4;
+    const uint32_t nb = (uint32_t)min(g * kBigKG / 4 + 1, blocks - 1);
 #pragma unroll
-    for (int nt = 0; nt < NTW; ++nt) {
+    for (int nt = 0; nt < 2; ++nt) {
       sblk[SLOT ^ 1][nt] = load_param_block(src.sr, src.p_off[nt], nb);
       bblk[SLOT ^ 1][nt] = load_param_block(src.br, src.p_off[nt], nb);
     }
   }
-  big_issue<MTW, NTW, WM, KG, SA>(g + C::kAhead, steps, ring, src, wr, wave);
-  __builtin_amdgcn_sched_barrier(0);  // the loads go out before this step's compute
-
-  const uint4* at = ring.a[ST];
+  big_issue<MT, ST ^ 1>(g + 1, steps, ring, src, wr, wave);
+  big_mfmas<T, MT, 1>(f, acc);  // the previous step's last k-slice
+  {
+    // LDS reads first, then each deferred MFMA followed by a share of the
+    // loads and of slice 0's dequant.
+    constexpr int kVmem = 2 * kBigKG + BigCfg<MT>::kA + (S % 2 == 0 ? 4 : 0);
+    constexpr int kVmemPer = (kVmem + kMfma - 1) / kMfma;
+    constexpr int kValuPer = (2 * 17 + 8 + kMfma - 1) / kMfma;
 #pragma unroll
-  for (int q = 0; q < KG; ++q) {
-    u32x4_t wraw[NTW];
+    for (int i = 0; i < MT; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
 #pragma unroll
-    for (int nt = 0; nt < NTW; ++nt) wraw[nt] = wr[ST][nt][q];
-    float s24[NTW], s20[NTW], bb[NTW];
-#pragma unroll
-    for (int nt = 0; nt < NTW; ++nt) {
-      const float sv = Elem<T>::param((typename Elem<T>::S)param_at(sblk[SLOT][nt], J0 + q));
-      s24[nt] = sv * 0x1p24f;
-      s20[nt] = sv * 0x1p20f;
-      bb[nt] = Elem<T>::param((typename Elem<T>::S)param_at(bblk[SLOT][nt], J0 + q));
-    }
-    // Activation chunk of group q, k-slice kk: 8 q + 4 h + kk (8 chunks per
-    // group and row, rows of 8 KG chunks).
-    u32x4_t afrag[2][MTW];
-    u32x4_t bfrag[2][NTW];
-#pragma unroll
-    for (int mt = 0; mt < MTW; ++mt)
-      afrag[0][mt] = __builtin_bit_cast(u32x4_t, at[a_slot_kg<KG>(arow0 + mt * 32 + r32, 8 * q + 4 * h)]);
-#pragma unroll
-    for (int nt = 0; nt < NTW; ++nt) {
-      uint32_t p[4];
-      Elem<T>::dequant(wraw[nt].x, s24[nt], s20[nt], bb[nt], p);
-      bfrag[0][nt] = u32x4_t{p[0], p[1], p[2], p[3]};
-    }
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int cb = kk & 1;
-      __builtin_amdgcn_sched_barrier(0);
-      if (kk < 3) {
-#pragma unroll
-        for (int mt = 0; mt < MTW; ++mt)
-          afrag[cb ^ 1][mt] = __builtin_bit_cast(
-              u32x4_t, at[a_slot_kg<KG>(arow0 + mt * 32 + r32, 8 * q + 4 * h + kk + 1)]);
-#pragma unroll
-        for (int nt = 0; nt < NTW; ++nt) {
-          const uint32_t word = (kk == 0) ? wraw[nt].y : (kk == 1) ? wraw[nt].z : wraw[nt].w;
-          uint32_t p[4];
-          Elem<T>::dequant(word, s24[nt], s20[nt], bb[nt], p);
-          bfrag[cb ^ 1][nt] = u32x4_t{p[0], p[1], p[2], p[3]};
-        }
-      }
-#pragma unroll
-      for (int mt = 0; mt < MTW; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NTW; ++nt)
-          acc[mt][nt] = mfma32<T>(afrag[cb][mt], bfrag[cb][nt], acc[mt][nt]);
-      if (kk < 3) {
-        // Interleave: every MFMA of this k-slice is followed by a share of the
-        // next slice's dequant VALU work and, for the first MTW, one LDS read,
-        // so a single wave keeps the matrix core fed while it dequantizes.
-        constexpr int kMfma = MTW * NTW;
-        constexpr int kValuPer = (NTW * 17 + kMfma - 1) / kMfma;
-#pragma unroll
-        for (int i = 0; i < kMfma; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          if (i < MTW) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-          __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);  // VALU
-        }
-      }
+    for (int i = 0; i < kMfma; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, kVmemPer, 0);   // VMEM read
+      __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);   // VALU
     }
   }
+
+#pragma unroll
+  for (int t = 0; t + 1 < kBigSlices; ++t) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (((t + 1) & 3) == 0) gp = group_params<T>(sblk[SLOT], bblk[SLOT], J0 + ((t + 1) >> 2));
+    if (t & 1) {
+      big_operands<T, MT, 0>(t + 1, at, wr[ST], gp, f, arow0, r32, h);
+      big_mfmas<T, MT, 1>(f, acc);
+    } else {
+      big_operands<T, MT, 1>(t + 1, at, wr[ST], gp, f, arow0, r32, h);
+      big_mfmas<T, MT, 0>(f, acc);
+    }
+    // Every MFMA of this k-slice is followed by a share of the next slice's
+    // dequant VALU work and, for the first MT, one LDS read, so a single wave
+    // keeps the matrix core fed while it dequantizes.
+    constexpr int kValuPer = (2 * 17 + kMfma - 1) / kMfma;
+#pragma unroll
+    for (int i = 0; i < kMfma; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // MFMA
+      if (i < MT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // DS read
+      __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);          // VALU
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // EP is the output stage (epilogue.hpp).  With EP::kPair (SwiGLU) the
 // workgroup's 256 weight rows are 128 gate rows and the 128 matching up rows:
 // a wave's column tile 0 holds gate rows, tile 1 the up rows of the same 32
 // output columns, so each lane has both accumulators of an output.
-template <int T, int MTW, int NTW, int WM, int KG, class EP>
+template <int T, int MT, class EP>
 __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, const EP ep,
     int M, int N, int K, int tiles_m, int tiles_n) {
-  static_assert(!EP::kPair || NTW == 2, "paired epilogue needs two column tiles per wave");
-  using C = BigCfg<MTW, NTW, WM, KG>;
-  constexpr int A_SLOTS = C::kBM * 8 * KG;
-  __shared__ uint4 a_st0[A_SLOTS], a_st1[A_SLOTS], a_st2[C::kStages > 2 ? A_SLOTS : 1],
-      a_st3[C::kStages > 2 ? A_SLOTS : 1];
-  const BigRing ring = {{a_st0, a_st1, a_st2, a_st3}};
+  using C = BigCfg<MT>;
+  __shared__ uint4 a_st0[C::kSlots], a_st1[C::kSlots];
+  const BigRing ring = {{a_st0, a_st1}};
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / C::kWN;
-  const int wn = wave - wm * C::kWN;
   const int r32 = lane & 31;
   const int h = lane >> 5;
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * C::kBM;
   const int n0 = tn * kBigBN;
-  const int arow0 = wm * 32 * MTW;        // this wave's first row inside the tile
-  const int ncol0 = n0 + wn * 32 * NTW;   // this wave's first output column
-  const int pcol0 = tn * (kBigBN / 2) + wn * 32;  // paired epilogue: first output column
+  const int arow0 = 0;                      // every wave covers all rows of the tile
+  const int ncol0 = n0 + wave * 64;         // this wave's first output column
+  const int pcol0 = tn * (kBigBN / 2) + wave * 32;  // paired epilogue: first output column
   const int gpr = K >> 6;
-  const int steps = gpr / KG;
+  const int steps = gpr / kBigKG;
 
-  BigSrc<MTW, NTW, WM, KG> src;
+  BigSrc<MT> src;
   src.xr = make_rsrc(x, (uint32_t)((size_t)M * K * 2));
   src.wr = make_rsrc(w, (uint32_t)((size_t)N * K / 2));
   src.sr = make_rsrc(scales, (uint32_t)((size_t)N * gpr * 2));
   src.br = make_rsrc(biases, (uint32_t)((size_t)N * gpr * 2));
-  // Activation slot s = i*256 + tid holds tile row s / (8 KG), physical chunk
-  // s % (8 KG), i.e. logical chunk a_slot_kg's inverse of that row.  Rows past
-  // M are clamped.
+  // Activation slot s = i*256 + tid holds tile row s / 16, physical chunk
+  // s % 16, i.e. logical chunk a_slot_kg's inverse of that row.  Rows past M
+  // are clamped.
 #pragma unroll
   for (int i = 0; i < C::kA; ++i) {
     const int slot = i * kThreads + tid;
-    const int row = slot / (8 * KG);
-    const int c = a_chunk_kg<KG>(row, slot % (8 * KG));
+    const int row = slot / (8 * kBigKG);
+    const int c = a_chunk_kg<kBigKG>(row, slot % (8 * kBigKG));
     const uint32_t gr = (uint32_t)min(m0 + row, M - 1);
     src.a_off[i] = (gr * (uint32_t)K + (uint32_t)c * 8u) * 2u;
   }
   // In MFMA operand layout lane (r32, h) of column tile nt owns weight row
   // ncol0 + 32 nt + r32 and bytes [16 h, 16 h + 16) of each group.
 #pragma unroll
-  for (int nt = 0; nt < NTW; ++nt) {
+  for (int nt = 0; nt < 2; ++nt) {
     int wrow = ncol0 + nt * 32 + r32;
     if constexpr (EP::kPair) wrow = (nt == 0 ? ep.gate_row : ep.up_row) + min(pcol0 + r32, ep.width - 1);
     const int gr = min(wrow, N - 1);
@@ -509,51 +524,43 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     src.p_off[nt] = (uint32_t)gr * (uint32_t)gpr * 2u;
   }
 
-  f32x16_t acc[MTW][NTW];
+  f32x16_t acc[MT][2];
 #pragma unroll
-  for (int mt = 0; mt < MTW; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < NTW; ++nt)
+    for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.f;
 
-  // Prologue: the scale block of the first steps, then weights and activations
-  // of the first kAhead steps in the loop's per-step order.
-  uint2 sblk[2][NTW], bblk[2][NTW];
-  u32x4_t wr[C::kStages][NTW][KG];
+  // Prologue: the first scale block, the loads of step 0, and zero operands
+  // for the first step's deferred MFMAs (they add nothing).
+  uint2 sblk[2][2], bblk[2][2];
+  u32x4_t wr[2][2][kBigKG];
 #pragma unroll
-  for (int nt = 0; nt < NTW; ++nt) {
+  for (int nt = 0; nt < 2; ++nt) {
     sblk[0][nt] = load_param_block(src.sr, src.p_off[nt], 0u);
     bblk[0][nt] = load_param_block(src.br, src.p_off[nt], 0u);
   }
-  big_issue<MTW, NTW, WM, KG, 0>(0, steps, ring, src, wr, wave);
-  if constexpr (C::kAhead == 2) big_issue<MTW, NTW, WM, KG, 1>(1, steps, ring, src, wr, wave);
+  big_issue<MT, 0>(0, steps, ring, src, wr, wave);
+  BigFrags<MT> f;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) f.a[1][mt] = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) f.b[1][nt] = u32x4_t{0u, 0u, 0u, 0u};
 
-  // steps * KG is a multiple of 4: full unrolls, then possibly one block.
+  // steps is even (K % 256 == 0): full unrolls, then possibly one block.
   int g = 0;
-  for (; g + C::kUnroll <= steps; g += C::kUnroll) {
-    big_step<T, MTW, NTW, WM, KG, 0>(g, steps, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
-    big_step<T, MTW, NTW, WM, KG, 1>(g + 1, steps, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
-    if constexpr (C::kUnroll > 2) {
-      big_step<T, MTW, NTW, WM, KG, 2>(g + 2, steps, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
-      big_step<T, MTW, NTW, WM, KG, 3>(g + 3, steps, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
-    }
-    if constexpr (C::kUnroll > 4) {
-      big_step<T, MTW, NTW, WM, KG, 4>(g + 4, steps, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
-      big_step<T, MTW, NTW, WM, KG, 5>(g + 5, steps, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
-      big_step<T, MTW, NTW, WM, KG, 6>(g + 6, steps, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
-      big_step<T, MTW, NTW, WM, KG, 7>(g + 7, steps, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
-    }
+  for (; g + kBigUnroll <= steps; g += kBigUnroll) {
+    big_step<T, MT, 0>(g, steps, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, 1>(g + 1, steps, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, 2>(g + 2, steps, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, 3>(g + 3, steps, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
   }
   if (g < steps) {
-    big_step<T, MTW, NTW, WM, KG, 0>(g, steps, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
-    if constexpr (C::kSpb > 1)
-      big_step<T, MTW, NTW, WM, KG, 1>(g + 1, steps, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
-    if constexpr (C::kSpb > 2) {
-      big_step<T, MTW, NTW, WM, KG, 2>(g + 2, steps, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
-      big_step<T, MTW, NTW, WM, KG, 3>(g + 3, steps, ring, src, sblk, bblk, wr, acc, wave, arow0, r32, h);
-    }
+    big_step<T, MT, 0>(g, steps, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, 1>(g + 1, steps, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
   }
+  big_mfmas<T, MT, 1>(f, acc);  // the last step's last k-slice
   IMQ_WAIT_VMCNT(0);  // drain the clamped tail loads before the workgroup ends
 
   // Accumulator r of a 32x32 tile holds row 8*(r/4) + 4*h + r%4, column r32.
@@ -561,7 +568,7 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     const int j = pcol0 + r32;
     if (j < ep.width) {
 #pragma unroll
-      for (int mt = 0; mt < MTW; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int row = m0 + arow0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -570,9 +577,9 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     }
   } else {
 #pragma unroll
-    for (int mt = 0; mt < MTW; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-      for (int nt = 0; nt < NTW; ++nt) {
+      for (int nt = 0; nt < 2; ++nt) {
         const int col = ncol0 + nt * 32 + r32;
         if (col >= N) continue;
 #pragma unroll
@@ -585,17 +592,17 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   }
 }
 
-template <int T, int MTW, int NTW, int WM, int KG, class EP>
+template <int T, int MT, class EP>
 hipError_t launch_big(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                       const uint16_t* x, const EP& ep, int k, int n, int m, hipStream_t stream) {
-  constexpr int BM = BigCfg<MTW, NTW, WM, KG>::kBM;
+  constexpr int BM = BigCfg<MT>::kBM;
   const int tiles_m = (m + BM - 1) / BM;
   int cols = n;  // weight rows the workgroups cover
   if constexpr (EP::kPair) cols = 2 * ep.width;
   const int tiles_n = (cols + kBigBN - 1) / kBigBN;
   const dim3 grid((unsigned)tiles_m * (unsigned)tiles_n);
-  hipLaunchKernelGGL((qgemm_big_kernel<T, MTW, NTW, WM, KG, EP>), grid, dim3(kThreads), 0, stream,
-                     w, scales, biases, x, ep, m, n, k, tiles_m, tiles_n);
+  hipLaunchKernelGGL((qgemm_big_kernel<T, MT, EP>), grid, dim3(kThreads), 0, stream, w, scales,
+                     biases, x, ep, m, n, k, tiles_m, tiles_n);
   return hipGetLastError();
 }
 
@@ -649,9 +656,9 @@ hipError_t launch_big_ep(const uint32_t* w, const uint16_t* scales, const uint16
   int cols = n;
   if constexpr (EP::kPair) cols = 2 * ep.width;
   switch (pick_big_mt(m, cols, device_cus())) {
-    case 4: return launch_big<T, 4, 2, 1, 2>(w, scales, biases, x, ep, k, n, m, stream);
-    case 6: return launch_big<T, 6, 2, 1, 2>(w, scales, biases, x, ep, k, n, m, stream);
-    default: return launch_big<T, 8, 2, 1, 2>(w, scales, biases, x, ep, k, n, m, stream);
+    case 4: return launch_big<T, 4>(w, scales, biases, x, ep, k, n, m, stream);
+    case 6: return launch_big<T, 6>(w, scales, biases, x, ep, k, n, m, stream);
+    default: return launch_big<T, 8>(w, scales, biases, x, ep, k, n, m, stream);
   }
 }
 
