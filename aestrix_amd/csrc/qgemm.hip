@@ -347,22 +347,35 @@ __device__ __forceinline__ GroupParams group_params(const uint2 (&sblk)[2], cons
   return p;
 }
 
-// Issue the weight and activation loads of step gl (clamped into range) into
-// ring stage ST: weights to registers, activations to LDS.
+// The loads of a step are spread over kIssuePts points of the previous step
+// (its top and its first k-slices): a burst of some twenty 1 KiB loads per
+// wave at one point stalls the wave's issue behind the memory pipeline.
+constexpr int kIssuePts = 7;
+template <int MT>
+__device__ __forceinline__ constexpr int a_split(int p) {
+  return p * BigCfg<MT>::kA / kIssuePts;
+}
+
+// Weight loads of step gs into register set ST.
 template <int MT, int ST>
-__device__ __forceinline__ void big_issue(int gl, int steps, const BigRing& ring,
-                                          const BigSrc<MT>& src, u32x4_t (&wr)[2][2][kBigKG],
-                                          int wave) {
-  const uint32_t gs = (uint32_t)min(gl, steps - 1);
+__device__ __forceinline__ void big_issue_w(uint32_t gs, const BigSrc<MT>& src,
+                                            u32x4_t (&wr)[2][2][kBigKG]) {
 #pragma unroll
   for (int q = 0; q < kBigKG; ++q)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)
       wr[ST][nt][q] = load_b128(src.wr, src.w_off[nt], (gs * kBigKG + q) * 32u);
+}
+
+// Activation loads [a_split(p), a_split(p + 1)) of step gs into stage ST.
+template <int MT, int ST>
+__device__ __forceinline__ void big_issue_a(int p, uint32_t gs, const BigRing& ring,
+                                            const BigSrc<MT>& src, int wave) {
   uint4* ab = ring.a[ST] + wave * 64;
 #pragma unroll
   for (int i = 0; i < BigCfg<MT>::kA; ++i)
-    load_lds16(src.xr, src.a_off[i], gs * (128u * kBigKG), ab + i * kThreads);
+    if (i >= a_split<MT>(p) && i < a_split<MT>(p + 1))
+      load_lds16(src.xr, src.a_off[i], gs * (128u * kBigKG), ab + i * kThreads);
 }
 
 // LDS reads and weight dequant of k-slice t of a step into buffer B.  In
@@ -426,12 +439,14 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
       bblk[SLOT ^ 1][nt] = load_param_block(src.br, src.p_off[nt], nb);
     }
   }
-  big_issue<MT, ST ^ 1>(g + 1, steps, ring, src, wr, wave);
+  const uint32_t gs1 = (uint32_t)min(g + 1, steps - 1);
+  big_issue_w<MT, ST ^ 1>(gs1, src, wr);
+  big_issue_a<MT, ST ^ 1>(0, gs1, ring, src, wave);
   big_mfmas<T, MT, 1>(f, acc);  // the previous step's last k-slice
   {
     // LDS reads first, then each deferred MFMA followed by a share of the
     // loads and of slice 0's dequant.
-    constexpr int kVmem = 2 * kBigKG + BigCfg<MT>::kA + (S % 2 == 0 ? 4 : 0);
+    constexpr int kVmem = 2 * kBigKG + a_split<MT>(1) + (S % 2 == 0 ? 4 : 0);
     constexpr int kVmemPer = (kVmem + kMfma - 1) / kMfma;
     constexpr int kValuPer = (2 * 17 + 8 + kMfma - 1) / kMfma;
 #pragma unroll
@@ -448,6 +463,7 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
   for (int t = 0; t + 1 < kBigSlices; ++t) {
     __builtin_amdgcn_sched_barrier(0);
     if (((t + 1) & 3) == 0) gp = group_params<T>(sblk[SLOT], bblk[SLOT], J0 + ((t + 1) >> 2));
+    if (t + 1 < kIssuePts) big_issue_a<MT, ST ^ 1>(t + 1, gs1, ring, src, wave);
     if (t & 1) {
       big_operands<T, MT, 0>(t + 1, at, wr[ST], gp, f, arow0, r32, h);
       big_mfmas<T, MT, 1>(f, acc);
@@ -456,13 +472,16 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
       big_mfmas<T, MT, 0>(f, acc);
     }
     // Every MFMA of this k-slice is followed by a share of the next slice's
-    // dequant VALU work and, for the first MT, one LDS read, so a single wave
-    // keeps the matrix core fed while it dequantizes.
+    // dequant VALU work, for the first MT one LDS read, and for the first few
+    // one of the next step's activation loads, so a single wave keeps the
+    // matrix core fed while it dequantizes.
     constexpr int kValuPer = (2 * 17 + kMfma - 1) / kMfma;
+    const int n_dma = t + 1 < kIssuePts ? a_split<MT>(t + 2) - a_split<MT>(t + 1) : 0;
 #pragma unroll
     for (int i = 0; i < kMfma; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // MFMA
       if (i < MT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // DS read
+      if (i < n_dma) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
       __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);          // VALU
     }
   }
@@ -541,7 +560,9 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     sblk[0][nt] = load_param_block(src.sr, src.p_off[nt], 0u);
     bblk[0][nt] = load_param_block(src.br, src.p_off[nt], 0u);
   }
-  big_issue<MT, 0>(0, steps, ring, src, wr, wave);
+  big_issue_w<MT, 0>(0u, src, wr);
+#pragma unroll
+  for (int p = 0; p < kIssuePts; ++p) big_issue_a<MT, 0>(p, 0u, ring, src, wave);
   BigFrags<MT> f;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) f.a[1][mt] = u32x4_t{0u, 0u, 0u, 0u};
