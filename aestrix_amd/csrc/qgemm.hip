@@ -634,7 +634,7 @@ int pick_big_mt(int m, int n, int cus) {
   const int tiles_n = (n + kBigBN - 1) / kBigBN;
   int best = 8;
   double best_cost = 1e30;
-  for (int mt : {8, 6, 4}) {
+  for (int mt : {8, 7, 6, 4}) {
     const long tiles = (long)((m + 32 * mt - 1) / (32 * mt)) * tiles_n;
     const long rounds = (tiles + cus - 1) / cus;
     const double cost = (double)rounds * (mt + 1.5);
@@ -679,6 +679,7 @@ hipError_t launch_big_ep(const uint32_t* w, const uint16_t* scales, const uint16
   switch (pick_big_mt(m, cols, device_cus())) {
     case 4: return launch_big<T, 4>(w, scales, biases, x, ep, k, n, m, stream);
     case 6: return launch_big<T, 6>(w, scales, biases, x, ep, k, n, m, stream);
+    case 7: return launch_big<T, 7>(w, scales, biases, x, ep, k, n, m, stream);
     default: return launch_big<T, 8>(w, scales, biases, x, ep, k, n, m, stream);
   }
 }
