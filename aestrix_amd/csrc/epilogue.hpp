@@ -1,15 +1,22 @@
 // epilogue.hpp -- output stages of the quantized matmul kernels.
 //
-// Each functor receives the fp32 accumulator of output (row, col) and writes
-// it out.  The fused ones replace the reference's glue kernels that run right
-// after a qmm on its f16 output (Sources/ImarelloDirect/DirectDiTKernels.swift):
-// they first round the accumulator to T, as the qmm's store would, and then
-// apply the glue arithmetic in fp32, so the result equals qmm + glue kernel.
+// Each functor turns the fp32 accumulator of output (row, col) into its T
+// value and writes outputs out.  The fused ones replace the reference's glue
+// kernels that run right after a qmm on its f16 output
+// (Sources/ImarelloDirect/DirectDiTKernels.swift): they first round the
+// accumulator to T, as the qmm's store would, and then apply the glue
+// arithmetic in fp32, so the result equals qmm + glue kernel.
 #pragma once
 
 #include "imq_device.hpp"
 
 namespace imq {
+
+// Interface.  The large-M kernel first stages each output's T-rounded value
+// (stage, or stage2 for a gate/up pair) in LDS, then writes the staged tile
+// out row by row: emit8 for 8 consecutive outputs starting at a multiple of 8
+// when `vec` (set by the host: every pointer and row pitch the functor
+// touches allows 16-byte accesses there), emit1 for single outputs otherwise.
 
 // y[row][col] = T(acc): the plain qmm output (row pitch ldy).
 template <int T>
@@ -17,8 +24,13 @@ struct EpStore {
   static constexpr bool kPair = false;
   typename Elem<T>::S* y;
   int ldy;
-  __device__ __forceinline__ void store(int row, int col, float acc) const {
-    y[(size_t)row * ldy + col] = Elem<T>::out(acc);
+  bool vec;
+  __device__ __forceinline__ uint16_t stage(float acc) const { return Elem<T>::out(acc); }
+  __device__ __forceinline__ void emit1(int row, int col, uint16_t v) const {
+    y[(size_t)row * ldy + col] = v;
+  }
+  __device__ __forceinline__ void emit8(int row, int col, uint4 v) const {
+    *reinterpret_cast<uint4*>(y + (size_t)row * ldy + col) = v;
   }
 };
 
@@ -26,6 +38,13 @@ __device__ __forceinline__ float round_to(float v, int t) {
   if (t == kBf16) return bf16_to_f32(f32_to_bf16_int(v));
   if (t == kF16) return (float)(_Float16)v;
   return v;
+}
+
+// The float value of a staged T.
+template <int T>
+__device__ __forceinline__ float staged_value(uint32_t bits) {
+  if constexpr (T == kBf16) return __builtin_bit_cast(float, bits << 16);
+  else return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
 }
 
 // y[row][col] = float(T(acc)) * scale, fp32 out: dd_cast_postscale
@@ -36,8 +55,22 @@ struct EpPostscale {
   float* y;
   int ldy;
   float scale;
-  __device__ __forceinline__ void store(int row, int col, float acc) const {
-    y[(size_t)row * ldy + col] = round_to(acc, T) * scale;
+  bool vec;
+  __device__ __forceinline__ uint16_t stage(float acc) const { return Elem<T>::out(acc); }
+  __device__ __forceinline__ void emit1(int row, int col, uint16_t v) const {
+    y[(size_t)row * ldy + col] = staged_value<T>(v) * scale;
+  }
+  __device__ __forceinline__ void emit8(int row, int col, uint4 v) const {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[2 * e] = staged_value<T>(w[e] & 0xFFFFu) * scale;
+      o[2 * e + 1] = staged_value<T>(w[e] >> 16) * scale;
+    }
+    float4* d = reinterpret_cast<float4*>(y + (size_t)row * ldy + col);
+    d[0] = make_float4(o[0], o[1], o[2], o[3]);
+    d[1] = make_float4(o[4], o[5], o[6], o[7]);
   }
 };
 
@@ -51,9 +84,29 @@ struct EpGateAdd {
   const float* gate;
   int ld;
   float scale;
-  __device__ __forceinline__ void store(int row, int col, float acc) const {
+  bool vec;
+  __device__ __forceinline__ uint16_t stage(float acc) const { return Elem<T>::out(acc); }
+  __device__ __forceinline__ void emit1(int row, int col, uint16_t v) const {
     const size_t i = (size_t)row * ld + col;
-    y[i] = __builtin_fmaf(gate[col], round_to(acc, T) * scale, x[i]);
+    y[i] = __builtin_fmaf(gate[col], staged_value<T>(v) * scale, x[i]);
+  }
+  __device__ __forceinline__ void emit8(int row, int col, uint4 v) const {
+    const size_t i = (size_t)row * ld + col;
+    const float4* xs = reinterpret_cast<const float4*>(x + i);
+    const float4* gs = reinterpret_cast<const float4*>(gate + col);
+    const float4 x0 = xs[0], x1 = xs[1], g0 = gs[0], g1 = gs[1];
+    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t bits = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xFFFFu);
+      o[e] = __builtin_fmaf(gv[e], staged_value<T>(bits) * scale, xv[e]);
+    }
+    float4* d = reinterpret_cast<float4*>(y + i);
+    d[0] = make_float4(o[0], o[1], o[2], o[3]);
+    d[1] = make_float4(o[4], o[5], o[6], o[7]);
   }
 };
 
@@ -71,11 +124,18 @@ struct EpSwiGLU {
   int up_row;
   float in_scale;
   float out_scale;
-  __device__ __forceinline__ void store2(int row, int j, float acc_g, float acc_u) const {
+  bool vec;
+  __device__ __forceinline__ uint16_t stage2(float acc_g, float acc_u) const {
     const float g = round_to(acc_g, T) * in_scale;
     const float u = round_to(acc_u, T) * in_scale;
     const float sig = 1.0f / (1.0f + __expf(-g));
-    y[(size_t)row * ldy + j] = Elem<T>::out(g * sig * u * out_scale);
+    return Elem<T>::out(g * sig * u * out_scale);
+  }
+  __device__ __forceinline__ void emit1(int row, int j, uint16_t v) const {
+    y[(size_t)row * ldy + j] = v;
+  }
+  __device__ __forceinline__ void emit8(int row, int j, uint4 v) const {
+    *reinterpret_cast<uint4*>(y + (size_t)row * ldy + j) = v;
   }
 };
 

@@ -488,6 +488,70 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Output tile staging.  Row r of the tile's kCW T values (kCW = 256 outputs,
+// 128 for a gate/up pair) sits in ring stage r / (kBM / 2) at row r % (kBM / 2)
+// of kCW * 2 bytes, its 16-byte chunk c at slot c ^ (4 * ((r / 4) % 2)): a
+// wave's 2-byte writes (rows r and r + 4 in its two lane halves) then hit
+// disjoint banks.
+template <class EP>
+constexpr int tile_cols() {
+  return EP::kPair ? kBigBN / 2 : kBigBN;
+}
+
+template <int MT, class EP>
+__device__ __forceinline__ uint16_t* staged_at(const BigRing& ring, int row, int col) {
+  constexpr int kHalf = BigCfg<MT>::kBM / 2;
+  constexpr int kCW = tile_cols<EP>();
+  const int chunk = (col >> 3) ^ (((row >> 2) & 1) << 2);
+  uint16_t* base = reinterpret_cast<uint16_t*>(row < kHalf ? ring.a[0] : ring.a[1]);
+  return base + (row % kHalf) * kCW + chunk * 8 + (col & 7);
+}
+
+// Accumulator r of a 32x32 tile holds row 8*(r/4) + 4*h + r%4, column r32.
+template <int T, int MT, class EP>
+__device__ __forceinline__ void big_stage_tile(const EP& ep, const f32x16_t (&acc)[MT][2],
+                                               const BigRing& ring, int wave, int r32, int h) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+      if constexpr (EP::kPair) {
+        *staged_at<MT, EP>(ring, row, wave * 32 + r32) = ep.stage2(acc[mt][0][r], acc[mt][1][r]);
+      } else {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          *staged_at<MT, EP>(ring, row, wave * 64 + nt * 32 + r32) = ep.stage(acc[mt][nt][r]);
+      }
+    }
+}
+
+// Write the staged tile to output rows m0.., columns col0.. (< ncols).
+template <int MT, class EP>
+__device__ __forceinline__ void big_write_tile(const EP& ep, const BigRing& ring, int tid, int m0,
+                                               int col0, int M, int ncols) {
+  constexpr int kCPR = tile_cols<EP>() / 8;  // 16-byte chunks per row
+  constexpr int kIters = BigCfg<MT>::kBM * kCPR / kThreads;
+#pragma unroll
+  for (int i = 0; i < kIters; ++i) {
+    const int q = i * kThreads + tid;
+    const int row = q / kCPR;
+    const int c = q % kCPR;
+    const int grow = m0 + row;
+    const int col = col0 + c * 8;
+    if (grow >= M || col >= ncols) continue;
+    const uint4 v = *reinterpret_cast<const uint4*>(staged_at<MT, EP>(ring, row, c * 8));
+    if (ep.vec && col + 8 <= ncols) {
+      ep.emit8(grow, col, v);
+    } else {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (col + e < ncols) ep.emit1(grow, col + e, (uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+    }
+  }
+}
+
 // EP is the output stage (epilogue.hpp).  With EP::kPair (SwiGLU) the
 // workgroup's 256 weight rows are 128 gate rows and the 128 matching up rows:
 // a wave's column tile 0 holds gate rows, tile 1 the up rows of the same 32
@@ -582,35 +646,22 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     big_step<T, MT, 1>(g + 1, steps, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
   }
   big_mfmas<T, MT, 1>(f, acc);  // the last step's last k-slice
-  IMQ_WAIT_VMCNT(0);  // drain the clamped tail loads before the workgroup ends
 
-  // Accumulator r of a 32x32 tile holds row 8*(r/4) + 4*h + r%4, column r32.
-  if constexpr (EP::kPair) {
-    const int j = pcol0 + r32;
-    if (j < ep.width) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + arow0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (row < M) ep.store2(row, j, acc[mt][0][r], acc[mt][1][r]);
-        }
-    }
-  } else {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int col = ncol0 + nt * 32 + r32;
-        if (col >= N) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + arow0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (row < M) ep.store(row, col, acc[mt][nt][r]);
-        }
-      }
-    }
-  }
+  // Output: the tile's T values are staged in the LDS ring, then written out
+  // row by row, 16 bytes per lane.  Written straight from the MFMA layout, a
+  // lane holds one column of 16 rows per 32x32 tile: 2-byte stores, 14 of
+  // them per 32 output bytes per wave, and every CU issues them at the same
+  // moment of each tile round; that cost about 10% of the kernel.  The ring is
+  // free once every wave is past this barrier (its LDS reads returned, the
+  // clamped tail loads landed).
+  IMQ_WAIT_VM_LGKM_0();
+  __builtin_amdgcn_s_barrier();
+  big_stage_tile<T, MT>(ep, acc, ring, wave, r32, h);
+  __syncthreads();
+  if constexpr (EP::kPair)
+    big_write_tile<MT>(ep, ring, tid, m0, tn * (kBigBN / 2), M, ep.width);
+  else
+    big_write_tile<MT>(ep, ring, tid, m0, n0, M, N);
 }
 
 template <int T, int MT, class EP>
@@ -657,6 +708,9 @@ hipError_t launch_tile(const uint32_t* w, const uint16_t* scales, const uint16_t
   return hipGetLastError();
 }
 
+// 16-byte alignment of an output or residual pointer (vector output stores).
+bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
 int device_cus() {
   static const int cus = [] {
     int dev = 0, v = 0;
@@ -688,7 +742,7 @@ template <int T>
 hipError_t launch_t(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                     const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
   if (!qgemm_big_supported(k, n, m)) return launch_tile<T, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
-  return launch_big_ep<T>(w, scales, biases, x, EpStore<T>{y, n}, k, n, m, stream);
+  return launch_big_ep<T>(w, scales, biases, x, EpStore<T>{y, n, al16(y) && n % 8 == 0}, k, n, m, stream);
 }
 
 }  // namespace
@@ -719,9 +773,12 @@ hipError_t launch_qgemm_postscale(const uint32_t* w, const void* scales, const v
   const auto* s = static_cast<const uint16_t*>(scales);
   const auto* b = static_cast<const uint16_t*>(biases);
   const auto* xx = static_cast<const uint16_t*>(x);
+  const bool vec = al16(y) && n % 4 == 0;
   switch (dtype) {
-    case kBf16: return launch_big_ep<kBf16>(w, s, b, xx, EpPostscale<kBf16>{y, n, scale}, k, n, m, stream);
-    case kF16: return launch_big_ep<kF16>(w, s, b, xx, EpPostscale<kF16>{y, n, scale}, k, n, m, stream);
+    case kBf16:
+      return launch_big_ep<kBf16>(w, s, b, xx, EpPostscale<kBf16>{y, n, scale, vec}, k, n, m, stream);
+    case kF16:
+      return launch_big_ep<kF16>(w, s, b, xx, EpPostscale<kF16>{y, n, scale, vec}, k, n, m, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -732,13 +789,14 @@ hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const vo
   const auto* s = static_cast<const uint16_t*>(scales);
   const auto* b = static_cast<const uint16_t*>(biases);
   const auto* xx = static_cast<const uint16_t*>(x);
+  const bool vec = al16(y) && al16(residual) && al16(gate) && n % 4 == 0;
   switch (dtype) {
     case kBf16:
-      return launch_big_ep<kBf16>(w, s, b, xx, EpGateAdd<kBf16>{y, residual, gate, n, scale}, k, n, m,
-                                  stream);
+      return launch_big_ep<kBf16>(w, s, b, xx, EpGateAdd<kBf16>{y, residual, gate, n, scale, vec},
+                                  k, n, m, stream);
     case kF16:
-      return launch_big_ep<kF16>(w, s, b, xx, EpGateAdd<kF16>{y, residual, gate, n, scale}, k, n, m,
-                                 stream);
+      return launch_big_ep<kF16>(w, s, b, xx, EpGateAdd<kF16>{y, residual, gate, n, scale, vec}, k,
+                                 n, m, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -751,15 +809,18 @@ hipError_t launch_qgemm_swiglu(const uint32_t* w, const void* scales, const void
   const auto* b = static_cast<const uint16_t*>(biases);
   const auto* xx = static_cast<const uint16_t*>(x);
   auto* yy = static_cast<uint16_t*>(y);
+  const bool vec = al16(y) && ldy % 8 == 0;
   switch (dtype) {
     case kBf16:
       return launch_big_ep<kBf16>(
-          w, s, b, xx, EpSwiGLU<kBf16>{yy, ldy, width, gate_row, up_row, in_scale, out_scale}, k, n,
-          m, stream);
+          w, s, b, xx,
+          EpSwiGLU<kBf16>{yy, ldy, width, gate_row, up_row, in_scale, out_scale, vec}, k, n, m,
+          stream);
     case kF16:
       return launch_big_ep<kF16>(
-          w, s, b, xx, EpSwiGLU<kF16>{yy, ldy, width, gate_row, up_row, in_scale, out_scale}, k, n,
-          m, stream);
+          w, s, b, xx,
+          EpSwiGLU<kF16>{yy, ldy, width, gate_row, up_row, in_scale, out_scale, vec}, k, n, m,
+          stream);
     default: return hipErrorInvalidValue;
   }
 }
