@@ -12,11 +12,12 @@
 
 namespace imq {
 
-// Interface.  The large-M kernel first stages each output's T-rounded value
-// (stage, or stage2 for a gate/up pair) in LDS, then writes the staged tile
-// out row by row: emit8 for 8 consecutive outputs starting at a multiple of 8
-// when `vec` (set by the host: every pointer and row pitch the functor
-// touches allows 16-byte accesses there), emit1 for single outputs otherwise.
+// Interface.  The large-M kernel stages each output in LDS as the T rounding
+// (Elem<T>::pack2, two rows at a time) of value(acc) -- value2(acc_g, acc_u)
+// for a gate/up pair -- then writes the staged tile out row by row: emit8 for
+// 8 consecutive outputs starting at a multiple of 8 when `vec` (set by the
+// host: every pointer and row pitch the functor touches allows 16-byte
+// accesses there), emit1 for single outputs otherwise.
 
 // y[row][col] = T(acc): the plain qmm output (row pitch ldy).
 template <int T>
@@ -25,7 +26,7 @@ struct EpStore {
   typename Elem<T>::S* y;
   int ldy;
   bool vec;
-  __device__ __forceinline__ uint16_t stage(float acc) const { return Elem<T>::out(acc); }
+  __device__ __forceinline__ float value(float acc) const { return acc; }
   __device__ __forceinline__ void emit1(int row, int col, uint16_t v) const {
     y[(size_t)row * ldy + col] = v;
   }
@@ -56,7 +57,7 @@ struct EpPostscale {
   int ldy;
   float scale;
   bool vec;
-  __device__ __forceinline__ uint16_t stage(float acc) const { return Elem<T>::out(acc); }
+  __device__ __forceinline__ float value(float acc) const { return acc; }
   __device__ __forceinline__ void emit1(int row, int col, uint16_t v) const {
     y[(size_t)row * ldy + col] = staged_value<T>(v) * scale;
   }
@@ -85,7 +86,7 @@ struct EpGateAdd {
   int ld;
   float scale;
   bool vec;
-  __device__ __forceinline__ uint16_t stage(float acc) const { return Elem<T>::out(acc); }
+  __device__ __forceinline__ float value(float acc) const { return acc; }
   __device__ __forceinline__ void emit1(int row, int col, uint16_t v) const {
     const size_t i = (size_t)row * ld + col;
     y[i] = __builtin_fmaf(gate[col], staged_value<T>(v) * scale, x[i]);
@@ -125,11 +126,11 @@ struct EpSwiGLU {
   float in_scale;
   float out_scale;
   bool vec;
-  __device__ __forceinline__ uint16_t stage2(float acc_g, float acc_u) const {
+  __device__ __forceinline__ float value2(float acc_g, float acc_u) const {
     const float g = round_to(acc_g, T) * in_scale;
     const float u = round_to(acc_u, T) * in_scale;
     const float sig = 1.0f / (1.0f + __expf(-g));
-    return Elem<T>::out(g * sig * u * out_scale);
+    return g * sig * u * out_scale;
   }
   __device__ __forceinline__ void emit1(int row, int j, uint16_t v) const {
     y[(size_t)row * ldy + j] = v;

@@ -127,6 +127,7 @@ struct Elem<kBf16> {
   static constexpr int kBytes = 2;
   static __device__ __forceinline__ float param(S v) { return bf16_to_f32(v); }
   static __device__ __forceinline__ S out(float v) { return (S)f32_to_bf16_int(v); }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return pack_bf16x2(lo, hi); }
   static __device__ __forceinline__ void dequant(uint32_t word, float s24, float s20, float b,
                                                  uint32_t o[4]) {
     dequant_word_bf16(word, s24, s20, b, o);
@@ -141,6 +142,7 @@ struct Elem<kF16> {
     return (float)__builtin_bit_cast(_Float16, v);
   }
   static __device__ __forceinline__ S out(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return pack_f16x2(lo, hi); }
   static __device__ __forceinline__ void dequant(uint32_t word, float s24, float s20, float b,
                                                  uint32_t o[4]) {
     dequant_word_f16(word, s24, s20, b, o);

@@ -507,44 +507,64 @@ __device__ __forceinline__ uint16_t* staged_at(const BigRing& ring, int row, int
   return base + (row % kHalf) * kCW + chunk * 8 + (col & 7);
 }
 
-// Accumulator r of a 32x32 tile holds row 8*(r/4) + 4*h + r%4, column r32.
+// Accumulator r of a 32x32 tile holds row 8*(r/4) + 4*h + r%4, column r32:
+// registers r and r+1 are rows one apart in the same column, rounded to T as a
+// pair.
 template <int T, int MT, class EP>
 __device__ __forceinline__ void big_stage_tile(const EP& ep, const f32x16_t (&acc)[MT][2],
                                                const BigRing& ring, int wave, int r32, int h) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
+    for (int r = 0; r < 16; r += 2) {
       const int row = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
       if constexpr (EP::kPair) {
-        *staged_at<MT, EP>(ring, row, wave * 32 + r32) = ep.stage2(acc[mt][0][r], acc[mt][1][r]);
+        const int col = wave * 32 + r32;
+        const uint32_t v = Elem<T>::pack2(ep.value2(acc[mt][0][r], acc[mt][1][r]),
+                                          ep.value2(acc[mt][0][r + 1], acc[mt][1][r + 1]));
+        *staged_at<MT, EP>(ring, row, col) = (uint16_t)v;
+        *staged_at<MT, EP>(ring, row + 1, col) = (uint16_t)(v >> 16);
       } else {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-          *staged_at<MT, EP>(ring, row, wave * 64 + nt * 32 + r32) = ep.stage(acc[mt][nt][r]);
+        for (int nt = 0; nt < 2; ++nt) {
+          const int col = wave * 64 + nt * 32 + r32;
+          const uint32_t v =
+              Elem<T>::pack2(ep.value(acc[mt][nt][r]), ep.value(acc[mt][nt][r + 1]));
+          *staged_at<MT, EP>(ring, row, col) = (uint16_t)v;
+          *staged_at<MT, EP>(ring, row + 1, col) = (uint16_t)(v >> 16);
+        }
       }
     }
 }
 
-// Write the staged tile to output rows m0.., columns col0.. (< ncols).
+// Write the staged tile to output rows m0.., columns col0.. (< ncols): all of
+// a thread's LDS reads first, so their latencies overlap, then the stores.
 template <int MT, class EP>
 __device__ __forceinline__ void big_write_tile(const EP& ep, const BigRing& ring, int tid, int m0,
                                                int col0, int M, int ncols) {
   constexpr int kCPR = tile_cols<EP>() / 8;  // 16-byte chunks per row
   constexpr int kIters = BigCfg<MT>::kBM * kCPR / kThreads;
+  uint4 v[kIters];
 #pragma unroll
   for (int i = 0; i < kIters; ++i) {
     const int q = i * kThreads + tid;
-    const int row = q / kCPR;
-    const int c = q % kCPR;
-    const int grow = m0 + row;
-    const int col = col0 + c * 8;
-    if (grow >= M || col >= ncols) continue;
-    const uint4 v = *reinterpret_cast<const uint4*>(staged_at<MT, EP>(ring, row, c * 8));
-    if (ep.vec && col + 8 <= ncols) {
-      ep.emit8(grow, col, v);
-    } else {
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    v[i] = *reinterpret_cast<const uint4*>(staged_at<MT, EP>(ring, q / kCPR, (q % kCPR) * 8));
+  }
+  const int c = tid % kCPR;
+  const int col = col0 + c * 8;
+  if (col >= ncols) return;
+  if (ep.vec && col + 8 <= ncols) {
+#pragma unroll
+    for (int i = 0; i < kIters; ++i) {
+      const int grow = m0 + (i * kThreads + tid) / kCPR;
+      if (grow < M) ep.emit8(grow, col, v[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kIters; ++i) {
+      const int grow = m0 + (i * kThreads + tid) / kCPR;
+      if (grow >= M) continue;
+      const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         if (col + e < ncols) ep.emit1(grow, col + e, (uint16_t)(w[e >> 1] >> (16 * (e & 1))));
