@@ -118,7 +118,10 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
       load_lds16(xr, off, 0u, xs + base + wave * 64);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // 2. weight chunks and their scales/biases.
+    // 2. weight chunks and their scales/biases, chunk by chunk: loads retire
+    //    in issue order, so chunk u's dot products then wait for chunk u's
+    //    loads only (grouping all weight loads first made the first chunk
+    //    wait for every weight load of the tile).
     u32x4_t q[R][U];
     typename E::S sv[R][U], bv[R][U];
 #pragma unroll
@@ -126,12 +129,12 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
       const int c = c0 + min(gl + u * G, tch - 1);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        q[r][u] = __builtin_nontemporal_load(wrow[r] + c);
         sv[r][u] = srow[r][c >> 1];
         bv[r][u] = brow[r][c >> 1];
+        q[r][u] = __builtin_nontemporal_load(wrow[r] + c);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
     // 3. x visible; the weight loads may still be in flight.
     IMQ_WAIT_VMCNT(3 * U * R);
     __builtin_amdgcn_s_barrier();
