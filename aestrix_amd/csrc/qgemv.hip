@@ -62,6 +62,22 @@ struct XTile {
   static __device__ __forceinline__ int swz(int j) { return (j >> kSh) & (kP - 1); }
 };
 
+// One scale or bias of T at byte offset voff + soff.
+template <int T>
+__device__ __forceinline__ typename Elem<T>::S load_param(__amdgpu_buffer_rsrc_t rs, uint32_t voff,
+                                                          uint32_t soff) {
+  if constexpr (T == kF32)
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff, 0));
+  else
+    return __builtin_amdgcn_raw_buffer_load_b16(rs, voff, soff, 0);
+}
+
+// 16 weight bytes, streamed (non-temporal: bit 1 of the cache policy).
+__device__ __forceinline__ u32x4_t load_b128_nt(__amdgpu_buffer_rsrc_t rs, uint32_t voff,
+                                               uint32_t soff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 2));
+}
+
 template <int T, int MR, int G, int U, int R>
 __global__ __launch_bounds__(kThreads) void qgemv_kernel(
     const uint32_t* __restrict__ w, const typename Elem<T>::S* __restrict__ scales,
@@ -78,16 +94,20 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
   const int gl = lane & (G - 1);
   const int row0 = (blockIdx.x * kWaves + wave) * RPW + (lane / G) * R;
   const int gpr = K >> 6;
+  if constexpr (MR == 1) M = 1;  // lets the compiler drop the row arithmetic of x
 
-  const u32x4_t* wrow[R];
-  const typename E::S* srow[R];
-  const typename E::S* brow[R];
+  // Weights, scales and biases through buffer resources: one 32-bit byte
+  // offset per row, the chunk offset added per load (the host keeps every
+  // operand under 2 GiB).
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(w, (uint32_t)((size_t)N * K / 2));
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(scales, (uint32_t)((size_t)N * gpr * E::kBytes));
+  const __amdgpu_buffer_rsrc_t br = make_rsrc(biases, (uint32_t)((size_t)N * gpr * E::kBytes));
+  uint32_t woff[R], poff[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const size_t rr = (size_t)min(row0 + r, N - 1);
-    wrow[r] = reinterpret_cast<const u32x4_t*>(w + rr * (K >> 3));
-    srow[r] = scales + rr * gpr;
-    brow[r] = biases + rr * gpr;
+    const uint32_t rr = (uint32_t)min(row0 + r, N - 1);
+    woff[r] = rr * (uint32_t)(K / 2);
+    poff[r] = rr * (uint32_t)gpr * E::kBytes;
   }
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)((size_t)M * K * E::kBytes));
 
@@ -110,7 +130,7 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
     //    duplicate into the padding.
     for (int base = 0; base < xtotal; base += kThreads) {
       const int sl = min(base + tid, xtotal - 1);
-      const int m = sl / vpr;
+      const int m = (MR == 1) ? 0 : sl / vpr;
       const int idx = sl - m * vpr;
       const int j = idx / P;
       const int pc = (idx & (P - 1)) ^ X::swz(j);
@@ -126,12 +146,12 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
     typename E::S sv[R][U], bv[R][U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int c = c0 + min(gl + u * G, tch - 1);
+      const uint32_t c = (uint32_t)min(gl + u * G, tch - 1);  // chunk within the tile
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        sv[r][u] = srow[r][c >> 1];
-        bv[r][u] = brow[r][c >> 1];
-        q[r][u] = __builtin_nontemporal_load(wrow[r] + c);
+        sv[r][u] = load_param<T>(sr, poff[r] + (c >> 1) * E::kBytes, (uint32_t)(c0 >> 1) * E::kBytes);
+        bv[r][u] = load_param<T>(br, poff[r] + (c >> 1) * E::kBytes, (uint32_t)(c0 >> 1) * E::kBytes);
+        q[r][u] = load_b128_nt(wr, woff[r] + c * 16u, (uint32_t)c0 * 16u);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
