@@ -22,6 +22,8 @@ imq_ctx::~imq_ctx() {
     if (staging_done[i]) (void)hipEventDestroy(staging_done[i]);
     if (staging[i]) (void)hipHostFree(staging[i]);
   }
+  for (auto& kv : split_ws)
+    if (kv.second.first) (void)hipFree(kv.second.first);
 }
 
 namespace imq {
@@ -92,6 +94,37 @@ int check_qmm(imq_ctx* ctx, const char* fn, const uint32_t* w, const void* s, co
 
 enum class Regime { kAuto, kGemv, kGemm };
 
+// The split-K workspace of stream st, at least `need` bytes; empty (run
+// unsplit) when it would have to grow during stream capture or the
+// allocation fails.  Growing waits for the stream's earlier work, which may
+// still use the old buffer.
+imq::SplitWs split_ws(imq_ctx* ctx, hipStream_t st, size_t need) {
+  if (need == 0) return {};
+  std::lock_guard<std::mutex> lk(ctx->ws_mu);
+  auto& e = ctx->split_ws[st];
+  if (e.second >= need) return {static_cast<float*>(e.first), e.second};
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return {};
+  }
+  if (e.first) {
+    if (hipStreamSynchronize(st) != hipSuccess) {
+      (void)hipGetLastError();
+      return {};
+    }
+    (void)hipFree(e.first);
+    e = {nullptr, 0};
+  }
+  void* p = nullptr;
+  if (hipMalloc(&p, need) != hipSuccess) {
+    (void)hipGetLastError();
+    return {};
+  }
+  e = {p, need};
+  return {static_cast<float*>(p), need};
+}
+
 int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, const void* s,
             const void* b, const void* x, void* y, int k, int n, int m, int group_size, int bits,
             imq_dtype dtype, imq_stream stream) {
@@ -112,7 +145,12 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
   auto st = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
   if (!gemv) {
-    e = imq::launch_qgemm(w, s, b, x, y, k, n, m, (int)dtype, st);
+    // The dispatcher may split K over a workspace; imq_qgemm is the plain
+    // tile kernel (the fused output stages equal it bit for bit).
+    const imq::SplitWs ws = regime == Regime::kAuto
+                                ? split_ws(ctx, st, imq::qgemm_split_bytes(k, n, m))
+                                : imq::SplitWs{};
+    e = imq::launch_qgemm(w, s, b, x, y, k, n, m, (int)dtype, st, ws);
   } else {
     // f32 beyond 16 rows (the conditioner's multi-row calls): blocks of 16 rows.
     const auto* xb = static_cast<const char*>(x);

@@ -6,6 +6,7 @@
 
 #include <mutex>
 #include <string>
+#include <unordered_map>
 
 #include "imq.h"
 
@@ -22,6 +23,11 @@ struct imq_ctx {
   void* staging[kStagingBuffers] = {};
   hipEvent_t staging_done[kStagingBuffers] = {};
   int staging_next = 0;
+  // Split-K workspaces of the qGEMM, one per stream: calls on one stream run
+  // in order, so they never overlap on a workspace.  Grown (never shrunk) on
+  // demand outside stream capture.
+  std::mutex ws_mu;
+  std::unordered_map<hipStream_t, std::pair<void*, size_t>> split_ws;
 
   ~imq_ctx();
 };

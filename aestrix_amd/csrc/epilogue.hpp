@@ -23,6 +23,7 @@ namespace imq {
 template <int T>
 struct EpStore {
   static constexpr bool kPair = false;
+  static constexpr bool kPartial = false;
   typename Elem<T>::S* y;
   int ldy;
   bool vec;
@@ -53,6 +54,7 @@ __device__ __forceinline__ float staged_value(uint32_t bits) {
 template <int T>
 struct EpPostscale {
   static constexpr bool kPair = false;
+  static constexpr bool kPartial = false;
   float* y;
   int ldy;
   float scale;
@@ -80,6 +82,7 @@ struct EpPostscale {
 template <int T>
 struct EpGateAdd {
   static constexpr bool kPair = false;
+  static constexpr bool kPartial = false;
   float* y;
   const float* x;
   const float* gate;
@@ -118,6 +121,7 @@ struct EpGateAdd {
 template <int T>
 struct EpSwiGLU {
   static constexpr bool kPair = true;
+  static constexpr bool kPartial = false;
   typename Elem<T>::S* y;
   int ldy;
   int width;
@@ -138,6 +142,15 @@ struct EpSwiGLU {
   __device__ __forceinline__ void emit8(int row, int j, uint4 v) const {
     *reinterpret_cast<uint4*>(y + (size_t)row * ldy + j) = v;
   }
+};
+
+// Split-K partial sums: the fp32 accumulators themselves, unrounded, into
+// ws[split][row][col] (row pitch N); a second kernel adds the splits and
+// rounds to T.
+struct EpPartial {
+  static constexpr bool kPair = false;
+  static constexpr bool kPartial = true;
+  float* ws;
 };
 
 }  // namespace imq

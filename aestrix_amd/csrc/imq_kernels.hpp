@@ -17,9 +17,21 @@ hipError_t launch_dequant(const uint32_t* w, const void* scales, const void* bia
 hipError_t launch_qgemv(const uint32_t* w, const void* scales, const void* biases, const void* x,
                         void* y, int k, int n, int m, int dtype, hipStream_t stream);
 
+// fp32 scratch for split-K partial sums.  With too few output tiles to fill
+// the chip, the MFMA kernel splits K, writes each split's partial sums here
+// and a second kernel adds them; a null or short workspace runs unsplit.
+struct SplitWs {
+  float* p = nullptr;
+  size_t bytes = 0;
+};
+
 // y[m][n] = x . deq(W)^T, any m >= 1, T in {bf16, f16}; MFMA.
 hipError_t launch_qgemm(const uint32_t* w, const void* scales, const void* biases, const void* x,
-                        void* y, int k, int n, int m, int dtype, hipStream_t stream);
+                        void* y, int k, int n, int m, int dtype, hipStream_t stream,
+                        SplitWs ws = {});
+
+// Workspace bytes launch_qgemm uses for this shape (0: it does not split K).
+size_t qgemm_split_bytes(int k, int n, int m);
 
 // Whether the buffer-load MFMA kernel (and so the fused epilogues) takes
 // these shapes: K % 256 == 0 and x, w addressable with 32-bit byte offsets.

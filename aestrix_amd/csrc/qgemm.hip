@@ -580,7 +580,7 @@ template <int T, int MT, class EP>
 __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, const EP ep,
-    int M, int N, int K, int tiles_m, int tiles_n) {
+    int M, int N, int K, int tiles_m, int tiles_n, int split_steps) {
   using C = BigCfg<MT>;
   __shared__ uint4 a_st0[C::kSlots], a_st1[C::kSlots];
   const BigRing ring = {{a_st0, a_st1}};
@@ -598,7 +598,10 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   const int ncol0 = n0 + wave * 64;         // this wave's first output column
   const int pcol0 = tn * (kBigBN / 2) + wave * 32;  // paired epilogue: first output column
   const int gpr = K >> 6;
-  const int steps = gpr / kBigKG;
+  // K-steps [g0, g1) of split blockIdx.y (splits of `split_steps` steps, an
+  // even number: whole scale blocks).
+  const int g0 = (int)blockIdx.y * split_steps;
+  const int g1 = min(g0 + split_steps, gpr / kBigKG);
 
   BigSrc<MT> src;
   src.xr = make_rsrc(x, (uint32_t)((size_t)M * K * 2));
@@ -641,32 +644,52 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   u32x4_t wr[2][2][kBigKG];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    sblk[0][nt] = load_param_block(src.sr, src.p_off[nt], 0u);
-    bblk[0][nt] = load_param_block(src.br, src.p_off[nt], 0u);
+    sblk[0][nt] = load_param_block(src.sr, src.p_off[nt], (uint32_t)(g0 * kBigKG / 4));
+    bblk[0][nt] = load_param_block(src.br, src.p_off[nt], (uint32_t)(g0 * kBigKG / 4));
   }
-  big_issue_w<MT, 0>(0u, src, wr);
+  big_issue_w<MT, 0>((uint32_t)g0, src, wr);
 #pragma unroll
-  for (int p = 0; p < kIssuePts; ++p) big_issue_a<MT, 0>(p, 0u, ring, src, wave);
+  for (int p = 0; p < kIssuePts; ++p) big_issue_a<MT, 0>(p, (uint32_t)g0, ring, src, wave);
   BigFrags<MT> f;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) f.a[1][mt] = u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) f.b[1][nt] = u32x4_t{0u, 0u, 0u, 0u};
 
-  // steps is even (K % 256 == 0): full unrolls, then possibly one block.
-  int g = 0;
-  for (; g + kBigUnroll <= steps; g += kBigUnroll) {
-    big_step<T, MT, 0>(g, steps, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
-    big_step<T, MT, 1>(g + 1, steps, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
-    big_step<T, MT, 2>(g + 2, steps, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
-    big_step<T, MT, 3>(g + 3, steps, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+  // g1 - g0 is even: full unrolls, then possibly one block.  The ring stage
+  // and scale slot count from g0 (a block start); loads past g1 are clamped
+  // to g1 - 1.
+  int g = g0;
+  for (; g + kBigUnroll <= g1; g += kBigUnroll) {
+    big_step<T, MT, 0>(g, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, 1>(g + 1, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, 2>(g + 2, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, 3>(g + 3, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
   }
-  if (g < steps) {
-    big_step<T, MT, 0>(g, steps, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
-    big_step<T, MT, 1>(g + 1, steps, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+  if (g < g1) {
+    big_step<T, MT, 0>(g, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, 1>(g + 1, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
   }
   big_mfmas<T, MT, 1>(f, acc);  // the last step's last k-slice
 
+  if constexpr (EP::kPartial) {
+    // Split-K partial sums: fp32 straight from the MFMA layout into split
+    // blockIdx.y's [M][N] slice of the workspace.
+    IMQ_WAIT_VMCNT(0);  // drain the clamped tail loads before the workgroup ends
+    float* part = ep.ws + (size_t)blockIdx.y * M * N;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int col = ncol0 + nt * 32 + r32;
+        if (col >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (row < M) part[(size_t)row * N + col] = acc[mt][nt][r];
+        }
+      }
+  } else {
   // Output: the tile's T values are staged in the LDS ring, then written out
   // row by row, 16 bytes per lane.  Written straight from the MFMA layout, a
   // lane holds one column of 16 rows per 32x32 tile: 2-byte stores, 14 of
@@ -682,36 +705,84 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     big_write_tile<MT>(ep, ring, tid, m0, tn * (kBigBN / 2), M, ep.width);
   else
     big_write_tile<MT>(ep, ring, tid, m0, n0, M, N);
+  }
 }
 
 template <int T, int MT, class EP>
 hipError_t launch_big(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
-                      const uint16_t* x, const EP& ep, int k, int n, int m, hipStream_t stream) {
+                      const uint16_t* x, const EP& ep, int k, int n, int m, hipStream_t stream,
+                      int splits = 1, int split_steps = 0) {
   constexpr int BM = BigCfg<MT>::kBM;
   const int tiles_m = (m + BM - 1) / BM;
   int cols = n;  // weight rows the workgroups cover
   if constexpr (EP::kPair) cols = 2 * ep.width;
   const int tiles_n = (cols + kBigBN - 1) / kBigBN;
-  const dim3 grid((unsigned)tiles_m * (unsigned)tiles_n);
+  if (splits <= 1) split_steps = k / (64 * kBigKG);
+  const dim3 grid((unsigned)tiles_m * (unsigned)tiles_n, (unsigned)splits);
   hipLaunchKernelGGL((qgemm_big_kernel<T, MT, EP>), grid, dim3(kThreads), 0, stream, w, scales,
-                     biases, x, ep, m, n, k, tiles_m, tiles_n);
+                     biases, x, ep, m, n, k, tiles_m, tiles_n, split_steps);
   return hipGetLastError();
 }
 
-// Tile height for the large-M kernel: fewest estimated tile-rounds over the
-// chip, each round costing about (MT + 1.5) units (MFMA work plus per-tile
-// dequant, prologue and epilogue).
-int pick_big_mt(int m, int n, int cus) {
+// y[i] = T(sum over s of ws[s][i]), i < mn, the splits added in order.  Four
+// outputs per thread; vec: mn % 4 == 0 and y 8-byte aligned.
+template <int T>
+__global__ __launch_bounds__(256) void reduce_splits_kernel(const float* __restrict__ ws,
+                                                            int splits, long mn, bool vec,
+                                                            uint16_t* __restrict__ y) {
+  const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= mn) return;
+  if (vec) {
+    float4 a = *reinterpret_cast<const float4*>(ws + i);
+    for (int sp = 1; sp < splits; ++sp) {
+      const float4 b = *reinterpret_cast<const float4*>(ws + sp * mn + i);
+      a.x += b.x;
+      a.y += b.y;
+      a.z += b.z;
+      a.w += b.w;
+    }
+    *reinterpret_cast<uint2*>(y + i) = make_uint2(Elem<T>::pack2(a.x, a.y), Elem<T>::pack2(a.z, a.w));
+  } else {
+    for (long j = i; j < i + 4 && j < mn; ++j) {
+      float a = ws[j];
+      for (int sp = 1; sp < splits; ++sp) a += ws[sp * mn + j];
+      y[j] = (uint16_t)Elem<T>::pack2(a, 0.f);
+    }
+  }
+}
+
+// Tile height and K split of the large-M kernel (small: 32- and 64-row tiles
+// allowed, which only the plain output stage and the split-K partial sums are
+// built for; split: K may be split).  Cost in units of about
+// 0.36 us (a K-step of a 32-row slice of the tile): a round of tiles costs
+// split_steps * (MT + 1.5) plus 12 for its prologue and output; a split adds
+// the workspace traffic of its reduction (8 bytes per output and split, at
+// about 1.4 MB per unit) plus 3 for the extra launch.  Splits are taken only
+// when the tiles leave CUs idle.
+struct BigPlan {
+  int mt, splits, split_steps;
+};
+
+BigPlan pick_big_plan(int m, int n, int k, int cus, bool small, bool split) {
   const int tiles_n = (n + kBigBN - 1) / kBigBN;
-  int best = 8;
+  const int steps = k / (64 * kBigKG);
+  BigPlan best{8, 1, steps};
   double best_cost = 1e30;
-  for (int mt : {8, 7, 6, 4}) {
+  for (int mt : {8, 7, 6, 4, 2, 1}) {
+    if (!small && mt < 4) continue;
     const long tiles = (long)((m + 32 * mt - 1) / (32 * mt)) * tiles_n;
-    const long rounds = (tiles + cus - 1) / cus;
-    const double cost = (double)rounds * (mt + 1.5);
-    if (cost < best_cost - 1e-9) {
-      best_cost = cost;
-      best = mt;
+    const int max_splits = split && tiles < cus ? std::max(1, steps / 2) : 1;
+    for (int sp = 1; sp <= max_splits; ++sp) {
+      const int sps = ((steps + sp - 1) / sp + 1) / 2 * 2;  // even
+      const int eff = (steps + sps - 1) / sps;
+      if (eff != sp) continue;
+      const long rounds = (tiles * eff + cus - 1) / cus;
+      double cost = (double)rounds * (sps * (mt + 1.5) + 12.0);
+      if (eff > 1) cost += (double)eff * m * n * 8.0 / 1.4e6 + 3.0;
+      if (cost < best_cost - 1e-9) {
+        best_cost = cost;
+        best = BigPlan{mt, eff, sps};
+      }
     }
   }
   return best;
@@ -750,7 +821,7 @@ hipError_t launch_big_ep(const uint32_t* w, const uint16_t* scales, const uint16
                          const uint16_t* x, const EP& ep, int k, int n, int m, hipStream_t stream) {
   int cols = n;
   if constexpr (EP::kPair) cols = 2 * ep.width;
-  switch (pick_big_mt(m, cols, device_cus())) {
+  switch (pick_big_plan(m, cols, k, device_cus(), false, false).mt) {
     case 4: return launch_big<T, 4>(w, scales, biases, x, ep, k, n, m, stream);
     case 6: return launch_big<T, 6>(w, scales, biases, x, ep, k, n, m, stream);
     case 7: return launch_big<T, 7>(w, scales, biases, x, ep, k, n, m, stream);
@@ -760,9 +831,40 @@ hipError_t launch_big_ep(const uint32_t* w, const uint16_t* scales, const uint16
 
 template <int T>
 hipError_t launch_t(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
-                    const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
+                    const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream,
+                    SplitWs ws) {
   if (!qgemm_big_supported(k, n, m)) return launch_tile<T, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
-  return launch_big_ep<T>(w, scales, biases, x, EpStore<T>{y, n, al16(y) && n % 8 == 0}, k, n, m, stream);
+  BigPlan p = pick_big_plan(m, n, k, device_cus(), true, true);
+  const size_t need = (size_t)p.splits * m * n * sizeof(float);
+  if (p.splits > 1 && (ws.p == nullptr || ws.bytes < need))
+    p = pick_big_plan(m, n, k, device_cus(), true, false);  // no room for the partial sums
+  if (p.splits > 1) {
+    const EpPartial ep{ws.p};
+    hipError_t e;
+    switch (p.mt) {
+      case 1: e = launch_big<T, 1>(w, scales, biases, x, ep, k, n, m, stream, p.splits, p.split_steps); break;
+      case 2: e = launch_big<T, 2>(w, scales, biases, x, ep, k, n, m, stream, p.splits, p.split_steps); break;
+      case 4: e = launch_big<T, 4>(w, scales, biases, x, ep, k, n, m, stream, p.splits, p.split_steps); break;
+      case 6: e = launch_big<T, 6>(w, scales, biases, x, ep, k, n, m, stream, p.splits, p.split_steps); break;
+      case 7: e = launch_big<T, 7>(w, scales, biases, x, ep, k, n, m, stream, p.splits, p.split_steps); break;
+      default: e = launch_big<T, 8>(w, scales, biases, x, ep, k, n, m, stream, p.splits, p.split_steps); break;
+    }
+    if (e != hipSuccess) return e;
+    const long mn = (long)m * n;
+    const bool vec = mn % 4 == 0 && ((uintptr_t)y & 7u) == 0;
+    const dim3 grid((unsigned)((mn + 1023) / 1024));
+    hipLaunchKernelGGL(reduce_splits_kernel<T>, grid, dim3(256), 0, stream, ws.p, p.splits, mn, vec, y);
+    return hipGetLastError();
+  }
+  const EpStore<T> ep{y, n, al16(y) && n % 8 == 0};
+  switch (p.mt) {
+    case 1: return launch_big<T, 1>(w, scales, biases, x, ep, k, n, m, stream);
+    case 2: return launch_big<T, 2>(w, scales, biases, x, ep, k, n, m, stream);
+    case 4: return launch_big<T, 4>(w, scales, biases, x, ep, k, n, m, stream);
+    case 6: return launch_big<T, 6>(w, scales, biases, x, ep, k, n, m, stream);
+    case 7: return launch_big<T, 7>(w, scales, biases, x, ep, k, n, m, stream);
+    default: return launch_big<T, 8>(w, scales, biases, x, ep, k, n, m, stream);
+  }
 }
 
 }  // namespace
@@ -775,16 +877,22 @@ bool qgemm_big_supported(int k, int n, int m) {
 }
 
 hipError_t launch_qgemm(const uint32_t* w, const void* scales, const void* biases, const void* x,
-                        void* y, int k, int n, int m, int dtype, hipStream_t stream) {
+                        void* y, int k, int n, int m, int dtype, hipStream_t stream, SplitWs ws) {
   const auto* s = static_cast<const uint16_t*>(scales);
   const auto* b = static_cast<const uint16_t*>(biases);
   const auto* xx = static_cast<const uint16_t*>(x);
   auto* yy = static_cast<uint16_t*>(y);
   switch (dtype) {
-    case kBf16: return launch_t<kBf16>(w, s, b, xx, yy, k, n, m, stream);
-    case kF16: return launch_t<kF16>(w, s, b, xx, yy, k, n, m, stream);
+    case kBf16: return launch_t<kBf16>(w, s, b, xx, yy, k, n, m, stream, ws);
+    case kF16: return launch_t<kF16>(w, s, b, xx, yy, k, n, m, stream, ws);
     default: return hipErrorInvalidValue;
   }
+}
+
+size_t qgemm_split_bytes(int k, int n, int m) {
+  if (!qgemm_big_supported(k, n, m)) return 0;
+  const BigPlan p = pick_big_plan(m, n, k, device_cus(), true, true);
+  return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
 }
 
 hipError_t launch_qgemm_postscale(const uint32_t* w, const void* scales, const void* biases,

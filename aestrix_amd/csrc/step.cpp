@@ -9,6 +9,7 @@
 // encoders per step, the step here is one graph launch.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -36,6 +37,7 @@ struct imq_dit_step {
   char* C = nullptr;        // T [J, dim + ff_inner]
   float* norm_w = nullptr;  // fp32 [dim]
   float* gates = nullptr;   // fp32 [4 n_double + n_single][dim]
+  imq::SplitWs split;       // partial sums of the projections that split K
   hipStream_t cap = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -73,9 +75,9 @@ hipError_t encode(imq_dit_step* st, hipStream_t s) {
     char* outs[3] = {st->Q, st->K, st->V};
     for (int q = 0; q < 3; ++q) {
       ok(imq::launch_qgemm(W[q].w, W[q].scales, W[q].biases, nXi, rows(outs[q], d.l_txt, dim), dim,
-                           dim, d.l_img, T, s));
+                           dim, d.l_img, T, s, st->split));
       ok(imq::launch_qgemm(W[3 + q].w, W[3 + q].scales, W[3 + q].biases, nXt, rows(outs[q], 0, dim),
-                           dim, dim, d.l_txt, T, s));
+                           dim, dim, d.l_txt, T, s, st->split));
     }
     // to_out / to_add_out on the V rows (the attention output's stand-in).
     ok(imq::launch_qgemm_gate_add(W[6].w, W[6].scales, W[6].biases, rows(st->V, d.l_txt, dim), Xi,
@@ -97,7 +99,8 @@ hipError_t encode(imq_dit_step* st, hipStream_t s) {
     const imq_qweight* W = &st->w[(size_t)12 * d.n_double + 2 * b];
     const float* g = st->gates + ((size_t)4 * d.n_double + b) * dim;
     ok(imq::launch_rmsnorm(st->X, st->norm_w, st->nX, J, dim, kEps, T, s));
-    ok(imq::launch_qgemm(W[0].w, W[0].scales, W[0].biases, st->nX, st->QKV, dim, 3 * dim, J, T, s));
+    ok(imq::launch_qgemm(W[0].w, W[0].scales, W[0].biases, st->nX, st->QKV, dim, 3 * dim, J, T, s,
+                         st->split));
     ok(imq::launch_qgemm_swiglu(W[0].w, W[0].scales, W[0].biases, st->nX, st->C + (size_t)dim * es,
                                 cw, dim, 3 * dim + 2 * ffi, J, ffi, 3 * dim, 3 * dim + ffi, 1.0f,
                                 1.0f, T, s));
@@ -182,9 +185,12 @@ int imq_dit_step_create(imq_ctx* ctx, const imq_dit_dims* dims, const imq_qweigh
                           J * 3 * d.dim * es,
                           J * (d.dim + d.ff_inner) * es,
                           (size_t)d.dim * 4,
-                          ((size_t)4 * d.n_double + d.n_single) * d.dim * 4};
-  size_t off[10], total = 0;
-  for (int i = 0; i < 10; ++i) {
+                          ((size_t)4 * d.n_double + d.n_single) * d.dim * 4,
+                          std::max({imq::qgemm_split_bytes(d.dim, d.dim, d.l_img),
+                                    imq::qgemm_split_bytes(d.dim, d.dim, d.l_txt),
+                                    imq::qgemm_split_bytes(d.dim, 3 * d.dim, (int)J)})};
+  size_t off[11], total = 0;
+  for (int i = 0; i < 11; ++i) {
     off[i] = total;
     total += align256(sizes[i]);
   }
@@ -208,6 +214,7 @@ int imq_dit_step_create(imq_ctx* ctx, const imq_dit_dims* dims, const imq_qweigh
   st->C = a + off[7];
   st->norm_w = reinterpret_cast<float*>(a + off[8]);
   st->gates = reinterpret_cast<float*>(a + off[9]);
+  st->split = imq::SplitWs{reinterpret_cast<float*>(a + off[10]), sizes[10]};
   // Zero everything (the attention half of C stays zero), ones for the
   // conditioning vectors.  Plain (uncaptured) memsets at set-up.
   e = hipMemset(st->arena, 0, total);

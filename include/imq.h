@@ -111,7 +111,13 @@ int imq_dequantize(imq_ctx* ctx, const uint32_t* w, const void* scales, const vo
  * (DirectConditioner.swift:96-117) and MLX quantizedMM(transpose: true)
  * (Sources/ImarelloDiT/AttentionUtils.swift:212-221).  M <= 16 runs the qGEMV
  * kernel, larger M the MFMA qGEMM kernel (f32: the qGEMV kernel, 16 rows at a
- * time). */
+ * time).  When the output tiles are too few to fill the GPU, the qGEMM splits
+ * K: fp32 partial sums go to a workspace the context keeps per stream (grown
+ * on first use, outside stream capture; under capture a call that would need
+ * a larger one runs unsplit) and a second kernel adds them in order, so the
+ * result is deterministic but its fp32 summation order differs from
+ * imq_qgemm's.  Calls that share a context must not run on the same stream
+ * concurrently with a graph replay of an earlier call on that stream. */
 int imq_qmm_t(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
               const void* x, void* y, int k, int n, int m, int group_size, int bits,
               imq_dtype dtype, imq_stream stream);
@@ -123,8 +129,9 @@ int imq_qgemv(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* b
               imq_dtype dtype, imq_stream stream);
 
 /* The dense regime alone (any M >= 1): dequant fused into bf16 / f16 MFMA
- * tiles, fp32 accumulators.  Same contract as imq_qmm_t; f32 returns
- * IMQ_EUNSUPPORTED. */
+ * tiles, fp32 accumulators, K never split (the fused output stages below
+ * equal it plus the glue bit for bit).  Same contract as imq_qmm_t; f32
+ * returns IMQ_EUNSUPPORTED. */
 int imq_qgemm(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
               const void* x, void* y, int k, int n, int m, int group_size, int bits,
               imq_dtype dtype, imq_stream stream);

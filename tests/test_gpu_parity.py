@@ -188,13 +188,48 @@ def test_one_hot_rows_reproduce_dequant_bit_exact(fn_name, m, k):
 
 
 def test_dispatcher_routes_by_m():
+    """M <= 16 is the qGEMV kernel bit for bit; above, the MFMA kernel, whose
+    K may be split by the dispatcher (another fp32 summation order)."""
     p = synth.make_problem(17, 384, 512, seed=16)
     x, w, s, b = synth.to_device(p)
-    for m in (16, 17):
-        note(f"dispatcher M={m}")
-        y = bits(imq.quantized_matmul(x[:m], w, s, b))
-        ref_kernel = imq.qgemv if m <= 16 else imq.qgemm
-        assert np.array_equal(y, bits(ref_kernel(x[:m], w, s, b)))
+    note("dispatcher M=16")
+    assert np.array_equal(bits(imq.quantized_matmul(x[:16], w, s, b)), bits(imq.qgemv(x[:16], w, s, b)))
+    note("dispatcher M=17")
+    y = bits(imq.quantized_matmul(x, w, s, b))
+    assert_close(y, cref.qmm_t(p.x, p.w, p.scales, p.biases), "dispatcher M=17")
+
+
+@pytest.mark.parametrize("m,n,k", [(17, 384, 512), (40, 1000, 2560), (96, 512, 4096),
+                                   (300, 512, 768), (512, 2560, 9728)])
+def test_split_k_dispatcher(m, n, k):
+    """Shapes with too few output tiles for the chip: the dispatcher splits K
+    (and takes 32- or 64-row tiles).  Oracle within tolerance, the same bits on
+    a second call (deterministic order), and one-hot rows are single weights
+    even when summed over splits."""
+    note(f"split-K dispatcher M={m} N={n} K={k}")
+    p = synth.make_problem(m, n, k, seed=21)
+    x, w, s, b = synth.to_device(p)
+    y1 = bits(imq.quantized_matmul(x, w, s, b))
+    y2 = bits(imq.quantized_matmul(x, w, s, b))
+    assert np.array_equal(y1, y2)
+    if m * n * k <= 512 * 2560 * 9728 // 8:
+        assert_close(y1, cref.qmm_t(p.x, p.w, p.scales, p.biases), "split-K")
+    rng = np.random.default_rng(22)
+    cols = rng.choice(k, size=m, replace=m > k)
+    xh = np.zeros((m, k), dtype=np.uint16)
+    xh[np.arange(m), cols] = 0x3F80
+    yo = bits(imq.quantized_matmul(to_dev_bf16(xh), w, s, b))
+    assert np.array_equal(yo, bits(imq.dequantize(w, s, b))[:, cols].T)
+
+
+def test_small_tiles_plain_qgemm():
+    """imq_qgemm at M <= 64 runs 32- and 64-row tiles (no split)."""
+    for m in (17, 33, 64):
+        note(f"qgemm small tiles M={m}")
+        p = synth.make_problem(m, 768, 1024, seed=23 + m)
+        x, w, s, b = synth.to_device(p)
+        assert_close(bits(imq.qgemm(x, w, s, b)), cref.qmm_t(p.x, p.w, p.scales, p.biases),
+                     f"qgemm M={m}")
 
 
 # ----------------------------------------------------------- host interface
