@@ -12,6 +12,8 @@ over that synthetic batch, inputs resident in HBM.  The same line carries:
 * dequant    -- the two projections of a DiT single-stream block, GB/s;
 * qgemm_shapes -- the other qGEMM shapes (PR1 1024x9216x3072, single-block
                 pair);
+* qmm_small_m -- text-encoder shapes at M = 32, 128, 512 through the regime
+                dispatcher (K split when the output tiles are too few);
 * dit_single_block -- one DiT single-stream block's projections at 1024^2
                 (f16): to_qkv_mlp_proj with the SwiGLU fused into its epilogue,
                 to_out with the gated residual add fused;
@@ -75,7 +77,9 @@ def time_events(fn, reps: int) -> float:
 
 
 def time_graph(launches, replays: int = 5) -> float:
-    """Average milliseconds per launch of a captured back-to-back sequence."""
+    """Average milliseconds per launch of a captured back-to-back sequence.
+    The warm-up and the capture share one stream, so a split-K workspace the
+    warm-up grew is the one the graph uses."""
     import torch
 
     side = torch.cuda.Stream()
@@ -86,7 +90,7 @@ def time_graph(launches, replays: int = 5) -> float:
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=side):
         for f in launches:
             f()
     g.replay()
@@ -148,17 +152,23 @@ def bench_dequant(imq, synth, torch, copies: int = 6) -> dict:
     return out
 
 
-def bench_qgemm_shape(imq, synth, torch, m, n, k, reps=10) -> dict:
+def bench_qgemm_shape(imq, synth, torch, m, n, k, reps=10, dispatcher=False) -> dict:
+    """One qGEMM shape: imq_qgemm (the tile kernel), or with dispatcher=True
+    imq_qmm_t (which may split K for shapes with few output tiles)."""
     p = synth.make_problem(m, n, k, seed=0)
     x, w, s, b = synth.to_device(p)
     y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    fn = imq.quantized_matmul if dispatcher else imq.qgemm
     # Warm up for about 60 ms of MFMA work (past the clock transient).
-    warm = max(2, int(60e-3 * 1e15 / (2.0 * m * n * k)))
+    warm = max(2, min(2000, int(60e-3 * 1e15 / (2.0 * m * n * k))))
     for _ in range(warm):
-        imq.qgemm(x, w, s, b, out=y)
-    ms = time_events(lambda: imq.qgemm(x, w, s, b, out=y), max(reps, 20))
+        fn(x, w, s, b, out=y)
+    if dispatcher:  # microseconds per call: a captured graph keeps host launches out
+        ms = time_graph([lambda: fn(x, w, s, b, out=y)] * 20)
+    else:
+        ms = time_events(lambda: fn(x, w, s, b, out=y), max(reps, 20))
     tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-    log(f"qgemm M={m} N={n} K={k}: {ms:.3f} ms  {tf:.1f} TFLOP/s")
+    log(f"{'qmm_t' if dispatcher else 'qgemm'} M={m} N={n} K={k}: {ms:.3f} ms  {tf:.1f} TFLOP/s")
     return {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / PEAK_BF16_TFLOPS, 4)}
 
 
@@ -417,6 +427,13 @@ def main() -> int:
             "M1024_N9216_K3072": bench_qgemm_shape(imq, synth, torch, 1024, 9216, 3072),
             "M4608_N27648_K3072": bench_qgemm_shape(imq, synth, torch, 4608, 27648, 3072),
             "M4608_N3072_K9216": bench_qgemm_shape(imq, synth, torch, 4608, 3072, 9216),
+        }
+        # Text-encoder prefill and splice rows through the dispatcher (K split
+        # when the output tiles are too few to fill the GPU).
+        extra["qmm_small_m"] = {
+            f"M{m}_N{n}_K{k}": bench_qgemm_shape(imq, synth, torch, m, n, k, dispatcher=True)
+            for (m, n, k) in ((32, 9728, 2560), (128, 9728, 2560), (512, 9728, 2560),
+                              (512, 2560, 9728), (512, 4096, 2560))
         }
         extra["dit_single_block"] = bench_dit_single_block(imq, torch)
         extra["dit_step"] = bench_dit_step(torch)
