@@ -141,7 +141,7 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
     return fail(ctx, IMQ_EINVAL, "%s: K=%d too long for the qGEMV kernel", fn, k);
   if ((rc = bind_device(ctx)) != IMQ_OK) return rc;
   const bool gemv = regime == Regime::kGemv ||
-                    (regime == Regime::kAuto && (m <= imq::kQgemvMaxM || dtype == IMQ_F32));
+                    (regime == Regime::kAuto && (m <= imq::kDispatchGemvMaxM || dtype == IMQ_F32));
   auto st = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
   if (!gemv) {

@@ -59,7 +59,12 @@ hipError_t launch_qgemm_swiglu(const uint32_t* w, const void* scales, const void
 hipError_t launch_rmsnorm(const float* x, const float* w, void* y, int rows, int cols, float eps,
                           int dtype, hipStream_t stream);
 
-// Largest M routed to the qGEMV kernel by the regime dispatcher.
+// Largest M the qGEMV kernel takes.
 constexpr int kQgemvMaxM = 16;
+// Largest bf16 / f16 M the regime dispatcher routes to the qGEMV kernel: from
+// M = 5 the MFMA kernel (K split when its tiles are few) is faster on the
+// text-encoder shapes (M = 8: 10.2 vs 14.1 us at [9728 x 2560]; M = 16: 10.8
+// vs 30.6 us), the qGEMV's VALU dequant and dot products growing with M.
+constexpr int kDispatchGemvMaxM = 4;
 
 }  // namespace imq

@@ -156,7 +156,7 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                      out: torch.Tensor | None = None) -> torch.Tensor:
     """y[..., N] = x[..., K] . deq(W)^T (MLX quantizedMM with transpose=true).
 
-    M <= 16 rows run the qGEMV kernel, larger M the MFMA qGEMM kernel, with K
+    M <= 4 rows run the qGEMV kernel, larger M the MFMA qGEMM kernel, with K
     split over a per-stream workspace when its output tiles are too few to
     fill the GPU (deterministic; another fp32 summation order than qgemm)."""
     if not transpose:

@@ -109,7 +109,7 @@ int imq_dequantize(imq_ctx* ctx, const uint32_t* w, const void* scales, const vo
  * DirectDiTStep.qmm (DirectDiTStep.swift:374-406), DirectTELayerSpike.encodeQmm
  * (DirectTELayer.swift:109-128), DirectConditioner.qmm
  * (DirectConditioner.swift:96-117) and MLX quantizedMM(transpose: true)
- * (Sources/ImarelloDiT/AttentionUtils.swift:212-221).  M <= 16 runs the qGEMV
+ * (Sources/ImarelloDiT/AttentionUtils.swift:212-221).  M <= 4 runs the qGEMV
  * kernel, larger M the MFMA qGEMM kernel (f32: the qGEMV kernel, 16 rows at a
  * time).  When the output tiles are too few to fill the GPU, the qGEMM splits
  * K: fp32 partial sums go to a workspace the context keeps per stream (grown

@@ -188,15 +188,18 @@ def test_one_hot_rows_reproduce_dequant_bit_exact(fn_name, m, k):
 
 
 def test_dispatcher_routes_by_m():
-    """M <= 16 is the qGEMV kernel bit for bit; above, the MFMA kernel, whose
+    """M <= 4 is the qGEMV kernel bit for bit; above, the MFMA kernel, whose
     K may be split by the dispatcher (another fp32 summation order)."""
     p = synth.make_problem(17, 384, 512, seed=16)
     x, w, s, b = synth.to_device(p)
-    note("dispatcher M=16")
-    assert np.array_equal(bits(imq.quantized_matmul(x[:16], w, s, b)), bits(imq.qgemv(x[:16], w, s, b)))
-    note("dispatcher M=17")
-    y = bits(imq.quantized_matmul(x, w, s, b))
-    assert_close(y, cref.qmm_t(p.x, p.w, p.scales, p.biases), "dispatcher M=17")
+    for m in (1, 4):
+        note(f"dispatcher M={m}")
+        assert np.array_equal(bits(imq.quantized_matmul(x[:m], w, s, b)),
+                              bits(imq.qgemv(x[:m], w, s, b)))
+    for m in (5, 16, 17):
+        note(f"dispatcher M={m}")
+        y = bits(imq.quantized_matmul(x[:m], w, s, b))
+        assert_close(y, cref.qmm_t(p.x[:m], p.w, p.scales, p.biases), f"dispatcher M={m}")
 
 
 @pytest.mark.parametrize("m,n,k", [(17, 384, 512), (40, 1000, 2560), (96, 512, 4096),
