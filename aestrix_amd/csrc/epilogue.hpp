@@ -145,12 +145,19 @@ struct EpSwiGLU {
 };
 
 // Split-K partial sums: the fp32 accumulators themselves, unrounded, into
-// ws[split][row][col] (row pitch N); a second kernel adds the splits and
-// rounds to T.
+// ws[split][row][...] (row pitch ldp); a second kernel adds the splits and
+// applies the real output stage.  Plain: column col at col (ldp = N).  PAIR
+// (a SwiGLU projection): output j's gate sum at j and its up sum at width + j
+// (ldp = 2 width), with gate_row, up_row and width as in EpSwiGLU.
+template <bool PAIR>
 struct EpPartial {
-  static constexpr bool kPair = false;
+  static constexpr bool kPair = PAIR;
   static constexpr bool kPartial = true;
   float* ws;
+  int ldp;
+  int width;
+  int gate_row;
+  int up_row;
 };
 
 }  // namespace imq

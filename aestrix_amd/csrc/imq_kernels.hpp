@@ -30,30 +30,35 @@ hipError_t launch_qgemm(const uint32_t* w, const void* scales, const void* biase
                         void* y, int k, int n, int m, int dtype, hipStream_t stream,
                         SplitWs ws = {});
 
-// Workspace bytes launch_qgemm uses for this shape (0: it does not split K).
-size_t qgemm_split_bytes(int k, int n, int m);
+// Workspace bytes launch_qgemm (fused: a fused stage over n weight rows, 2 *
+// width for swiglu) uses for this shape (0: it does not split K).
+size_t qgemm_split_bytes(int k, int n, int m, bool fused = false);
 
 // Whether the buffer-load MFMA kernel (and so the fused epilogues) takes
 // these shapes: K % 256 == 0 and x, w addressable with 32-bit byte offsets.
 bool qgemm_big_supported(int k, int n, int m);
 
 // Fused output stages on the MFMA kernel (T in {bf16, f16}; the shapes must
-// satisfy qgemm_big_supported).  They equal the qmm followed by the
-// reference's glue kernel on its T output:
+// satisfy qgemm_big_supported).  Without a workspace they equal the qmm
+// followed by the reference's glue kernel on its T output bit for bit; with
+// one (ws.bytes >= qgemm_split_bytes(k, n, m, true)) K may be split, the
+// glue applied after the splits are added, which reorders the K sum:
+//
 //   postscale: y[m][n] (f32) = float(T(acc)) * scale
 //   gate_add:  y[m][n] (f32) = residual[m][n] + gate[n] * float(T(acc)) * scale
 //   swiglu:    y[m][j] (T, row pitch ldy) = T(g * sigmoid(g) * u * out_scale), j < width,
 //              g = float(T(x . W[gate_row + j])) * in_scale, u likewise with up_row.
 hipError_t launch_qgemm_postscale(const uint32_t* w, const void* scales, const void* biases,
                                   const void* x, float* y, int k, int n, int m, float scale,
-                                  int dtype, hipStream_t stream);
+                                  int dtype, hipStream_t stream, SplitWs ws = {});
 hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const void* biases,
                                  const void* x, const float* residual, const float* gate, float* y,
-                                 int k, int n, int m, float scale, int dtype, hipStream_t stream);
+                                 int k, int n, int m, float scale, int dtype, hipStream_t stream,
+                                 SplitWs ws = {});
 hipError_t launch_qgemm_swiglu(const uint32_t* w, const void* scales, const void* biases,
                                const void* x, void* y, int ldy, int k, int n, int m, int width,
                                int gate_row, int up_row, float in_scale, float out_scale, int dtype,
-                               hipStream_t stream);
+                               hipStream_t stream, SplitWs ws = {});
 
 // y[r][c] (T) = x[r][c] * rsqrt(mean(x[r]^2) + eps) * w[c], x fp32 [rows, cols].
 hipError_t launch_rmsnorm(const float* x, const float* w, void* y, int rows, int cols, float eps,

@@ -24,6 +24,8 @@
 //  * Workgroup ids are remapped so that each XCD (ids are dealt round-robin to
 //    the 8 XCDs) walks a contiguous, M-grouped stretch of tiles, keeping the
 //    shared x and W panels in that XCD's L2.
+#include <type_traits>
+
 #include "epilogue.hpp"
 #include "imq_device.hpp"
 #include "imq_kernels.hpp"
@@ -674,21 +676,37 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
 
   if constexpr (EP::kPartial) {
     // Split-K partial sums: fp32 straight from the MFMA layout into split
-    // blockIdx.y's [M][N] slice of the workspace.
+    // blockIdx.y's [M][ldp] slice of the workspace.
     IMQ_WAIT_VMCNT(0);  // drain the clamped tail loads before the workgroup ends
-    float* part = ep.ws + (size_t)blockIdx.y * M * N;
+    float* part = ep.ws + (size_t)blockIdx.y * M * ep.ldp;
+    if constexpr (EP::kPair) {
+      const int j = pcol0 + r32;
+      if (j < ep.width) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int col = ncol0 + nt * 32 + r32;
-        if (col >= N) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (row < M) part[(size_t)row * N + col] = acc[mt][nt][r];
-        }
+          for (int r = 0; r < 16; ++r) {
+            const int row = m0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (row < M) {
+              part[(size_t)row * ep.ldp + j] = acc[mt][0][r];
+              part[(size_t)row * ep.ldp + ep.width + j] = acc[mt][1][r];
+            }
+          }
       }
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const int col = ncol0 + nt * 32 + r32;
+          if (col >= N) continue;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = m0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (row < M) part[(size_t)row * ep.ldp + col] = acc[mt][nt][r];
+          }
+        }
+    }
   } else {
   // Output: the tile's T values are staged in the LDS ring, then written out
   // row by row, 16 bytes per lane.  Written straight from the MFMA layout, a
@@ -724,36 +742,79 @@ hipError_t launch_big(const uint32_t* w, const uint16_t* scales, const uint16_t*
   return hipGetLastError();
 }
 
-// y[i] = T(sum over s of ws[s][i]), i < mn, the splits added in order.  Four
-// outputs per thread; vec: mn % 4 == 0 and y 8-byte aligned.
-template <int T>
-__global__ __launch_bounds__(256) void reduce_splits_kernel(const float* __restrict__ ws,
-                                                            int splits, long mn, bool vec,
-                                                            uint16_t* __restrict__ y) {
-  const long i = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
-  if (i >= mn) return;
-  if (vec) {
-    float4 a = *reinterpret_cast<const float4*>(ws + i);
-    for (int sp = 1; sp < splits; ++sp) {
-      const float4 b = *reinterpret_cast<const float4*>(ws + sp * mn + i);
-      a.x += b.x;
-      a.y += b.y;
-      a.z += b.z;
-      a.w += b.w;
+// Adds the split-K partial sums of each output in split order and applies
+// the output stage ep (its T rounding of value / value2, then emit8 or
+// emit1): 8 consecutive outputs of a row per thread.  Partials of split s
+// sit at ws + s * M * ldp; plain stages read column c at c, pair stages the
+// gate sum at c and the up sum at width + c.  vload: ldp % 4 == 0 and
+// ncols % 8 == 0 (16-byte partial loads).
+template <int T, class EP>
+__global__ __launch_bounds__(256) void reduce_ep_kernel(const float* __restrict__ ws, int splits,
+                                                        int M, int ncols, int ldp, bool vload,
+                                                        const EP ep) {
+  const int cpr = (ncols + 7) / 8;
+  const long t = (long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long)M * cpr) return;
+  const int row = (int)(t / cpr);
+  const int c0 = (int)(t % cpr) * 8;
+  const size_t stride = (size_t)M * ldp;
+  float a[8], u[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a[e] = u[e] = 0.f;
+  for (int sp = 0; sp < splits; ++sp) {
+    const float* pr = ws + sp * stride + (size_t)row * ldp + c0;
+    if (vload) {
+      const float4 p0 = reinterpret_cast<const float4*>(pr)[0];
+      const float4 p1 = reinterpret_cast<const float4*>(pr)[1];
+      a[0] += p0.x; a[1] += p0.y; a[2] += p0.z; a[3] += p0.w;
+      a[4] += p1.x; a[5] += p1.y; a[6] += p1.z; a[7] += p1.w;
+      if constexpr (EP::kPair) {
+        const float4 q0 = reinterpret_cast<const float4*>(pr + ep.width)[0];
+        const float4 q1 = reinterpret_cast<const float4*>(pr + ep.width)[1];
+        u[0] += q0.x; u[1] += q0.y; u[2] += q0.z; u[3] += q0.w;
+        u[4] += q1.x; u[5] += q1.y; u[6] += q1.z; u[7] += q1.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (c0 + e < ncols) {
+          a[e] += pr[e];
+          if constexpr (EP::kPair) u[e] += pr[ep.width + e];
+        }
     }
-    *reinterpret_cast<uint2*>(y + i) = make_uint2(Elem<T>::pack2(a.x, a.y), Elem<T>::pack2(a.z, a.w));
+  }
+  uint32_t w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (EP::kPair)
+      w[e] = Elem<T>::pack2(ep.value2(a[2 * e], u[2 * e]), ep.value2(a[2 * e + 1], u[2 * e + 1]));
+    else
+      w[e] = Elem<T>::pack2(ep.value(a[2 * e]), ep.value(a[2 * e + 1]));
+  }
+  if (ep.vec && c0 + 8 <= ncols) {
+    ep.emit8(row, c0, make_uint4(w[0], w[1], w[2], w[3]));
   } else {
-    for (long j = i; j < i + 4 && j < mn; ++j) {
-      float a = ws[j];
-      for (int sp = 1; sp < splits; ++sp) a += ws[sp * mn + j];
-      y[j] = (uint16_t)Elem<T>::pack2(a, 0.f);
-    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (c0 + e < ncols) ep.emit1(row, c0 + e, (uint16_t)(w[e >> 1] >> (16 * (e & 1))));
   }
 }
 
+template <int T, class EP>
+hipError_t launch_reduce(const SplitWs& ws, int splits, int m, int ncols, int ldp, const EP& ep,
+                         hipStream_t stream) {
+  const long threads = (long)m * ((ncols + 7) / 8);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  const bool vload = ldp % 4 == 0 && ncols % 8 == 0;
+  hipLaunchKernelGGL((reduce_ep_kernel<T, EP>), grid, dim3(256), 0, stream, ws.p, splits, m, ncols,
+                     ldp, vload, ep);
+  return hipGetLastError();
+}
+
 // Tile height and K split of the large-M kernel (small: 32- and 64-row tiles
-// allowed, which only the plain output stage and the split-K partial sums are
-// built for; split: K may be split).  Cost in units of about
+// allowed without a split -- the plain output stage is built for them, the
+// fused stages are not, the split-K partial sums always are; split: K may be
+// split).  Cost in units of about
 // 0.36 us (a K-step of a 32-row slice of the tile): a round of tiles costs
 // split_steps * (MT + 1.5) plus 12 for its prologue and output; a split adds
 // the workspace traffic of its reduction (8 bytes per output and split, at
@@ -769,13 +830,12 @@ BigPlan pick_big_plan(int m, int n, int k, int cus, bool small, bool split) {
   BigPlan best{8, 1, steps};
   double best_cost = 1e30;
   for (int mt : {8, 7, 6, 4, 2, 1}) {
-    if (!small && mt < 4) continue;
     const long tiles = (long)((m + 32 * mt - 1) / (32 * mt)) * tiles_n;
     const int max_splits = split && tiles < cus ? std::max(1, steps / 2) : 1;
     for (int sp = 1; sp <= max_splits; ++sp) {
       const int sps = ((steps + sp - 1) / sp + 1) / 2 * 2;  // even
       const int eff = (steps + sps - 1) / sps;
-      if (eff != sp) continue;
+      if (eff != sp || (eff == 1 && mt < 4 && !small)) continue;
       const long rounds = (tiles * eff + cus - 1) / cus;
       double cost = (double)rounds * (sps * (mt + 1.5) + 12.0);
       if (eff > 1) cost += (double)eff * m * n * 8.0 / 1.4e6 + 3.0;
@@ -813,20 +873,54 @@ int device_cus() {
   return cus;
 }
 
-// The large-M kernel with output stage ep.  Two groups per K-step (2-stage
-// ring): half the barriers and waits of one group per step (4-stage ring),
-// measured 3.5% faster at M=4608 K=3072 N=18432.
+template <int T, class EP>
+hipError_t launch_big_mt(int mt, const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                         const uint16_t* x, const EP& ep, int k, int n, int m, hipStream_t stream,
+                         int splits = 1, int split_steps = 0) {
+  // Plain and partial-sum stages are built for every tile height, the fused
+  // ones for 128 rows and more.
+  constexpr bool kSmall = EP::kPartial || (!EP::kPair && std::is_same<EP, EpStore<T>>::value);
+  switch (mt) {
+    case 1:
+      if constexpr (kSmall) return launch_big<T, 1>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
+      return hipErrorInvalidValue;
+    case 2:
+      if constexpr (kSmall) return launch_big<T, 2>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
+      return hipErrorInvalidValue;
+    case 4: return launch_big<T, 4>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
+    case 6: return launch_big<T, 6>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
+    case 7: return launch_big<T, 7>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
+    default: return launch_big<T, 8>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
+  }
+}
+
+// The large-M kernel with output stage ep (two groups per K-step, 2-stage
+// ring: half the barriers and waits of one group per step, measured 3.5%
+// faster at M=4608 K=3072 N=18432).  When the planner splits K and ws holds
+// the partial sums, the kernel writes fp32 partials and reduce_ep_kernel adds
+// them and applies ep; otherwise one pass.
 template <int T, class EP>
 hipError_t launch_big_ep(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
-                         const uint16_t* x, const EP& ep, int k, int n, int m, hipStream_t stream) {
-  int cols = n;
-  if constexpr (EP::kPair) cols = 2 * ep.width;
-  switch (pick_big_plan(m, cols, k, device_cus(), false, false).mt) {
-    case 4: return launch_big<T, 4>(w, scales, biases, x, ep, k, n, m, stream);
-    case 6: return launch_big<T, 6>(w, scales, biases, x, ep, k, n, m, stream);
-    case 7: return launch_big<T, 7>(w, scales, biases, x, ep, k, n, m, stream);
-    default: return launch_big<T, 8>(w, scales, biases, x, ep, k, n, m, stream);
+                         const uint16_t* x, const EP& ep, int k, int n, int m, hipStream_t stream,
+                         SplitWs ws) {
+  constexpr bool kSmall = !EP::kPair && std::is_same<EP, EpStore<T>>::value;
+  int cols = n;  // weight rows covered
+  int width = n, gate_row = 0, up_row = 0;
+  if constexpr (EP::kPair) {
+    cols = 2 * ep.width;
+    width = ep.width;
+    gate_row = ep.gate_row;
+    up_row = ep.up_row;
   }
+  BigPlan p = pick_big_plan(m, cols, k, device_cus(), kSmall, ws.p != nullptr);
+  if (p.splits > 1 && ws.bytes < (size_t)p.splits * m * cols * sizeof(float))
+    p = pick_big_plan(m, cols, k, device_cus(), kSmall, false);  // no room for the partial sums
+  if (p.splits == 1) return launch_big_mt<T>(p.mt, w, scales, biases, x, ep, k, n, m, stream);
+  const EpPartial<EP::kPair> part{ws.p, cols, width, gate_row, up_row};
+  const hipError_t e =
+      launch_big_mt<T>(p.mt, w, scales, biases, x, part, k, n, m, stream, p.splits, p.split_steps);
+  if (e != hipSuccess) return e;
+  return launch_reduce<T>(ws, p.splits, m, width, cols, ep, stream);
 }
 
 template <int T>
@@ -834,37 +928,8 @@ hipError_t launch_t(const uint32_t* w, const uint16_t* scales, const uint16_t* b
                     const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream,
                     SplitWs ws) {
   if (!qgemm_big_supported(k, n, m)) return launch_tile<T, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
-  BigPlan p = pick_big_plan(m, n, k, device_cus(), true, true);
-  const size_t need = (size_t)p.splits * m * n * sizeof(float);
-  if (p.splits > 1 && (ws.p == nullptr || ws.bytes < need))
-    p = pick_big_plan(m, n, k, device_cus(), true, false);  // no room for the partial sums
-  if (p.splits > 1) {
-    const EpPartial ep{ws.p};
-    hipError_t e;
-    switch (p.mt) {
-      case 1: e = launch_big<T, 1>(w, scales, biases, x, ep, k, n, m, stream, p.splits, p.split_steps); break;
-      case 2: e = launch_big<T, 2>(w, scales, biases, x, ep, k, n, m, stream, p.splits, p.split_steps); break;
-      case 4: e = launch_big<T, 4>(w, scales, biases, x, ep, k, n, m, stream, p.splits, p.split_steps); break;
-      case 6: e = launch_big<T, 6>(w, scales, biases, x, ep, k, n, m, stream, p.splits, p.split_steps); break;
-      case 7: e = launch_big<T, 7>(w, scales, biases, x, ep, k, n, m, stream, p.splits, p.split_steps); break;
-      default: e = launch_big<T, 8>(w, scales, biases, x, ep, k, n, m, stream, p.splits, p.split_steps); break;
-    }
-    if (e != hipSuccess) return e;
-    const long mn = (long)m * n;
-    const bool vec = mn % 4 == 0 && ((uintptr_t)y & 7u) == 0;
-    const dim3 grid((unsigned)((mn + 1023) / 1024));
-    hipLaunchKernelGGL(reduce_splits_kernel<T>, grid, dim3(256), 0, stream, ws.p, p.splits, mn, vec, y);
-    return hipGetLastError();
-  }
-  const EpStore<T> ep{y, n, al16(y) && n % 8 == 0};
-  switch (p.mt) {
-    case 1: return launch_big<T, 1>(w, scales, biases, x, ep, k, n, m, stream);
-    case 2: return launch_big<T, 2>(w, scales, biases, x, ep, k, n, m, stream);
-    case 4: return launch_big<T, 4>(w, scales, biases, x, ep, k, n, m, stream);
-    case 6: return launch_big<T, 6>(w, scales, biases, x, ep, k, n, m, stream);
-    case 7: return launch_big<T, 7>(w, scales, biases, x, ep, k, n, m, stream);
-    default: return launch_big<T, 8>(w, scales, biases, x, ep, k, n, m, stream);
-  }
+  return launch_big_ep<T>(w, scales, biases, x, EpStore<T>{y, n, al16(y) && n % 8 == 0}, k, n, m,
+                          stream, ws);
 }
 
 }  // namespace
@@ -889,31 +954,34 @@ hipError_t launch_qgemm(const uint32_t* w, const void* scales, const void* biase
   }
 }
 
-size_t qgemm_split_bytes(int k, int n, int m) {
+size_t qgemm_split_bytes(int k, int n, int m, bool fused) {
   if (!qgemm_big_supported(k, n, m)) return 0;
-  const BigPlan p = pick_big_plan(m, n, k, device_cus(), true, true);
+  const BigPlan p = pick_big_plan(m, n, k, device_cus(), !fused, true);
   return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
 }
 
 hipError_t launch_qgemm_postscale(const uint32_t* w, const void* scales, const void* biases,
                                   const void* x, float* y, int k, int n, int m, float scale,
-                                  int dtype, hipStream_t stream) {
+                                  int dtype, hipStream_t stream, SplitWs ws) {
   const auto* s = static_cast<const uint16_t*>(scales);
   const auto* b = static_cast<const uint16_t*>(biases);
   const auto* xx = static_cast<const uint16_t*>(x);
   const bool vec = al16(y) && n % 4 == 0;
   switch (dtype) {
     case kBf16:
-      return launch_big_ep<kBf16>(w, s, b, xx, EpPostscale<kBf16>{y, n, scale, vec}, k, n, m, stream);
+      return launch_big_ep<kBf16>(w, s, b, xx, EpPostscale<kBf16>{y, n, scale, vec}, k, n, m, stream,
+                                  ws);
     case kF16:
-      return launch_big_ep<kF16>(w, s, b, xx, EpPostscale<kF16>{y, n, scale, vec}, k, n, m, stream);
+      return launch_big_ep<kF16>(w, s, b, xx, EpPostscale<kF16>{y, n, scale, vec}, k, n, m, stream,
+                                 ws);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const void* biases,
                                  const void* x, const float* residual, const float* gate, float* y,
-                                 int k, int n, int m, float scale, int dtype, hipStream_t stream) {
+                                 int k, int n, int m, float scale, int dtype, hipStream_t stream,
+                                 SplitWs ws) {
   const auto* s = static_cast<const uint16_t*>(scales);
   const auto* b = static_cast<const uint16_t*>(biases);
   const auto* xx = static_cast<const uint16_t*>(x);
@@ -921,10 +989,10 @@ hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const vo
   switch (dtype) {
     case kBf16:
       return launch_big_ep<kBf16>(w, s, b, xx, EpGateAdd<kBf16>{y, residual, gate, n, scale, vec},
-                                  k, n, m, stream);
+                                  k, n, m, stream, ws);
     case kF16:
       return launch_big_ep<kF16>(w, s, b, xx, EpGateAdd<kF16>{y, residual, gate, n, scale, vec}, k,
-                                 n, m, stream);
+                                 n, m, stream, ws);
     default: return hipErrorInvalidValue;
   }
 }
@@ -932,7 +1000,7 @@ hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const vo
 hipError_t launch_qgemm_swiglu(const uint32_t* w, const void* scales, const void* biases,
                                const void* x, void* y, int ldy, int k, int n, int m, int width,
                                int gate_row, int up_row, float in_scale, float out_scale, int dtype,
-                               hipStream_t stream) {
+                               hipStream_t stream, SplitWs ws) {
   const auto* s = static_cast<const uint16_t*>(scales);
   const auto* b = static_cast<const uint16_t*>(biases);
   const auto* xx = static_cast<const uint16_t*>(x);
@@ -943,12 +1011,12 @@ hipError_t launch_qgemm_swiglu(const uint32_t* w, const void* scales, const void
       return launch_big_ep<kBf16>(
           w, s, b, xx,
           EpSwiGLU<kBf16>{yy, ldy, width, gate_row, up_row, in_scale, out_scale, vec}, k, n, m,
-          stream);
+          stream, ws);
     case kF16:
       return launch_big_ep<kF16>(
           w, s, b, xx,
           EpSwiGLU<kF16>{yy, ldy, width, gate_row, up_row, in_scale, out_scale, vec}, k, n, m,
-          stream);
+          stream, ws);
     default: return hipErrorInvalidValue;
   }
 }

@@ -81,18 +81,20 @@ hipError_t encode(imq_dit_step* st, hipStream_t s) {
     }
     // to_out / to_add_out on the V rows (the attention output's stand-in).
     ok(imq::launch_qgemm_gate_add(W[6].w, W[6].scales, W[6].biases, rows(st->V, d.l_txt, dim), Xi,
-                                  g, Xi, dim, dim, d.l_img, 1.0f, T, s));
+                                  g, Xi, dim, dim, d.l_img, 1.0f, T, s, st->split));
     ok(imq::launch_qgemm_gate_add(W[7].w, W[7].scales, W[7].biases, rows(st->V, 0, dim), Xt,
-                                  g + dim, Xt, dim, dim, d.l_txt, 1.0f, T, s));
+                                  g + dim, Xt, dim, dim, d.l_txt, 1.0f, T, s, st->split));
     ok(imq::launch_rmsnorm(st->X, st->norm_w, st->nX, J, dim, kEps, T, s));
     ok(imq::launch_qgemm_swiglu(W[8].w, W[8].scales, W[8].biases, nXi, rows(st->SW, d.l_txt, ffi),
-                                ffi, dim, 2 * ffi, d.l_img, ffi, 0, ffi, 1.0f, 1.0f, T, s));
+                                ffi, dim, 2 * ffi, d.l_img, ffi, 0, ffi, 1.0f, 1.0f, T, s,
+                                st->split));
     ok(imq::launch_qgemm_gate_add(W[9].w, W[9].scales, W[9].biases, rows(st->SW, d.l_txt, ffi), Xi,
-                                  g + 2 * dim, Xi, ffi, dim, d.l_img, 1.0f, T, s));
+                                  g + 2 * dim, Xi, ffi, dim, d.l_img, 1.0f, T, s, st->split));
     ok(imq::launch_qgemm_swiglu(W[10].w, W[10].scales, W[10].biases, nXt, rows(st->SW, 0, ffi), ffi,
-                                dim, 2 * ffi, d.l_txt, ffi, 0, ffi, 1.0f, 1.0f, T, s));
+                                dim, 2 * ffi, d.l_txt, ffi, 0, ffi, 1.0f, 1.0f, T, s,
+                                st->split));
     ok(imq::launch_qgemm_gate_add(W[11].w, W[11].scales, W[11].biases, rows(st->SW, 0, ffi), Xt,
-                                  g + 3 * dim, Xt, ffi, dim, d.l_txt, 1.0f, T, s));
+                                  g + 3 * dim, Xt, ffi, dim, d.l_txt, 1.0f, T, s, st->split));
   }
   const int cw = dim + ffi;
   for (int b = 0; b < d.n_single; ++b) {
@@ -103,9 +105,9 @@ hipError_t encode(imq_dit_step* st, hipStream_t s) {
                          st->split));
     ok(imq::launch_qgemm_swiglu(W[0].w, W[0].scales, W[0].biases, st->nX, st->C + (size_t)dim * es,
                                 cw, dim, 3 * dim + 2 * ffi, J, ffi, 3 * dim, 3 * dim + ffi, 1.0f,
-                                1.0f, T, s));
+                                1.0f, T, s, st->split));
     ok(imq::launch_qgemm_gate_add(W[1].w, W[1].scales, W[1].biases, st->C, st->X, g, st->X, cw, dim,
-                                  J, 1.0f, T, s));
+                                  J, 1.0f, T, s, st->split));
   }
   return e;
 }
@@ -115,6 +117,22 @@ void release(imq_dit_step* st) {
   if (st->graph) (void)hipGraphDestroy(st->graph);
   if (st->cap) (void)hipStreamDestroy(st->cap);
   if (st->arena) (void)hipFree(st->arena);
+}
+
+// Split-K workspace of the plan: the largest any of its projections takes
+// (fused ones over their weight rows, 2 * ff_inner for a SwiGLU pair).
+size_t split_bytes(const imq_dit_dims& d) {
+  const int J = d.l_txt + d.l_img, ffi = d.ff_inner, cw = d.dim + d.ff_inner;
+  size_t b = 0;
+  for (int m : {d.l_img, d.l_txt}) {
+    b = std::max({b, imq::qgemm_split_bytes(d.dim, d.dim, m),
+                  imq::qgemm_split_bytes(d.dim, d.dim, m, true),
+                  imq::qgemm_split_bytes(d.dim, 2 * ffi, m, true),
+                  imq::qgemm_split_bytes(ffi, d.dim, m, true)});
+  }
+  return std::max({b, imq::qgemm_split_bytes(d.dim, 3 * d.dim, J),
+                   imq::qgemm_split_bytes(d.dim, 2 * ffi, J, true),
+                   imq::qgemm_split_bytes(cw, d.dim, J, true)});
 }
 
 // Expected [N, K] of projection i of the plan.
@@ -186,9 +204,7 @@ int imq_dit_step_create(imq_ctx* ctx, const imq_dit_dims* dims, const imq_qweigh
                           J * (d.dim + d.ff_inner) * es,
                           (size_t)d.dim * 4,
                           ((size_t)4 * d.n_double + d.n_single) * d.dim * 4,
-                          std::max({imq::qgemm_split_bytes(d.dim, d.dim, d.l_img),
-                                    imq::qgemm_split_bytes(d.dim, d.dim, d.l_txt),
-                                    imq::qgemm_split_bytes(d.dim, 3 * d.dim, (int)J)})};
+                          split_bytes(d)};
   size_t off[11], total = 0;
   for (int i = 0; i < 11; ++i) {
     off[i] = total;

@@ -202,11 +202,12 @@ def test_dispatcher_routes_by_m():
         assert_close(y, cref.qmm_t(p.x[:m], p.w, p.scales, p.biases), f"dispatcher M={m}")
 
 
-@pytest.mark.parametrize("m,n,k", [(17, 384, 512), (40, 1000, 2560), (96, 512, 4096),
-                                   (300, 512, 768), (512, 2560, 9728)])
+@pytest.mark.parametrize("m,n,k", [(17, 384, 512), (40, 1000, 2560), (24, 1001, 1024),
+                                   (96, 512, 4096), (300, 512, 768), (512, 2560, 9728)])
 def test_split_k_dispatcher(m, n, k):
     """Shapes with too few output tiles for the chip: the dispatcher splits K
-    (and takes 32- or 64-row tiles).  Oracle within tolerance, the same bits on
+    (and takes 32- or 64-row tiles); N = 1001 takes the reduction's
+    single-element path.  Oracle within tolerance, the same bits on
     a second call (deterministic order), and one-hot rows are single weights
     even when summed over splits."""
     note(f"split-K dispatcher M={m} N={n} K={k}")

@@ -22,6 +22,9 @@ from oracle import ref
 pytestmark = pytest.mark.gpu
 
 TINY = DitDims(l_img=64, l_txt=32, dim=256, ff_inner=256, n_double=2, n_single=2)
+# Few output tiles and K of 512..1536: every projection splits K, the fused
+# gated-residual and SwiGLU stages applied after the partial sums are added.
+SPLIT = DitDims(l_img=128, l_txt=64, dim=512, ff_inner=1024, n_double=1, n_single=1)
 
 
 @pytest.fixture(autouse=True)
@@ -98,9 +101,9 @@ def oracle_step(d: DitDims, projs, norm_w, gates, h, e, tdt):
     return X
 
 
+@pytest.mark.parametrize("d", [TINY, SPLIT], ids=["tiny", "split_k"])
 @pytest.mark.parametrize("tdt", [torch.float16, torch.bfloat16])
-def test_tiny_step_matches_oracle_and_graph_matches_eager(tdt):
-    d = TINY
+def test_step_matches_oracle_and_graph_matches_eager(tdt, d):
     note(f"dit step {tdt} {d}")
     projs = random_projections(d, tdt, seed=7)
     step = DitStep(d, projs)
