@@ -21,7 +21,7 @@
 //    rounding, RNE_T(fl32(s*q + b)); for f32 the weight is fl32(s*q + b)) and
 //    multiplied into fp32 accumulators with v_dot2_f32_bf16 / v_dot2_f32_f16
 //    (16-bit T) or fma (f32);
-//  * the G partial sums of a row are combined with cross-lane shuffles.
+//  * the G partial sums of a row are combined with DPP adds.
 #include "imq_device.hpp"
 #include "imq_kernels.hpp"
 
@@ -76,6 +76,30 @@ __device__ __forceinline__ typename Elem<T>::S load_param(__amdgpu_buffer_rsrc_t
 __device__ __forceinline__ u32x4_t load_b128_nt(__amdgpu_buffer_rsrc_t rs, uint32_t voff,
                                                uint32_t soff) {
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 2));
+}
+
+// v plus the DPP-permuted v of the lanes in rows `rows` (16-lane rows of
+// the wave); other lanes add 0.
+template <int kCtrl, int kRows = 0xF>
+__device__ __forceinline__ float add_dpp(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                   kCtrl, kRows, 0xF, false));
+}
+
+// Sum of v over each aligned group of G lanes (G in {16, 32, 64}) by DPP
+// adds, no LDS traffic: quad swaps, half-row and row mirrors give every lane
+// its 16-lane row's sum; row_bcast15 adds row 0 (2) into row 1 (3), and
+// row_bcast31 adds rows 0-1 into rows 2-3.  The group's total is then held by
+// the lanes of its last row, among them lane G - 1 of the group.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  v = add_dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = add_dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = add_dpp<0x141>(v);  // row_half_mirror
+  v = add_dpp<0x140>(v);  // row_mirror
+  if constexpr (G >= 32) v = add_dpp<0x142, 0xA>(v);  // row_bcast15 into rows 1, 3
+  if constexpr (G == 64) v = add_dpp<0x143, 0xC>(v);  // row_bcast31 into rows 2, 3
+  return v;
 }
 
 template <int T, int MR, int G, int U, int R>
@@ -243,10 +267,8 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
-#pragma unroll
-      for (int off = G >> 1; off > 0; off >>= 1) acc[r][m] += __shfl_xor(acc[r][m], off, 64);
-  if (gl == 0) {
+    for (int m = 0; m < MR; ++m) acc[r][m] = group_sum<G>(acc[r][m]);
+  if (gl == G - 1) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (row0 + r < N) {
