@@ -60,16 +60,20 @@ class DitDims:
 
 def random_projections(dims: DitDims, dtype: torch.dtype = torch.float16, seed: int = 0,
                        device=None) -> list[Q]:
-    """Synthetic resident projections of the plan's shapes (random packed words,
-    scale = |N(0, 0.02)|, bias = -8 scale + N(0, 0.002)), generated on the device."""
+    """Synthetic resident projections of the plan's shapes, generated on the
+    device: random packed words, scale = |N(0, 1)| / (4 sqrt(K)), bias = -8 scale
+    + N(0, 1) / (40 sqrt(K)).  Weights of rms about 1.2 / sqrt(K) keep a
+    projection's output at the scale of its normalized input, so the residual
+    stream stays finite in f16 through all blocks, as trained weights do."""
     dev = torch.device("cuda", device_index(device))
     g = torch.Generator(device=dev).manual_seed(seed)
     out = []
     for _, n, k in dims.projection_shapes():
         w = torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k // 8), dtype=torch.int32, device=dev,
                           generator=g)
-        s = (torch.randn((n, k // 64), device=dev, generator=g).abs() * 0.02)
-        b = -8.0 * s + torch.randn((n, k // 64), device=dev, generator=g) * 0.002
+        unit = 1.0 / (4.0 * k ** 0.5)
+        s = torch.randn((n, k // 64), device=dev, generator=g).abs() * unit
+        b = -8.0 * s + torch.randn((n, k // 64), device=dev, generator=g) * (0.1 * unit)
         out.append(Q(w=w, s=s.to(dtype), b=b.to(dtype), n=n, k=k))
     return out
 

@@ -279,12 +279,14 @@ def bench_dit_step(torch) -> dict:
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / 10
+    finite = bool(torch.isfinite(out).all().item())
     flop = d.step_flops()
     wbytes = sum(q.w.numel() * 4 + 2 * q.s.numel() * 2 for q in projs)
     log(f"dit step (graph, {step.launches} launches): {ms:.2f} ms {flop / ms / 1e9:.1f} TFLOP/s")
     res = {"ms": round(ms, 3), "TFLOP/s": round(flop / ms / 1e9, 1),
            "frac_mfma": round(flop / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
            "tflop_per_step": round(flop / 1e12, 3), "launches": step.launches,
+           "output_finite": finite,
            "packed_weight_bytes": wbytes,
            "config": "5 double + 20 single blocks, l_img 4096 + l_txt 512, dim 3072, "
                      "ff_inner 9216, f16, RMSNorm before each block's projections"}
