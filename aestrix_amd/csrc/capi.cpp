@@ -27,6 +27,63 @@ imq_ctx::~imq_ctx() {
 }
 
 namespace imq {
+
+CopyPool::CopyPool(int workers) {
+  for (int i = 0; i < workers; ++i) {
+    try {
+      threads_.emplace_back([this] { work(); });
+    } catch (...) {
+      break;  // fewer workers: the calling thread does the rest
+    }
+  }
+}
+
+CopyPool::~CopyPool() {
+  {
+    std::lock_guard<std::mutex> lk(mu_);
+    stop_ = true;
+  }
+  start_cv_.notify_all();
+  for (auto& t : threads_) t.join();
+}
+
+void CopyPool::run(int parts, const std::function<void(int)>& fn) {
+  std::unique_lock<std::mutex> lk(mu_);
+  fn_ = &fn;
+  parts_ = parts;
+  next_ = 0;
+  remaining_ = parts;
+  ++gen_;
+  start_cv_.notify_all();
+  while (next_ < parts_) {
+    const int i = next_++;
+    lk.unlock();
+    fn(i);
+    lk.lock();
+    --remaining_;
+  }
+  done_cv_.wait(lk, [this] { return remaining_ == 0; });
+  fn_ = nullptr;
+}
+
+void CopyPool::work() {
+  unsigned long seen = 0;
+  std::unique_lock<std::mutex> lk(mu_);
+  for (;;) {
+    start_cv_.wait(lk, [&] { return stop_ || gen_ != seen; });
+    if (stop_) return;
+    seen = gen_;
+    while (fn_ && next_ < parts_) {
+      const int i = next_++;
+      const std::function<void(int)>* fn = fn_;
+      lk.unlock();
+      (*fn)(i);
+      lk.lock();
+      if (--remaining_ == 0) done_cv_.notify_all();
+    }
+  }
+}
+
 namespace detail {
 
 thread_local std::string g_create_error;  // failures before a context exists

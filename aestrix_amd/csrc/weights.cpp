@@ -494,6 +494,38 @@ float f16_to_f32(uint16_t u) {
 // Element conversion from a stored safetensors dtype into a library dtype.
 enum class Conv { kCopy, kBf16ToF16, kBf16ToF32, kF16ToF32 };
 
+// Elements [i0, i1) of one chunk into the staging buffer, converted.
+void fill_stage(uint8_t* stage, const uint8_t* s, size_t i0, size_t i1, size_t src_es,
+                Conv conv) {
+  switch (conv) {
+    case Conv::kCopy: memcpy(stage + i0 * src_es, s + i0 * src_es, (i1 - i0) * src_es); break;
+    case Conv::kBf16ToF16: {
+      auto* o = reinterpret_cast<uint16_t*>(stage);
+      for (size_t i = i0; i < i1; ++i) {
+        uint16_t h;
+        memcpy(&h, s + 2 * i, 2);
+        o[i] = f32_to_f16(bf16_to_f32(h));
+      }
+      break;
+    }
+    case Conv::kBf16ToF32:
+    case Conv::kF16ToF32: {
+      auto* o = reinterpret_cast<float*>(stage);
+      for (size_t i = i0; i < i1; ++i) {
+        uint16_t h;
+        memcpy(&h, s + 2 * i, 2);
+        o[i] = conv == Conv::kBf16ToF32 ? bf16_to_f32(h) : f16_to_f32(h);
+      }
+      break;
+    }
+  }
+}
+
+// Threads that fill one staging chunk (the caller and kCopyThreads - 1
+// workers) and the smallest part worth a thread.
+constexpr int kCopyThreads = 4;
+constexpr size_t kMinPartBytes = 1u << 20;
+
 // Copy (and convert) `count` elements in chunks through the pinned buffers.
 // Chunk i waits for the copy that last read its buffer, is filled on the host
 // and then copied asynchronously on `stream`.
@@ -514,6 +546,10 @@ int staged_copy(imq_ctx* ctx, const char* fn, uint8_t* dst, const uint8_t* src, 
       }
     }
   }
+  if (!ctx->copy_pool) {
+    ctx->copy_pool.reset(new (std::nothrow) imq::CopyPool(kCopyThreads - 1));
+    if (!ctx->copy_pool) return fail(ctx, IMQ_ENOMEM, "%s: out of host memory", fn);
+  }
   const size_t per_chunk = imq_ctx::kStagingBytes / std::max(src_es, dst_es);
   for (size_t e0 = 0; e0 < count; e0 += per_chunk) {
     const size_t n = std::min(per_chunk, count - e0);
@@ -523,27 +559,17 @@ int staged_copy(imq_ctx* ctx, const char* fn, uint8_t* dst, const uint8_t* src, 
     if (e != hipSuccess) return hip_fail(ctx, e, fn);
     auto* stage = static_cast<uint8_t*>(ctx->staging[b]);
     const uint8_t* s = src + e0 * src_es;
-    switch (conv) {
-      case Conv::kCopy: memcpy(stage, s, n * src_es); break;
-      case Conv::kBf16ToF16: {
-        auto* o = reinterpret_cast<uint16_t*>(stage);
-        for (size_t i = 0; i < n; ++i) {
-          uint16_t h;
-          memcpy(&h, s + 2 * i, 2);
-          o[i] = f32_to_f16(bf16_to_f32(h));
-        }
-        break;
-      }
-      case Conv::kBf16ToF32:
-      case Conv::kF16ToF32: {
-        auto* o = reinterpret_cast<float*>(stage);
-        for (size_t i = 0; i < n; ++i) {
-          uint16_t h;
-          memcpy(&h, s + 2 * i, 2);
-          o[i] = conv == Conv::kBf16ToF32 ? bf16_to_f32(h) : f16_to_f32(h);
-        }
-        break;
-      }
+    const int parts = (int)std::min<size_t>(kCopyThreads, std::max<size_t>(1, n * src_es / kMinPartBytes));
+    if (parts == 1) {
+      fill_stage(stage, s, 0, n, src_es, conv);
+    } else {
+      // Part boundaries on 64-element multiples (whole cache lines either side).
+      const size_t step = (n / parts + 63) / 64 * 64;
+      ctx->copy_pool->run(parts, [&](int i) {
+        const size_t i0 = std::min(n, (size_t)i * step);
+        const size_t i1 = (i == parts - 1) ? n : std::min(n, i0 + step);
+        fill_stage(stage, s, i0, i1, src_es, conv);
+      });
     }
     e = hipMemcpyAsync(dst + e0 * dst_es, stage, n * dst_es, hipMemcpyHostToDevice, stream);
     if (e != hipSuccess) return hip_fail(ctx, e, fn);

@@ -20,14 +20,16 @@ over that synthetic batch, inputs resident in HBM.  The same line carries:
 * dit_step     -- a whole DiT step's quantized linear layers (5 double + 20
                 single blocks, l_img 4096 + l_txt 512, f16, random-init packed
                 weights of the model's shapes) replayed as one HIP graph;
-* upload       -- the loader's host -> device path (pinned double buffer) in GB/s;
+* upload       -- the loader's host -> device path (pinned double buffer, each
+                chunk filled by four host threads) in GB/s;
 * cpu_baseline -- the C oracle's f32-accumulating CPU quantized matmul
                 (MLX is not available) on a bounded sample of the same problem.
 
 Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 100] [--no-cpu-baseline]
 
-The default warm-up (about 60 ms of qGEMM work) is past the clock transient
-that the first ~15 ms of sustained MFMA load shows on this GPU.
+Before its W warmup steps the headline runs untimed launches for 0.5 s, so
+the clock and power state have settled whatever W is (short warm-ups landed
+inside the transient of the first tens of ms of sustained MFMA load).
 """
 
 from __future__ import annotations
@@ -42,6 +44,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "4-bit qGEMM TFLOP/s (% MFMA peak) at M=4608; qGEMV GB/s (% HBM) at M=1"
+PREWARM_S = 0.5  # untimed launches before the warmup steps of the headline
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 TARGET = (4608, 18432, 3072)  # M, N, K
@@ -393,6 +396,13 @@ def main() -> int:
     p = synth.make_problem(m, n, k, seed=0)
     x, w, s, b = synth.to_device(p)
     y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    # Untimed pre-warm until PREWARM_S of wall time has passed (the GPU leaves
+    # its idle clock and power state), then the W warmup steps.
+    t_pre = time.perf_counter()
+    while time.perf_counter() - t_pre < PREWARM_S:
+        for _ in range(20):
+            imq.quantized_matmul(x, w, s, b, out=y)
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         imq.quantized_matmul(x, w, s, b, out=y)
     torch.cuda.synchronize()

@@ -67,6 +67,23 @@ def test_upload_raw_and_converted(tmp_path):
             st.upload("a.f32", torch.float16)  # no narrowing
 
 
+def test_converted_upload_split_over_copy_threads(tmp_path):
+    """Conversions of tensors large enough that each staging chunk is filled
+    by several host threads (ragged element counts, chunk and part seams)."""
+    note("loader: converted uploads over the copy threads")
+    g = torch.Generator().manual_seed(3)
+    src = {"big.bf16": (torch.randn((9 * 2 ** 20 + 77,), generator=g) * 50).to(torch.bfloat16),
+           "big.f16": torch.randn((3 * 2 ** 20 + 5,), generator=g).to(torch.float16)}
+    save_file(src, str(tmp_path / "0.safetensors"))
+    with SafetensorsSet.open_dir(tmp_path) as st:
+        b = src["big.bf16"].cuda()
+        assert torch.equal(st.upload("big.bf16"), b)
+        assert torch.equal(st.upload("big.bf16", torch.float32), b.float())
+        assert torch.equal(st.upload("big.bf16", torch.float16).view(torch.int16),
+                           b.to(torch.float16).view(torch.int16))
+        assert torch.equal(st.upload("big.f16", torch.float32), src["big.f16"].cuda().float())
+
+
 def test_upload_many_staging_chunks():
     """160 MiB through the two 32 MiB pinned buffers, with a ragged tail."""
     note("loader: imq_upload 160 MiB")
