@@ -57,7 +57,10 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    # Export the C ABI only (imq_*), the C++ internals stay local.
+    exports = os.path.join(CSRC, "exports.map")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC",
+           f"-Wl,--version-script={exports}", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")

@@ -39,6 +39,22 @@ def test_every_declared_symbol_is_exported_and_bound():
     assert set(_lib.SIGNATURES) == set(declared)
 
 
+def test_only_the_c_abi_is_exported():
+    """The dynamic symbol table holds exactly the header's imq_* functions: the
+    C++ internals are local, so another copy of them in the process cannot
+    interpose on this library's calls (nor this library on its)."""
+    import shutil
+    import subprocess
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    assert exported == set(header_functions()), sorted(exported ^ set(header_functions()))
+
+
 def test_status_strings_and_version():
     L = _lib.load()
     assert L.imq_abi_version() == 1
