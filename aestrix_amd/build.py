@@ -67,7 +67,31 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources")
+    build_abi_check(verbose)
     return LIB
+
+
+ABI_CHECK_SRC = os.path.join(ROOT, "tests", "c", "abi_check.c")
+ABI_CHECK = os.path.join(ROOT, "tests", "c", "abi_check")
+
+
+def build_abi_check(verbose: bool = False) -> str | None:
+    """The plain-C11 caller of the C ABI (tests/c/abi_check.c), linked against
+    the in-tree libimq.so with an rpath relative to itself."""
+    if not os.path.exists(ABI_CHECK_SRC):
+        return None
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        return None
+    cmd = [cc, "-std=c11", "-O2", "-Wall", "-Wextra", "-Werror", "-ffp-contract=off",
+           "-I", INCLUDE, ABI_CHECK_SRC, "-o", ABI_CHECK, "-L", PKG, "-limq",
+           "-Wl,-rpath,$ORIGIN/../../aestrix_amd"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"building {ABI_CHECK_SRC} failed:\n{r.stdout}\n{r.stderr}")
+    if verbose:
+        print(f"built {ABI_CHECK}")
+    return ABI_CHECK
 
 
 if __name__ == "__main__":

@@ -315,6 +315,20 @@ def test_argument_errors_are_reported():
     assert L.imq_create(10_000, ctypes.byref(out)) == _lib.IMQ_EINVAL
 
 
+def test_plain_c_caller_on_the_device():
+    """tests/c/abi_check.c, a C11 program linked against libimq.so: dequant
+    against the closed form, one-hot qmm_t in both regimes, error statuses."""
+    import subprocess
+
+    from aestrix_amd import build
+
+    note("plain C11 caller of the ABI")
+    assert os.path.exists(build.ABI_CHECK), "abi_check is not built (python -m aestrix_amd.build)"
+    r = subprocess.run([build.ABI_CHECK], capture_output=True, text=True, timeout=90)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "checks passed" in r.stdout
+
+
 def test_pure_c_abi_memory_stream_and_kernel():
     """Everything through the C ABI: imq_malloc / memcpy / stream / dequant / qmm."""
     note("pure C-ABI round trip")

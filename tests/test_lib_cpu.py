@@ -102,3 +102,18 @@ def test_device_index_normalisation():
     assert ops.device_index(torch.device("cuda", 1)) == 1
     with pytest.raises(ValueError):
         ops.device_index("cpu")
+
+
+def test_plain_c_caller_without_device():
+    """tests/c/abi_check.c binds the C ABI from C11 (no ctypes): version,
+    status strings and null-context validation need no GPU."""
+    import subprocess
+
+    from aestrix_amd import build
+
+    if not os.path.exists(build.ABI_CHECK):
+        pytest.skip("abi_check is not built (python -m aestrix_amd.build)")
+    r = subprocess.run([build.ABI_CHECK, "--no-device"], capture_output=True, text=True,
+                       timeout=60)
+    assert r.returncode == 0, r.stderr
+    assert "checks passed" in r.stdout
