@@ -71,12 +71,16 @@ __device__ __forceinline__ void dequant_word_bf16(uint32_t word, float s24, floa
   out[3] = pack_bf16x2(__builtin_fmaf(s24, f16_hi(d2), b), __builtin_fmaf(s20, f16_hi(d3), b));
 }
 
-// Pack two floats into an f16 pair, each rounded to nearest even
-// (v_cvt_f16_f32 in the default round mode).
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// Pack two floats into an f16 pair, each rounded to nearest even: one
+// v_cvt_pk_f16_f32 on gfx950 (two v_cvt_f16_f32 and a pack when written as
+// two scalar conversions).
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
-  const uint32_t a = __builtin_bit_cast(uint16_t, (_Float16)lo);
-  const uint32_t b = __builtin_bit_cast(uint16_t, (_Float16)hi);
-  return a | (b << 16);
+  f16x2_t p;
+  p[0] = (_Float16)lo;
+  p[1] = (_Float16)hi;
+  return __builtin_bit_cast(uint32_t, p);
 }
 
 // dequant_word_bf16 with f16 results: out[p] = (w[2p], w[2p+1]) as RNE_f16(fl32(s*q + b)).
@@ -189,7 +193,6 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
                                          __builtin_bit_cast(bf16x2_t, b), acc, false);
 }
 
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float acc) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b),
                                 acc, false);
