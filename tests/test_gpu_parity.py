@@ -226,6 +226,46 @@ def test_split_k_dispatcher(m, n, k):
     assert np.array_equal(yo, bits(imq.dequantize(w, s, b))[:, cols].T)
 
 
+def test_split_k_dispatcher_under_graph_capture():
+    """A split-K call captured in a graph on a stream whose workspace exists
+    replays to the eager bits, with other device work and synchronizations
+    between replays; captured on a stream that never ran it (no workspace, none
+    grown under capture) it runs unsplit, within tolerance of the oracle."""
+    m, n, k = 40, 1000, 2560
+    note(f"split-K dispatcher under graph capture M={m} N={n} K={k}")
+    p = synth.make_problem(m, n, k, seed=25)
+    x, w, s, b = synth.to_device(p)
+    side = torch.cuda.Stream()
+    y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        imq.quantized_matmul(x, w, s, b, out=y)  # grows this stream's workspace
+    side.synchronize()
+    eager = bits(y)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        imq.quantized_matmul(x, w, s, b, out=y)
+    for rep in range(3):
+        y.zero_()
+        torch.randn(1000, device="cuda").sum().item()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(y), eager), f"replay {rep}"
+    fresh = torch.cuda.Stream()
+    y2 = torch.empty_like(y)
+    g2 = torch.cuda.CUDAGraph()
+    fresh.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(g2, stream=fresh):
+        imq.quantized_matmul(x, w, s, b, out=y2)
+    want = cref.qmm_t(p.x, p.w, p.scales, p.biases)
+    for rep in range(2):
+        y2.zero_()
+        torch.cuda.synchronize()
+        g2.replay()
+        torch.cuda.synchronize()
+        assert_close(bits(y2), want, f"unsplit capture, replay {rep}")
+
+
 def test_small_tiles_plain_qgemm():
     """imq_qgemm at M <= 64 runs 32- and 64-row tiles (no split)."""
     for m in (17, 33, 64):
