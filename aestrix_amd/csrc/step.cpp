@@ -38,7 +38,13 @@ struct imq_dit_step {
   float* norm_w = nullptr;  // fp32 [dim]
   float* gates = nullptr;   // fp32 [4 n_double + n_single][dim]
   imq::SplitWs split;       // partial sums of the projections that split K
+  imq::SplitWs split_txt;   // the same for the double blocks' text rows (side stream)
   hipStream_t cap = nullptr;
+  // The double blocks' text-row projections run on `side`, beside the image
+  // rows on the main stream, forked and joined by these events.
+  hipStream_t side = nullptr;
+  hipEvent_t ev_fork = nullptr;
+  hipEvent_t ev_join = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   int launches = 0;
@@ -63,7 +69,20 @@ hipError_t encode(imq_dit_step* st, hipStream_t s) {
     ++st->launches;
     if (e == hipSuccess) e = r;
   };
+  auto sync = [&](hipError_t r) {
+    if (e == hipSuccess) e = r;
+  };
+  // The text rows' chain (on st->side) depends on the main stream up to here.
+  auto fork = [&]() {
+    sync(hipEventRecord(st->ev_fork, s));
+    sync(hipStreamWaitEvent(st->side, st->ev_fork, 0));
+  };
+  auto join = [&]() {
+    sync(hipEventRecord(st->ev_join, st->side));
+    sync(hipStreamWaitEvent(s, st->ev_join, 0));
+  };
   auto rows = [&](char* base, int row0, int width) { return base + (size_t)row0 * width * es; };
+  hipStream_t t = st->side;
   float* Xt = st->X;
   float* Xi = st->X + (size_t)d.l_txt * dim;
   for (int b = 0; b < d.n_double; ++b) {
@@ -73,28 +92,36 @@ hipError_t encode(imq_dit_step* st, hipStream_t s) {
     char* nXt = rows(st->nX, 0, dim);
     char* nXi = rows(st->nX, d.l_txt, dim);
     char* outs[3] = {st->Q, st->K, st->V};
-    for (int q = 0; q < 3; ++q) {
+    // Image rows (4096 at 1024^2) on s and text rows (512) on t at the same
+    // time: an image-row projection leaves CUs idle in its last tile round
+    // and a text-row one never fills the GPU.  The two chains touch disjoint
+    // rows of every buffer and have their own split-K workspaces.
+    fork();
+    for (int q = 0; q < 3; ++q)
       ok(imq::launch_qgemm(W[q].w, W[q].scales, W[q].biases, nXi, rows(outs[q], d.l_txt, dim), dim,
                            dim, d.l_img, T, s, st->split));
-      ok(imq::launch_qgemm(W[3 + q].w, W[3 + q].scales, W[3 + q].biases, nXt, rows(outs[q], 0, dim),
-                           dim, dim, d.l_txt, T, s, st->split));
-    }
     // to_out / to_add_out on the V rows (the attention output's stand-in).
     ok(imq::launch_qgemm_gate_add(W[6].w, W[6].scales, W[6].biases, rows(st->V, d.l_txt, dim), Xi,
                                   g, Xi, dim, dim, d.l_img, 1.0f, T, s, st->split));
+    for (int q = 0; q < 3; ++q)
+      ok(imq::launch_qgemm(W[3 + q].w, W[3 + q].scales, W[3 + q].biases, nXt, rows(outs[q], 0, dim),
+                           dim, dim, d.l_txt, T, t, st->split_txt));
     ok(imq::launch_qgemm_gate_add(W[7].w, W[7].scales, W[7].biases, rows(st->V, 0, dim), Xt,
-                                  g + dim, Xt, dim, dim, d.l_txt, 1.0f, T, s, st->split));
+                                  g + dim, Xt, dim, dim, d.l_txt, 1.0f, T, t, st->split_txt));
+    join();
     ok(imq::launch_rmsnorm(st->X, st->norm_w, st->nX, J, dim, kEps, T, s));
+    fork();
     ok(imq::launch_qgemm_swiglu(W[8].w, W[8].scales, W[8].biases, nXi, rows(st->SW, d.l_txt, ffi),
                                 ffi, dim, 2 * ffi, d.l_img, ffi, 0, ffi, 1.0f, 1.0f, T, s,
                                 st->split));
     ok(imq::launch_qgemm_gate_add(W[9].w, W[9].scales, W[9].biases, rows(st->SW, d.l_txt, ffi), Xi,
                                   g + 2 * dim, Xi, ffi, dim, d.l_img, 1.0f, T, s, st->split));
     ok(imq::launch_qgemm_swiglu(W[10].w, W[10].scales, W[10].biases, nXt, rows(st->SW, 0, ffi), ffi,
-                                dim, 2 * ffi, d.l_txt, ffi, 0, ffi, 1.0f, 1.0f, T, s,
-                                st->split));
+                                dim, 2 * ffi, d.l_txt, ffi, 0, ffi, 1.0f, 1.0f, T, t,
+                                st->split_txt));
     ok(imq::launch_qgemm_gate_add(W[11].w, W[11].scales, W[11].biases, rows(st->SW, 0, ffi), Xt,
-                                  g + 3 * dim, Xt, ffi, dim, d.l_txt, 1.0f, T, s, st->split));
+                                  g + 3 * dim, Xt, ffi, dim, d.l_txt, 1.0f, T, t, st->split_txt));
+    join();
   }
   const int cw = dim + ffi;
   for (int b = 0; b < d.n_single; ++b) {
@@ -116,6 +143,9 @@ void release(imq_dit_step* st) {
   if (st->exec) (void)hipGraphExecDestroy(st->exec);
   if (st->graph) (void)hipGraphDestroy(st->graph);
   if (st->cap) (void)hipStreamDestroy(st->cap);
+  if (st->side) (void)hipStreamDestroy(st->side);
+  if (st->ev_fork) (void)hipEventDestroy(st->ev_fork);
+  if (st->ev_join) (void)hipEventDestroy(st->ev_join);
   if (st->arena) (void)hipFree(st->arena);
 }
 
@@ -204,9 +234,10 @@ int imq_dit_step_create(imq_ctx* ctx, const imq_dit_dims* dims, const imq_qweigh
                           J * (d.dim + d.ff_inner) * es,
                           (size_t)d.dim * 4,
                           ((size_t)4 * d.n_double + d.n_single) * d.dim * 4,
+                          split_bytes(d),
                           split_bytes(d)};
-  size_t off[11], total = 0;
-  for (int i = 0; i < 11; ++i) {
+  size_t off[12], total = 0;
+  for (int i = 0; i < 12; ++i) {
     off[i] = total;
     total += align256(sizes[i]);
   }
@@ -231,6 +262,7 @@ int imq_dit_step_create(imq_ctx* ctx, const imq_dit_dims* dims, const imq_qweigh
   st->norm_w = reinterpret_cast<float*>(a + off[8]);
   st->gates = reinterpret_cast<float*>(a + off[9]);
   st->split = imq::SplitWs{reinterpret_cast<float*>(a + off[10]), sizes[10]};
+  st->split_txt = imq::SplitWs{reinterpret_cast<float*>(a + off[11]), sizes[11]};
   // Zero everything (the attention half of C stays zero), ones for the
   // conditioning vectors.  Plain (uncaptured) memsets at set-up.
   e = hipMemset(st->arena, 0, total);
@@ -238,6 +270,9 @@ int imq_dit_step_create(imq_ctx* ctx, const imq_dit_dims* dims, const imq_qweigh
   if (e == hipSuccess)
     e = hipMemsetD32(st->gates, 0x3F800000u, ((size_t)4 * d.n_double + d.n_single) * d.dim);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&st->cap, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&st->side, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&st->ev_fork, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&st->ev_join, hipEventDisableTiming);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     release(st);

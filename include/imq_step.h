@@ -76,7 +76,9 @@ int imq_dit_step_set_conditioning(imq_dit_step* step, const float* norm_weight,
  * copied in, never written), the blocks, and x_out (fp32 [l_txt + l_img, dim],
  * text rows first) = the final X.  use_graph != 0 replays the captured graph
  * (captured on the first such call), 0 launches the same kernels one by one.
- * Asynchronous on stream. */
+ * Asynchronous on stream: the double blocks' text-row projections run on a
+ * stream of the plan forked from and joined back into `stream` by events, so
+ * work queued on `stream` after this call still sees the whole step. */
 int imq_dit_step_run(imq_dit_step* step, const float* h_in, const float* e_in, float* x_out,
                      int use_graph, imq_stream stream);
 
