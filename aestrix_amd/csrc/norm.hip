@@ -4,7 +4,8 @@
 // between the blocks of a DiT step, in the shape of the reference's
 // dd_rmsnorm_pitched (Sources/ImarelloDirect/DirectDiTKernels.swift:61-99:
 // fp32 sum of squares, rsqrt(mean + eps), times an fp32 weight; eps 1e-5 at
-// DirectDiTStep.swift:416).  HBM-bound: one workgroup per row.
+// DirectDiTStep.swift:416).  HBM-bound: one workgroup per row.  Rounding to
+// T is RNE (the hardware pair conversion in the vector kernel).
 #include "imq_device.hpp"
 #include "imq_kernels.hpp"
 
@@ -34,23 +35,81 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float* __restri
   for (int c = threadIdx.x; c < cols; c += kThreads) yr[c] = Elem<T>::out(xr[c] * inv * w[c]);
 }
 
+// The same for cols % 4 == 0 and cols <= 1024 * V: each thread loads its V
+// float4 pieces of the row once (16-byte loads), keeps them in registers for
+// the scaling pass and stores 4 outputs as one 8-byte store.  The row is read
+// from memory once instead of twice.
+template <int T, int V>
+__global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(const float* __restrict__ x,
+                                                               const float* __restrict__ w,
+                                                               typename Elem<T>::S* __restrict__ y,
+                                                               int cols, float eps) {
+  __shared__ float part[kThreads / 64];
+  const int n4 = cols >> 2;
+  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)blockIdx.x * cols);
+  float4 v[V];
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int idx = threadIdx.x + i * kThreads;
+    v[i] = idx < n4 ? xr[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+    acc = __builtin_fmaf(v[i].x, v[i].x, acc);
+    acc = __builtin_fmaf(v[i].y, v[i].y, acc);
+    acc = __builtin_fmaf(v[i].z, v[i].z, acc);
+    acc = __builtin_fmaf(v[i].w, v[i].w, acc);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int i = 0; i < kThreads / 64; ++i) total += part[i];
+  const float inv = __frsqrt_rn(total / (float)cols + eps);
+  const float4* wr = reinterpret_cast<const float4*>(w);
+  uint2* yr = reinterpret_cast<uint2*>(y + (size_t)blockIdx.x * cols);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int idx = threadIdx.x + i * kThreads;
+    if (idx < n4) {
+      const float4 ww = wr[idx];
+      yr[idx] = make_uint2(Elem<T>::pack2(v[i].x * inv * ww.x, v[i].y * inv * ww.y),
+                           Elem<T>::pack2(v[i].z * inv * ww.z, v[i].w * inv * ww.w));
+    }
+  }
+}
+
+template <int T>
+hipError_t launch_t(const float* x, const float* w, void* y, int rows, int cols, float eps,
+                    hipStream_t stream) {
+  auto* yy = static_cast<typename Elem<T>::S*>(y);
+  const bool vec = cols % 4 == 0 && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)w & 15u) == 0 &&
+                   ((uintptr_t)y & 7u) == 0;
+  const int v = (cols / 4 + kThreads - 1) / kThreads;
+  const dim3 grid(rows), block(kThreads);
+  if (vec && v <= 1)
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, 1>), grid, block, 0, stream, x, w, yy, cols, eps);
+  else if (vec && v == 2)
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, 2>), grid, block, 0, stream, x, w, yy, cols, eps);
+  else if (vec && v == 3)
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, 3>), grid, block, 0, stream, x, w, yy, cols, eps);
+  else if (vec && v == 4)
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, 4>), grid, block, 0, stream, x, w, yy, cols, eps);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<T>, grid, block, 0, stream, x, w, yy, cols, eps);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_rmsnorm(const float* x, const float* w, void* y, int rows, int cols, float eps,
                           int dtype, hipStream_t stream) {
   if (rows <= 0) return hipSuccess;
   switch (dtype) {
-    case kBf16:
-      hipLaunchKernelGGL(rmsnorm_kernel<kBf16>, dim3(rows), dim3(kThreads), 0, stream, x, w,
-                         static_cast<uint16_t*>(y), cols, eps);
-      break;
-    case kF16:
-      hipLaunchKernelGGL(rmsnorm_kernel<kF16>, dim3(rows), dim3(kThreads), 0, stream, x, w,
-                         static_cast<uint16_t*>(y), cols, eps);
-      break;
+    case kBf16: return launch_t<kBf16>(x, w, y, rows, cols, eps, stream);
+    case kF16: return launch_t<kF16>(x, w, y, rows, cols, eps, stream);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 }  // namespace imq
