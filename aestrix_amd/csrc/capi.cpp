@@ -24,6 +24,7 @@ imq_ctx::~imq_ctx() {
   }
   for (auto& kv : split_ws)
     if (kv.second.first) (void)hipFree(kv.second.first);
+  for (void* p : retired_ws) (void)hipFree(p);
 }
 
 namespace imq {
@@ -153,8 +154,9 @@ enum class Regime { kAuto, kGemv, kGemm };
 
 // The split-K workspace of stream st, at least `need` bytes; empty (run
 // unsplit) when it would have to grow during stream capture or the
-// allocation fails.  Growing waits for the stream's earlier work, which may
-// still use the old buffer.
+// allocation fails.  A workspace that is outgrown is retired, not freed: a
+// graph captured earlier on this stream still addresses it, and so may the
+// stream's queued work; retired buffers are freed with the context.
 imq::SplitWs split_ws(imq_ctx* ctx, hipStream_t st, size_t need) {
   if (need == 0) return {};
   std::lock_guard<std::mutex> lk(ctx->ws_mu);
@@ -165,19 +167,12 @@ imq::SplitWs split_ws(imq_ctx* ctx, hipStream_t st, size_t need) {
     (void)hipGetLastError();
     return {};
   }
-  if (e.first) {
-    if (hipStreamSynchronize(st) != hipSuccess) {
-      (void)hipGetLastError();
-      return {};
-    }
-    (void)hipFree(e.first);
-    e = {nullptr, 0};
-  }
   void* p = nullptr;
   if (hipMalloc(&p, need) != hipSuccess) {
     (void)hipGetLastError();
     return {};
   }
+  if (e.first) ctx->retired_ws.push_back(e.first);
   e = {p, need};
   return {static_cast<float*>(p), need};
 }

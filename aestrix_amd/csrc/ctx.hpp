@@ -57,9 +57,11 @@ struct imq_ctx {
   std::unique_ptr<imq::CopyPool> copy_pool;  // created with the staging buffers
   // Split-K workspaces of the qGEMM, one per stream: calls on one stream run
   // in order, so they never overlap on a workspace.  Grown (never shrunk) on
-  // demand outside stream capture.
+  // demand outside stream capture; an outgrown one is kept until the context
+  // is destroyed (graphs captured earlier may still address it).
   std::mutex ws_mu;
   std::unordered_map<hipStream_t, std::pair<void*, size_t>> split_ws;
+  std::vector<void*> retired_ws;  // outgrown workspaces, freed with the context
 
   ~imq_ctx();
 };

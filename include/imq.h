@@ -114,10 +114,12 @@ int imq_dequantize(imq_ctx* ctx, const uint32_t* w, const void* scales, const vo
  * time).  When the output tiles are too few to fill the GPU, the qGEMM splits
  * K: fp32 partial sums go to a workspace the context keeps per stream (grown
  * on first use, outside stream capture; under capture a call that would need
- * a larger one runs unsplit) and a second kernel adds them in order, so the
- * result is deterministic but its fp32 summation order differs from
- * imq_qgemm's.  Calls that share a context must not run on the same stream
- * concurrently with a graph replay of an earlier call on that stream. */
+ * a larger one runs unsplit; an outgrown workspace stays allocated until
+ * imq_destroy, so graphs captured earlier stay valid) and a second kernel
+ * adds them in order, so the result is deterministic but its fp32 summation
+ * order differs from imq_qgemm's.  A graph replay of a captured call and
+ * other calls on the stream it was captured on share that stream's
+ * workspace: do not run them concurrently. */
 int imq_qmm_t(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
               const void* x, void* y, int k, int n, int m, int group_size, int bits,
               imq_dtype dtype, imq_stream stream);

@@ -229,8 +229,9 @@ def test_split_k_dispatcher(m, n, k):
 def test_split_k_dispatcher_under_graph_capture():
     """A split-K call captured in a graph on a stream whose workspace exists
     replays to the eager bits, with other device work and synchronizations
-    between replays; captured on a stream that never ran it (no workspace, none
-    grown under capture) it runs unsplit, within tolerance of the oracle."""
+    between replays, also after a larger call outgrew that workspace; captured
+    on a stream that never ran it (no workspace, none grown under capture) it
+    runs unsplit, within tolerance of the oracle."""
     m, n, k = 40, 1000, 2560
     note(f"split-K dispatcher under graph capture M={m} N={n} K={k}")
     p = synth.make_problem(m, n, k, seed=25)
@@ -251,6 +252,17 @@ def test_split_k_dispatcher_under_graph_capture():
         g.replay()
         torch.cuda.synchronize()
         assert np.array_equal(bits(y), eager), f"replay {rep}"
+    # A larger split call on the same stream outgrows its workspace; the
+    # graph still addresses the old one, which must stay allocated.
+    pb = synth.make_problem(512, 2560, 9728, seed=26)
+    xb, wb, sb, bb = synth.to_device(pb)
+    with torch.cuda.stream(side):
+        imq.quantized_matmul(xb, wb, sb, bb)
+    side.synchronize()
+    y.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(y), eager), "replay after the workspace grew"
     fresh = torch.cuda.Stream()
     y2 = torch.empty_like(y)
     g2 = torch.cuda.CUDAGraph()
