@@ -191,9 +191,15 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
   // The qGEMV kernel addresses one 16-row block of x with 32-bit byte offsets.
   if (regime != Regime::kGemm && (size_t)std::min(m, imq::kQgemvMaxM) * k * es >= ((size_t)1 << 31))
     return fail(ctx, IMQ_EINVAL, "%s: K=%d too long for the qGEMV kernel", fn, k);
+  // The qGEMV kernel addresses the packed weights with 32-bit byte offsets.
+  const bool w_fits_gemv = (size_t)n * (size_t)k / 2 < ((size_t)1 << 32);
+  if (!w_fits_gemv && (regime == Regime::kGemv || dtype == IMQ_F32))
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: %zu bytes of packed weights: the qGEMV kernel takes "
+                "under 4 GiB", fn, (size_t)n * (size_t)k / 2);
   if ((rc = bind_device(ctx)) != IMQ_OK) return rc;
   const bool gemv = regime == Regime::kGemv ||
-                    (regime == Regime::kAuto && (m <= imq::kDispatchGemvMaxM || dtype == IMQ_F32));
+                    (regime == Regime::kAuto && w_fits_gemv &&
+                     (m <= imq::kDispatchGemvMaxM || dtype == IMQ_F32));
   auto st = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
   if (!gemv) {

@@ -125,7 +125,9 @@ int imq_qmm_t(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* b
               imq_dtype dtype, imq_stream stream);
 
 /* The skinny regime alone (1 <= M <= 16): register dequant, fp32 dot products,
- * cross-lane reductions; no matrix cores.  Same contract as imq_qmm_t. */
+ * cross-lane reductions; no matrix cores.  Same contract as imq_qmm_t, for
+ * packed weights under 4 GiB (IMQ_EUNSUPPORTED above; imq_qmm_t then runs
+ * bf16 / f16 at any M on the MFMA kernel). */
 int imq_qgemv(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
               const void* x, void* y, int k, int n, int m, int group_size, int bits,
               imq_dtype dtype, imq_stream stream);

@@ -278,6 +278,36 @@ def test_split_k_dispatcher_under_graph_capture():
         assert_close(bits(y2), want, f"unsplit capture, replay {rep}")
 
 
+def test_weights_of_4_gib_take_the_64_bit_path():
+    """Packed weights of 4 GiB are past the qGEMV kernel's 32-bit offsets: the
+    dispatcher runs M=1 on the MFMA path's register-staged kernel, imq_qgemv
+    refuses.  Every word is 0x76543210 (codes 0..7 in k order) with one scale
+    and bias, so a one-hot x row picks the weight of code k % 8 in every row."""
+    n, k = 262144, 32768  # n * k / 2 = 4 GiB
+    note(f"4 GiB weights N={n} K={k} M=1")
+    w = torch.full((n, k // 8), 0x76543210, dtype=torch.int32, device="cuda")
+    s_bits, b_bits = 0x3C23, 0xBD23  # bf16 0.00995..., -0.0398...
+    def as_i16(v):
+        return int(np.array([v], np.uint16).view(np.int16)[0])
+
+    s = torch.full((n, k // 64), as_i16(s_bits), dtype=torch.int16, device="cuda")
+    b = torch.full((n, k // 64), as_i16(b_bits), dtype=torch.int16, device="cuda")
+    s, b = s.view(torch.bfloat16), b.view(torch.bfloat16)
+    col = 12345
+    x = torch.zeros((1, k), dtype=torch.bfloat16, device="cuda")
+    x[0, col] = 1.0
+    y = bits(imq.quantized_matmul(x, w, s, b))
+    q = col % 8
+    sv = ref.bf16_to_f32(np.array([s_bits], np.uint16))[0]
+    bv = ref.bf16_to_f32(np.array([b_bits], np.uint16))[0]
+    want = ref.f32_to_bf16(np.array([np.float32(sv * np.float32(q)) + bv], np.float32))[0]
+    assert np.all(y == want), (np.unique(y), want)
+    with pytest.raises(_lib.ImqUnsupported):
+        imq.qgemv(x, w, s, b)
+    del w, s, b
+    torch.cuda.empty_cache()
+
+
 def test_small_tiles_plain_qgemm():
     """imq_qgemm at M <= 64 runs 32- and 64-row tiles (no split)."""
     for m in (17, 33, 64):
