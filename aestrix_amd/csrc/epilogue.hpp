@@ -31,8 +31,12 @@ struct EpStore {
   __device__ __forceinline__ void emit1(int row, int col, uint16_t v) const {
     y[(size_t)row * ldy + col] = v;
   }
+  // Streamed (non-temporal): the output is not read back by this kernel and
+  // should not push the activation and weight panels other tiles still read
+  // out of the L2 (+0.3-0.7% on the large shapes).
   __device__ __forceinline__ void emit8(int row, int col, uint4 v) const {
-    *reinterpret_cast<uint4*>(y + (size_t)row * ldy + col) = v;
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v),
+                                reinterpret_cast<u32x4_t*>(y + (size_t)row * ldy + col));
   }
 };
 
