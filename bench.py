@@ -9,6 +9,7 @@ over that synthetic batch, inputs resident in HBM.  The same line carries:
 * qgemv      -- M=1/4/16 on the text-encoder MLP shapes [9728x2560] and
                 [2560x9728], GB/s of algorithmic bytes against 8 TB/s, with the
                 weights rotated over enough copies to miss the 256 MB MALL;
+* qgemv_f32  -- the conditioner's M=1 f32 qmm ([18432x3072], [3072x256]), GB/s;
 * dequant    -- the two projections of a DiT single-stream block, GB/s;
 * qgemm_shapes -- the other qGEMM shapes (PR1 1024x9216x3072, single-block
                 pair);
@@ -129,6 +130,33 @@ def bench_qgemv(imq, synth, torch, copies: int = 48, ms_list=(1, 4, 16)) -> dict
                                       "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts}
             log(f"qgemv M={m} N={n} K={k}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
         del ws, ss, bs
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_qgemv_f32(imq, synth, torch, copies: int = 24) -> dict:
+    """The conditioner's M=1 qmm with f32 x, scales, biases and y
+    (DirectConditioner.swift:48,75-84): its largest projection [18432x3072]
+    and a [3072x256] one, weights rotated over enough copies to miss the MALL."""
+    out = {}
+    for (n, k) in ((18432, 3072), (3072, 256)):
+        p = synth.make_problem(1, n, k, seed=5)
+        x, w, s, b = synth.to_device(p)
+        x, s, b = x.float(), s.float(), b.float()
+        reps = copies if n * k >= (1 << 24) else 4
+        ws = [w.clone() for _ in range(reps)]
+        ss = [s.clone() for _ in range(reps)]
+        bs = [b.clone() for _ in range(reps)]
+        ys = [torch.empty((1, n), dtype=torch.float32, device="cuda") for _ in range(reps)]
+        launches = [(lambda i=i: imq.quantized_matmul(x, ws[i], ss[i], bs[i], out=ys[i]))
+                    for i in range(reps)]
+        ms = time_graph(launches)
+        byts = 4 * k + n * k // 2 + 2 * 4 * n * (k // 64) + 4 * n
+        gbs = byts / (ms * 1e-3) / 1e9
+        out[f"M1_N{n}_K{k}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                                "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts}
+        log(f"qgemv f32 M=1 N={n} K={k}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
+        del ws, ss, bs, ys
         torch.cuda.empty_cache()
     return out
 
@@ -434,6 +462,7 @@ def main() -> int:
     extra = {}
     if not args.only_target:
         extra["qgemv"] = bench_qgemv(imq, synth, torch)
+        extra["qgemv_f32"] = bench_qgemv_f32(imq, synth, torch)
         extra["dequant"] = bench_dequant(imq, synth, torch)
         extra["qgemm_shapes"] = {
             "M1024_N9216_K3072": bench_qgemm_shape(imq, synth, torch, 1024, 9216, 3072),
