@@ -30,9 +30,12 @@
  *   - Kernel calls are asynchronous on the given stream (NULL = the device's
  *     null stream).  imq_stream_sync is the blocking wait, the counterpart of
  *     waitUntilCompleted (DirectDiTStep.swift:968-970).
- *   - Caller inputs are never written.  Kernels allocate nothing.
+ *   - Caller inputs are never written.  The kernel entry points allocate
+ *     nothing, except that imq_qmm_t grows the context's split-K workspace of
+ *     a stream (hipMalloc) the first time a call on that stream needs it.
  *   - A context belongs to one device.  Calls on one context from several
- *     threads are safe; the last-error text is per context.
+ *     threads are safe; the last-error text is per context (with several
+ *     threads, that of whichever call failed last).
  */
 #ifndef IMQ_H
 #define IMQ_H

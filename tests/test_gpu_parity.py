@@ -357,6 +357,41 @@ def test_runs_on_a_side_stream():
     assert np.array_equal(bits(y), base)
 
 
+def test_one_context_from_several_threads():
+    """Four host threads share the device's context, each on its own stream,
+    with split-K shapes (each stream's workspace is created and grown while the
+    others run): every result equals the single-threaded one."""
+    import threading
+
+    note("one context, four threads, four streams")
+    shapes = [(40, 1000, 2560), (96, 512, 4096), (300, 512, 768), (17, 384, 512)]
+    probs = [synth.make_problem(m, n, k, seed=40 + i) for i, (m, n, k) in enumerate(shapes)]
+    devs = [synth.to_device(p) for p in probs]
+    want = [bits(imq.quantized_matmul(*d)) for d in devs]
+    got = [[None] * 5 for _ in devs]
+    errors = []
+
+    def worker(i):
+        try:
+            st = torch.cuda.Stream()
+            with torch.cuda.stream(st):
+                for r in range(5):
+                    got[i][r] = imq.quantized_matmul(*devs[i])
+            st.synchronize()
+        except Exception as e:  # reported below, on the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(devs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not errors, errors
+    for i, ys in enumerate(got):
+        for r, y in enumerate(ys):
+            assert np.array_equal(bits(y), want[i]), (shapes[i], r)
+
+
 def test_argument_errors_are_reported():
     p = synth.make_problem(4, 64, 128, seed=20)
     x, w, s, b = synth.to_device(p)
