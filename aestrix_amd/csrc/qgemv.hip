@@ -298,9 +298,10 @@ int tile_len(int k, int mr, int g, int eb) {
 
 // Each candidate G gives n * G / (64 R) waves and uses tch / (G U) of its
 // lanes' chunk slots per tile; pick the one with the most useful waves,
-// counting at most 4096 for M <= 2 and 2048 above (where more waves stopped
-// paying for idle lanes on the shapes measured, 9728 x 2560 and 2560 x 9728
-// at M = 1 ... 16).
+// counting at most 4096 for M <= 4, 2048 for M <= 8 and 1024 above: beyond
+// those counts more waves stopped paying for idle lanes (a sweep of every G
+// on 9728 x 2560 and 2560 x 9728 at M = 1, 2, 4, 8, 16 picks the fastest G
+// in all ten cases with these caps).
 // IMQ_QGEMV_LANES=16|32|64 overrides.
 Plan make_plan(int k, int n, int mr, int eb) {
   static const int forced = [] {
@@ -316,7 +317,8 @@ Plan make_plan(int k, int n, int mr, int eb) {
     const int kt = tile_len(k, mr, g, eb);
     const int tch = kt / 32;
     const int u = (tch + g - 1) / g;
-    const double waves = std::min((double)n * g / (64.0 * r), mr <= 2 ? 4096.0 : 2048.0);
+    const double cap = mr <= 4 ? 4096.0 : mr <= 8 ? 2048.0 : 1024.0;
+    const double waves = std::min((double)n * g / (64.0 * r), cap);
     const double score = waves * tch / (double)(g * u);
     if (score > best_score * 1.02) {
       best = Plan{g, kt, u};
