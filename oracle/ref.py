@@ -152,7 +152,13 @@ def _stats(y: np.ndarray, o: np.ndarray) -> dict:
     omax = float(np.max(np.abs(o))) if o.size else 0.0
     rms = float(np.sqrt(np.mean(o * o))) if o.size else 0.0
     floor = np.maximum(np.abs(o), 1e-3 * rms) if o.size else o
+    # Cosine similarity of the flattened outputs: the reference's own qmm
+    # parity criterion is cosine >= 0.99999 (DirectQmmSpike.swift:141-153).
+    ny, no = float(np.linalg.norm(y)), float(np.linalg.norm(o))
+    cosine = float(np.dot(y.ravel(), o.ravel()) / (ny * no)) if ny > 0 and no > 0 else \
+        (1.0 if ny == no else 0.0)
     return {
+        "cosine": cosine,
         "mae": float(np.mean(d)) if d.size else 0.0,
         "max_abs": float(np.max(d)) if d.size else 0.0,
         "max_rel_normwise": float(np.max(d) / omax) if d.size and omax > 0 else 0.0,

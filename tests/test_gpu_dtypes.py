@@ -30,6 +30,7 @@ pytestmark = pytest.mark.gpu
 
 MAE_TOL = 1e-3
 NORMWISE_TOL = 1e-2
+COSINE_MIN = 0.99999  # the reference's qmm parity bar (DirectQmmSpike.swift:141-153)
 TORCH = {np.float16: torch.float16, np.float32: torch.float32}
 
 
@@ -69,10 +70,11 @@ def host(t: torch.Tensor) -> np.ndarray:
 def assert_close(y: np.ndarray, want: np.ndarray, what: str) -> None:
     st = ref.error_stats_values(y, want)
     note(f"  {what}: mae={st['mae']:.3g} normwise={st['max_rel_normwise']:.3g} "
-         f"bit_exact={st['bit_exact_frac']:.4f}")
+         f"bit_exact={st['bit_exact_frac']:.4f} cosine={st['cosine']:.7f}")
     assert np.all(np.isfinite(y)), what
     assert st["mae"] <= MAE_TOL, (what, st)
     assert st["max_rel_normwise"] <= NORMWISE_TOL, (what, st)
+    assert st["cosine"] >= COSINE_MIN, (what, st)
 
 
 @pytest.mark.parametrize("dtype", [np.float16, np.float32])

@@ -22,6 +22,7 @@ pytestmark = pytest.mark.gpu
 
 MAE_TOL = 1e-3
 NORMWISE_TOL = 1e-2
+COSINE_MIN = 0.99999  # the reference's qmm parity bar (DirectQmmSpike.swift:141-153)
 TORCH = {np.float16: torch.float16}
 
 
@@ -65,8 +66,9 @@ def to_np(t: torch.Tensor) -> np.ndarray:
 def assert_close(y: np.ndarray, want: np.ndarray, what: str) -> None:
     st = ref.error_stats_values(y.astype(np.float64), want.astype(np.float64))
     note(f"  {what}: mae={st['mae']:.3g} normwise={st['max_rel_normwise']:.3g} "
-         f"bit_exact={st['bit_exact_frac']:.4f}")
+         f"bit_exact={st['bit_exact_frac']:.4f} cosine={st['cosine']:.7f}")
     assert st["mae"] <= MAE_TOL and st["max_rel_normwise"] <= NORMWISE_TOL, (what, st)
+    assert st["cosine"] >= COSINE_MIN, (what, st)
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])

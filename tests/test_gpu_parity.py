@@ -3,8 +3,9 @@
 Bars (stated here, applied below):
 * dequantize: bit-exact against RNE_bf16(fl32(fl32(s*q) + b)).
 * qGEMV / qGEMM: against oracle = RNE_bf16(x . deq(W)^T accumulated in double)
-  with the bit-exact bf16 dequant: mean |y - oracle| <= MAE_TOL and
-  max |y - oracle| / max |oracle| <= NORMWISE_TOL.
+  with the bit-exact bf16 dequant: mean |y - oracle| <= MAE_TOL,
+  max |y - oracle| / max |oracle| <= NORMWISE_TOL, and the reference's own
+  qmm criterion, cosine(y, oracle) >= COSINE_MIN (DirectQmmSpike.swift:141-153).
 * one-hot activations make y a column of deq(W): that must be bit-exact in
   both matmul kernels (it pins their fused in-register dequantization).
 """
@@ -26,6 +27,7 @@ pytestmark = pytest.mark.gpu
 
 MAE_TOL = 1e-3
 NORMWISE_TOL = 1e-2
+COSINE_MIN = 0.99999  # the reference's qmm parity bar (DirectQmmSpike.swift:141-153)
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
 
 
@@ -55,9 +57,10 @@ def bits(t: torch.Tensor) -> np.ndarray:
 def assert_close(y_bits: np.ndarray, oracle_bits: np.ndarray, what: str) -> dict:
     st = ref.error_stats(y_bits, oracle_bits)
     note(f"  {what}: mae={st['mae']:.3g} normwise={st['max_rel_normwise']:.3g} "
-         f"bit_exact={st['bit_exact_frac']:.4f}")
+         f"bit_exact={st['bit_exact_frac']:.4f} cosine={st['cosine']:.7f}")
     assert st["mae"] <= MAE_TOL, (what, st)
     assert st["max_rel_normwise"] <= NORMWISE_TOL, (what, st)
+    assert st["cosine"] >= COSINE_MIN, (what, st)
     return st
 
 
