@@ -134,10 +134,14 @@ struct EpSwiGLU {
   float in_scale;
   float out_scale;
   bool vec;
+  // The sigmoid's reciprocal is v_rcp_f32 (1 ulp) rather than a correctly
+  // rounded division: the stage runs after the K loop with nothing to hide
+  // it, and the division's ten-instruction sequence per output was most of
+  // its cost.  exp(-g) = inf for very negative g gives rcp = 0, g * 0 = -0.
   __device__ __forceinline__ float value2(float acc_g, float acc_u) const {
     const float g = round_to(acc_g, T) * in_scale;
     const float u = round_to(acc_u, T) * in_scale;
-    const float sig = 1.0f / (1.0f + __expf(-g));
+    const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
     return g * sig * u * out_scale;
   }
   __device__ __forceinline__ void emit1(int row, int j, uint16_t v) const {

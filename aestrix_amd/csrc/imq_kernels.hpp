@@ -20,9 +20,12 @@ hipError_t launch_qgemv(const uint32_t* w, const void* scales, const void* biase
 // fp32 scratch for split-K partial sums.  With too few output tiles to fill
 // the chip, the MFMA kernel splits K, writes each split's partial sums here
 // and a second kernel adds them; a null or short workspace runs unsplit.
+// cus: the compute units the tile planner counts on (0: the device's); a
+// launch that shares the GPU with another stream's plans for its share.
 struct SplitWs {
   float* p = nullptr;
   size_t bytes = 0;
+  int cus = 0;
 };
 
 // y[m][n] = x . deq(W)^T, any m >= 1, T in {bf16, f16}; MFMA.

@@ -912,9 +912,10 @@ hipError_t launch_big_ep(const uint32_t* w, const uint16_t* scales, const uint16
     gate_row = ep.gate_row;
     up_row = ep.up_row;
   }
-  BigPlan p = pick_big_plan(m, cols, k, device_cus(), kSmall, ws.p != nullptr);
+  const int cus = ws.cus > 0 ? ws.cus : device_cus();
+  BigPlan p = pick_big_plan(m, cols, k, cus, kSmall, ws.p != nullptr);
   if (p.splits > 1 && ws.bytes < (size_t)p.splits * m * cols * sizeof(float))
-    p = pick_big_plan(m, cols, k, device_cus(), kSmall, false);  // no room for the partial sums
+    p = pick_big_plan(m, cols, k, cus, kSmall, false);  // no room for the partial sums
   if (p.splits == 1) return launch_big_mt<T>(p.mt, w, scales, biases, x, ep, k, n, m, stream);
   const EpPartial<EP::kPair> part{ws.p, cols, width, gate_row, up_row};
   const hipError_t e =

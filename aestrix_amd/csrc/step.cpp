@@ -39,6 +39,9 @@ struct imq_dit_step {
   float* gates = nullptr;   // fp32 [4 n_double + n_single][dim]
   imq::SplitWs split;       // partial sums of the projections that split K
   imq::SplitWs split_txt;   // the same for the double blocks' text rows (side stream)
+  // CUs the double blocks' image / text chains plan for where they run side by
+  // side (rows in proportion, the text share rounded up).
+  int cus_img = 0, cus_txt = 0;
   hipStream_t cap = nullptr;
   // The double blocks' text-row projections run on `side`, beside the image
   // rows on the main stream, forked and joined by these events.
@@ -83,6 +86,14 @@ hipError_t encode(imq_dit_step* st, hipStream_t s) {
   };
   auto rows = [&](char* base, int row0, int width) { return base + (size_t)row0 * width * es; };
   hipStream_t t = st->side;
+  // The image and text chains each plan their tiles for their share of the
+  // CUs, so that both fit side by side in one tile round: at 4096 + 512 rows
+  // and dim 3072, 192 + 24 tiles of 256 rows on 256 CUs instead of the 228
+  // tiles of 224 rows the image rows take alone.  The SwiGLU projections keep
+  // the whole device (1152 tiles, 4.5 rounds): the text rows fill the last.
+  imq::SplitWs wi = st->split, wt = st->split_txt;
+  wi.cus = st->cus_img;
+  wt.cus = st->cus_txt;
   float* Xt = st->X;
   float* Xi = st->X + (size_t)d.l_txt * dim;
   for (int b = 0; b < d.n_double; ++b) {
@@ -99,15 +110,15 @@ hipError_t encode(imq_dit_step* st, hipStream_t s) {
     fork();
     for (int q = 0; q < 3; ++q)
       ok(imq::launch_qgemm(W[q].w, W[q].scales, W[q].biases, nXi, rows(outs[q], d.l_txt, dim), dim,
-                           dim, d.l_img, T, s, st->split));
+                           dim, d.l_img, T, s, wi));
     // to_out / to_add_out on the V rows (the attention output's stand-in).
     ok(imq::launch_qgemm_gate_add(W[6].w, W[6].scales, W[6].biases, rows(st->V, d.l_txt, dim), Xi,
-                                  g, Xi, dim, dim, d.l_img, 1.0f, T, s, st->split));
+                                  g, Xi, dim, dim, d.l_img, 1.0f, T, s, wi));
     for (int q = 0; q < 3; ++q)
       ok(imq::launch_qgemm(W[3 + q].w, W[3 + q].scales, W[3 + q].biases, nXt, rows(outs[q], 0, dim),
-                           dim, dim, d.l_txt, T, t, st->split_txt));
+                           dim, dim, d.l_txt, T, t, wt));
     ok(imq::launch_qgemm_gate_add(W[7].w, W[7].scales, W[7].biases, rows(st->V, 0, dim), Xt,
-                                  g + dim, Xt, dim, dim, d.l_txt, 1.0f, T, t, st->split_txt));
+                                  g + dim, Xt, dim, dim, d.l_txt, 1.0f, T, t, wt));
     join();
     ok(imq::launch_rmsnorm(st->X, st->norm_w, st->nX, J, dim, kEps, T, s));
     fork();
@@ -115,12 +126,12 @@ hipError_t encode(imq_dit_step* st, hipStream_t s) {
                                 ffi, dim, 2 * ffi, d.l_img, ffi, 0, ffi, 1.0f, 1.0f, T, s,
                                 st->split));
     ok(imq::launch_qgemm_gate_add(W[9].w, W[9].scales, W[9].biases, rows(st->SW, d.l_txt, ffi), Xi,
-                                  g + 2 * dim, Xi, ffi, dim, d.l_img, 1.0f, T, s, st->split));
+                                  g + 2 * dim, Xi, ffi, dim, d.l_img, 1.0f, T, s, wi));
     ok(imq::launch_qgemm_swiglu(W[10].w, W[10].scales, W[10].biases, nXt, rows(st->SW, 0, ffi), ffi,
                                 dim, 2 * ffi, d.l_txt, ffi, 0, ffi, 1.0f, 1.0f, T, t,
                                 st->split_txt));
     ok(imq::launch_qgemm_gate_add(W[11].w, W[11].scales, W[11].biases, rows(st->SW, 0, ffi), Xt,
-                                  g + 3 * dim, Xt, ffi, dim, d.l_txt, 1.0f, T, t, st->split_txt));
+                                  g + 3 * dim, Xt, ffi, dim, d.l_txt, 1.0f, T, t, wt));
     join();
   }
   const int cw = dim + ffi;
@@ -263,6 +274,15 @@ int imq_dit_step_create(imq_ctx* ctx, const imq_dit_dims* dims, const imq_qweigh
   st->gates = reinterpret_cast<float*>(a + off[9]);
   st->split = imq::SplitWs{reinterpret_cast<float*>(a + off[10]), sizes[10]};
   st->split_txt = imq::SplitWs{reinterpret_cast<float*>(a + off[11]), sizes[11]};
+  {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    st->cus_txt = std::max(1, (int)(((size_t)cus * d.l_txt + J - 1) / J));
+    st->cus_img = std::max(1, cus - st->cus_txt);
+  }
   // Zero everything (the attention half of C stays zero), ones for the
   // conditioning vectors.  Plain (uncaptured) memsets at set-up.
   e = hipMemset(st->arena, 0, total);
