@@ -299,9 +299,10 @@ def bench_dit_step(torch) -> dict:
     h = torch.randn((d.l_img, d.dim), device="cuda")
     e = torch.randn((d.l_txt, d.dim), device="cuda")
     out = torch.empty((d.joint, d.dim), device="cuda")
-    for _ in range(3):
+    t_pre = time.perf_counter()
+    while time.perf_counter() - t_pre < PREWARM_S:
         step.run(h, e, out)
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -390,6 +391,8 @@ def main() -> int:
                          "(for counter runs)")
     ap.add_argument("--floors", action="store_true",
                     help="run the launch and streaming-read floor kernels only (for profiling runs)")
+    ap.add_argument("--only-step", action="store_true",
+                    help="run the whole DiT step benchmark only (for profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} requested, but this path runs on one GPU "
@@ -409,6 +412,9 @@ def main() -> int:
         return floors(torch)
     imq._lib.load()
     props = torch.cuda.get_device_properties(0)
+    if args.only_step:
+        bench_dit_step(torch)
+        return 0
     if args.only_hbm:
         bench_qgemv(imq, synth, torch, ms_list=(1,))
         bench_dequant(imq, synth, torch)
