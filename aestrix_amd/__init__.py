@@ -11,7 +11,8 @@ the C ABI of ``include/imq.h`` (``aestrix_amd/libimq.so``):
 
 ``quantized_matmul`` dispatches between the two matmul regimes;
 ``qmm_postscale`` / ``qmm_gate_add`` / ``qmm_swiglu`` fold the reference's
-post-qmm glue kernels into the MFMA kernel's epilogue.
+post-qmm glue kernels into the MFMA kernel's epilogue; ``cast_prescale`` and
+``apply_linear`` are the f16 sandwich around them (x / 16 to f16, qmm, x 16).
 """
 
 from ._lib import ImqError, ImqInvalid, ImqLibraryMissing, ImqUnsupported  # noqa: F401
@@ -20,6 +21,8 @@ from .ops import (  # noqa: F401
     GROUP_SIZE,
     Q,
     QuantizedLinear,
+    apply_linear,
+    cast_prescale,
     context,
     dequantize,
     qgemm,

@@ -73,6 +73,7 @@ SIGNATURES = {
     "imq_qmm_t": (_QMM, _i),
     "imq_qgemv": (_QMM, _i),
     "imq_qgemm": (_QMM, _i),
+    "imq_cast_prescale": ([_p, _p, _p, _sz, ctypes.c_float, _i, _p], _i),
     "imq_qmm_postscale": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, ctypes.c_float, _i, _i, _i, _p], _i),
     "imq_qmm_gate_add": ([_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, ctypes.c_float, _i, _i, _i,
                           _p], _i),

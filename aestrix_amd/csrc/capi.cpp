@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
@@ -401,6 +402,25 @@ int imq_qgemm(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* b
                  bits, dtype, stream);
 }
 
+
+int imq_cast_prescale(imq_ctx* ctx, const float* x, void* y, size_t count, float scale,
+                      imq_dtype dtype, imq_stream stream) {
+  const char* fn = "imq_cast_prescale";
+  if (!ctx) return fail(nullptr, IMQ_EINVAL, "%s: null context", fn);
+  if (dtype != IMQ_BF16 && dtype != IMQ_F16)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: dtype %d (bf16 and f16 are provided)", fn, (int)dtype);
+  if (!std::isfinite(scale) || scale == 0.0f)
+    return fail(ctx, IMQ_EINVAL, "%s: scale %g must be finite and nonzero", fn, (double)scale);
+  if (count == 0) return IMQ_OK;
+  if (!x || !y) return fail(ctx, IMQ_EINVAL, "%s: null device pointer", fn);
+  if (!aligned(x, 4) || !aligned(y, 2))
+    return fail(ctx, IMQ_EINVAL, "%s: x must be 4-byte and y 2-byte aligned", fn);
+  int rc = bind_device(ctx);
+  if (rc != IMQ_OK) return rc;
+  const hipError_t e =
+      imq::launch_prescale(x, y, count, scale, (int)dtype, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
+}
 
 int imq_qmm_postscale(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
                       const void* x, float* y, int k, int n, int m, float scale, int group_size,

@@ -63,6 +63,10 @@ hipError_t launch_qgemm_swiglu(const uint32_t* w, const void* scales, const void
                                int gate_row, int up_row, float in_scale, float out_scale, int dtype,
                                hipStream_t stream, SplitWs ws = {});
 
+// y[i] (T) = T(x[i] / scale) for i < count, x fp32; T in {bf16, f16}.
+hipError_t launch_prescale(const float* x, void* y, size_t count, float scale, int dtype,
+                           hipStream_t stream);
+
 // y[r][c] (T) = x[r][c] * rsqrt(mean(x[r]^2) + eps) * w[c], x fp32 [rows, cols].
 hipError_t launch_rmsnorm(const float* x, const float* w, void* y, int rows, int cols, float eps,
                           int dtype, hipStream_t stream);

@@ -1,0 +1,83 @@
+// prescale.hip -- the input half of the f16 quantized-linear sandwich.
+//
+// y[i] = T(x[i] / scale): AttentionUtils.compiledPreScale
+// (Sources/ImarelloMLX/AttentionUtils.swift:155-160, `(x / s).asType(.float16)`),
+// which applyLinearCore (:198-230) runs before the f16 qmm so that its f16
+// accumulation cannot overflow (scale 16, AttentionTuning.linearF16Scale).
+// The quotient is the correctly rounded fp32 division and the conversion to
+// T rounds to nearest even, as MLX's f32 divide and astype do, so the result
+// is bit-exact.  HBM-bound: 4 bytes read and 2 written per element.
+#include "imq_device.hpp"
+#include "imq_kernels.hpp"
+
+namespace imq {
+namespace {
+
+constexpr int kThreads = 256;
+
+// Eight elements per thread and iteration: two 16-byte loads, one 16-byte
+// store.  Requires x and y 16-byte aligned; n8 = count / 8.
+template <int T>
+__global__ __launch_bounds__(kThreads) void prescale_vec_kernel(const float4* __restrict__ x,
+                                                                uint4* __restrict__ y, size_t n8,
+                                                                float scale) {
+  const size_t stride = (size_t)gridDim.x * kThreads;
+  for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n8; i += stride) {
+    const float4 a = x[2 * i], b = x[2 * i + 1];
+    y[i] = make_uint4(Elem<T>::pack2(__fdiv_rn(a.x, scale), __fdiv_rn(a.y, scale)),
+                      Elem<T>::pack2(__fdiv_rn(a.z, scale), __fdiv_rn(a.w, scale)),
+                      Elem<T>::pack2(__fdiv_rn(b.x, scale), __fdiv_rn(b.y, scale)),
+                      Elem<T>::pack2(__fdiv_rn(b.z, scale), __fdiv_rn(b.w, scale)));
+  }
+}
+
+// Elements [first, count) one at a time (unaligned buffers, or the tail).
+template <int T>
+__global__ __launch_bounds__(kThreads) void prescale_kernel(const float* __restrict__ x,
+                                                            uint16_t* __restrict__ y, size_t first,
+                                                            size_t count, float scale) {
+  const size_t stride = (size_t)gridDim.x * kThreads;
+  for (size_t i = first + (size_t)blockIdx.x * kThreads + threadIdx.x; i < count; i += stride)
+    y[i] = Elem<T>::out(__fdiv_rn(x[i], scale));
+}
+
+// Enough workgroups to fill the device several times over; the kernels loop.
+unsigned grid_for(size_t items) {
+  const size_t want = (items + kThreads - 1) / kThreads;
+  return (unsigned)(want < 4096 ? (want > 0 ? want : 1) : 4096);
+}
+
+template <int T>
+hipError_t launch_t(const float* x, void* y, size_t count, float scale, hipStream_t stream) {
+  auto* yy = static_cast<uint16_t*>(y);
+  size_t done = 0;
+  if (((uintptr_t)x & 15u) == 0 && ((uintptr_t)y & 15u) == 0) {
+    const size_t n8 = count / 8;
+    if (n8 > 0) {
+      hipLaunchKernelGGL(prescale_vec_kernel<T>, dim3(grid_for(n8)), dim3(kThreads), 0, stream,
+                         reinterpret_cast<const float4*>(x), reinterpret_cast<uint4*>(yy), n8,
+                         scale);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+    done = n8 * 8;
+  }
+  if (done < count)
+    hipLaunchKernelGGL(prescale_kernel<T>, dim3(grid_for(count - done)), dim3(kThreads), 0, stream,
+                       x, yy, done, count, scale);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_prescale(const float* x, void* y, size_t count, float scale, int dtype,
+                           hipStream_t stream) {
+  if (count == 0) return hipSuccess;
+  switch (dtype) {
+    case kBf16: return launch_t<kBf16>(x, y, count, scale, stream);
+    case kF16: return launch_t<kF16>(x, y, count, scale, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace imq

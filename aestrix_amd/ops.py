@@ -9,6 +9,9 @@ The reference reaches the path through MLX ops and its direct engine:
   ``Sources/ImarelloDirect/DirectQmmSpike.swift:55-58``)          -> ``quantized_matmul``
 * ``QuantizedLinear`` built by ``quantize(model:groupSize:64,bits:4)``
   (``Sources/ImarelloDiT/TransformerWeights.swift:20``)            -> ``QuantizedLinear``
+* ``applyLinear`` / ``applyLinearCore`` with ``linearF16`` on
+  (``Sources/ImarelloDiT/AttentionUtils.swift:140-150,198-230``)  -> ``apply_linear``
+  (``cast_prescale`` + ``qmm_postscale``)
 * ``DirectDiTStep.qmm(enc, q, x:, xOff:, y:, yOff:, m:)``
   (``Sources/ImarelloDirect/DirectDiTStep.swift:374-406``)         -> ``qmm``
 
@@ -194,6 +197,25 @@ def _f32_out(out, shape, device, what):
     return out
 
 
+def cast_prescale(x: torch.Tensor, scale: float = 16.0, dtype: torch.dtype = torch.float16,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """T y = T(x / scale) for float32 x (``AttentionUtils.compiledPreScale``,
+    ``Sources/ImarelloDiT/AttentionUtils.swift:155-160``): bit-exact, one HIP kernel."""
+    _require(x.is_cuda and x.dtype == torch.float32, "x must be a float32 HIP tensor")
+    _require(dtype in (torch.float16, torch.bfloat16), f"dtype {dtype}: float16 or bfloat16")
+    x = x if x.is_contiguous() else x.contiguous()
+    if out is None:
+        out = torch.empty(x.shape, dtype=dtype, device=x.device)
+    _require(out.dtype == dtype and out.is_contiguous() and out.shape == x.shape
+             and out.device == x.device, f"out must be a contiguous {dtype} tensor shaped like x")
+    ctx = context(x.device)
+    with torch.cuda.device(x.device):
+        st = _lib.load().imq_cast_prescale(ctx, _ptr(x), _ptr(out), x.numel(), float(scale),
+                                           _DTYPES[dtype], _stream(x))
+    _lib.check(st, ctx)
+    return out
+
+
 def qmm_postscale(x, w, scales, biases, scale: float, group_size: int = GROUP_SIZE,
                   bits: int = BITS, out=None) -> torch.Tensor:
     """float32 y = float(T(x . deq(W)^T)) * scale in one kernel (the reference's
@@ -309,3 +331,21 @@ class QuantizedLinear:
 
     def dequantized(self) -> torch.Tensor:
         return dequantize(self.weight, self.scales, self.biases, self.group_size, self.bits)
+
+
+def apply_linear(linear: QuantizedLinear, x: torch.Tensor, scale: float = 16.0) -> torch.Tensor:
+    """float32 y = linear(x) through the f16 sandwich of ``AttentionUtils.applyLinear`` /
+    ``applyLinearCore`` with ``linearF16`` on (``Sources/ImarelloDiT/AttentionUtils.swift:140-150,
+    198-230``): x / scale rounded to f16 (``cast_prescale``), then the f16 qmm and the float32
+    x scale rescale in one kernel (``qmm_postscale``).  x is float32 of any leading shape; the
+    linear's scales and biases must be float16 (the DiT pack casts them at load,
+    ``TransformerWeights.swift:40-54``, exact for that pack; ``load_qlinear(..., IMQ_F16)``
+    does the same).  The static scale (``AttentionTuning.linearF16Scale``, 16) is mirrored;
+    ``linearDynamicScale``'s per-tensor scale is not.  ``linearChunkedSequence``
+    (``:233-261``) runs this in 512-row chunks to bound MLX temporaries; rows are independent,
+    so one launch over all rows gives the same values."""
+    _require(linear.scales.dtype == torch.float16,
+             f"the f16 path needs float16 scales and biases, got {linear.scales.dtype}")
+    x16 = cast_prescale(x, scale, torch.float16)
+    return qmm_postscale(x16, linear.weight, linear.scales, linear.biases, scale,
+                         linear.group_size, linear.bits)

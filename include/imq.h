@@ -151,6 +151,16 @@ int imq_qgemm(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* b
  * IMQ_EUNSUPPORTED); K % 256 == 0 (else IMQ_EUNSUPPORTED); any M >= 1.  Other
  * arguments as imq_qmm_t; fp32 arrays must be 4-byte aligned. */
 
+/* y[i] (T) = T(x[i] / scale) for i < count, x fp32: the pre-scale half of the
+ * f16 qmm sandwich, AttentionUtils.compiledPreScale (`(x / s).asType(.float16)`,
+ * AttentionUtils.swift:155-160, run by applyLinearCore :198-230 with s = 16).
+ * Bit-exact: the correctly rounded fp32 quotient, rounded to nearest even in
+ * T.  T is f16 or bf16 (f32: IMQ_EUNSUPPORTED); scale finite and nonzero;
+ * x 4-byte and y 2-byte aligned (16-byte alignment of both takes the vector
+ * kernel); count 0 is a no-op. */
+int imq_cast_prescale(imq_ctx* ctx, const float* x, void* y, size_t count, float scale,
+                      imq_dtype dtype, imq_stream stream);
+
 /* y[M, N] (fp32) = float(T(x . deq(W)^T)) * scale: dd_cast_postscale
  * (DirectDiTKernels.swift:199-209), the x16 after a /16 pre-scaled qmm. */
 int imq_qmm_postscale(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,

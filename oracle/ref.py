@@ -167,6 +167,17 @@ def _stats(y: np.ndarray, o: np.ndarray) -> dict:
 
 
 # ------------------------------------------------------------- glue stages
+def glue_prescale(x: np.ndarray, scale: float, dtype: str) -> np.ndarray:
+    """AttentionUtils.compiledPreScale (Sources/ImarelloDiT/AttentionUtils.swift:155-160):
+    ``(x / s).asType(T)`` on float32 x -- the fp32 quotient (IEEE, correctly
+    rounded), then RNE to T.  Returns float16 values ("f16") or bf16 bits ("bf16")."""
+    q = (np.asarray(x, dtype=np.float32) / np.float32(scale)).astype(np.float32)
+    if dtype == "f16":
+        with np.errstate(over="ignore"):
+            return q.astype(np.float16)
+    return f32_to_bf16(q)
+
+
 # The reference's post-qmm glue kernels (Sources/ImarelloDirect/DirectDiTKernels.swift)
 # on the T output of a qmm, in fp32 (the Metal kernels compute in float).
 # `y_t` is the qmm output as float32 values of T.

@@ -141,3 +141,65 @@ def test_epilogue_argument_checks():
     p2, x2, w2, s2, b2 = problem(8, 128, 192, "bf16", seed=53)
     with pytest.raises(NotImplementedError):
         imq.qmm_postscale(x2, w2, s2, b2, 1.0)  # K % 256 != 0
+
+
+def _t16_bits(t: torch.Tensor) -> np.ndarray:
+    torch.cuda.synchronize()
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("count,offset", [(1, 0), (7, 0), (8, 0), (1000003, 0), (4099, 1)])
+@pytest.mark.parametrize("scale", [16.0, 3.0, -0.5])
+def test_cast_prescale_bit_exact(dtype, count, offset, scale):
+    """cast_prescale equals the oracle's (x / s).asType(T) bit for bit: the vector
+    kernel (aligned, count / 8 chunks), the scalar tail and the unaligned path
+    (y one element into its buffer), with zeros of both signs, f16 overflow and NaN."""
+    note(f"cast_prescale {dtype} count={count} offset={offset} scale={scale}")
+    rng = np.random.default_rng(count + offset)
+    x = (rng.standard_normal(count) * np.exp2(rng.integers(-30, 22, count))).astype(np.float32)
+    specials = np.float32([0.0, -0.0, 65520 * 16, np.nan, 16 * (1 + 3 * 2 ** -11)])
+    x[:min(count, 5)] = specials[:min(count, 5)]
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    buf = torch.full((count + offset,), 1.5, dtype=tdt, device="cuda")
+    out = buf[offset:]
+    imq.cast_prescale(torch.from_numpy(x).cuda(), scale, tdt, out=out)
+    got = _t16_bits(out)
+    want = ref.glue_prescale(x, scale, dtype)
+    want = want.view(np.uint16) if dtype == "f16" else want
+    nan = np.isnan(x)
+    exp_mask, man_mask = (0x7C00, 0x03FF) if dtype == "f16" else (0x7F80, 0x007F)
+    assert np.all((got[nan] & exp_mask) == exp_mask) and np.all((got[nan] & man_mask) != 0)
+    assert np.array_equal(got[~nan], want[~nan]), np.flatnonzero(got[~nan] != want[~nan])[:8]
+    if offset:
+        assert torch.all(buf[:offset] == 1.5).item()
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 512, 768), (1, 64, 512)])
+def test_apply_linear_f16_sandwich(m, n, k):
+    """apply_linear (x / 16 to f16, f16 qmm, x 16 to f32) equals cast_prescale +
+    qmm_postscale bit for bit and the oracle's sandwich within the tolerance."""
+    note(f"apply_linear M={m} N={n} K={k}")
+    p, x, w, s, b = problem(m, n, k, "f16", seed=60)
+    xf = (x.float() * 24.0).reshape((1, m, k))  # float32 activations, |x| up to ~100
+    lin = imq.QuantizedLinear(w, s, b)
+    y = imq.apply_linear(lin, xf)
+    assert y.dtype == torch.float32 and tuple(y.shape) == (1, m, n)
+    unfused = imq.qmm_postscale(imq.cast_prescale(xf, 16.0), w, s, b, 16.0)
+    assert np.array_equal(to_np(y), to_np(unfused))
+    x16 = ref.glue_prescale(xf.cpu().numpy().reshape(m, k), 16.0, "f16")
+    q = ref.qmm_t_as(x16, p.w, s.cpu().numpy(), b.cpu().numpy(), np.float16).astype(np.float32)
+    assert_close(to_np(y).reshape(m, n), ref.glue_postscale(q, 16.0), "apply_linear")
+
+
+def test_prescale_argument_checks():
+    x = torch.ones(16, device="cuda")
+    with pytest.raises(ValueError):
+        imq.cast_prescale(x.half())  # x must be float32
+    with pytest.raises(imq.ImqInvalid):
+        imq.cast_prescale(x, 0.0)  # scale 0
+    with pytest.raises(imq.ImqInvalid):
+        imq.cast_prescale(x, float("inf"))
+    p, xb, w, s, b = problem(8, 128, 256, "bf16", seed=54)
+    with pytest.raises(ValueError):
+        imq.apply_linear(imq.QuantizedLinear(w, s, b), xb.float())  # bf16 scales

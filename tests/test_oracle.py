@@ -545,3 +545,65 @@ def test_rmsnorm_rows_matches_torch():
     want = torch.nn.functional.rms_norm(torch.from_numpy(x), (300,), torch.from_numpy(w),
                                         eps=1e-5).numpy()
     assert np.allclose(ref.rmsnorm_rows(x, w), want, rtol=1e-12, atol=1e-12)
+
+
+def _rne_format(fr: Fraction, mant: int, emin: int, emax: int) -> Fraction | float:
+    """Exact rational -> nearest value of a binary format with `mant` significand
+    bits (hidden bit included), normal exponents [emin, emax], subnormals,
+    ties to even; +-inf past the largest finite value."""
+    if fr == 0:
+        return Fraction(0)
+    sign = -1 if fr < 0 else 1
+    a = abs(fr)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    e = max(e, emin)
+    ulp = Fraction(2) ** (e - mant + 1)
+    units = a / ulp
+    n = units.numerator // units.denominator
+    rem = units - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    v = n * ulp
+    if v >= Fraction(2) ** (emax + 1):
+        return sign * float("inf")
+    return sign * v
+
+
+def test_glue_prescale_matches_exact_double_rounding():
+    """(x / s).asType(T): the fp32 quotient of the exact ratio (RNE), then RNE to
+    T, checked with rational arithmetic and an independent rounding, and against
+    torch's CPU division and conversions."""
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal(1500) * np.exp2(rng.integers(-30, 22, 1500))).astype(np.float32)
+    x = np.concatenate([x, np.float32([0.0, -0.0, 16.0, 16 * (1 + 2 ** -11), 16 * (1 + 3 * 2 ** -11),
+                                       65504 * 16, 65520 * 16, 2 ** -24 * 16, 2 ** -25 * 16,
+                                       3 * 2 ** -26 * 16])])
+    for scale in (16.0, 3.0, -0.5, 1e-3):
+        s32 = np.float32(scale)
+        for dtype, mant, emin, emax in (("f16", 11, -14, 15), ("bf16", 8, -126, 127)):
+            got = ref.glue_prescale(x, scale, dtype)
+            vals = got.astype(np.float64) if dtype == "f16" else ref.bf16_to_f32(got).astype(np.float64)
+            for xi, gi in zip(x.tolist(), vals.tolist()):
+                q32 = _rne_format(Fraction(xi) / Fraction(float(s32)), 24, -126, 127)
+                want = q32 if isinstance(q32, float) else _rne_format(Fraction(q32), mant, emin, emax)
+                assert gi == float(want), (xi, scale, dtype, gi, want)
+                if gi == 0:  # a zero keeps the quotient's sign
+                    assert np.signbit(gi) == (np.signbit(xi) != np.signbit(s32)), (xi, scale)
+            t = torch.from_numpy(x) / torch.tensor(s32)
+            tt = t.to(torch.float16 if dtype == "f16" else torch.bfloat16).float().numpy()
+            assert np.array_equal(vals.astype(np.float32), tt), (scale, dtype)
+
+
+def test_glue_prescale_checks_catch_truncation_mutant():
+    """A conversion by truncation instead of rounding must fail the exact check:
+    1 + 3 * 2^-11 is a tie that rounds to the even 1 + 2^-9 in f16, and
+    1 + 2^-8 + 2^-12 rounds up to 1 + 2^-7 in bf16; truncation keeps 1 + 2^-10 / 1."""
+    x = np.float32([16 * (1 + 3 * 2 ** -11), 16 * (1 + 2 ** -8 + 2 ** -12)])
+    f16 = ref.glue_prescale(x, 16.0, "f16")
+    bf16 = ref.bf16_to_f32(ref.glue_prescale(x, 16.0, "bf16"))
+    assert float(f16[0]) == float(_rne_format(Fraction(1 + 3 * 2 ** -11), 11, -14, 15)) == 1 + 2 ** -9
+    assert float(bf16[1]) == float(_rne_format(Fraction(1 + 2 ** -8 + 2 ** -12), 8, -126, 127)) == 1 + 2 ** -7
+    trunc_bf16 = ((x / np.float32(16)).view(np.uint32) >> np.uint32(16)).astype(np.uint16)
+    assert float(ref.bf16_to_f32(trunc_bf16)[1]) != float(bf16[1])
