@@ -11,6 +11,7 @@ over that synthetic batch, inputs resident in HBM.  The same line carries:
                 weights rotated over enough copies to miss the 256 MB MALL;
 * qgemv_f32  -- the conditioner's M=1 f32 qmm ([18432x3072], [3072x256]), GB/s;
 * dequant    -- the two projections of a DiT single-stream block, GB/s;
+* prescale   -- the f16 sandwich's pre-scale cast (x / 16 to f16) on [4608x3072] float32, GB/s;
 * qgemm_shapes -- the other qGEMM shapes (PR1 1024x9216x3072, single-block
                 pair);
 * qmm_small_m -- text-encoder shapes at M = 32, 128, 512 through the regime
@@ -181,6 +182,24 @@ def bench_dequant(imq, synth, torch, copies: int = 6) -> dict:
         del ws, ss, bs, os_
         torch.cuda.empty_cache()
     return out
+
+
+def bench_prescale(imq, torch, copies: int = 4) -> dict:
+    """The f16 sandwich's pre-scale cast (x / 16 to f16) on the single block's input
+    [4608 x 3072] float32: 6 bytes per element, buffers rotated past the MALL."""
+    m, k = 4608, 3072
+    xs = [torch.randn((m, k), device="cuda") for _ in range(copies)]
+    ys = [torch.empty((m, k), dtype=torch.float16, device="cuda") for _ in range(copies)]
+    launches = [(lambda i=i: imq.cast_prescale(xs[i], 16.0, torch.float16, out=ys[i]))
+                for i in range(copies)]
+    ms = time_graph(launches, replays=4)
+    byts = m * k * 6
+    gbs = byts / (ms * 1e-3) / 1e9
+    log(f"prescale [{m}x{k}] f32 -> f16: {ms * 1e3:.1f} us  {gbs:.0f} GB/s")
+    del xs, ys
+    torch.cuda.empty_cache()
+    return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts}
 
 
 def bench_qgemm_shape(imq, synth, torch, m, n, k, reps=10, dispatcher=False) -> dict:
@@ -470,6 +489,7 @@ def main() -> int:
         extra["qgemv"] = bench_qgemv(imq, synth, torch)
         extra["qgemv_f32"] = bench_qgemv_f32(imq, synth, torch)
         extra["dequant"] = bench_dequant(imq, synth, torch)
+        extra["prescale"] = bench_prescale(imq, torch)
         extra["qgemm_shapes"] = {
             "M1024_N9216_K3072": bench_qgemm_shape(imq, synth, torch, 1024, 9216, 3072),
             "M4608_N27648_K3072": bench_qgemm_shape(imq, synth, torch, 4608, 27648, 3072),
