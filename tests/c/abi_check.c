@@ -78,6 +78,8 @@ static void no_device_checks(void) {
         imq_last_error(NULL));
   imq_ctx** no_out = NULL;
   CHECK(imq_create(0, no_out) == IMQ_EINVAL, "imq_create with a null output pointer");
+  st = imq_cast_prescale(NULL, NULL, NULL, 4, 16.0f, IMQ_F16, NULL);
+  CHECK(st == IMQ_EINVAL, "prescale without a context -> %s", imq_status_string(st));
 }
 
 int main(int argc, char** argv) {
@@ -149,6 +151,30 @@ int main(int argc, char** argv) {
         CHECK(y[i * N + n] == want[n * K + cols[i]],
               "qmm_t M=%d one-hot row %d, column %d: 0x%04x, weight 0x%04x", m, i, n,
               y[i * N + n], want[n * K + cols[i]]);
+  }
+
+  /* x / 16 to f16, closed forms: 1, -2, 2^-5, the f16 maximum, and the tie
+   * 1 + 3 * 2^-11 that rounds to the even 1 + 2^-9. */
+  {
+    const float px[5] = {16.0f, -32.0f, 0.5f, 65504.0f * 16.0f, 16.0f * (1.0f + 3.0f / 2048.0f)};
+    const uint16_t pwant[5] = {0x3C00, 0xC000, 0x2800, 0x7BFF, 0x3C02};
+    uint16_t py[5] = {0};
+    void *dpx, *dpy;
+    OK(ctx, imq_malloc(ctx, sizeof(px), &dpx));
+    OK(ctx, imq_malloc(ctx, sizeof(py), &dpy));
+    OK(ctx, imq_memcpy_h2d(ctx, dpx, px, sizeof(px), stream));
+    OK(ctx, imq_cast_prescale(ctx, dpx, dpy, 5, 16.0f, IMQ_F16, stream));
+    OK(ctx, imq_memcpy_d2h(ctx, py, dpy, sizeof(py), stream));
+    OK(ctx, imq_stream_sync(ctx, stream));
+    for (int i = 0; i < 5; ++i)
+      CHECK(py[i] == pwant[i], "prescale element %d: 0x%04x, closed form 0x%04x", i, py[i], pwant[i]);
+    int pst = imq_cast_prescale(ctx, dpx, dpy, 5, 0.0f, IMQ_F16, stream);
+    CHECK(pst == IMQ_EINVAL, "prescale by 0 -> %s", imq_status_string(pst));
+    pst = imq_cast_prescale(ctx, dpx, dpy, 5, 16.0f, IMQ_F32, stream);
+    CHECK(pst == IMQ_EUNSUPPORTED, "prescale to f32 -> %s", imq_status_string(pst));
+    OK(ctx, imq_cast_prescale(ctx, NULL, NULL, 0, 16.0f, IMQ_F16, stream));
+    OK(ctx, imq_free(ctx, dpx));
+    OK(ctx, imq_free(ctx, dpy));
   }
 
   int st = imq_qmm_t(ctx, dw, ds, db, dx, dy, 100, N, 1, 64, 4, IMQ_BF16, stream);
