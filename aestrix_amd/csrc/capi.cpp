@@ -203,7 +203,10 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
                      (m <= imq::kDispatchGemvMaxM || dtype == IMQ_F32));
   auto st = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
-  if (!gemv) {
+  if (regime == Regime::kAuto && m >= imq::kDispatchSkinnyMinM && m <= imq::kDispatchSkinnyMaxM &&
+      imq::qskinny_supported(k, n, m, (int)dtype)) {
+    e = imq::launch_qskinny(w, s, b, x, y, k, n, m, (int)dtype, st);
+  } else if (!gemv) {
     // The dispatcher may split K over a workspace; imq_qgemm is the plain
     // tile kernel (the fused output stages equal it bit for bit).
     const imq::SplitWs ws = regime == Regime::kAuto

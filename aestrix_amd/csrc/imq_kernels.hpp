@@ -74,9 +74,26 @@ hipError_t launch_rmsnorm(const float* x, const float* w, void* y, int rows, int
 // Largest M the qGEMV kernel takes.
 constexpr int kQgemvMaxM = 16;
 // Largest bf16 / f16 M the regime dispatcher routes to the qGEMV kernel: from
-// M = 5 the MFMA kernel (K split when its tiles are few) is faster on the
-// text-encoder shapes (M = 8: 10.2 vs 14.1 us at [9728 x 2560]; M = 16: 10.8
-// vs 30.6 us), the qGEMV's VALU dequant and dot products growing with M.
+// M = 5 the matrix-core kernels are faster, the qGEMV's VALU dot products and
+// reductions growing with M.
 constexpr int kDispatchGemvMaxM = 4;
+
+// Largest M the weight-streaming MFMA kernel (qskinny.hip) takes.
+constexpr int kQskinnyMaxM = 16;
+// The M range the regime dispatcher routes to it (bf16 / f16, K % 128 == 0).
+// With the weights coming from HBM (text-encoder MLP shapes, 48 rotated
+// copies): M = 5 at [9728 x 2560] 9.96 us against 13.4 us for the split-K tile
+// kernel and 12.8 us for the qGEMV, M = 8 11.0 / 13.6 / 13.2 us, M = 16 14.1 /
+// 14.2 us; at [2560 x 9728] M = 5 12.0 / 18.3 / 20.5 us, M = 16 17.8 / 18.9 us.
+// At M <= 4 the qGEMV stays faster on [9728 x 2560] (M = 4: 9.0 vs 9.9 us).
+constexpr int kDispatchSkinnyMinM = 5;
+constexpr int kDispatchSkinnyMaxM = 16;
+
+// Whether the weight-streaming kernel takes this call: 1 <= m <= 16,
+// k % 128 == 0, T in {bf16, f16}, 32-bit byte offsets.
+bool qskinny_supported(int k, int n, int m, int dtype);
+// y[m][n] = x . deq(W)^T on the matrix cores, 16 weight rows per workgroup.
+hipError_t launch_qskinny(const uint32_t* w, const void* scales, const void* biases, const void* x,
+                          void* y, int k, int n, int m, int dtype, hipStream_t stream);
 
 }  // namespace imq

@@ -1,0 +1,177 @@
+// qskinny.hip -- y[m][n] = x . deq(W)^T for 1 <= m <= 16 with the products on
+// the matrix cores: a weight-streaming kernel for the few-row shapes between
+// the qGEMV (whose dot products and reductions grow with M) and the tiled
+// qGEMM (whose split-K plans read the weights at a fraction of HBM speed).
+//
+// A workgroup owns 16 weight rows (output features) and all of K; its W waves
+// take interleaved chunks of 128 k (64 bytes of each row, two quantization
+// groups).  In a v_mfma_f32_16x16x32 lane (c, h) = (lane % 16, lane / 16)
+// supplies k = 8 h .. 8 h + 7 of a 32-k slice for A row c and B column c.
+// Lane (c, h) loads bytes [16 h, 16 h + 16) of weight row c's 64-byte chunk
+// (one wave instruction: 16 rows x 64 contiguous bytes); word j of those 16
+// bytes feeds slice j, so slice j covers k = 32 h + 8 j .. +8 of the chunk in
+// lane group h.  The activations take the same mapping as B: lane (c, h)
+// loads x[c][32 h .. 32 h + 32) of the chunk, 64 contiguous bytes, when token
+// c < M (other columns of B only feed outputs that are never stored).  Each
+// lane's four words lie in one quantization group (group h / 2 of the chunk),
+// so one scale and one bias per lane and chunk.  Weights A are dequantized in
+// registers exactly as in the other kernels (RNE_T(fl32(s q + b))); the MFMA
+// accumulates the products in fp32.  The waves' partial 16 x 16 sums are added
+// in wave order through LDS (deterministic) and rounded to T.
+#include "imq_device.hpp"
+#include "imq_kernels.hpp"
+
+namespace imq {
+namespace {
+
+constexpr int kRows = 16;     // weight rows per workgroup
+constexpr int kChunkK = 128;  // k per chunk
+
+template <int T>
+__device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+  if constexpr (T == kBf16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+template <int T, int W, int U>
+__global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restrict__ w,
+                                                         const uint16_t* __restrict__ scales,
+                                                         const uint16_t* __restrict__ biases,
+                                                         const uint16_t* __restrict__ x,
+                                                         uint16_t* __restrict__ y, int M, int N,
+                                                         int K, bool vec) {
+  __shared__ f32x4_t part[W][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, h = lane >> 4;
+  const int n0 = blockIdx.x * kRows;
+  const int row = min(n0 + c, N - 1);  // rows past N are clamped; their outputs are not stored
+  const int gpr = K >> 6;
+  const int chunks = K / kChunkK;
+  const auto wr = make_rsrc(w, (uint32_t)((size_t)N * K / 2));
+  const auto sr = make_rsrc(scales, (uint32_t)((size_t)N * gpr * 2));
+  const auto br = make_rsrc(biases, (uint32_t)((size_t)N * gpr * 2));
+  const auto xr = make_rsrc(x, (uint32_t)((size_t)M * K * 2));
+  const uint32_t w_off = (uint32_t)row * (uint32_t)(K / 2) + (uint32_t)h * 16u;
+  const uint32_t p_off = ((uint32_t)row * (uint32_t)gpr + (uint32_t)(h >> 1)) * 2u;
+  const uint32_t x_off = (uint32_t)c * (uint32_t)K * 2u + (uint32_t)h * 64u;
+  const bool has_x = c < M;
+
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int ch0 = wave; ch0 < chunks; ch0 += W * U) {
+    u32x4_t wv[U], xv[U][4];
+    uint16_t sv[U], bv[U];
+    // Chunks past the end are clamped to the last one (in range) and dropped.
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t ch = (uint32_t)min(ch0 + u * W, chunks - 1);
+      wv[u] = load_b128(wr, w_off + ch * 64u, 0);
+      sv[u] = __builtin_amdgcn_raw_buffer_load_b16(sr, p_off + ch * 4u, 0, 0);
+      bv[u] = __builtin_amdgcn_raw_buffer_load_b16(br, p_off + ch * 4u, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t ch = (uint32_t)min(ch0 + u * W, chunks - 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        xv[u][j] = has_x ? load_b128(xr, x_off + ch * 256u + (uint32_t)j * 16u, 0)
+                         : u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (ch0 + u * W >= chunks) break;  // uniform across the wave
+      const float s = Elem<T>::param(sv[u]);
+      const float s24 = s * 0x1p24f, s20 = s * 0x1p20f;
+      const float b = Elem<T>::param(bv[u]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t p[4];
+        Elem<T>::dequant(wv[u][j], s24, s20, b, p);
+        acc = mfma16x16x32<T>(u32x4_t{p[0], p[1], p[2], p[3]}, xv[u][j], acc);
+      }
+    }
+  }
+  part[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0 || !has_x) return;
+  f32x4_t sum = part[0][lane];
+#pragma unroll
+  for (int i = 1; i < W; ++i) sum += part[i][lane];
+  // Lane (c, h) holds outputs (token c, features n0 + 4 h + v), v = 0..3.
+  const int f0 = n0 + 4 * h;
+  uint16_t* yr = y + (size_t)c * N;
+  if (vec && f0 + 3 < N) {
+    *reinterpret_cast<uint2*>(yr + f0) =
+        make_uint2(Elem<T>::pack2(sum[0], sum[1]), Elem<T>::pack2(sum[2], sum[3]));
+  } else {
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      if (f0 + v < N) yr[f0 + v] = Elem<T>::out(sum[v]);
+  }
+}
+
+// Waves per workgroup: enough that the device holds about 2048 waves and
+// each wave at most 8 chunks, at most 16 waves and at most half the chunks.
+int skinny_waves(int n, int k) {
+  const long blocks = (n + kRows - 1) / kRows;
+  const int chunks = k / kChunkK;
+  int wv = 1;
+  while (wv < 16 && (blocks * wv < 2048 || chunks > 8 * wv) && wv * 2 <= chunks) wv *= 2;
+  return wv;
+}
+
+template <int T, int W>
+hipError_t launch_w(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
+                    uint16_t* y, int k, int n, int m, bool vec, hipStream_t stream) {
+  // Chunks per wave, all loaded before any is computed (one memory round trip).
+  const int chunks = k / kChunkK, u = (chunks + W - 1) / W;
+  const dim3 grid((unsigned)((n + kRows - 1) / kRows)), block(64 * W);
+#define IMQ_SKINNY(UU) \
+  hipLaunchKernelGGL((qskinny_kernel<T, W, UU>), grid, block, 0, stream, w, s, b, x, y, m, n, k, vec)
+  if (u <= 2) IMQ_SKINNY(2);
+  else if (u <= 3) IMQ_SKINNY(3);
+  else if (u <= 4) IMQ_SKINNY(4);
+  else if (u <= 5) IMQ_SKINNY(5);
+  else if (u <= 6) IMQ_SKINNY(6);
+  else IMQ_SKINNY(8);
+#undef IMQ_SKINNY
+  return hipGetLastError();
+}
+
+template <int T>
+hipError_t launch_t(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
+                    uint16_t* y, int k, int n, int m, hipStream_t stream) {
+  const bool vec = n % 4 == 0 && ((uintptr_t)y & 7u) == 0;
+  switch (skinny_waves(n, k)) {
+    case 1: return launch_w<T, 1>(w, s, b, x, y, k, n, m, vec, stream);
+    case 2: return launch_w<T, 2>(w, s, b, x, y, k, n, m, vec, stream);
+    case 4: return launch_w<T, 4>(w, s, b, x, y, k, n, m, vec, stream);
+    case 8: return launch_w<T, 8>(w, s, b, x, y, k, n, m, vec, stream);
+    default: return launch_w<T, 16>(w, s, b, x, y, k, n, m, vec, stream);
+  }
+}
+
+}  // namespace
+
+bool qskinny_supported(int k, int n, int m, int dtype) {
+  return m >= 1 && m <= kQskinnyMaxM && n >= 1 && k >= kChunkK && k % kChunkK == 0 &&
+         (dtype == kBf16 || dtype == kF16) && (size_t)n * k / 2 < ((size_t)1 << 32) &&
+         (size_t)m * k * 2 < ((size_t)1 << 31);
+}
+
+hipError_t launch_qskinny(const uint32_t* w, const void* scales, const void* biases, const void* x,
+                          void* y, int k, int n, int m, int dtype, hipStream_t stream) {
+  if (!qskinny_supported(k, n, m, dtype)) return hipErrorInvalidValue;
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* b = static_cast<const uint16_t*>(biases);
+  const auto* xx = static_cast<const uint16_t*>(x);
+  auto* yy = static_cast<uint16_t*>(y);
+  if (dtype == kBf16) return launch_t<kBf16>(w, s, b, xx, yy, k, n, m, stream);
+  return launch_t<kF16>(w, s, b, xx, yy, k, n, m, stream);
+}
+
+}  // namespace imq

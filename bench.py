@@ -110,7 +110,10 @@ def time_graph(launches, replays: int = 5) -> float:
     return start.elapsed_time(end) / (replays * len(launches))
 
 
-def bench_qgemv(imq, synth, torch, copies: int = 48, ms_list=(1, 4, 16)) -> dict:
+def bench_qgemv(imq, synth, torch, copies: int = 48, ms_list=(1, 4, 16),
+                few_rows=(8, 16)) -> dict:
+    """The qGEMV at M in ms_list, and the regime dispatcher at M in few_rows (the
+    weight-streaming matrix-core kernel), weights rotated over `copies` copies."""
     out = {}
     for (n, k) in ((9728, 2560), (2560, 9728)):
         p = synth.make_problem(16, n, k, seed=0)
@@ -119,17 +122,19 @@ def bench_qgemv(imq, synth, torch, copies: int = 48, ms_list=(1, 4, 16)) -> dict
         ss = [s.clone() for _ in range(copies)]
         bs = [b.clone() for _ in range(copies)]
         del w, s, b
-        for m in ms_list:
+        for m, fn, tag in ([(m, imq.qgemv, "qgemv") for m in ms_list]
+                           + [(m, imq.quantized_matmul, "qmm_t") for m in few_rows]):
             xm = x[:m].contiguous()
             ys = [torch.empty((m, n), dtype=torch.bfloat16, device="cuda") for _ in range(copies)]
-            launches = [(lambda i=i: imq.qgemv(xm, ws[i], ss[i], bs[i], out=ys[i]))
+            launches = [(lambda i=i, fn=fn: fn(xm, ws[i], ss[i], bs[i], out=ys[i]))
                         for i in range(copies)]
             ms = time_graph(launches)
             byts = qmm_bytes(m, n, k)
             gbs = byts / (ms * 1e-3) / 1e9
-            out[f"M{m}_N{n}_K{k}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
-                                      "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts}
-            log(f"qgemv M={m} N={n} K={k}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
+            key = f"M{m}_N{n}_K{k}" if tag == "qgemv" else f"qmm_t_M{m}_N{n}_K{k}"
+            out[key] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                        "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts}
+            log(f"{tag} M={m} N={n} K={k}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
         del ws, ss, bs
         torch.cuda.empty_cache()
     return out
@@ -435,7 +440,7 @@ def main() -> int:
         bench_dit_step(torch)
         return 0
     if args.only_hbm:
-        bench_qgemv(imq, synth, torch, ms_list=(1,))
+        bench_qgemv(imq, synth, torch, ms_list=(1,), few_rows=())
         bench_dequant(imq, synth, torch)
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)

@@ -191,8 +191,9 @@ def test_one_hot_rows_reproduce_dequant_bit_exact(fn_name, m, k):
 
 
 def test_dispatcher_routes_by_m():
-    """M <= 4 is the qGEMV kernel bit for bit; above, the MFMA kernel, whose
-    K may be split by the dispatcher (another fp32 summation order)."""
+    """M <= 4 is the qGEMV kernel bit for bit; above, the matrix-core kernels
+    (5 <= M <= 16 the weight-streaming one, then the tiled one, whose K may be
+    split by the dispatcher: other fp32 summation orders)."""
     p = synth.make_problem(17, 384, 512, seed=16)
     x, w, s, b = synth.to_device(p)
     for m in (1, 4):
@@ -227,6 +228,43 @@ def test_split_k_dispatcher(m, n, k):
     xh[np.arange(m), cols] = 0x3F80
     yo = bits(imq.quantized_matmul(to_dev_bf16(xh), w, s, b))
     assert np.array_equal(yo, bits(imq.dequantize(w, s, b))[:, cols].T)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("m,n,k", [(5, 384, 512), (16, 1001, 1024), (13, 17, 128), (8, 9728, 2560),
+                                   (16, 2560, 9728), (9, 384, 192)])
+def test_few_row_matrix_core_dispatch(dtype, m, n, k):
+    """5 <= M <= 16 through the dispatcher: the weight-streaming kernel (16 rows
+    per workgroup; N = 1001 and 17 end in a partial row block and take the
+    single-element stores; K = 128 one chunk) or, for K % 128 != 0 (K = 192),
+    the tiled kernel.  Oracle within tolerance, the same bits on a second call,
+    and one-hot rows reproduce the dequantized weights bit for bit."""
+    note(f"few-row dispatch {dtype} M={m} N={n} K={k}")
+    p = synth.make_problem(m, n, k, seed=23)
+    x, w, s, b = synth.to_device(p)
+    if dtype == "f16":
+        x, s, b = x.half(), s.half(), b.half()
+    y1 = imq.quantized_matmul(x, w, s, b)
+    y2 = imq.quantized_matmul(x, w, s, b)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    if dtype == "bf16":
+        assert_close(bits(y1), cref.qmm_t(p.x, p.w, p.scales, p.biases), "few-row")
+    else:
+        want = ref.qmm_t_as(x.cpu().numpy(), p.w, s.cpu().numpy(), b.cpu().numpy(), np.float16)
+        st = ref.error_stats_values(y1.float().cpu().numpy(), want.astype(np.float32))
+        note(f"  f16: mae={st['mae']:.3g} normwise={st['max_rel_normwise']:.3g}")
+        assert st["mae"] <= MAE_TOL and st["max_rel_normwise"] <= NORMWISE_TOL, st
+        assert st["cosine"] >= COSINE_MIN, st
+    rng = np.random.default_rng(24)
+    cols = rng.choice(k, size=m, replace=False)
+    xh = np.zeros((m, k), dtype=np.uint16)
+    xh[np.arange(m), cols] = 0x3F80 if dtype == "bf16" else 0x3C00
+    xo = torch.from_numpy(xh.view(np.int16)).cuda().view(x.dtype)
+    yo = imq.quantized_matmul(xo, w, s, b)
+    deq = imq.dequantize(w, s, b)
+    torch.cuda.synchronize()
+    assert torch.equal(yo, deq[:, torch.from_numpy(cols).cuda()].T.contiguous())
 
 
 def test_split_k_dispatcher_under_graph_capture():
