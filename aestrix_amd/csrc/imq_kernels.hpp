@@ -80,13 +80,13 @@ constexpr int kDispatchGemvMaxM = 4;
 
 // Largest M the weight-streaming MFMA kernel (qskinny.hip) takes.
 constexpr int kQskinnyMaxM = 16;
-// The M range the regime dispatcher routes to it (bf16 / f16, K % 128 == 0).
-// With the weights coming from HBM (text-encoder MLP shapes, 48 rotated
-// copies): M = 5 at [9728 x 2560] 9.96 us against 13.4 us for the split-K tile
-// kernel and 12.8 us for the qGEMV, M = 8 11.0 / 13.6 / 13.2 us, M = 16 14.1 /
-// 14.2 us; at [2560 x 9728] M = 5 12.0 / 18.3 / 20.5 us, M = 16 17.8 / 18.9 us.
-// At M <= 4 the qGEMV stays faster on [9728 x 2560] (M = 4: 9.0 vs 9.9 us).
-constexpr int kDispatchSkinnyMinM = 5;
+// The M range the regime dispatcher routes to it (bf16 / f16, K % 128 == 0),
+// ahead of the qGEMV.  With the weights coming from HBM (text-encoder MLP
+// shapes, 48 rotated copies), [9728 x 2560]: M = 4 7.8 us against 9.2 us for
+// the qGEMV, M = 8 8.5 us against 13.6 us for the split-K tile kernel, M = 16
+// 14.2 / 14.2 us; [2560 x 9728]: M = 4 11.9 / 13.0 us (qGEMV), M = 5 12.0 /
+// 18.3 us.  At M <= 2 the qGEMV stays faster (M = 1: 5.9 vs 7.6 us).
+constexpr int kDispatchSkinnyMinM = 4;
 constexpr int kDispatchSkinnyMaxM = 16;
 
 // Whether the weight-streaming kernel takes this call: 1 <= m <= 16,

@@ -11,8 +11,11 @@
 // (one wave instruction: 16 rows x 64 contiguous bytes); word j of those 16
 // bytes feeds slice j, so slice j covers k = 32 h + 8 j .. +8 of the chunk in
 // lane group h.  The activations take the same mapping as B: lane (c, h)
-// loads x[c][32 h .. 32 h + 32) of the chunk, 64 contiguous bytes, when token
-// c < M (other columns of B only feed outputs that are never stored).  Each
+// reads x[c][32 h .. 32 h + 32) of the chunk, 64 contiguous bytes, when token
+// c < M (other columns of B only feed outputs that are never stored) -- from
+// an LDS copy of all of x when it fits 64 KiB (staged by direct buffer->LDS
+// loads while the weights are in flight; 52 VGPRs, 8 waves per SIMD), else
+// straight from memory (about 130 VGPRs).  Each
 // lane's four words lie in one quantization group (group h / 2 of the chunk),
 // so one scale and one bias per lane and chunk.  Weights A are dequantized in
 // registers exactly as in the other kernels (RNE_T(fl32(s q + b))); the MFMA
@@ -37,7 +40,12 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c)
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
-template <int T, int W, int U>
+// x staged in LDS when the whole [M, K] tile fits kXLdsMax bytes (rounded up
+// to whole wave instructions): one 16-byte DMA per lane and slot instead of
+// four register loads per chunk and lane.
+constexpr int kXLdsMax = 64 * 1024;
+
+template <int T, int W, int U, bool XLDS>
 __global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restrict__ w,
                                                          const uint16_t* __restrict__ scales,
                                                          const uint16_t* __restrict__ biases,
@@ -45,6 +53,7 @@ __global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restr
                                                          uint16_t* __restrict__ y, int M, int N,
                                                          int K, bool vec) {
   __shared__ f32x4_t part[W][64];
+  extern __shared__ uint4 xs[];  // XLDS: x[M][K] as 16-byte slots, row-major
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, h = lane >> 4;
@@ -61,6 +70,15 @@ __global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restr
   const uint32_t x_off = (uint32_t)c * (uint32_t)K * 2u + (uint32_t)h * 64u;
   const bool has_x = c < M;
 
+  if constexpr (XLDS) {
+    // Slot i * 64 W + 64 wave + lane; lanes past the tile read past x (zeros)
+    // into the rounded-up part of the allocation.
+    const int slots = M * K / 8, per = 64 * W;
+    for (int i = 0; i * per < slots; ++i)
+      load_lds16(xr, (uint32_t)(i * per + wave * 64 + lane) * 16u, 0u, xs + i * per + wave * 64);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   for (int ch0 = wave; ch0 < chunks; ch0 += W * U) {
     u32x4_t wv[U], xv[U][4];
@@ -73,13 +91,25 @@ __global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restr
       sv[u] = __builtin_amdgcn_raw_buffer_load_b16(sr, p_off + ch * 4u, 0, 0);
       bv[u] = __builtin_amdgcn_raw_buffer_load_b16(br, p_off + ch * 4u, 0, 0);
     }
+    if constexpr (XLDS) {
+      // The x tile is in LDS once this wave's DMA loads (issued before the 3 U
+      // loads above) have landed and every wave has passed the barrier; only
+      // the first pass waits (U covers every chunk of a wave).
+      __builtin_amdgcn_sched_barrier(0);
+      if (ch0 == wave) {
+        IMQ_WAIT_VMCNT(3 * U);
+        __builtin_amdgcn_s_barrier();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t ch = (uint32_t)min(ch0 + u * W, chunks - 1);
+      for (int u = 0; u < U; ++u) {
+        const uint32_t ch = (uint32_t)min(ch0 + u * W, chunks - 1);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        xv[u][j] = has_x ? load_b128(xr, x_off + ch * 256u + (uint32_t)j * 16u, 0)
-                         : u32x4_t{0u, 0u, 0u, 0u};
+        for (int j = 0; j < 4; ++j)
+          xv[u][j] = has_x ? load_b128(xr, x_off + ch * 256u + (uint32_t)j * 16u, 0)
+                           : u32x4_t{0u, 0u, 0u, 0u};
+      }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -91,7 +121,17 @@ __global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restr
       for (int j = 0; j < 4; ++j) {
         uint32_t p[4];
         Elem<T>::dequant(wv[u][j], s24, s20, b, p);
-        acc = mfma16x16x32<T>(u32x4_t{p[0], p[1], p[2], p[3]}, xv[u][j], acc);
+        u32x4_t xj;
+        if constexpr (XLDS) {
+          // B fragment read from the staged tile right before its MFMA.
+          const uint32_t ch = (uint32_t)(ch0 + u * W);
+          xj = has_x ? *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(xs) +
+                                                          x_off + ch * 256u + j * 16u)
+                     : u32x4_t{0u, 0u, 0u, 0u};
+        } else {
+          xj = xv[u][j];
+        }
+        acc = mfma16x16x32<T>(u32x4_t{p[0], p[1], p[2], p[3]}, xj, acc);
       }
     }
   }
@@ -130,8 +170,19 @@ hipError_t launch_w(const uint32_t* w, const uint16_t* s, const uint16_t* b, con
   // Chunks per wave, all loaded before any is computed (one memory round trip).
   const int chunks = k / kChunkK, u = (chunks + W - 1) / W;
   const dim3 grid((unsigned)((n + kRows - 1) / kRows)), block(64 * W);
-#define IMQ_SKINNY(UU) \
-  hipLaunchKernelGGL((qskinny_kernel<T, W, UU>), grid, block, 0, stream, w, s, b, x, y, m, n, k, vec)
+  // LDS for the x tile: the slots rounded up to whole wave-instruction rounds.
+  const size_t per = 64 * (size_t)W, slots = (size_t)m * k / 8;
+  const size_t xbytes = (slots + per - 1) / per * per * 16;
+  const bool xlds = xbytes <= (size_t)kXLdsMax;
+#define IMQ_SKINNY(UU)                                                                            \
+  do {                                                                                           \
+    if (xlds)                                                                                    \
+      hipLaunchKernelGGL((qskinny_kernel<T, W, UU, true>), grid, block, xbytes, stream, w, s, b, \
+                         x, y, m, n, k, vec);                                                    \
+    else                                                                                         \
+      hipLaunchKernelGGL((qskinny_kernel<T, W, UU, false>), grid, block, 0, stream, w, s, b, x,  \
+                         y, m, n, k, vec);                                                       \
+  } while (0)
   if (u <= 2) IMQ_SKINNY(2);
   else if (u <= 3) IMQ_SKINNY(3);
   else if (u <= 4) IMQ_SKINNY(4);

@@ -112,10 +112,10 @@ int imq_dequantize(imq_ctx* ctx, const uint32_t* w, const void* scales, const vo
  * DirectDiTStep.qmm (DirectDiTStep.swift:374-406), DirectTELayerSpike.encodeQmm
  * (DirectTELayer.swift:109-128), DirectConditioner.qmm
  * (DirectConditioner.swift:96-117) and MLX quantizedMM(transpose: true)
- * (Sources/ImarelloDiT/AttentionUtils.swift:212-221).  M <= 4 runs the qGEMV
- * kernel; 5 <= M <= 16 with K % 128 == 0 a weight-streaming matrix-core kernel
- * (16 weight rows per workgroup, K over its waves, no workspace); other M the
- * MFMA qGEMM kernel (f32: the qGEMV kernel, 16 rows at a time).  When the
+ * (Sources/ImarelloDiT/AttentionUtils.swift:212-221).  4 <= M <= 16 with
+ * K % 128 == 0 runs a weight-streaming matrix-core kernel (16 weight rows per
+ * workgroup, K over its waves, no workspace); other M <= 4 the qGEMV kernel;
+ * larger M the MFMA qGEMM kernel (f32: the qGEMV kernel, 16 rows at a time).  When the
  * output tiles are too few to fill the GPU, the qGEMM splits
  * K: fp32 partial sums go to a workspace the context keeps per stream (grown
  * on first use, outside stream capture; under capture a call that would need

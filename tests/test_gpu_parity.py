@@ -191,16 +191,16 @@ def test_one_hot_rows_reproduce_dequant_bit_exact(fn_name, m, k):
 
 
 def test_dispatcher_routes_by_m():
-    """M <= 4 is the qGEMV kernel bit for bit; above, the matrix-core kernels
-    (5 <= M <= 16 the weight-streaming one, then the tiled one, whose K may be
+    """M <= 3 is the qGEMV kernel bit for bit; above, the matrix-core kernels
+    (4 <= M <= 16 the weight-streaming one, then the tiled one, whose K may be
     split by the dispatcher: other fp32 summation orders)."""
     p = synth.make_problem(17, 384, 512, seed=16)
     x, w, s, b = synth.to_device(p)
-    for m in (1, 4):
+    for m in (1, 3):
         note(f"dispatcher M={m}")
         assert np.array_equal(bits(imq.quantized_matmul(x[:m], w, s, b)),
                               bits(imq.qgemv(x[:m], w, s, b)))
-    for m in (5, 16, 17):
+    for m in (4, 5, 16, 17):
         note(f"dispatcher M={m}")
         y = bits(imq.quantized_matmul(x[:m], w, s, b))
         assert_close(y, cref.qmm_t(p.x[:m], p.w, p.scales, p.biases), f"dispatcher M={m}")
@@ -231,13 +231,14 @@ def test_split_k_dispatcher(m, n, k):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
-@pytest.mark.parametrize("m,n,k", [(5, 384, 512), (16, 1001, 1024), (13, 17, 128), (8, 9728, 2560),
-                                   (16, 2560, 9728), (9, 384, 192)])
+@pytest.mark.parametrize("m,n,k", [(4, 384, 512), (5, 384, 512), (16, 1001, 1024), (13, 17, 128),
+                                   (8, 9728, 2560), (4, 2560, 9728), (16, 2560, 9728), (9, 384, 192)])
 def test_few_row_matrix_core_dispatch(dtype, m, n, k):
-    """5 <= M <= 16 through the dispatcher: the weight-streaming kernel (16 rows
-    per workgroup; N = 1001 and 17 end in a partial row block and take the
-    single-element stores; K = 128 one chunk) or, for K % 128 != 0 (K = 192),
-    the tiled kernel.  Oracle within tolerance, the same bits on a second call,
+    """4 <= M <= 16 through the dispatcher: the weight-streaming kernel (16 rows
+    per workgroup; x staged in LDS when M K 2 <= 64 KiB, else loaded per chunk:
+    M = 4 and 16 at K = 9728 take the second path; N = 1001 and 17 end in a
+    partial row block and take the single-element stores; K = 128 one chunk)
+    or, for K % 128 != 0 (K = 192), the tiled kernel.  Oracle within tolerance, the same bits on a second call,
     and one-hot rows reproduce the dequantized weights bit for bit."""
     note(f"few-row dispatch {dtype} M={m} N={n} K={k}")
     p = synth.make_problem(m, n, k, seed=23)
