@@ -13,7 +13,7 @@
 // lane group h.  The activations take the same mapping as B: lane (c, h)
 // reads x[c][32 h .. 32 h + 32) of the chunk, 64 contiguous bytes, when token
 // c < M (other columns of B only feed outputs that are never stored) -- from
-// an LDS copy of all of x when it fits 64 KiB (staged by direct buffer->LDS
+// an LDS copy of all of x when it fits 96 KiB (staged by direct buffer->LDS
 // loads while the weights are in flight; 52 VGPRs, 8 waves per SIMD), else
 // straight from memory (about 130 VGPRs).  Each
 // lane's four words lie in one quantization group (group h / 2 of the chunk),
@@ -42,8 +42,9 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c)
 
 // x staged in LDS when the whole [M, K] tile fits kXLdsMax bytes (rounded up
 // to whole wave instructions): one 16-byte DMA per lane and slot instead of
-// four register loads per chunk and lane.
-constexpr int kXLdsMax = 64 * 1024;
+// four register loads per chunk and lane.  96 KiB against 64: [9728 x 2560]
+// M = 16 14.1 -> 13.3 us, [2560 x 9728] M = 4 12.0 -> 11.3 us, the rest equal.
+constexpr int kXLdsMax = 96 * 1024;
 
 template <int T, int W, int U, bool XLDS>
 __global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restrict__ w,
