@@ -73,9 +73,10 @@ hipError_t launch_rmsnorm(const float* x, const float* w, void* y, int rows, int
 
 // Largest M the qGEMV kernel takes.
 constexpr int kQgemvMaxM = 16;
-// Largest bf16 / f16 M the regime dispatcher routes to the qGEMV kernel: from
-// M = 5 the matrix-core kernels are faster, the qGEMV's VALU dot products and
-// reductions growing with M.
+// Largest bf16 / f16 M the regime dispatcher routes to the qGEMV kernel when
+// the few-row kernel below does not take the call: from M = 5 the tiled
+// matrix-core kernel is faster, the qGEMV's VALU dot products and reductions
+// growing with M.
 constexpr int kDispatchGemvMaxM = 4;
 
 // Largest M the weight-streaming MFMA kernel (qskinny.hip) takes.

@@ -159,9 +159,10 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                      out: torch.Tensor | None = None) -> torch.Tensor:
     """y[..., N] = x[..., K] . deq(W)^T (MLX quantizedMM with transpose=true).
 
-    M <= 4 rows run the qGEMV kernel, larger M the MFMA qGEMM kernel, with K
-    split over a per-stream workspace when its output tiles are too few to
-    fill the GPU (deterministic; another fp32 summation order than qgemm)."""
+    4 <= M <= 16 rows with K % 128 == 0 run the few-row matrix-core kernel,
+    other M <= 4 (and f32) the qGEMV kernel, larger M the MFMA qGEMM kernel,
+    with K split over a per-stream workspace when its output tiles are too few
+    to fill the GPU (deterministic; another fp32 summation order than qgemm)."""
     if not transpose:
         raise NotImplementedError("only transpose=true (y = x . deq(w)^T) is on the path")
     return _qmm_call("imq_qmm_t", x, w, scales, biases, group_size, bits, out)
