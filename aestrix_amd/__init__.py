@@ -29,6 +29,7 @@ from .ops import (  # noqa: F401
     qgemv,
     qmm,
     qmm_gate_add,
+    qmm_plan,
     qmm_postscale,
     qmm_swiglu,
     quantized_matmul,

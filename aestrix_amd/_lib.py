@@ -44,6 +44,16 @@ class QWeight(ctypes.Structure):
                 ("base", ctypes.c_void_p)]
 
 
+class Plan(ctypes.Structure):
+    """imq_plan."""
+    _fields_ = [("kernel", ctypes.c_int), ("tile_rows", ctypes.c_int), ("splits", ctypes.c_int),
+                ("workspace_bytes", ctypes.c_size_t)]
+
+
+IMQ_ENTRY_QMM_T, IMQ_ENTRY_QGEMM, IMQ_ENTRY_QGEMV, IMQ_ENTRY_FUSED = 0, 1, 2, 3
+KERNEL_NAMES = {0: "qgemv", 1: "few_row", 2: "tile", 3: "tile_reg"}
+
+
 class DitDims(ctypes.Structure):
     """imq_dit_dims."""
     _fields_ = [("l_img", ctypes.c_int), ("l_txt", ctypes.c_int), ("dim", ctypes.c_int),
@@ -71,6 +81,7 @@ SIGNATURES = {
     "imq_memcpy_d2h": ([_p, _p, _p, _sz, _p], _i),
     "imq_dequantize": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "imq_qmm_t": (_QMM, _i),
+    "imq_qmm_plan": ([_p, _i, _i, _i, _i, _i, ctypes.POINTER(Plan)], _i),
     "imq_qgemv": (_QMM, _i),
     "imq_qgemm": (_QMM, _i),
     "imq_cast_prescale": ([_p, _p, _p, _sz, ctypes.c_float, _i, _p], _i),

@@ -151,6 +151,8 @@ int check_qmm(imq_ctx* ctx, const char* fn, const uint32_t* w, const void* s, co
   return IMQ_OK;
 }
 
+// kAuto: the regime dispatcher (imq_qmm_t); kGemv / kGemm: one kernel family
+// alone.
 enum class Regime { kAuto, kGemv, kGemm };
 
 // The split-K workspace of stream st, at least `need` bytes; empty (run
@@ -198,20 +200,20 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
     return fail(ctx, IMQ_EUNSUPPORTED, "%s: %zu bytes of packed weights: the qGEMV kernel takes "
                 "under 4 GiB", fn, (size_t)n * (size_t)k / 2);
   if ((rc = bind_device(ctx)) != IMQ_OK) return rc;
+  const bool automatic = regime == Regime::kAuto;
   const bool gemv = regime == Regime::kGemv ||
-                    (regime == Regime::kAuto && w_fits_gemv &&
-                     (m <= imq::kDispatchGemvMaxM || dtype == IMQ_F32));
+                    (automatic && w_fits_gemv && (m <= imq::kDispatchGemvMaxM || dtype == IMQ_F32));
+  const bool skinny = automatic && m >= imq::kDispatchSkinnyMinM &&
+                      m <= imq::kDispatchSkinnyMaxM && imq::qskinny_supported(k, n, m, (int)dtype);
   auto st = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
-  if (regime == Regime::kAuto && m >= imq::kDispatchSkinnyMinM && m <= imq::kDispatchSkinnyMaxM &&
-      imq::qskinny_supported(k, n, m, (int)dtype)) {
+  if (skinny) {
     e = imq::launch_qskinny(w, s, b, x, y, k, n, m, (int)dtype, st);
   } else if (!gemv) {
     // The dispatcher may split K over a workspace; imq_qgemm is the plain
     // tile kernel (the fused output stages equal it bit for bit).
-    const imq::SplitWs ws = regime == Regime::kAuto
-                                ? split_ws(ctx, st, imq::qgemm_split_bytes(k, n, m))
-                                : imq::SplitWs{};
+    imq::SplitWs ws{};
+    if (regime == Regime::kAuto) ws = split_ws(ctx, st, imq::qgemm_split_bytes(k, n, m));
     e = imq::launch_qgemm(w, s, b, x, y, k, n, m, (int)dtype, st, ws);
   } else {
     // f32 beyond 16 rows (the conditioner's multi-row calls): blocks of 16 rows.
@@ -389,6 +391,59 @@ int imq_qmm_t(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* b
               imq_dtype dtype, imq_stream stream) {
   return run_qmm(ctx, "imq_qmm_t", Regime::kAuto, w, scales, biases, x, y, k, n, m, group_size,
                  bits, dtype, stream);
+}
+
+int imq_qmm_plan(imq_ctx* ctx, int entry, int k, int n, int m, imq_dtype dtype, imq_plan* out) {
+  const char* fn = "imq_qmm_plan";
+  if (!ctx) return fail(nullptr, IMQ_EINVAL, "%s: null context", fn);
+  if (!out) return fail(ctx, IMQ_EINVAL, "%s: null output", fn);
+  *out = imq_plan{};
+  if (dtype != IMQ_BF16 && dtype != IMQ_F16 && dtype != IMQ_F32)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: dtype %d", fn, (int)dtype);
+  if (k <= 0 || n <= 0 || m <= 0 || k % 64 != 0)
+    return fail(ctx, IMQ_EINVAL, "%s: shape K=%d N=%d M=%d (K a multiple of 64, all > 0)", fn, k,
+                n, m);
+  int rc = bind_device(ctx);
+  if (rc != IMQ_OK) return rc;
+  const bool w_fits_gemv = (size_t)n * (size_t)k / 2 < ((size_t)1 << 32);
+  auto tile = [&](bool fused, bool split) {
+    const imq::QgemmPlan p = imq::qgemm_plan(k, n, m, fused, split, 0);
+    *out = imq_plan{p.big ? IMQ_KERNEL_TILE : IMQ_KERNEL_TILE_REG, p.tile_rows, p.splits,
+                    p.workspace_bytes};
+    return IMQ_OK;
+  };
+  switch (entry) {
+    case IMQ_ENTRY_QGEMV:
+      if (m > imq::kQgemvMaxM)
+        return fail(ctx, IMQ_EINVAL, "%s: M=%d exceeds the qGEMV limit %d", fn, m,
+                    imq::kQgemvMaxM);
+      if (!w_fits_gemv)
+        return fail(ctx, IMQ_EUNSUPPORTED, "%s: packed weights of 4 GiB or more", fn);
+      *out = imq_plan{IMQ_KERNEL_QGEMV, 0, 1, 0};
+      return IMQ_OK;
+    case IMQ_ENTRY_QGEMM:
+    case IMQ_ENTRY_FUSED:
+      if (dtype == IMQ_F32) return fail(ctx, IMQ_EUNSUPPORTED, "%s: f32 has no MFMA kernel", fn);
+      if (entry == IMQ_ENTRY_FUSED && !imq::qgemm_big_supported(k, n, m))
+        return fail(ctx, IMQ_EUNSUPPORTED, "%s: fused stages need K %% 256 == 0", fn);
+      return tile(entry == IMQ_ENTRY_FUSED, false);
+    case IMQ_ENTRY_QMM_T: {
+      const bool gemv = w_fits_gemv && (m <= imq::kDispatchGemvMaxM || dtype == IMQ_F32);
+      if (m >= imq::kDispatchSkinnyMinM && m <= imq::kDispatchSkinnyMaxM &&
+          imq::qskinny_supported(k, n, m, (int)dtype)) {
+        *out = imq_plan{IMQ_KERNEL_FEW_ROW, 0, 1, 0};
+        return IMQ_OK;
+      }
+      if (gemv) {
+        *out = imq_plan{IMQ_KERNEL_QGEMV, 0, 1, 0};
+        return IMQ_OK;
+      }
+      if (dtype == IMQ_F32) return fail(ctx, IMQ_EUNSUPPORTED, "%s: f32 weights of 4 GiB", fn);
+      return tile(false, true);
+    }
+    default:
+      return fail(ctx, IMQ_EINVAL, "%s: unknown entry %d", fn, entry);
+  }
 }
 
 int imq_qgemv(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,

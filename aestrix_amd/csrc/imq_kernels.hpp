@@ -37,6 +37,20 @@ hipError_t launch_qgemm(const uint32_t* w, const void* scales, const void* biase
 // width for swiglu) uses for this shape (0: it does not split K).
 size_t qgemm_split_bytes(int k, int n, int m, bool fused = false);
 
+// The plan launch_qgemm / the fused launchers choose: big = the buffer-load
+// MFMA kernel (else the register-staged 128 x 256 tile kernel), its tile
+// height in rows, its K splits and their fp32 workspace bytes.  fused: an
+// output stage other than the plain store over n weight rows (2 * width for a
+// SwiGLU pair); split: a workspace is available; cus: the compute units the
+// planner counts on (0: the device's).
+struct QgemmPlan {
+  bool big;
+  int tile_rows;
+  int splits;
+  size_t workspace_bytes;
+};
+QgemmPlan qgemm_plan(int k, int n, int m, bool fused, bool split, int cus);
+
 // Whether the buffer-load MFMA kernel (and so the fused epilogues) takes
 // these shapes: K % 256 == 0 and x, w addressable with 32-bit byte offsets.
 bool qgemm_big_supported(int k, int n, int m);

@@ -961,6 +961,13 @@ size_t qgemm_split_bytes(int k, int n, int m, bool fused) {
   return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
 }
 
+QgemmPlan qgemm_plan(int k, int n, int m, bool fused, bool split, int cus) {
+  if (!qgemm_big_supported(k, n, m)) return QgemmPlan{false, 128, 1, 0};
+  const BigPlan p = pick_big_plan(m, n, k, cus > 0 ? cus : device_cus(), !fused, split);
+  return QgemmPlan{true, 32 * p.mt, p.splits,
+                   p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0};
+}
+
 hipError_t launch_qgemm_postscale(const uint32_t* w, const void* scales, const void* biases,
                                   const void* x, float* y, int k, int n, int m, float scale,
                                   int dtype, hipStream_t stream, SplitWs ws) {

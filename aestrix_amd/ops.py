@@ -283,6 +283,24 @@ def qmm_swiglu(x, w, scales, biases, width: int, gate_row: int, up_row: int,
     return out
 
 
+_ENTRIES = {"qmm_t": _lib.IMQ_ENTRY_QMM_T, "qgemm": _lib.IMQ_ENTRY_QGEMM,
+            "qgemv": _lib.IMQ_ENTRY_QGEMV, "fused": _lib.IMQ_ENTRY_FUSED}
+
+
+def qmm_plan(m: int, n: int, k: int, dtype: torch.dtype = torch.bfloat16, entry: str = "qmm_t",
+             device=None) -> dict:
+    """The kernel, tile height and K split a call of ``entry`` ("qmm_t", "qgemm",
+    "qgemv", or "fused": the fused output stages, n = the weight rows they read)
+    would run for these sizes, without launching anything (``imq_qmm_plan``)."""
+    _require(entry in _ENTRIES, f"entry must be one of {sorted(_ENTRIES)}")
+    ctx = context(device)
+    out = _lib.Plan()
+    _lib.check(_lib.load().imq_qmm_plan(ctx, _ENTRIES[entry], k, n, m, _DTYPES.get(dtype, -1),
+                                        ctypes.byref(out)), ctx)
+    return {"kernel": _lib.KERNEL_NAMES[out.kernel], "tile_rows": out.tile_rows,
+            "splits": out.splits, "workspace_bytes": out.workspace_bytes}
+
+
 @dataclass
 class Q:
     """A resident packed projection, the reference's ``Q(w:s:b:n:k:)``

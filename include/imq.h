@@ -145,6 +145,39 @@ int imq_qgemm(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* b
               const void* x, void* y, int k, int n, int m, int group_size, int bits,
               imq_dtype dtype, imq_stream stream);
 
+/* ---- plan introspection --------------------------------------------------
+ * No counterpart in the reference (MLX picks its kernels internally): the
+ * kernel, tile height and K split a call of the given entry point would run,
+ * for callers that size workspaces or pin a kernel choice in tests. */
+
+typedef enum imq_entry {
+    IMQ_ENTRY_QMM_T = 0,   /* imq_qmm_t */
+    IMQ_ENTRY_QGEMM = 1,   /* imq_qgemm */
+    IMQ_ENTRY_QGEMV = 2,   /* imq_qgemv */
+    IMQ_ENTRY_FUSED = 3    /* imq_qmm_postscale / _gate_add (n = weight rows), imq_qmm_swiglu
+                              (n = 2 * width: the gate and up rows it reads) */
+} imq_entry;
+
+typedef enum imq_kernel {
+    IMQ_KERNEL_QGEMV = 0,    /* register dequant, fp32 dot products, no matrix cores */
+    IMQ_KERNEL_FEW_ROW = 1,  /* weight-streaming matrix-core kernel, 16 weight rows per workgroup */
+    IMQ_KERNEL_TILE = 2,     /* MFMA tiles, activations staged by direct buffer->LDS loads
+                                (K % 256 == 0) */
+    IMQ_KERNEL_TILE_REG = 3  /* MFMA tiles, activations staged through registers (other K) */
+} imq_kernel;
+
+typedef struct imq_plan {
+    int kernel;             /* an imq_kernel */
+    int tile_rows;          /* output rows per workgroup tile (tile kernels; 0 otherwise) */
+    int splits;             /* K ranges summed by a second kernel (1: K not split) */
+    size_t workspace_bytes; /* fp32 partial sums of a split plan (0 when not split) */
+} imq_plan;
+
+/* The plan of a call of `entry` with these sizes and dtype on ctx's device,
+ * without launching anything; the same argument checks as the entry point on
+ * the sizes (IMQ_EINVAL / IMQ_EUNSUPPORTED). */
+int imq_qmm_plan(imq_ctx* ctx, int entry, int k, int n, int m, imq_dtype dtype, imq_plan* out);
+
 /* ---- fused output stages ------------------------------------------------
  * The MFMA kernel with the reference's post-qmm glue kernel folded into its
  * epilogue (Sources/ImarelloDirect/DirectDiTKernels.swift).  Each equals the
