@@ -81,6 +81,7 @@ SIGNATURES = {
     "imq_memcpy_d2h": ([_p, _p, _p, _sz, _p], _i),
     "imq_dequantize": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "imq_qmm_t": (_QMM, _i),
+    "imq_qmm_t_noalloc": (_QMM, _i),
     "imq_qmm_plan": ([_p, _i, _i, _i, _i, _i, ctypes.POINTER(Plan)], _i),
     "imq_qgemv": (_QMM, _i),
     "imq_qgemm": (_QMM, _i),

@@ -151,9 +151,10 @@ int check_qmm(imq_ctx* ctx, const char* fn, const uint32_t* w, const void* s, co
   return IMQ_OK;
 }
 
-// kAuto: the regime dispatcher (imq_qmm_t); kGemv / kGemm: one kernel family
-// alone.
-enum class Regime { kAuto, kGemv, kGemm };
+// kAuto: the regime dispatcher (imq_qmm_t); kAutoNoAlloc: the same plan with
+// the split-K partial sums in the library's static scratch
+// (imq_qmm_t_noalloc); kGemv / kGemm: one kernel family alone.
+enum class Regime { kAuto, kAutoNoAlloc, kGemv, kGemm };
 
 // The split-K workspace of stream st, at least `need` bytes; empty (run
 // unsplit) when it would have to grow during stream capture or the
@@ -200,7 +201,7 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
     return fail(ctx, IMQ_EUNSUPPORTED, "%s: %zu bytes of packed weights: the qGEMV kernel takes "
                 "under 4 GiB", fn, (size_t)n * (size_t)k / 2);
   if ((rc = bind_device(ctx)) != IMQ_OK) return rc;
-  const bool automatic = regime == Regime::kAuto;
+  const bool automatic = regime == Regime::kAuto || regime == Regime::kAutoNoAlloc;
   const bool gemv = regime == Regime::kGemv ||
                     (automatic && w_fits_gemv && (m <= imq::kDispatchGemvMaxM || dtype == IMQ_F32));
   const bool skinny = automatic && m >= imq::kDispatchSkinnyMinM &&
@@ -213,7 +214,17 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
     // The dispatcher may split K over a workspace; imq_qgemm is the plain
     // tile kernel (the fused output stages equal it bit for bit).
     imq::SplitWs ws{};
-    if (regime == Regime::kAuto) ws = split_ws(ctx, st, imq::qgemm_split_bytes(k, n, m));
+    if (regime == Regime::kAuto) {
+      ws = split_ws(ctx, st, imq::qgemm_split_bytes(k, n, m));
+    } else if (regime == Regime::kAutoNoAlloc) {
+      const size_t need = imq::qgemm_split_bytes(k, n, m);
+      if (need > imq::kStaticScratchBytes)
+        return fail(ctx, IMQ_EINVAL,
+                    "%s: M=%d N=%d K=%d needs %zu bytes of split-K scratch; the static scratch "
+                    "holds %zu (imq_qmm_t takes this shape)",
+                    fn, m, n, k, need, imq::kStaticScratchBytes);
+      if (need > 0) ws = imq::SplitWs{static_cast<float*>(ctx->static_scratch), need};
+    }
     e = imq::launch_qgemm(w, s, b, x, y, k, n, m, (int)dtype, st, ws);
   } else {
     // f32 beyond 16 rows (the conditioner's multi-row calls): blocks of 16 rows.
@@ -274,9 +285,17 @@ int imq_create(int device, imq_ctx** out) {
   if (e != hipSuccess) return hip_fail(nullptr, e, "imq_create: hipGetDeviceCount");
   if (device < 0 || device >= count)
     return fail(nullptr, IMQ_EINVAL, "imq_create: device %d out of range [0, %d)", device, count);
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "imq_create: hipSetDevice");
+  // The device address of this GPU's copy of the static split-K scratch
+  // (imq_qmm_t_noalloc), looked up once per device with the device current.
+  void* scratch = nullptr;
+  e = imq::static_scratch(device, &scratch);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "imq_create: static scratch address");
   auto* c = new (std::nothrow) imq_ctx;
   if (!c) return fail(nullptr, IMQ_ENOMEM, "imq_create: out of host memory");
   c->device = device;
+  c->static_scratch = scratch;
   *out = c;
   return IMQ_OK;
 }
@@ -391,6 +410,13 @@ int imq_qmm_t(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* b
               imq_dtype dtype, imq_stream stream) {
   return run_qmm(ctx, "imq_qmm_t", Regime::kAuto, w, scales, biases, x, y, k, n, m, group_size,
                  bits, dtype, stream);
+}
+
+int imq_qmm_t_noalloc(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                      const void* x, void* y, int k, int n, int m, int group_size, int bits,
+                      imq_dtype dtype, imq_stream stream) {
+  return run_qmm(ctx, "imq_qmm_t_noalloc", Regime::kAutoNoAlloc, w, scales, biases, x, y, k, n, m,
+                 group_size, bits, dtype, stream);
 }
 
 int imq_qmm_plan(imq_ctx* ctx, int entry, int k, int n, int m, imq_dtype dtype, imq_plan* out) {

@@ -62,6 +62,9 @@ struct imq_ctx {
   std::mutex ws_mu;
   std::unordered_map<hipStream_t, std::pair<void*, size_t>> split_ws;
   std::vector<void*> retired_ws;  // outgrown workspaces, freed with the context
+  // Device address of the library's static split-K scratch on this device
+  // (imq_qmm_t_noalloc), looked up at imq_create.
+  void* static_scratch = nullptr;
 
   ~imq_ctx();
 };

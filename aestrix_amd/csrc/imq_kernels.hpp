@@ -104,6 +104,15 @@ constexpr int kQskinnyMaxM = 16;
 constexpr int kDispatchSkinnyMinM = 4;
 constexpr int kDispatchSkinnyMaxM = 16;
 
+// Bytes of the statically allocated split-K scratch of the allocation-free
+// dispatcher (one copy per GPU, scratch.hip).  64 MiB covers the split plans
+// of the text-encoder, conditioner and DiT shapes up to M = 2048 (the largest:
+// M = 2048 [2560 x 9728], three splits, 60 MiB).
+constexpr size_t kStaticScratchBytes = (size_t)64 << 20;
+// Device address of that scratch on `device`, which must be current; looked
+// up with hipGetSymbolAddress on the first call for a device.
+hipError_t static_scratch(int device, void** out);
+
 // Whether the weight-streaming kernel takes this call: 1 <= m <= 16,
 // k % 128 == 0, T in {bf16, f16}, 32-bit byte offsets.
 bool qskinny_supported(int k, int n, int m, int dtype);

@@ -129,6 +129,24 @@ int imq_qmm_t(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* b
               const void* x, void* y, int k, int n, int m, int group_size, int bits,
               imq_dtype dtype, imq_stream stream);
 
+/* imq_qmm_t that allocates nothing.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels, plan and results (bit for bit) as imq_qmm_t, except
+ * that a split-K plan keeps its fp32 partial sums in the library's static
+ * scratch: 64 MiB of device memory per GPU, part of the library's code object,
+ * held from the first imq_create on that GPU until the process ends.  Every
+ * partial sum a call reads it has written first, so nothing needs clearing.
+ * A shape whose plan needs more scratch than that returns IMQ_EINVAL (the
+ * largest plans of the text-encoder, conditioner and DiT shapes up to
+ * M = 2048 fit).  All calls on one GPU share the one scratch: calls that
+ * overlap in time on that GPU (several streams, several contexts, several
+ * threads, or a graph replay beside another call) race and may return wrong
+ * results; order them on one stream. */
+int imq_qmm_t_noalloc(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                      const void* x, void* y, int k, int n, int m, int group_size, int bits,
+                      imq_dtype dtype, imq_stream stream);
+
 /* The skinny regime alone (1 <= M <= 16): register dequant, fp32 dot products,
  * cross-lane reductions; no matrix cores.  Same contract as imq_qmm_t, for
  * packed weights under 4 GiB (IMQ_EUNSUPPORTED above; imq_qmm_t then runs
@@ -151,7 +169,7 @@ int imq_qgemm(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* b
  * for callers that size workspaces or pin a kernel choice in tests. */
 
 typedef enum imq_entry {
-    IMQ_ENTRY_QMM_T = 0,   /* imq_qmm_t */
+    IMQ_ENTRY_QMM_T = 0,   /* imq_qmm_t and imq_qmm_t_noalloc */
     IMQ_ENTRY_QGEMM = 1,   /* imq_qgemm */
     IMQ_ENTRY_QGEMV = 2,   /* imq_qgemv */
     IMQ_ENTRY_FUSED = 3    /* imq_qmm_postscale / _gate_add (n = weight rows), imq_qmm_swiglu
