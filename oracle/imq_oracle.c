@@ -94,6 +94,138 @@ static void set_threads(int threads) {
 #endif
 }
 
+/* IEEE binary16 bits -> f32 (exact: every f16 value is an f32 value).  The f16
+ * element type of the reference's DiT kernels (affine_qmm_t_float16_t,
+ * DirectDiTStep.swift:82-85) with its scales precast to f16
+ * (TransformerWeights.swift:40-54). */
+float oracle_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    uint32_t u;
+    if (e == 0x1Fu) {
+        u = sign | 0x7F800000u | (m << 13);
+    } else if (e != 0) {
+        u = sign | ((e + 112u) << 23) | (m << 13);
+    } else {
+        const float v = (float)m * 0x1p-24f; /* subnormal (or zero): m * 2^-24, exact */
+        return sign ? -v : v;
+    }
+    float f;
+    memcpy(&f, &u, sizeof f);
+    return f;
+}
+
+/* f32 -> IEEE binary16 bits, round to nearest even (overflow to inf, NaN kept
+ * quiet), by integer arithmetic on the f32 pattern. */
+uint16_t oracle_f32_to_f16(float v) {
+    uint32_t u;
+    memcpy(&u, &v, sizeof u);
+    const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    const uint32_t a = u & 0x7FFFFFFFu;
+    if (a >= 0x7F800000u) /* inf, NaN */
+        return (uint16_t)(sign | 0x7C00u | (a > 0x7F800000u ? 0x200u | ((a >> 13) & 0x3FFu) : 0u));
+    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u); /* >= 65520: rounds to inf */
+    if (a >= 0x38800000u) {                                   /* normal f16: >= 2^-14 */
+        const uint32_t r = a - 0x38000000u;                    /* exponent bias 127 -> 15 */
+        return (uint16_t)(sign | ((r + 0xFFFu + ((r >> 13) & 1u)) >> 13));
+    }
+    if (a < 0x33000000u) return sign; /* <= 2^-25: zero (2^-25 itself ties to even 0) */
+    /* subnormal f16: m = RNE(value * 2^24) */
+    const uint32_t mant = (a & 0x7FFFFFu) | 0x800000u;
+    const int shift = 126 - (int)(a >> 23);                   /* 14 .. 24 */
+    uint32_t m = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1u), half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (m & 1u))) ++m;
+    return (uint16_t)(sign | m);
+}
+
+void oracle_f16_to_f32_n(const uint16_t* in, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = oracle_f16_to_f32(in[i]);
+}
+
+void oracle_f32_to_f16_n(const float* in, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = oracle_f32_to_f16(in[i]);
+}
+
+/* T = bf16 (dtype 0) or f16 (dtype 1) bit patterns. */
+static float t_to_f32(int dtype, uint16_t h) {
+    return dtype == 0 ? oracle_bf16_to_f32(h) : oracle_f16_to_f32(h);
+}
+
+/* dequant_row in T: RNE_T(fl32(fl32(s * q) + b)) with s, b given in T
+ * (DirectTEEncoder.swift:106-123 for bf16; the f16 DiT pack for f16). */
+static void dequant_row_t(int dtype, const uint32_t* wrow, const uint16_t* srow,
+                          const uint16_t* brow, uint16_t* out, int64_t k) {
+    for (int64_t g = 0; g < k / 64; ++g) {
+        const float scale = t_to_f32(dtype, srow[g]);
+        const float bias = t_to_f32(dtype, brow[g]);
+        for (int64_t wd = 0; wd < 8; ++wd) {
+            const uint32_t packed = wrow[g * 8 + wd];
+            for (int nib = 0; nib < 8; ++nib) {
+                const float q = (float)((packed >> (4u * (uint32_t)nib)) & 0xFu);
+                volatile float prod = scale * q;
+                volatile float sum = prod + bias;
+                out[g * 64 + wd * 8 + nib] =
+                    dtype == 0 ? oracle_f32_to_bf16(sum) : oracle_f32_to_f16(sum);
+            }
+        }
+    }
+}
+
+int oracle_dequantize_t(int dtype, const uint32_t* w, const uint16_t* scales,
+                        const uint16_t* biases, uint16_t* out, int64_t n, int64_t k) {
+    if ((dtype != 0 && dtype != 1) || !shape_ok(n, k) || !w || !scales || !biases || !out)
+        return -1;
+    const int64_t wpr = k / 8, gpr = k / 64;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < n; ++r)
+        dequant_row_t(dtype, w + r * wpr, scales + r * gpr, biases + r * gpr, out + r * k, k);
+    return 0;
+}
+
+/* Unrounded y[m][n] = sum_k x[m][k] * deq_T(W)[n][k] accumulated in double, in
+ * k order: the contraction of quantizedMM(transpose: true)
+ * (DirectQmmSpike.swift:55-58) before the output rounding, which the caller
+ * applies (RNE to T once, from double). */
+int oracle_qmm_t_f64(int dtype, const uint16_t* x, const uint32_t* w, const uint16_t* scales,
+                     const uint16_t* biases, double* y, int64_t m, int64_t n, int64_t k,
+                     int threads) {
+    if ((dtype != 0 && dtype != 1) || m <= 0 || !shape_ok(n, k) || !x || !w || !scales ||
+        !biases || !y)
+        return -1;
+    set_threads(threads);
+    double* xd = (double*)malloc((size_t)(m * k) * sizeof(double));
+    if (!xd) return -1;
+    for (int64_t i = 0; i < m * k; ++i) xd[i] = (double)t_to_f32(dtype, x[i]);
+    const int64_t wpr = k / 8, gpr = k / 64;
+    int failed = 0;
+#pragma omp parallel
+    {
+        uint16_t* row = (uint16_t*)malloc((size_t)k * sizeof(uint16_t));
+        double* rowd = (double*)malloc((size_t)k * sizeof(double));
+        if (!row || !rowd) {
+#pragma omp atomic write
+            failed = 1;
+        } else {
+#pragma omp for schedule(static)
+            for (int64_t c = 0; c < n; ++c) {
+                dequant_row_t(dtype, w + c * wpr, scales + c * gpr, biases + c * gpr, row, k);
+                for (int64_t i = 0; i < k; ++i) rowd[i] = (double)t_to_f32(dtype, row[i]);
+                for (int64_t r = 0; r < m; ++r) {
+                    const double* xr = xd + r * k;
+                    double acc = 0.0;
+                    for (int64_t i = 0; i < k; ++i) acc += xr[i] * rowd[i];
+                    y[r * n + c] = acc;
+                }
+            }
+        }
+        free(row);
+        free(rowd);
+    }
+    free(xd);
+    return failed ? -1 : 0;
+}
+
 int oracle_max_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

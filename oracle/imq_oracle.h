@@ -56,6 +56,28 @@ int oracle_qmm_t_f32acc(const uint16_t* x, const uint32_t* w, const uint16_t* sc
                         const uint16_t* biases, uint16_t* y, int64_t m, int64_t n, int64_t k,
                         int threads);
 
+/* IEEE binary16 <-> f32: exact widening, and RNE narrowing (overflow to inf).
+ * f16 is the element type of the reference's DiT kernels
+ * (DirectDiTStep.swift:82-85, scales precast by TransformerWeights.swift:40-54). */
+float oracle_f16_to_f32(uint16_t h);
+uint16_t oracle_f32_to_f16(float v);
+/* The two conversions over arrays of n elements. */
+void oracle_f16_to_f32_n(const uint16_t* in, float* out, int64_t n);
+void oracle_f32_to_f16_n(const float* in, uint16_t* out, int64_t n);
+
+/* oracle_dequantize for T = bf16 (dtype 0) or f16 (dtype 1): scales, biases
+ * and out are T bit patterns; out = RNE_T(fl32(fl32(s*q) + b)). */
+int oracle_dequantize_t(int dtype, const uint32_t* w, const uint16_t* scales,
+                        const uint16_t* biases, uint16_t* out, int64_t n, int64_t k);
+
+/* y[m][n] = sum_k x[m][k] * deq_T(W)[n][k], accumulated in double and NOT
+ * rounded (the caller rounds once to T); x, scales, biases are T bit
+ * patterns, T = bf16 (dtype 0) or f16 (dtype 1).  For checks on a few rows of
+ * large problems: each weight row is dequantized once for all m rows. */
+int oracle_qmm_t_f64(int dtype, const uint16_t* x, const uint32_t* w, const uint16_t* scales,
+                     const uint16_t* biases, double* y, int64_t m, int64_t n, int64_t k,
+                     int threads);
+
 /* Number of OpenMP threads a parallel region would use (for reporting). */
 int oracle_max_threads(void);
 

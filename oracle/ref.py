@@ -85,18 +85,6 @@ def qmm_t(x: np.ndarray, w: np.ndarray, scales: np.ndarray, biases: np.ndarray) 
     return f64_to_bf16(qmm_t_f64(x, w, scales, biases))
 
 
-def qmm_t_f32_dequant_f64(x: np.ndarray, w: np.ndarray, scales: np.ndarray,
-                          biases: np.ndarray) -> np.ndarray:
-    """Unrounded float64 y with the dequant left unrounded (fl32(s*q+b)), for
-    reporting the literal 'fp32 dequant-then-matmul' reading of the tolerance."""
-    q = unpack_codes(w).astype(np.float32)
-    n, k = q.shape
-    s = np.repeat(bf16_to_f32(scales), GROUP_SIZE, axis=-1).reshape(n, k)
-    b = np.repeat(bf16_to_f32(biases), GROUP_SIZE, axis=-1).reshape(n, k)
-    wd = (s * q + b).astype(np.float64)
-    return bf16_to_f32(x).astype(np.float64) @ wd.T
-
-
 def dequantize_as(w: np.ndarray, scales: np.ndarray, biases: np.ndarray,
                   dtype) -> np.ndarray:
     """deq(W) [N, K] in T = float16 or float32, with scales and biases given in T:

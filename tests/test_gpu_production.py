@@ -1,0 +1,270 @@
+"""The kernel instances the DiT runs, at its production shapes, against the oracle.
+
+The DiT step's trace runs the tile kernel at 192-, 224- and 256-row tiles
+with the plain, gated-residual and SwiGLU output stages (f16), the double
+blocks' image and text chains each planned for their share of the CUs.  The
+tests here run those shapes through the C entry points (asserting, through
+imq_qmm_plan, the tile height each takes) and the whole step at its full
+size (5 double + 20 single blocks, 4096 image + 512 text rows, dim 3072,
+ff_inner 9216), in f16 and bf16.
+
+Oracle: every op on the path is row-local (RMSNorm per row, qmm per row,
+SwiGLU and the gated residual per element), so the CPU oracle follows a few
+sampled rows through the full-size problem: RNE_T of the double-accumulated
+product with the bit-exact dequant (oracle.cref.qmm_t_f64), then the
+reference's glue arithmetic (oracle.ref glue_*).  Bars as in the other GPU
+tests: MAE <= 1e-3, normwise max error <= 1e-2, cosine >= 0.99999 per
+projection; the step's final fp32 residual within normwise 1e-2, and graph
+replays equal to the eager launches bit for bit.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import aestrix_amd as imq
+from aestrix_amd import synth
+from aestrix_amd.step import DitDims, DitStep, random_projections
+from oracle import cref, ref
+
+pytestmark = pytest.mark.gpu
+
+MAE_TOL = 1e-3
+NORMWISE_TOL = 1e-2
+COSINE_MIN = 0.99999  # the reference's qmm parity bar (DirectQmmSpike.swift:141-153)
+TDT = {"bf16": torch.bfloat16, "f16": torch.float16}
+
+
+@pytest.fixture(autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+
+
+def note(msg: str) -> None:
+    print(msg, flush=True)
+
+
+def host_bits(t: torch.Tensor) -> np.ndarray:
+    """A bf16 / f16 device tensor as uint16 bit patterns on the host."""
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def t_values(bits: np.ndarray, dtype: str) -> np.ndarray:
+    """T bit patterns -> float64 values."""
+    if dtype == "bf16":
+        return ref.bf16_to_f32(bits).astype(np.float64)
+    return bits.view(np.float16).astype(np.float64)
+
+
+def round_t(v: np.ndarray, dtype: str) -> np.ndarray:
+    """float64 values -> T bit patterns, rounded once (RNE)."""
+    if dtype == "bf16":
+        return ref.f64_to_bf16(v)
+    return np.asarray(v, np.float64).astype(np.float16).view(np.uint16)
+
+
+def oracle_qmm(x_bits, w, s_bits, b_bits, dtype) -> np.ndarray:
+    """float64 values of RNE_T(x . deq_T(W)^T) (T bit patterns in)."""
+    return t_values(round_t(cref.qmm_t_f64(x_bits, w, s_bits, b_bits, dtype), dtype), dtype)
+
+
+def assert_close(y: np.ndarray, want: np.ndarray, what: str) -> None:
+    st = ref.error_stats_values(np.asarray(y, np.float64), np.asarray(want, np.float64))
+    note(f"  {what}: mae={st['mae']:.3g} normwise={st['max_rel_normwise']:.3g} "
+         f"bit_exact={st['bit_exact_frac']:.4f} cosine={st['cosine']:.7f}")
+    assert st["mae"] <= MAE_TOL and st["max_rel_normwise"] <= NORMWISE_TOL, (what, st)
+    assert st["cosine"] >= COSINE_MIN, (what, st)
+
+
+def problem(m, n, k, dtype, seed, x_scale=1.0):
+    """Seeded problem on the device in T; the host copies are the device's bytes."""
+    p = synth.make_problem(m, n, k, seed=seed)
+    x, w, s, b = synth.to_device(p)
+    x = x * x_scale  # a power of two: exact
+    if dtype == "f16":
+        x, s, b = x.half(), s.half(), b.half()
+    return p.w, x, w, s, b
+
+
+def sample_rows(m: int, count: int) -> np.ndarray:
+    return np.unique(np.linspace(0, m - 1, count).astype(np.int64))
+
+
+# --------------------------------------------- fused stages at step tile heights
+
+
+# (M, N weight rows, K, width, gate_row, up_row, tile rows): the single block's
+# to_qkv_mlp_proj MLP half (J = 4608), the double blocks' ff.linear_in over the
+# image rows (4096) and ff_context.linear_in over the text rows (512).
+SWIGLU = [(4608, 27648, 3072, 9216, 9216, 18432, 224),
+          (4096, 18432, 3072, 9216, 0, 9216, 256),
+          (512, 18432, 3072, 9216, 0, 9216, 192)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("case", SWIGLU, ids=[f"M{c[0]}" for c in SWIGLU])
+def test_swiglu_at_production_tile_heights(dtype, case):
+    m, n, k, width, gate_row, up_row, tile_rows = case
+    note(f"qmm_swiglu {dtype} M={m} N={n} K={k} width={width} gate_row={gate_row} "
+         f"up_row={up_row} seed=80")
+    plan = imq.qmm_plan(m, 2 * width, k, TDT[dtype], entry="fused")
+    note(f"  plan {plan}")
+    assert plan["kernel"] == "tile" and plan["tile_rows"] == tile_rows and plan["splits"] == 1
+    # x / 16 with the reference's in/out scales 16 and 1/16 (the f16 protocol
+    # of dd_swiglu_pitched, DirectDiTStep.swift:521-543).
+    w_h, x, w, s, b = problem(m, n, k, dtype, seed=80, x_scale=1.0 / 16)
+    y = imq.qmm_swiglu(x, w, s, b, width, gate_row, up_row, in_scale=16.0, out_scale=1.0 / 16)
+    rows = sample_rows(m, 24)
+    got = t_values(host_bits(y)[rows], dtype)
+    xb, sb, bb = host_bits(x)[rows], host_bits(s), host_bits(b)
+    g = oracle_qmm(xb, w_h[gate_row:gate_row + width], sb[gate_row:gate_row + width],
+                   bb[gate_row:gate_row + width], dtype)
+    u = oracle_qmm(xb, w_h[up_row:up_row + width], sb[up_row:up_row + width],
+                   bb[up_row:up_row + width], dtype)
+    want = t_values(round_t(ref.glue_swiglu(g, u, 16.0, 1.0 / 16), dtype), dtype)
+    assert np.all(np.isfinite(got))
+    assert_close(got, want, f"swiglu M={m} rows={len(rows)}")
+
+
+# (M, N, K, tile rows): the single block's to_out (K = 12288) over J = 4608
+# rows and the double blocks' ff.linear_out (K = 9216) over the image rows.
+GATE_ADD = [(4608, 3072, 12288, 224), (4096, 3072, 9216, 224)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("case", GATE_ADD, ids=[f"M{c[0]}_K{c[2]}" for c in GATE_ADD])
+def test_gate_add_at_production_tile_heights(dtype, case):
+    m, n, k, tile_rows = case
+    note(f"qmm_gate_add {dtype} M={m} N={n} K={k} seed=81 (in place)")
+    plan = imq.qmm_plan(m, n, k, TDT[dtype], entry="fused")
+    note(f"  plan {plan}")
+    assert plan["kernel"] == "tile" and plan["tile_rows"] == tile_rows and plan["splits"] == 1
+    w_h, x, w, s, b = problem(m, n, k, dtype, seed=81, x_scale=1.0 / 16)
+    rng = np.random.default_rng(81)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    gate = rng.standard_normal(n).astype(np.float32)
+    r_dev = torch.from_numpy(res).cuda()
+    y = imq.qmm_gate_add(x, w, s, b, r_dev, torch.from_numpy(gate).cuda(), 16.0, out=r_dev)
+    torch.cuda.synchronize()
+    rows = sample_rows(m, 32)
+    got = y.cpu().numpy()[rows]
+    v = oracle_qmm(host_bits(x)[rows], w_h, host_bits(s), host_bits(b), dtype)
+    want = ref.glue_gate_add(v.astype(np.float32), res[rows], gate, 16.0)
+    assert_close(got, want, f"gate_add M={m} K={k} rows={len(rows)}")
+
+
+# (M, N, K, tile rows, splits): the double blocks' Q/K/V over image rows and
+# text rows, and the image rows' MLP-in width as a plain store (256-row tiles).
+PLAIN = [(4096, 3072, 3072, 224, 1), (512, 3072, 3072, 32, 1), (4096, 18432, 3072, 256, 1)]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("case", PLAIN, ids=[f"M{c[0]}_N{c[1]}" for c in PLAIN])
+def test_plain_qmm_at_production_tile_heights(dtype, case):
+    m, n, k, tile_rows, splits = case
+    note(f"qmm_t {dtype} M={m} N={n} K={k} seed=82")
+    plan = imq.qmm_plan(m, n, k, TDT[dtype])
+    note(f"  plan {plan}")
+    assert plan["kernel"] == "tile" and plan["tile_rows"] == tile_rows
+    assert plan["splits"] == splits
+    w_h, x, w, s, b = problem(m, n, k, dtype, seed=82)
+    y = imq.quantized_matmul(x, w, s, b)
+    rows = sample_rows(m, 32)
+    got = t_values(host_bits(y)[rows], dtype)
+    want = oracle_qmm(host_bits(x)[rows], w_h, host_bits(s), host_bits(b), dtype)
+    assert_close(got, want, f"qmm_t M={m} N={n} rows={len(rows)}")
+
+
+# -------------------------------------------------------- the full-size step
+
+
+def oracle_step_rows(d: DitDims, hp, norm_w, gates, X0, txt_rows, img_rows, dtype):
+    """Final fp32 residual rows of the step, following `txt_rows` (of the l_txt
+    text rows) and `img_rows` (of the l_img image rows) through every block.
+    hp: per projection (w, scale bits, bias bits) on the host.  X0: the
+    sampled rows of the initial joint residual, text rows first."""
+    dim, ffi = d.dim, d.ff_inner
+    nt = len(txt_rows)
+    X = X0.astype(np.float32).copy()
+    T, I = slice(0, nt), slice(nt, None)
+
+    def rms(Xr):
+        return round_t(ref.rmsnorm_rows(Xr, norm_w), dtype)
+
+    def qmm(x_bits, q, rows=None):
+        w, s, b = hp[q]
+        if rows is not None:
+            w, s, b = w[rows], s[rows], b[rows]
+        return oracle_qmm(x_bits, w, s, b, dtype)
+
+    def swiglu(x_bits, q, gate_row, up_row):
+        g = qmm(x_bits, q, slice(gate_row, gate_row + ffi))
+        u = qmm(x_bits, q, slice(up_row, up_row + ffi))
+        return round_t(ref.glue_swiglu(g, u, 1.0, 1.0), dtype)
+
+    def gate_add(v, Xr, gate):
+        return ref.glue_gate_add(v.astype(np.float32), Xr, gate, 1.0)
+
+    for blk in range(d.n_double):
+        base = 12 * blk
+        g = gates[4 * blk:4 * blk + 4]
+        nX = rms(X)
+        v_i = round_t(qmm(nX[I], base + 2), dtype)   # to_v over image rows
+        v_t = round_t(qmm(nX[T], base + 5), dtype)   # add_v_proj over text rows
+        X[I] = gate_add(qmm(v_i, base + 6), X[I], g[0])
+        X[T] = gate_add(qmm(v_t, base + 7), X[T], g[1])
+        nX = rms(X)
+        X[I] = gate_add(qmm(swiglu(nX[I], base + 8, 0, ffi), base + 9), X[I], g[2])
+        X[T] = gate_add(qmm(swiglu(nX[T], base + 10, 0, ffi), base + 11), X[T], g[3])
+    for blk in range(d.n_single):
+        base = 12 * d.n_double + 2 * blk
+        g = gates[4 * d.n_double + blk]
+        nX = rms(X)
+        sw = swiglu(nX, base, 3 * dim, 3 * dim + ffi)
+        # C = [attention half (zeros) | SwiGLU]; the zero half adds exact zeros.
+        C = np.zeros((X.shape[0], dim + ffi), np.uint16)
+        C[:, dim:] = sw
+        X = gate_add(qmm(C, base + 1), X, g)
+    return X
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_full_size_step_sampled_rows_and_graph_replays(dtype):
+    d = DitDims()
+    note(f"dit step {dtype} full size {d} seed=83")
+    tdt = TDT[dtype]
+    projs = random_projections(d, tdt, seed=83)
+    step = DitStep(d, projs)
+    try:
+        rng = np.random.default_rng(83)
+        norm_w = (1.0 + 0.1 * rng.standard_normal(d.dim)).astype(np.float32)
+        gates = (0.5 * rng.standard_normal((4 * d.n_double + d.n_single, d.dim))).astype(np.float32)
+        step.set_conditioning(torch.from_numpy(norm_w).cuda(), torch.from_numpy(gates).cuda())
+        h = rng.standard_normal((d.l_img, d.dim)).astype(np.float32)
+        e = rng.standard_normal((d.l_txt, d.dim)).astype(np.float32)
+        h_d, e_d = torch.from_numpy(h).cuda(), torch.from_numpy(e).cuda()
+        eager = step.run(h_d, e_d, use_graph=False).cpu().numpy()
+        assert step.launches == d.n_double * 14 + d.n_single * 4
+        assert np.all(np.isfinite(eager))
+        for rep in range(3):  # replays with other device work in between
+            torch.randn(1000, device="cuda").sum().item()
+            graph = step.run(h_d, e_d, use_graph=True).cpu().numpy()
+            assert np.array_equal(graph, eager), f"graph replay {rep} differs from eager"
+        note("  graph == eager over 3 replays; oracle on sampled rows ...")
+        hp = [(q.w.cpu().numpy().view(np.uint32), host_bits(q.s), host_bits(q.b)) for q in projs]
+    finally:
+        step.close()
+    txt_rows = sample_rows(d.l_txt, 8)
+    img_rows = sample_rows(d.l_img, 16)
+    X0 = np.concatenate([e[txt_rows], h[img_rows]])
+    want = oracle_step_rows(d, hp, norm_w, gates, X0, txt_rows, img_rows, dtype)
+    got = np.concatenate([eager[txt_rows], eager[d.l_txt + img_rows]])
+    diff = np.abs(got.astype(np.float64) - want)
+    normwise = diff.max() / np.abs(want).max()
+    mean_rel = diff.mean() / np.abs(want).mean()
+    note(f"  {len(txt_rows)} text + {len(img_rows)} image rows: normwise={normwise:.3g} "
+         f"mean_rel={mean_rel:.3g}")
+    assert normwise <= NORMWISE_TOL, normwise

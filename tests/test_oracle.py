@@ -528,6 +528,29 @@ def test_glue_swiglu_matches_torch_silu():
     assert np.all(ref.glue_swiglu(np.zeros(3, np.float32), np.ones(3, np.float32), 1, 1) == 0)
 
 
+def test_glue_gate_add_matches_torch_float64_per_column_gate():
+    """fma(gate[j], float(v) * scale, x) with a random per-column gate, scale
+    1/16 and a non-square shape, against torch float64 arithmetic done
+    independently: v * scale rounded to f32 (the kernel's multiply), then the
+    exact product with the gate plus x, rounded once to f32 (the fma)."""
+    rng = np.random.default_rng(44)
+    m, n = 7, 19
+    y = rng.standard_normal((m, n)).astype(np.float32)
+    x = rng.standard_normal((m, n)).astype(np.float32)
+    gate = rng.standard_normal(n).astype(np.float32)
+    scale = 1.0 / 16
+    vs = (torch.from_numpy(y) * torch.tensor(np.float32(scale))).double()
+    want = (torch.from_numpy(gate).double()[None, :] * vs + torch.from_numpy(x).double()).float()
+    got = ref.glue_gate_add(y, x, gate, scale)
+    assert got.dtype == np.float32 and got.shape == (m, n)
+    assert np.array_equal(got, want.numpy())
+    # Mutants: the gate indexed by row instead of column, and the scale dropped.
+    row_gate = np.resize(gate, m)[:, None] * (y * np.float32(scale)).astype(np.float64) + x
+    assert not np.array_equal(got, row_gate.astype(np.float32))
+    no_scale = gate[None, :].astype(np.float64) * y + x
+    assert not np.array_equal(got, no_scale.astype(np.float32))
+
+
 def test_glue_gate_add_and_postscale_closed_forms():
     rng = np.random.default_rng(4)
     y = rng.standard_normal((5, 8)).astype(np.float32)
@@ -607,3 +630,110 @@ def test_glue_prescale_checks_catch_truncation_mutant():
     assert float(bf16[1]) == float(_rne_format(Fraction(1 + 2 ** -8 + 2 ** -12), 8, -126, 127)) == 1 + 2 ** -7
     trunc_bf16 = ((x / np.float32(16)).view(np.uint32) >> np.uint32(16)).astype(np.uint16)
     assert float(ref.bf16_to_f32(trunc_bf16)[1]) != float(bf16[1])
+
+
+# --------------------------------------------------- f16 and the f64 contraction
+
+
+def test_c_f16_widening_matches_numpy_on_every_pattern():
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    got = cref.f16_to_f32(h)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def _f16_neighbourhood() -> np.ndarray:
+    """Every finite f16 value, every midpoint between consecutive f16 values
+    (the ties), and the f32 values one ulp either side of both, both signs,
+    plus the overflow boundary and specials."""
+    h = np.arange(0, 0x7C00, dtype=np.uint16)
+    v = h.view(np.float16).astype(np.float64)
+    mids = (v[:-1] + v[1:]) / 2  # exact in f32: at most 12 significant bits
+    base = np.concatenate([v, mids, [65504.0, 65520.0, 65536.0, 2.0 ** -24, 2.0 ** -25,
+                                     3 * 2.0 ** -26, 2.0 ** -26, 1e-30, 3e38]]).astype(np.float32)
+    up = np.nextafter(base, np.float32(np.inf))
+    dn = np.nextafter(base, np.float32(0))
+    allv = np.concatenate([base, up, dn])
+    return np.concatenate([allv, -allv, np.float32([np.inf, -np.inf, 0.0, -0.0])])
+
+
+def test_c_f16_narrowing_matches_numpy_on_every_tie_and_neighbour():
+    v = _f16_neighbourhood()
+    got = cref.f32_to_f16(v)
+    want = v.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    rng = np.random.default_rng(45)
+    r = rng.integers(0, 1 << 32, size=1 << 20, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    r = r[np.isfinite(r)]
+    assert np.array_equal(cref.f32_to_f16(r), r.astype(np.float16).view(np.uint16))
+    nan = cref.f32_to_f16(np.float32([np.nan]))[0]
+    assert (nan & 0x7C00) == 0x7C00 and (nan & 0x3FF) != 0
+
+
+def test_c_f16_narrowing_matches_exact_rational_rounding():
+    """Independent of numpy: 3000 values of the neighbourhood rounded with
+    rational arithmetic (11-bit significand, exponents -14..15, ties to even)."""
+    v = _f16_neighbourhood()
+    v = v[np.isfinite(v)]
+    rng = np.random.default_rng(46)
+    pick = v[rng.choice(v.size, 3000, replace=False)]
+    got = cref.f32_to_f16(pick).view(np.float16).astype(np.float64)
+    for xi, gi in zip(pick.tolist(), got.tolist()):
+        want = _rne_format(Fraction(xi), 11, -14, 15)
+        assert gi == float(want), (xi, gi, want)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_c_dequantize_t_matches_pinned_dequant(dtype):
+    """The C T-generic dequant equals the numpy one (pinned above against exact
+    rational arithmetic) bit for bit, for bf16 and f16 parameters, including
+    the f16 parameter grid of zero, subnormal, negative and huge values."""
+    p = synth.make_problem(0, 96, 512, seed=47)
+    if dtype == "bf16":
+        assert np.array_equal(cref.dequantize_t(p.w, p.scales, p.biases, "bf16"),
+                              ref.dequantize(p.w, p.scales, p.biases))
+        return
+    s16 = ref.bf16_to_f32(p.scales).astype(np.float16)
+    b16 = ref.bf16_to_f32(p.biases).astype(np.float16)
+    want = ref.dequantize_as(p.w, s16, b16, np.float16).view(np.uint16)
+    assert np.array_equal(cref.dequantize_t(p.w, s16, b16, "f16"), want)
+    vals = _f16_param_values()
+    rng = np.random.default_rng(48)
+    n = 64
+    s = rng.choice(vals, size=(n, 2)).astype(np.float16)
+    b = rng.choice(vals, size=(n, 2)).astype(np.float16)
+    w = rng.integers(0, 1 << 32, size=(n, 16), dtype=np.uint64).astype(np.uint32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = ref.dequantize_as(w, s, b, np.float16).view(np.uint16)
+    got = cref.dequantize_t(w, s, b, "f16")
+    same = (got == want) | (np.isnan(got.view(np.float16)) & np.isnan(want.view(np.float16)))
+    assert np.all(same)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_c_qmm_t_f64_matches_pinned_float64_product(dtype):
+    """The unrounded double contraction equals the numpy float64 product of the
+    pinned dequant (same terms, another summation order: agreement to a few
+    ulps of double), and its RNE to T equals the pinned oracle's."""
+    p = synth.make_problem(9, 200, 1024, seed=49)
+    if dtype == "bf16":
+        got = cref.qmm_t_f64(p.x, p.w, p.scales, p.biases, "bf16")
+        want = ref.qmm_t_f64(p.x, p.w, p.scales, p.biases)
+        assert np.array_equal(ref.f64_to_bf16(got), ref.qmm_t(p.x, p.w, p.scales, p.biases))
+    else:
+        x16 = ref.bf16_to_f32(p.x).astype(np.float16)
+        s16 = ref.bf16_to_f32(p.scales).astype(np.float16)
+        b16 = ref.bf16_to_f32(p.biases).astype(np.float16)
+        got = cref.qmm_t_f64(x16, p.w, s16, b16, "f16")
+        want = x16.astype(np.float64) @ ref.dequantize_as(p.w, s16, b16, np.float16).astype(
+            np.float64).T
+        assert np.array_equal(got.astype(np.float16), ref.qmm_t_as(x16, p.w, s16, b16, np.float16))
+    assert np.max(np.abs(got - want)) <= 1e-12 * np.max(np.abs(want))
+    # A transposed-weight mutant (rows read as K-reversed) must fail.
+    rev = ref.pack_codes(ref.unpack_codes(p.w)[:, ::-1].copy())
+    bad = cref.qmm_t_f64(p.x if dtype == "bf16" else x16, rev,
+                         p.scales if dtype == "bf16" else s16,
+                         p.biases if dtype == "bf16" else b16, dtype)
+    assert np.max(np.abs(bad - want)) > 1e-3 * np.max(np.abs(want))
