@@ -244,7 +244,8 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
 namespace {
 
 // Shared checks of the fused-epilogue entry points: the qmm checks, then T in
-// {bf16, f16} and the MFMA kernel's shape condition.
+// {bf16, f16} (any K % 64 == 0: K % 256 != 0 runs the register-staged tile
+// kernel with the same output stage).
 int check_epilogue(imq_ctx* ctx, const char* fn, const uint32_t* w, const void* s, const void* b,
                    const void* x, const void* y, int k, int n, int m, int group_size, int bits,
                    imq_dtype dtype) {
@@ -253,10 +254,6 @@ int check_epilogue(imq_ctx* ctx, const char* fn, const uint32_t* w, const void* 
   if (dtype == IMQ_F32)
     return fail(ctx, IMQ_EUNSUPPORTED, "%s: f32 has no MFMA kernel (bf16 and f16 are provided)",
                 fn);
-  if (!imq::qgemm_big_supported(k, n, m))
-    return fail(ctx, IMQ_EUNSUPPORTED,
-                "%s: K=%d must be a multiple of 256 (and x, w under 2 GiB) for fused epilogues",
-                fn, k);
   return bind_device(ctx);
 }
 
@@ -450,8 +447,6 @@ int imq_qmm_plan(imq_ctx* ctx, int entry, int k, int n, int m, imq_dtype dtype, 
     case IMQ_ENTRY_QGEMM:
     case IMQ_ENTRY_FUSED:
       if (dtype == IMQ_F32) return fail(ctx, IMQ_EUNSUPPORTED, "%s: f32 has no MFMA kernel", fn);
-      if (entry == IMQ_ENTRY_FUSED && !imq::qgemm_big_supported(k, n, m))
-        return fail(ctx, IMQ_EUNSUPPORTED, "%s: fused stages need K %% 256 == 0", fn);
       return tile(entry == IMQ_ENTRY_FUSED, false);
     case IMQ_ENTRY_QMM_T: {
       const bool gemv = w_fits_gemv && (m <= imq::kDispatchGemvMaxM || dtype == IMQ_F32);

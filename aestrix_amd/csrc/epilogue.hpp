@@ -83,6 +83,8 @@ struct EpPostscale {
 
 // y[row][col] = fma(gate[col], float(T(acc)) * scale, x[row][col]), fp32
 // residual stream: dd_gate_add (DirectDiTKernels.swift:211-224).  y may alias x.
+// With scale_dev set, the scale is read from device memory when the kernel runs
+// (a graph replay with the Euler step's 16 dt of the current step).
 template <int T>
 struct EpGateAdd {
   static constexpr bool kPair = false;
@@ -93,12 +95,15 @@ struct EpGateAdd {
   int ld;
   float scale;
   bool vec;
+  const float* scale_dev;
   __device__ __forceinline__ float value(float acc) const { return acc; }
+  __device__ __forceinline__ float the_scale() const { return scale_dev ? *scale_dev : scale; }
   __device__ __forceinline__ void emit1(int row, int col, uint16_t v) const {
     const size_t i = (size_t)row * ld + col;
-    y[i] = __builtin_fmaf(gate[col], staged_value<T>(v) * scale, x[i]);
+    y[i] = __builtin_fmaf(gate[col], staged_value<T>(v) * the_scale(), x[i]);
   }
   __device__ __forceinline__ void emit8(int row, int col, uint4 v) const {
+    const float scale = the_scale();
     const size_t i = (size_t)row * ld + col;
     const float4* xs = reinterpret_cast<const float4*>(x + i);
     const float4* gs = reinterpret_cast<const float4*>(gate + col);

@@ -55,14 +55,16 @@ QgemmPlan qgemm_plan(int k, int n, int m, bool fused, bool split, int cus);
 // these shapes: K % 256 == 0 and x, w addressable with 32-bit byte offsets.
 bool qgemm_big_supported(int k, int n, int m);
 
-// Fused output stages on the MFMA kernel (T in {bf16, f16}; the shapes must
-// satisfy qgemm_big_supported).  Without a workspace they equal the qmm
+// Fused output stages on the MFMA kernels (T in {bf16, f16}; any K % 64 == 0:
+// shapes outside qgemm_big_supported run the register-staged tile kernel,
+// never split).  Without a workspace they equal the qmm
 // followed by the reference's glue kernel on its T output bit for bit; with
 // one (ws.bytes >= qgemm_split_bytes(k, n, m, true)) K may be split, the
 // glue applied after the splits are added, which reorders the K sum:
 //
 //   postscale: y[m][n] (f32) = float(T(acc)) * scale
 //   gate_add:  y[m][n] (f32) = residual[m][n] + gate[n] * float(T(acc)) * scale
+//              (scale read from scale_dev when the kernel runs, if given)
 //   swiglu:    y[m][j] (T, row pitch ldy) = T(g * sigmoid(g) * u * out_scale), j < width,
 //              g = float(T(x . W[gate_row + j])) * in_scale, u likewise with up_row.
 hipError_t launch_qgemm_postscale(const uint32_t* w, const void* scales, const void* biases,
@@ -71,7 +73,7 @@ hipError_t launch_qgemm_postscale(const uint32_t* w, const void* scales, const v
 hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const void* biases,
                                  const void* x, const float* residual, const float* gate, float* y,
                                  int k, int n, int m, float scale, int dtype, hipStream_t stream,
-                                 SplitWs ws = {});
+                                 SplitWs ws = {}, const float* scale_dev = nullptr);
 hipError_t launch_qgemm_swiglu(const uint32_t* w, const void* scales, const void* biases,
                                const void* x, void* y, int ldy, int k, int n, int m, int width,
                                int gate_row, int up_row, float in_scale, float out_scale, int dtype,
@@ -81,9 +83,14 @@ hipError_t launch_qgemm_swiglu(const uint32_t* w, const void* scales, const void
 hipError_t launch_prescale(const float* x, void* y, size_t count, float scale, int dtype,
                            hipStream_t stream);
 
-// y[r][c] (T) = x[r][c] * rsqrt(mean(x[r]^2) + eps) * w[c], x fp32 [rows, cols].
+// y[r][c] (T) = x[r][c] * rsqrt(mean(x[r]^2) + eps) * w[c] * out_scale, x fp32
+// [rows, cols]; out_scale a power of two.
 hipError_t launch_rmsnorm(const float* x, const float* w, void* y, int rows, int cols, float eps,
-                          int dtype, hipStream_t stream);
+                          int dtype, hipStream_t stream, float out_scale = 1.0f);
+
+// p[i] = v for i < n (a kernel, so that it can precede a graph launch on a
+// stream without a host buffer that must outlive the call).
+hipError_t launch_fill_f32(float* p, float v, int n, hipStream_t stream);
 
 // Largest M the qGEMV kernel takes.
 constexpr int kQgemvMaxM = 16;

@@ -1,11 +1,14 @@
 // norm.hip -- row RMSNorm from the fp32 residual stream into a qmm input.
 //
-// y[r][c] = T(x[r][c] * rsqrt(mean_c(x[r][c]^2) + eps) * w[c]): the RMSNorm
+// y[r][c] = T(x[r][c] * rsqrt(mean_c(x[r][c]^2) + eps) * w[c] * s): the RMSNorm
 // between the blocks of a DiT step, in the shape of the reference's
 // dd_rmsnorm_pitched (Sources/ImarelloDirect/DirectDiTKernels.swift:61-99:
 // fp32 sum of squares, rsqrt(mean + eps), times an fp32 weight; eps 1e-5 at
 // DirectDiTStep.swift:416).  HBM-bound: one workgroup per row.  Rounding to
-// T is RNE (the hardware pair conversion in the vector kernel).
+// T is RNE (the hardware pair conversion in the vector kernel).  s is 1 between
+// the blocks and 1/16 before the head's proj_out (the ÷16 of the f16 protocol
+// that dd_ln_mod_prescale folds into its output, DirectDiTKernels.swift:16-59);
+// a power of two, so it never changes a rounding.
 #include "imq_device.hpp"
 #include "imq_kernels.hpp"
 
@@ -18,7 +21,7 @@ template <int T>
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float* __restrict__ x,
                                                            const float* __restrict__ w,
                                                            typename Elem<T>::S* __restrict__ y,
-                                                           int cols, float eps) {
+                                                           int cols, float eps, float s) {
   __shared__ float part[kThreads / 64];
   const float* xr = x + (size_t)blockIdx.x * cols;
   float acc = 0.f;
@@ -32,7 +35,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float* __restri
   for (int i = 0; i < kThreads / 64; ++i) total += part[i];
   const float inv = __frsqrt_rn(total / (float)cols + eps);
   typename Elem<T>::S* yr = y + (size_t)blockIdx.x * cols;
-  for (int c = threadIdx.x; c < cols; c += kThreads) yr[c] = Elem<T>::out(xr[c] * inv * w[c]);
+  for (int c = threadIdx.x; c < cols; c += kThreads) yr[c] = Elem<T>::out(xr[c] * inv * w[c] * s);
 }
 
 // The same for cols % 4 == 0 and cols <= 1024 * V: each thread loads its V
@@ -43,7 +46,7 @@ template <int T, int V>
 __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(const float* __restrict__ x,
                                                                const float* __restrict__ w,
                                                                typename Elem<T>::S* __restrict__ y,
-                                                               int cols, float eps) {
+                                                               int cols, float eps, float s) {
   __shared__ float part[kThreads / 64];
   const int n4 = cols >> 2;
   const float4* xr = reinterpret_cast<const float4*>(x + (size_t)blockIdx.x * cols);
@@ -73,41 +76,53 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(const float* __re
     const int idx = threadIdx.x + i * kThreads;
     if (idx < n4) {
       const float4 ww = wr[idx];
-      yr[idx] = make_uint2(Elem<T>::pack2(v[i].x * inv * ww.x, v[i].y * inv * ww.y),
-                           Elem<T>::pack2(v[i].z * inv * ww.z, v[i].w * inv * ww.w));
+      yr[idx] = make_uint2(Elem<T>::pack2(v[i].x * inv * ww.x * s, v[i].y * inv * ww.y * s),
+                           Elem<T>::pack2(v[i].z * inv * ww.z * s, v[i].w * inv * ww.w * s));
     }
   }
 }
 
 template <int T>
 hipError_t launch_t(const float* x, const float* w, void* y, int rows, int cols, float eps,
-                    hipStream_t stream) {
+                    float s, hipStream_t stream) {
   auto* yy = static_cast<typename Elem<T>::S*>(y);
   const bool vec = cols % 4 == 0 && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)w & 15u) == 0 &&
                    ((uintptr_t)y & 7u) == 0;
   const int v = (cols / 4 + kThreads - 1) / kThreads;
   const dim3 grid(rows), block(kThreads);
   if (vec && v <= 1)
-    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, 1>), grid, block, 0, stream, x, w, yy, cols, eps);
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, 1>), grid, block, 0, stream, x, w, yy, cols, eps, s);
   else if (vec && v == 2)
-    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, 2>), grid, block, 0, stream, x, w, yy, cols, eps);
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, 2>), grid, block, 0, stream, x, w, yy, cols, eps, s);
   else if (vec && v == 3)
-    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, 3>), grid, block, 0, stream, x, w, yy, cols, eps);
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, 3>), grid, block, 0, stream, x, w, yy, cols, eps, s);
   else if (vec && v == 4)
-    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, 4>), grid, block, 0, stream, x, w, yy, cols, eps);
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, 4>), grid, block, 0, stream, x, w, yy, cols, eps, s);
   else
-    hipLaunchKernelGGL(rmsnorm_kernel<T>, grid, block, 0, stream, x, w, yy, cols, eps);
+    hipLaunchKernelGGL(rmsnorm_kernel<T>, grid, block, 0, stream, x, w, yy, cols, eps, s);
   return hipGetLastError();
+}
+
+__global__ __launch_bounds__(kThreads) void fill_f32_kernel(float* __restrict__ p, float v, int n) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) p[i] = v;
 }
 
 }  // namespace
 
+hipError_t launch_fill_f32(float* p, float v, int n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_f32_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, stream, p, v, n);
+  return hipGetLastError();
+}
+
 hipError_t launch_rmsnorm(const float* x, const float* w, void* y, int rows, int cols, float eps,
-                          int dtype, hipStream_t stream) {
+                          int dtype, hipStream_t stream, float out_scale) {
   if (rows <= 0) return hipSuccess;
   switch (dtype) {
-    case kBf16: return launch_t<kBf16>(x, w, y, rows, cols, eps, stream);
-    case kF16: return launch_t<kF16>(x, w, y, rows, cols, eps, stream);
+    case kBf16: return launch_t<kBf16>(x, w, y, rows, cols, eps, out_scale, stream);
+    case kF16: return launch_t<kF16>(x, w, y, rows, cols, eps, out_scale, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -92,11 +92,16 @@ __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
 
 // One workgroup = 4 waves along N; a wave owns MT x NT MFMA tiles of 32x32,
 // i.e. a (32 MT) x (32 NT) sub-tile; the workgroup tile is (32 MT) x (128 NT).
-template <int T, int MT, int NT>
+// EP is the output stage (epilogue.hpp), applied per output straight from the
+// MFMA layout (emit1).  With EP::kPair (SwiGLU, NT == 2) a wave's column tile
+// 0 holds gate rows and tile 1 the up rows of the same 32 output columns.
+template <int T, int MT, int NT, class EP>
 __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
-    const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, const EP ep,
     int M, int N, int K, int tiles_m, int tiles_n) {
+  static_assert(!EP::kPair || NT == 2, "a gate/up pair takes two column tiles per wave");
+  static_assert(!EP::kPartial, "the register-staged kernel does not split K");
   constexpr int BM = 32 * MT;
   constexpr int BN = 128 * NT;
   constexpr int A_CHUNKS = BM * 8;                 // 16-byte chunks per activation tile
@@ -112,6 +117,7 @@ __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM;
   const int nw0 = tn * BN + wave * (NT * 32);
+  const int pcol0 = tn * (BN / 2) + wave * 32;  // paired stage: this wave's first output
   const int wpr = K >> 3;
   const int gpr = K >> 6;
 
@@ -122,7 +128,9 @@ __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_
   const uint16_t* bbrow[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int n = nw0 + nt * 32 + r32;
+    int n = nw0 + nt * 32 + r32;
+    if constexpr (EP::kPair)
+      n = (nt == 0 ? ep.gate_row : ep.up_row) + min(pcol0 + r32, ep.width - 1);
     const size_t nn = (n < N) ? (size_t)n : 0;
     brow[nt] = reinterpret_cast<const uint4*>(w + nn * wpr) + h;
     srow[nt] = scales + nn * gpr;
@@ -230,17 +238,32 @@ __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_
     __syncthreads();
   }
 
-  // Epilogue: accumulator r of a 32x32 tile holds row 8*(r/4) + 4*h + r%4, column r32.
+  // Epilogue: accumulator r of a 32x32 tile holds row 8*(r/4) + 4*h + r%4,
+  // column r32.  Each output is rounded to T (Elem::out, the same RNE as the
+  // staged stores of the large-M kernel) and handed to the output stage.
+  if constexpr (EP::kPair) {
+    const int j = pcol0 + r32;
+    if (j < ep.width) {
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int col = nw0 + nt * 32 + r32;
-      if (col >= N) continue;
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (row < M) ep.emit1(row, j, Elem<T>::out(ep.value2(acc[mt][0][r], acc[mt][1][r])));
+        }
+    }
+  } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (row < M) y[(size_t)row * N + col] = Elem<T>::out(acc[mt][nt][r]);
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int col = nw0 + nt * 32 + r32;
+        if (col >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (row < M) ep.emit1(row, col, Elem<T>::out(ep.value(acc[mt][nt][r])));
+        }
       }
     }
   }
@@ -848,14 +871,18 @@ BigPlan pick_big_plan(int m, int n, int k, int cus, bool small, bool split) {
   return best;
 }
 
-template <int T, int MT, int NT>
+// The register-staged kernel (any K % 64 == 0) with output stage ep; a
+// gate/up pair covers 2 * width weight rows.
+template <int T, int MT, int NT, class EP>
 hipError_t launch_tile(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
-                       const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream) {
+                       const uint16_t* x, const EP& ep, int k, int n, int m, hipStream_t stream) {
+  int cols = n;
+  if constexpr (EP::kPair) cols = 2 * ep.width;
   const int tiles_m = (m + 32 * MT - 1) / (32 * MT);
-  const int tiles_n = (n + 128 * NT - 1) / (128 * NT);
+  const int tiles_n = (cols + 128 * NT - 1) / (128 * NT);
   const dim3 grid((unsigned)tiles_m * (unsigned)tiles_n);
-  hipLaunchKernelGGL((qgemm_kernel<T, MT, NT>), grid, dim3(kThreads), 0, stream, w, scales, biases,
-                     x, y, m, n, k, tiles_m, tiles_n);
+  hipLaunchKernelGGL((qgemm_kernel<T, MT, NT, EP>), grid, dim3(kThreads), 0, stream, w, scales,
+                     biases, x, ep, m, n, k, tiles_m, tiles_n);
   return hipGetLastError();
 }
 
@@ -903,6 +930,9 @@ template <int T, class EP>
 hipError_t launch_big_ep(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                          const uint16_t* x, const EP& ep, int k, int n, int m, hipStream_t stream,
                          SplitWs ws) {
+  // K % 256 != 0 (e.g. the DiT's x_embedder, K = 128) or operands past 32-bit
+  // offsets: the register-staged kernel, one pass.
+  if (!qgemm_big_supported(k, n, m)) return launch_tile<T, 4, 2>(w, scales, biases, x, ep, k, n, m, stream);
   constexpr bool kSmall = !EP::kPair && std::is_same<EP, EpStore<T>>::value;
   int cols = n;  // weight rows covered
   int width = n, gate_row = 0, up_row = 0;
@@ -928,7 +958,6 @@ template <int T>
 hipError_t launch_t(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                     const uint16_t* x, uint16_t* y, int k, int n, int m, hipStream_t stream,
                     SplitWs ws) {
-  if (!qgemm_big_supported(k, n, m)) return launch_tile<T, 4, 2>(w, scales, biases, x, y, k, n, m, stream);
   return launch_big_ep<T>(w, scales, biases, x, EpStore<T>{y, n, al16(y) && n % 8 == 0}, k, n, m,
                           stream, ws);
 }
@@ -989,18 +1018,20 @@ hipError_t launch_qgemm_postscale(const uint32_t* w, const void* scales, const v
 hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const void* biases,
                                  const void* x, const float* residual, const float* gate, float* y,
                                  int k, int n, int m, float scale, int dtype, hipStream_t stream,
-                                 SplitWs ws) {
+                                 SplitWs ws, const float* scale_dev) {
   const auto* s = static_cast<const uint16_t*>(scales);
   const auto* b = static_cast<const uint16_t*>(biases);
   const auto* xx = static_cast<const uint16_t*>(x);
   const bool vec = al16(y) && al16(residual) && al16(gate) && n % 4 == 0;
   switch (dtype) {
     case kBf16:
-      return launch_big_ep<kBf16>(w, s, b, xx, EpGateAdd<kBf16>{y, residual, gate, n, scale, vec},
-                                  k, n, m, stream, ws);
+      return launch_big_ep<kBf16>(
+          w, s, b, xx, EpGateAdd<kBf16>{y, residual, gate, n, scale, vec, scale_dev}, k, n, m,
+          stream, ws);
     case kF16:
-      return launch_big_ep<kF16>(w, s, b, xx, EpGateAdd<kF16>{y, residual, gate, n, scale, vec}, k,
-                                 n, m, stream, ws);
+      return launch_big_ep<kF16>(
+          w, s, b, xx, EpGateAdd<kF16>{y, residual, gate, n, scale, vec, scale_dev}, k, n, m,
+          stream, ws);
     default: return hipErrorInvalidValue;
   }
 }

@@ -51,6 +51,22 @@ struct imq_dit_step {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   int launches = 0;
+  // The head (loadHead, DirectDiTStep.swift:844-884), once set: x_embedder
+  // [dim, C] and proj_out [C, dim] over C latent channels, with buffers of
+  // their own (a second arena) and the denoise step's own graph.
+  bool has_head = false;
+  imq_qweight x_emb{}, proj_out{};
+  int lat_ch = 0;
+  void* head_arena = nullptr;
+  float* lat_in = nullptr;    // fp32 [l_img, C], the caller's latents copied in
+  float* lat_out = nullptr;   // fp32 [l_img, C]
+  char* lat16 = nullptr;      // T [l_img, C]: lat_in / 16
+  char* nH = nullptr;         // T [l_img, dim]: the head norm's output / 16
+  float* ones = nullptr;      // fp32 [C]: the Euler gate-add's gate
+  float* euler = nullptr;     // fp32 [1]: 16 dt of the current step
+  imq::SplitWs split_head;    // proj_out's split-K partial sums
+  hipGraph_t dgraph = nullptr;
+  hipGraphExec_t dexec = nullptr;
 };
 
 namespace {
@@ -59,14 +75,13 @@ constexpr float kEps = 1e-5f;  // DirectDiTStep.swift:416
 
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
-// Launch every kernel of one step on stream s.
+// Launch every kernel of the blocks on stream s (st->launches counts them).
 hipError_t encode(imq_dit_step* st, hipStream_t s) {
   const imq_dit_dims& d = st->d;
   const int J = d.l_txt + d.l_img;
   const int dim = d.dim, ffi = d.ff_inner;
   const int T = (int)st->dtype;
   const size_t es = 2;
-  st->launches = 0;
   hipError_t e = hipSuccess;
   auto ok = [&](hipError_t r) {
     ++st->launches;
@@ -150,7 +165,48 @@ hipError_t encode(imq_dit_step* st, hipStream_t s) {
   return e;
 }
 
+// One denoise step (encodeDenoiseStep, DirectDiTStep.swift:908-971) on stream
+// s, the inputs already in the plan's buffers: lat16 = T(lat_in / 16), the
+// image rows of X = float(T(lat16 . x_embedder^T)) * 16 (cast ÷16, qmm,
+// cast ×16: :917-941), the blocks, then the head: nH = T(RMSNorm(image rows) /
+// 16) (the stand-in for lnMod "out", whose AdaLN modulation is outside the
+// quantized-linear path), and lat_out = lat_in + float(T(nH . proj_out^T)) *
+// 16 dt (proj_out and the Euler gate-add with gate ones, :947-965), the scale
+// read from st->euler when the kernel runs.
+hipError_t encode_denoise(imq_dit_step* st, hipStream_t s) {
+  const imq_dit_dims& d = st->d;
+  const int T = (int)st->dtype;
+  const int C = st->lat_ch;
+  float* Xi = st->X + (size_t)d.l_txt * d.dim;
+  hipError_t e = hipSuccess;
+  auto ok = [&](hipError_t r) {
+    ++st->launches;
+    if (e == hipSuccess) e = r;
+  };
+  ok(imq::launch_prescale(st->lat_in, st->lat16, (size_t)d.l_img * C, 16.0f, T, s));
+  ok(imq::launch_qgemm_postscale(st->x_emb.w, st->x_emb.scales, st->x_emb.biases, st->lat16, Xi,
+                                 C, d.dim, d.l_img, 16.0f, T, s));
+  const hipError_t eb = encode(st, s);
+  if (e == hipSuccess) e = eb;
+  ok(imq::launch_rmsnorm(Xi, st->norm_w, st->nH, d.l_img, d.dim, kEps, T, s, 1.0f / 16.0f));
+  ok(imq::launch_qgemm_gate_add(st->proj_out.w, st->proj_out.scales, st->proj_out.biases, st->nH,
+                                st->lat_in, st->ones, st->lat_out, d.dim, C, d.l_img, 0.0f, T, s,
+                                st->split_head, st->euler));
+  return e;
+}
+
+void release_head(imq_dit_step* st) {
+  if (st->dexec) (void)hipGraphExecDestroy(st->dexec);
+  if (st->dgraph) (void)hipGraphDestroy(st->dgraph);
+  if (st->head_arena) (void)hipFree(st->head_arena);
+  st->dexec = nullptr;
+  st->dgraph = nullptr;
+  st->head_arena = nullptr;
+  st->has_head = false;
+}
+
 void release(imq_dit_step* st) {
+  release_head(st);
   if (st->exec) (void)hipGraphExecDestroy(st->exec);
   if (st->graph) (void)hipGraphDestroy(st->graph);
   if (st->cap) (void)hipStreamDestroy(st->cap);
@@ -194,6 +250,27 @@ void expected_shape(const imq_dit_dims& d, int i, int& n, int& k) {
     n = dim;
     k = dim + ffi;
   }
+}
+
+// First graph run of an encoder: one eager pass on the plan's own stream does
+// the launches' first-use set-up (device queries) outside the capture, then
+// the pass is captured there once.  The eager pass only writes scratch that
+// every run rewrites.
+hipError_t capture(imq_dit_step* st, hipError_t (*enc)(imq_dit_step*, hipStream_t),
+                   hipGraph_t* graph, hipGraphExec_t* exec) {
+  hipError_t e = hipDeviceSynchronize();
+  st->launches = 0;
+  if (e == hipSuccess) e = enc(st, st->cap);
+  if (e == hipSuccess) e = hipStreamSynchronize(st->cap);
+  if (e == hipSuccess) e = hipStreamBeginCapture(st->cap, hipStreamCaptureModeRelaxed);
+  if (e == hipSuccess) {
+    st->launches = 0;
+    const hipError_t r = enc(st, st->cap);
+    e = hipStreamEndCapture(st->cap, graph);
+    if (e == hipSuccess) e = r;
+  }
+  if (e == hipSuccess) e = hipGraphInstantiate(exec, *graph, nullptr, nullptr, 0);
+  return e;
 }
 
 }  // namespace
@@ -334,16 +411,7 @@ int imq_dit_step_run(imq_dit_step* st, const float* h_in, const float* e_in, flo
     // launches' first-use set-up (device queries) outside the capture, then
     // the step is captured there once.  The eager step only writes scratch
     // that every run rewrites, and runs before the inputs are copied in.
-    e = hipDeviceSynchronize();
-    if (e == hipSuccess) e = encode(st, st->cap);
-    if (e == hipSuccess) e = hipStreamSynchronize(st->cap);
-    if (e == hipSuccess) e = hipStreamBeginCapture(st->cap, hipStreamCaptureModeRelaxed);
-    if (e == hipSuccess) {
-      const hipError_t enc = encode(st, st->cap);
-      e = hipStreamEndCapture(st->cap, &st->graph);
-      if (e == hipSuccess) e = enc;
-    }
-    if (e == hipSuccess) e = hipGraphInstantiate(&st->exec, st->graph, nullptr, nullptr, 0);
+    e = capture(st, encode, &st->graph, &st->exec);
     if (e != hipSuccess) return hip_fail(st->ctx, e, "imq_dit_step_run: graph capture");
   }
   const size_t row = (size_t)d.dim * 4;
@@ -351,9 +419,109 @@ int imq_dit_step_run(imq_dit_step* st, const float* h_in, const float* e_in, flo
   if (e == hipSuccess)
     e = hipMemcpyAsync(st->X + (size_t)d.l_txt * d.dim, h_in, (size_t)d.l_img * row,
                        hipMemcpyDefault, s);
-  if (e == hipSuccess) e = use_graph ? hipGraphLaunch(st->exec, s) : encode(st, s);
+  if (e == hipSuccess) {
+    if (use_graph) {
+      e = hipGraphLaunch(st->exec, s);
+    } else {
+      st->launches = 0;
+      e = encode(st, s);
+    }
+  }
   if (e == hipSuccess)
     e = hipMemcpyAsync(x_out, st->X, (size_t)(d.l_txt + d.l_img) * row, hipMemcpyDefault, s);
+  return e == hipSuccess ? IMQ_OK : hip_fail(st->ctx, e, fn);
+}
+
+int imq_dit_step_set_head(imq_dit_step* st, const imq_qweight* x_embedder,
+                          const imq_qweight* proj_out) {
+  const char* fn = "imq_dit_step_set_head";
+  if (!st) return fail(nullptr, IMQ_EINVAL, "%s: null step", fn);
+  if (!x_embedder || !proj_out) return fail(st->ctx, IMQ_EINVAL, "%s: null projection", fn);
+  const imq_dit_dims& d = st->d;
+  const imq_qweight& xe = *x_embedder;
+  const imq_qweight& po = *proj_out;
+  const int C = xe.k;
+  if (!xe.w || !xe.scales || !xe.biases || !po.w || !po.scales || !po.biases)
+    return fail(st->ctx, IMQ_EINVAL, "%s: null tensor in a projection", fn);
+  if (xe.n != d.dim || C <= 0 || C % 64 != 0 || po.k != d.dim || po.n != C)
+    return fail(st->ctx, IMQ_EINVAL,
+                "%s: x_embedder is [%d, %d] and proj_out [%d, %d]; expected [%d, C] and [C, %d] "
+                "with C a positive multiple of 64",
+                fn, xe.n, xe.k, po.n, po.k, d.dim, d.dim);
+  if (xe.dtype != st->dtype || po.dtype != st->dtype)
+    return fail(st->ctx, IMQ_EINVAL, "%s: projection dtypes %d / %d, the plan's is %d", fn,
+                (int)xe.dtype, (int)po.dtype, (int)st->dtype);
+  int rc = bind_device(st->ctx);
+  if (rc != IMQ_OK) return rc;
+  hipError_t e = hipDeviceSynchronize();  // a previous head's graph may still run
+  if (e != hipSuccess) return hip_fail(st->ctx, e, fn);
+  release_head(st);
+  const size_t li = (size_t)d.l_img;
+  const size_t ws = imq::qgemm_split_bytes(d.dim, C, d.l_img, true);
+  const size_t sizes[] = {li * C * 4, li * C * 4, li * C * 2, li * d.dim * 2, (size_t)C * 4, 4, ws};
+  size_t off[7], total = 0;
+  for (int i = 0; i < 7; ++i) {
+    off[i] = total;
+    total += align256(sizes[i]);
+  }
+  e = hipMalloc(&st->head_arena, total);
+  if (e != hipSuccess) {
+    st->head_arena = nullptr;
+    return e == hipErrorOutOfMemory
+               ? fail(st->ctx, IMQ_ENOMEM, "%s: %zu bytes: out of device memory", fn, total)
+               : hip_fail(st->ctx, e, fn);
+  }
+  char* a = static_cast<char*>(st->head_arena);
+  st->lat_in = reinterpret_cast<float*>(a + off[0]);
+  st->lat_out = reinterpret_cast<float*>(a + off[1]);
+  st->lat16 = a + off[2];
+  st->nH = a + off[3];
+  st->ones = reinterpret_cast<float*>(a + off[4]);
+  st->euler = reinterpret_cast<float*>(a + off[5]);
+  st->split_head = imq::SplitWs{ws ? reinterpret_cast<float*>(a + off[6]) : nullptr, ws};
+  e = hipMemset(st->head_arena, 0, total);
+  if (e == hipSuccess) e = hipMemsetD32(st->ones, 0x3F800000u, (size_t)C);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    release_head(st);
+    return hip_fail(st->ctx, e, fn);
+  }
+  st->x_emb = xe;
+  st->proj_out = po;
+  st->lat_ch = C;
+  st->has_head = true;
+  return IMQ_OK;
+}
+
+int imq_dit_step_denoise(imq_dit_step* st, const float* lat_in, const float* e_in, float* lat_out,
+                         float dt, int use_graph, imq_stream stream) {
+  const char* fn = "imq_dit_step_denoise";
+  if (!st) return fail(nullptr, IMQ_EINVAL, "%s: null step", fn);
+  if (!st->has_head) return fail(st->ctx, IMQ_EINVAL, "%s: no head set (imq_dit_step_set_head)", fn);
+  if (!lat_in || !e_in || !lat_out) return fail(st->ctx, IMQ_EINVAL, "%s: null buffer", fn);
+  int rc = bind_device(st->ctx);
+  if (rc != IMQ_OK) return rc;
+  const imq_dit_dims& d = st->d;
+  auto s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipSuccess;
+  if (use_graph && !st->dexec) {
+    e = capture(st, encode_denoise, &st->dgraph, &st->dexec);
+    if (e != hipSuccess) return hip_fail(st->ctx, e, "imq_dit_step_denoise: graph capture");
+  }
+  const size_t lat_bytes = (size_t)d.l_img * st->lat_ch * 4;
+  e = hipMemcpyAsync(st->lat_in, lat_in, lat_bytes, hipMemcpyDefault, s);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(st->X, e_in, (size_t)d.l_txt * d.dim * 4, hipMemcpyDefault, s);
+  if (e == hipSuccess) e = imq::launch_fill_f32(st->euler, 16.0f * dt, 1, s);
+  if (e == hipSuccess) {
+    if (use_graph) {
+      e = hipGraphLaunch(st->dexec, s);
+    } else {
+      st->launches = 0;
+      e = encode_denoise(st, s);
+    }
+  }
+  if (e == hipSuccess) e = hipMemcpyAsync(lat_out, st->lat_out, lat_bytes, hipMemcpyDefault, s);
   return e == hipSuccess ? IMQ_OK : hip_fail(st->ctx, e, fn);
 }
 

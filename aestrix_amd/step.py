@@ -78,6 +78,32 @@ def random_projections(dims: DitDims, dtype: torch.dtype = torch.float16, seed: 
     return out
 
 
+def random_head(dims: DitDims, channels: int = 128, dtype: torch.dtype = torch.float16,
+                seed: int = 0, device=None) -> tuple[Q, Q]:
+    """Synthetic x_embedder [dim, channels] and proj_out [channels, dim] with the
+    scale law of ``random_projections`` (``loadHead``, DirectDiTStep.swift:844-884)."""
+    dev = torch.device("cuda", device_index(device))
+    g = torch.Generator(device=dev).manual_seed(seed)
+    out = []
+    for n, k in ((dims.dim, channels), (channels, dims.dim)):
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k // 8), dtype=torch.int32, device=dev,
+                          generator=g)
+        unit = 1.0 / (4.0 * k ** 0.5)
+        s = torch.randn((n, k // 64), device=dev, generator=g).abs() * unit
+        b = -8.0 * s + torch.randn((n, k // 64), device=dev, generator=g) * (0.1 * unit)
+        out.append(Q(w=w, s=s.to(dtype), b=b.to(dtype), n=n, k=k))
+    return out[0], out[1]
+
+
+def _qweight(q: Q) -> "_lib.QWeight":
+    r = _lib.QWeight()
+    r.w, r.scales, r.biases = q.w.data_ptr(), q.s.data_ptr(), q.b.data_ptr()
+    r.n, r.k = q.n, q.k
+    r.dtype = _DTYPES.get(q.s.dtype, -1)
+    r.base = None
+    return r
+
+
 class DitStep:
     """A created step plan over resident projections (kept alive here)."""
 
@@ -149,6 +175,32 @@ class DitStep:
                                                 ctypes.c_void_p(e.data_ptr()),
                                                 ctypes.c_void_p(out.data_ptr()), int(use_graph),
                                                 ctypes.c_void_p(st)), self._ctx)
+        return out
+
+    def set_head(self, x_embedder: Q, proj_out: Q) -> None:
+        """``loadHead``: the x_embedder [dim, C] and proj_out [C, dim] projections
+        of ``denoise`` (kept alive here)."""
+        self.head = (x_embedder, proj_out)
+        with torch.cuda.device(self.device):
+            _lib.check(self._L.imq_dit_step_set_head(self._h, ctypes.byref(_qweight(x_embedder)),
+                                                     ctypes.byref(_qweight(proj_out))), self._ctx)
+
+    def denoise(self, lat_in: torch.Tensor, e: torch.Tensor, dt: float,
+                out: torch.Tensor | None = None, use_graph: bool = True) -> torch.Tensor:
+        """``encodeDenoiseStep``: lat_out [l_img, C] fp32 = lat_in + 16 dt times the
+        head's prediction, after the embedder, the blocks and proj_out."""
+        d = self.dims
+        assert lat_in.dtype == torch.float32 and lat_in.dim() == 2 and lat_in.shape[0] == d.l_img
+        assert lat_in.is_contiguous()
+        assert e.dtype == torch.float32 and tuple(e.shape) == (d.l_txt, d.dim) and e.is_contiguous()
+        if out is None:
+            out = torch.empty_like(lat_in)
+        st = torch.cuda.current_stream(self.device).cuda_stream
+        with torch.cuda.device(self.device):
+            _lib.check(self._L.imq_dit_step_denoise(
+                self._h, ctypes.c_void_p(lat_in.data_ptr()), ctypes.c_void_p(e.data_ptr()),
+                ctypes.c_void_p(out.data_ptr()), float(dt), int(use_graph),
+                ctypes.c_void_p(st)), self._ctx)
         return out
 
     @property

@@ -201,7 +201,8 @@ int imq_qmm_plan(imq_ctx* ctx, int entry, int k, int n, int m, imq_dtype dtype, 
  * epilogue (Sources/ImarelloDirect/DirectDiTKernels.swift).  Each equals the
  * qmm (T output) followed by that glue kernel: the accumulator is rounded to T
  * first, then the glue arithmetic runs in fp32.  T is bf16 or f16 (f32:
- * IMQ_EUNSUPPORTED); K % 256 == 0 (else IMQ_EUNSUPPORTED); any M >= 1.  Other
+ * IMQ_EUNSUPPORTED); any K % 64 == 0 (K % 256 != 0, e.g. the x_embedder's
+ * K = 128, runs the register-staged tile kernel); any M >= 1.  Other
  * arguments as imq_qmm_t; fp32 arrays must be 4-byte aligned. */
 
 /* y[i] (T) = T(x[i] / scale) for i < count, x fp32: the pre-scale half of the

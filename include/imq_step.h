@@ -82,7 +82,27 @@ int imq_dit_step_set_conditioning(imq_dit_step* step, const float* norm_weight,
 int imq_dit_step_run(imq_dit_step* step, const float* h_in, const float* e_in, float* x_out,
                      int use_graph, imq_stream stream);
 
-/* Kernel launches in one step (graph nodes). */
+/* The head of encodeDenoiseStep (loadHead, DirectDiTStep.swift:844-884):
+ * x_embedder [dim, C] and proj_out [C, dim] over C latent channels (128 for
+ * FLUX.2 klein), C a multiple of 64, dtype the plan's.  Allocates the head's
+ * buffers (replacing a head set before); the weights must outlive the plan. */
+int imq_dit_step_set_head(imq_dit_step* step, const imq_qweight* x_embedder,
+                          const imq_qweight* proj_out);
+
+/* One denoise step, encodeDenoiseStep (DirectDiTStep.swift:908-971) with every
+ * quantized projection of it:
+ *   lat16 = T(lat_in / 16); image rows of X = float(T(lat16 . x_embedder^T)) * 16
+ *   X = [e_in; image rows], the blocks as in imq_dit_step_run
+ *   nH = T(RMSNorm(X image rows) / 16)   (the stand-in for norm_out's lnMod)
+ *   lat_out = lat_in + float(T(nH . proj_out^T)) * (16 dt)   (the Euler gate-add)
+ * lat_in, lat_out fp32 [l_img, C], e_in fp32 [l_txt, dim]; inputs copied in,
+ * never written.  use_graph != 0 replays a graph of the whole step (captured
+ * on the first such call; dt is read when it runs, so one graph serves every
+ * step).  Needs imq_dit_step_set_head.  Asynchronous on stream. */
+int imq_dit_step_denoise(imq_dit_step* step, const float* lat_in, const float* e_in,
+                         float* lat_out, float dt, int use_graph, imq_stream stream);
+
+/* Kernel launches of the last pass encoded (eager run or graph capture). */
 int imq_dit_step_launches(const imq_dit_step* step);
 
 int imq_dit_step_destroy(imq_dit_step* step);

@@ -138,9 +138,8 @@ def test_epilogue_argument_checks():
         imq.qmm_swiglu(x, w, s, b, 100, 0, 64)  # up section past N
     with pytest.raises(NotImplementedError):
         imq.qmm_postscale(x.float(), w, s.float(), b.float(), 1.0)  # f32: no MFMA kernel
-    p2, x2, w2, s2, b2 = problem(8, 128, 192, "bf16", seed=53)
-    with pytest.raises(NotImplementedError):
-        imq.qmm_postscale(x2, w2, s2, b2, 1.0)  # K % 256 != 0
+    with pytest.raises(ValueError):
+        imq.qmm_postscale(x[:, :192], w[:, :24], s[:, :3], b[:, :3], 1.0)  # not contiguous
 
 
 def _t16_bits(t: torch.Tensor) -> np.ndarray:
@@ -203,3 +202,83 @@ def test_prescale_argument_checks():
     p, xb, w, s, b = problem(8, 128, 256, "bf16", seed=54)
     with pytest.raises(ValueError):
         imq.apply_linear(imq.QuantizedLinear(w, s, b), xb.float())  # bf16 scales
+
+
+# ------------------------------------- output stages on the register-staged kernel
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_x_embedder_sandwich_k128(dtype):
+    """The DiT's x_embedder at 1024^2: latents [4096, 128] fp32 / 16 to T, the qmm
+    with K = 128 (not a multiple of 256: the register-staged kernel) and the x16
+    post-scale to fp32 (DirectDiTStep.swift:917-941), against the oracle's
+    prescale, qmm and postscale; f16 through apply_linear, the operator surface."""
+    m, n, k = 4096, 3072, 128
+    note(f"x_embedder sandwich {dtype} M={m} N={n} K={k}")
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    plan = imq.qmm_plan(m, n, k, tdt, entry="fused")
+    assert plan["kernel"] == "tile_reg" and plan["splits"] == 1, plan
+    p, _, w, s, b = problem(1, n, k, dtype, seed=54)
+    rng = np.random.default_rng(54)
+    lat = rng.standard_normal((m, k)).astype(np.float32)
+    lat_d = torch.from_numpy(lat).cuda()
+    if dtype == "f16":
+        y = imq.apply_linear(imq.QuantizedLinear(w, s, b), lat_d, 16.0)
+    else:
+        y = imq.qmm_postscale(imq.cast_prescale(lat_d, 16.0, tdt), w, s, b, 16.0)
+    got = to_np(y)
+    x_t = ref.glue_prescale(lat, 16.0, dtype)
+    if dtype == "f16":
+        q = ref.qmm_t_as(x_t, p.w, s.cpu().numpy(), b.cpu().numpy(), np.float16).astype(np.float32)
+    else:
+        q = ref.bf16_to_f32(ref.qmm_t(x_t, p.w, p.scales, p.biases))
+    assert_close(got, ref.glue_postscale(q, 16.0), "x_embedder sandwich")
+    unfused = to_np(imq.qgemm(imq.cast_prescale(lat_d, 16.0, tdt), w, s, b)) * np.float32(16.0)
+    assert np.array_equal(got, unfused)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_gate_add_register_kernel_k192(dtype):
+    m, n, k = 300, 384, 192
+    note(f"qmm_gate_add (register-staged) {dtype} M={m} N={n} K={k}")
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    assert imq.qmm_plan(m, n, k, tdt, entry="fused")["kernel"] == "tile_reg"
+    p, x, w, s, b = problem(m, n, k, dtype, seed=55)
+    rng = np.random.default_rng(55)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    gate = rng.standard_normal(n).astype(np.float32)
+    r_dev = torch.from_numpy(res).cuda()
+    y = imq.qmm_gate_add(x, w, s, b, r_dev, torch.from_numpy(gate).cuda(), 0.3, out=r_dev)
+    got = to_np(y)
+    unfused = ref.glue_gate_add(to_np(imq.qgemm(x, w, s, b)), res, gate, 0.3)
+    assert np.array_equal(got, unfused)
+    assert_close(got, ref.glue_gate_add(oracle_qmm(p, x, s, b, dtype), res, gate, 0.3),
+                 "gate_add k192")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_swiglu_register_kernel_k192_pitched(dtype):
+    """A gate/up pair on the register-staged kernel (K = 192), written into
+    columns [8, 8 + width) of a wider buffer; a partial last tile of outputs."""
+    m, n, k, width, gate_row, up_row = 130, 600, 192, 200, 17, 300
+    note(f"qmm_swiglu (register-staged) {dtype} M={m} width={width} K={k}")
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    assert imq.qmm_plan(m, 2 * width, k, tdt, entry="fused")["kernel"] == "tile_reg"
+    p, x, w, s, b = problem(m, n, k, dtype, seed=56)
+    buf = torch.full((m, width + 20), 5.0, dtype=tdt, device="cuda")
+    imq.qmm_swiglu(x, w, s, b, width, gate_row, up_row, in_scale=16.0, out_scale=1.0 / 16,
+                   out=buf[:, 8:8 + width])
+    got = to_np(buf)
+    assert np.all(got[:, :8] == 5.0) and np.all(got[:, 8 + width:] == 5.0)
+    full = to_np(imq.qgemm(x, w, s, b))
+    unfused = ref.glue_swiglu(full[:, gate_row:gate_row + width], full[:, up_row:up_row + width],
+                              16.0, 1.0 / 16)
+    want = ref.glue_swiglu(oracle_qmm(p, x, s, b, dtype, np.arange(gate_row, gate_row + width)),
+                           oracle_qmm(p, x, s, b, dtype, np.arange(up_row, up_row + width)),
+                           16.0, 1.0 / 16)
+
+    def round_t(v):
+        return torch.from_numpy(v.astype(np.float32)).to(tdt).float().numpy()
+
+    assert_close(got[:, 8:8 + width], round_t(unfused), "swiglu k192 vs unfused")
+    assert_close(got[:, 8:8 + width], round_t(want), "swiglu k192 vs oracle")

@@ -26,7 +26,7 @@ import torch
 
 import aestrix_amd as imq
 from aestrix_amd import synth
-from aestrix_amd.step import DitDims, DitStep, random_projections
+from aestrix_amd.step import DitDims, DitStep, random_head, random_projections
 from oracle import cref, ref
 
 pytestmark = pytest.mark.gpu
@@ -213,12 +213,14 @@ def oracle_step_rows(d: DitDims, hp, norm_w, gates, X0, txt_rows, img_rows, dtyp
         g = gates[4 * blk:4 * blk + 4]
         nX = rms(X)
         v_i = round_t(qmm(nX[I], base + 2), dtype)   # to_v over image rows
-        v_t = round_t(qmm(nX[T], base + 5), dtype)   # add_v_proj over text rows
         X[I] = gate_add(qmm(v_i, base + 6), X[I], g[0])
-        X[T] = gate_add(qmm(v_t, base + 7), X[T], g[1])
+        if nt:
+            v_t = round_t(qmm(nX[T], base + 5), dtype)   # add_v_proj over text rows
+            X[T] = gate_add(qmm(v_t, base + 7), X[T], g[1])
         nX = rms(X)
         X[I] = gate_add(qmm(swiglu(nX[I], base + 8, 0, ffi), base + 9), X[I], g[2])
-        X[T] = gate_add(qmm(swiglu(nX[T], base + 10, 0, ffi), base + 11), X[T], g[3])
+        if nt:
+            X[T] = gate_add(qmm(swiglu(nX[T], base + 10, 0, ffi), base + 11), X[T], g[3])
     for blk in range(d.n_single):
         base = 12 * d.n_double + 2 * blk
         g = gates[4 * d.n_double + blk]
@@ -267,4 +269,57 @@ def test_full_size_step_sampled_rows_and_graph_replays(dtype):
     mean_rel = diff.mean() / np.abs(want).mean()
     note(f"  {len(txt_rows)} text + {len(img_rows)} image rows: normwise={normwise:.3g} "
          f"mean_rel={mean_rel:.3g}")
+    assert normwise <= NORMWISE_TOL, normwise
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_full_size_denoise_step_sampled_rows(dtype):
+    """encodeDenoiseStep at full size: the x_embedder sandwich (K = 128), the 25
+    blocks and the head (norm / 16, proj_out N = 128, Euler gate-add with 16 dt)
+    as one graph; two graph replays with different dt equal eager runs, and the
+    update lat_out - lat_in of sampled image rows matches the oracle (image rows
+    never mix with other rows on this path)."""
+    d = DitDims()
+    channels = 128
+    note(f"dit denoise {dtype} full size {d} C={channels} seed=84")
+    tdt = TDT[dtype]
+    projs = random_projections(d, tdt, seed=84)
+    xe, po = random_head(d, channels, tdt, seed=85)
+    step = DitStep(d, projs)
+    try:
+        step.set_head(xe, po)
+        rng = np.random.default_rng(84)
+        norm_w = (1.0 + 0.1 * rng.standard_normal(d.dim)).astype(np.float32)
+        gates = (0.5 * rng.standard_normal((4 * d.n_double + d.n_single, d.dim))).astype(np.float32)
+        step.set_conditioning(torch.from_numpy(norm_w).cuda(), torch.from_numpy(gates).cuda())
+        lat = rng.standard_normal((d.l_img, channels)).astype(np.float32)
+        e = rng.standard_normal((d.l_txt, d.dim)).astype(np.float32)
+        lat_d, e_d = torch.from_numpy(lat).cuda(), torch.from_numpy(e).cuda()
+        eager = {dt: step.denoise(lat_d, e_d, dt, use_graph=False).cpu().numpy()
+                 for dt in (-0.25, -0.1)}
+        assert step.launches == d.n_double * 14 + d.n_single * 4 + 4
+        for dt in (-0.1, -0.25):
+            torch.randn(1000, device="cuda").sum().item()
+            got = step.denoise(lat_d, e_d, dt, use_graph=True).cpu().numpy()
+            assert np.array_equal(got, eager[dt]), f"graph replay with dt={dt} differs"
+        hp = [(q.w.cpu().numpy().view(np.uint32), host_bits(q.s), host_bits(q.b)) for q in projs]
+        xe_h = (xe.w.cpu().numpy().view(np.uint32), host_bits(xe.s), host_bits(xe.b))
+        po_h = (po.w.cpu().numpy().view(np.uint32), host_bits(po.s), host_bits(po.b))
+    finally:
+        step.close()
+    img_rows = sample_rows(d.l_img, 16)
+    lat16 = ref.glue_prescale(lat[img_rows], 16.0, dtype)
+    lat16 = lat16.view(np.uint16) if dtype == "f16" else lat16
+    h = ref.glue_postscale(oracle_qmm(lat16, *xe_h, dtype).astype(np.float32), 16.0)
+    X = oracle_step_rows(d, hp, norm_w, gates, h, np.arange(0), img_rows, dtype)
+    nH = round_t(ref.rmsnorm_rows(X, norm_w) / 16.0, dtype)
+    pred = oracle_qmm(nH, *po_h, dtype)
+    dt = -0.25
+    want = ref.glue_gate_add(pred.astype(np.float32), lat[img_rows], np.ones(channels, np.float32),
+                             np.float32(16.0) * np.float32(dt))
+    upd = eager[dt][img_rows].astype(np.float64) - lat[img_rows]
+    upd_want = want.astype(np.float64) - lat[img_rows]
+    normwise = np.abs(upd - upd_want).max() / np.abs(upd_want).max()
+    note(f"  {len(img_rows)} image rows: update normwise={normwise:.3g}")
+    assert np.all(np.isfinite(eager[dt]))
     assert normwise <= NORMWISE_TOL, normwise

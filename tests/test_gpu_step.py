@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from aestrix_amd import _lib
-from aestrix_amd.step import DitDims, DitStep, random_projections
+from aestrix_amd.step import DitDims, DitStep, random_head, random_projections
 from oracle import ref
 
 pytestmark = pytest.mark.gpu
@@ -128,6 +128,76 @@ def test_step_matches_oracle_and_graph_matches_eager(tdt, d):
     note(f"  normwise={normwise:.3g} mean_rel={mean_rel:.3g}")
     assert np.all(np.isfinite(eager))
     assert normwise <= 1e-2, normwise
+    step.close()
+
+
+def oracle_denoise(d: DitDims, projs, head, norm_w, gates, lat, e, dt, tdt):
+    """encodeDenoiseStep on the CPU: x_embedder sandwich (x / 16 to T, qmm, x 16),
+    the blocks, the head norm / 16, proj_out and the Euler gate-add (gate ones,
+    scale 16 dt)."""
+    xe, po = head
+    lat16 = ref.glue_prescale(lat, 16.0, "f16" if tdt == torch.float16 else "bf16")
+    lat16 = lat16.astype(np.float32) if tdt == torch.float16 else ref.bf16_to_f32(lat16)
+    h = ref.glue_postscale(qmm_t(lat16, xe, tdt), 16.0)
+    X = oracle_step(d, projs, norm_w, gates, h, e, tdt)
+    nH = to_t(ref.rmsnorm_rows(X[d.l_txt:], norm_w) / 16.0, tdt)
+    pred = qmm_t(nH, po, tdt)
+    return ref.glue_gate_add(pred, lat, np.ones(po.n, np.float32), np.float32(16.0) * np.float32(dt))
+
+
+@pytest.mark.parametrize("d", [TINY, SPLIT], ids=["tiny", "split_k"])
+@pytest.mark.parametrize("tdt", [torch.float16, torch.bfloat16])
+def test_denoise_step_with_head(tdt, d):
+    """imq_dit_step_denoise: the embedder (K = 128: the register-staged kernel
+    with the post-scale stage), the blocks and the head.  Graph replays with
+    three different dt (read when the graph runs) equal eager runs with the
+    same dt; the update lat_out - lat_in matches the CPU restatement."""
+    channels = 128
+    note(f"dit denoise {tdt} {d} C={channels}")
+    projs = random_projections(d, tdt, seed=9)
+    head = random_head(d, channels, tdt, seed=10)
+    step = DitStep(d, projs)
+    step.set_head(*head)
+    rng = np.random.default_rng(9)
+    norm_w = (1.0 + 0.1 * rng.standard_normal(d.dim)).astype(np.float32)
+    gates = (0.5 * rng.standard_normal((4 * d.n_double + d.n_single, d.dim))).astype(np.float32)
+    step.set_conditioning(torch.from_numpy(norm_w).cuda(), torch.from_numpy(gates).cuda())
+    lat = rng.standard_normal((d.l_img, channels)).astype(np.float32)
+    e = rng.standard_normal((d.l_txt, d.dim)).astype(np.float32)
+    lat_d, e_d = torch.from_numpy(lat).cuda(), torch.from_numpy(e).cuda()
+    eager = {}
+    for dt in (-0.25, -0.125, 0.5):
+        eager[dt] = step.denoise(lat_d, e_d, dt, use_graph=False).cpu().numpy()
+    assert step.launches == d.n_double * 14 + d.n_single * 4 + 4
+    assert np.array_equal(lat_d.cpu().numpy(), lat)
+    for dt in (0.5, -0.25, -0.125):
+        torch.randn(1000, device="cuda").sum().item()
+        got = step.denoise(lat_d, e_d, dt, use_graph=True).cpu().numpy()
+        assert np.array_equal(got, eager[dt]), f"graph replay with dt={dt} differs from eager"
+    dt = -0.25
+    want = oracle_denoise(d, projs, head, norm_w, gates, lat, e, dt, tdt)
+    upd, upd_want = eager[dt].astype(np.float64) - lat, want.astype(np.float64) - lat
+    normwise = np.abs(upd - upd_want).max() / np.abs(upd_want).max()
+    note(f"  update normwise={normwise:.3g}")
+    assert np.all(np.isfinite(eager[dt]))
+    assert normwise <= 1e-2, normwise
+    step.close()
+
+
+def test_denoise_needs_a_head_and_checks_its_shapes():
+    d = TINY
+    projs = random_projections(d, torch.float16, seed=11)
+    step = DitStep(d, projs)
+    lat = torch.zeros((d.l_img, 128), device="cuda")
+    e = torch.zeros((d.l_txt, d.dim), device="cuda")
+    with pytest.raises(ValueError, match="no head"):
+        step.denoise(lat, e, 0.1)
+    xe, po = random_head(d, 128, torch.float16, seed=12)
+    with pytest.raises(ValueError, match="x_embedder"):
+        step.set_head(po, xe)  # swapped
+    xe32, _ = random_head(d, 128, torch.bfloat16, seed=12)
+    with pytest.raises(ValueError, match="dtypes"):
+        step.set_head(xe32, po)
     step.close()
 
 
