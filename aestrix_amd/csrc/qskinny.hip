@@ -21,6 +21,12 @@
 // registers exactly as in the other kernels (RNE_T(fl32(s q + b))); the MFMA
 // accumulates the products in fp32.  The waves' partial 16 x 16 sums are added
 // in wave order through LDS (deterministic) and rounded to T.
+//
+// For 12 <= M <= 16 with K <= 4096 a second kernel (qskinny_lds_kernel) takes
+// the call: its workgroups own up to four 16-row tiles and stage x in LDS once
+// for all of them (see plan_lds).
+#include <algorithm>
+
 #include "imq_device.hpp"
 #include "imq_kernels.hpp"
 
@@ -155,6 +161,142 @@ __global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restr
   }
 }
 
+// ---------------------------------------------------------------------------
+// x in LDS.  A workgroup owns TPW tiles of 16 weight rows over all of K and
+// stages x [M, K] once, by direct buffer->LDS loads (16 bytes per lane, no
+// registers), issued before its weight loads; its W waves split the chunks of
+// 128 k (wave w: chunks w, w + W, ...) and each wave computes all TPW tiles of
+// its chunks, reading one activation fragment from LDS per chunk for all of
+// them.  Activation bytes cross the memory pipeline once per workgroup
+// instead of once per wave and chunk.
+//
+// LDS x layout: row m, chunk j, 16-byte piece p (8 elements, 16 per chunk) at
+// slot 16 (chunks m + j) + (p ^ (m & 15)): the 16 lanes (c, h) of one B-operand
+// read (rows c = 0..15, piece 4 h + i) hit 16 different 16-byte bank groups.
+// The x staging waits (s_waitcnt vmcnt with the weight loads' count left
+// outstanding, then a raw barrier) while the weights are still in flight.
+template <int T, int TPW, int W, int U>
+__global__ __launch_bounds__(64 * W) void qskinny_lds_kernel(const uint32_t* __restrict__ w,
+                                                             const uint16_t* __restrict__ scales,
+                                                             const uint16_t* __restrict__ biases,
+                                                             const uint16_t* __restrict__ x,
+                                                             uint16_t* __restrict__ y, int M,
+                                                             int N, int K, bool vec) {
+  constexpr int kWeightLoads = 3 * U * TPW < 63 ? 3 * U * TPW : 63;
+  __shared__ f32x4_t part[W][TPW][64];
+  extern __shared__ uint4 xs[];  // x [M, K], rows 2 K + 16 bytes apart
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, h = lane >> 4;
+  const int n0 = blockIdx.x * (kRows * TPW);
+  const int gpr = K >> 6;
+  const int chunks = K / kChunkK;
+  const auto wr = make_rsrc(w, (uint32_t)((size_t)N * K / 2));
+  const auto sr = make_rsrc(scales, (uint32_t)((size_t)N * gpr * 2));
+  const auto br = make_rsrc(biases, (uint32_t)((size_t)N * gpr * 2));
+  const auto xr = make_rsrc(x, (uint32_t)((size_t)M * K * 2));
+
+  // 1. x -> LDS, one wave instruction per 1 KB piece q of the [M, K] tile (K %
+  //    512 == 0: a row is K / 512 pieces): row m = q / rp, part q % rp (both
+  //    wave-uniform, scalar arithmetic), to LDS row m at a stride of 2 K + 16
+  //    bytes; the 16-byte pad puts the 16 rows of one B-operand read into 16
+  //    different bank groups.
+  {
+    const int rp = K >> 9, pieces = M * rp;
+    for (int q = wave; q < pieces; q += W) {
+      const int m = q / rp, part = q - m * rp;
+      load_lds16(xr, (uint32_t)lane * 16u, (uint32_t)(m * K * 2 + part * 1024),
+                 reinterpret_cast<char*>(xs) + m * (2 * K + 16) + part * 1024);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. This wave's weight, scale and bias fragments, all of them.
+  uint32_t w_off[TPW], p_off[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const uint32_t row = (uint32_t)min(n0 + kRows * t + c, N - 1);
+    w_off[t] = row * (uint32_t)(K / 2) + (uint32_t)h * 16u;
+    p_off[t] = (row * (uint32_t)gpr + (uint32_t)(h >> 1)) * 2u;
+  }
+  f32x4_t acc[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int xrow = min(c, M - 1);
+  bool first = true;
+  for (int ch0 = wave; ch0 < chunks; ch0 += W * U) {
+    u32x4_t wv[U][TPW];
+    uint16_t sv[U][TPW], bv[U][TPW];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t ch = (uint32_t)min(ch0 + u * W, chunks - 1);
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        wv[u][t] = load_b128(wr, w_off[t], ch * 64u);
+        sv[u][t] = __builtin_amdgcn_raw_buffer_load_b16(sr, p_off[t], ch * 4u, 0);
+        bv[u][t] = __builtin_amdgcn_raw_buffer_load_b16(br, p_off[t], ch * 4u, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (first) {
+      // The x loads (issued first) have landed once at most the 3 U TPW
+      // weight-side loads are outstanding (the counter tracks at most 63: with
+      // more, the oldest had retired before the last could issue); after the
+      // barrier every wave's have.
+      IMQ_WAIT_VMCNT(kWeightLoads);
+      __builtin_amdgcn_s_barrier();
+      first = false;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // A chunk past the end gets scale and bias 0 (weights +0): no branch, so
+    // its loads stay above.
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool valid = ch0 + u * W < chunks;
+      const int j = min(ch0 + u * W, chunks - 1);
+      u32x4_t xf[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xf[i] = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(xs) +
+                                                   xrow * (2 * K + 16) + j * 256 + (4 * h + i) * 16);
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const float s = valid ? Elem<T>::param(sv[u][t]) : 0.0f;
+        const float s24 = s * 0x1p24f, s20 = s * 0x1p20f;
+        const float b = valid ? Elem<T>::param(bv[u][t]) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          uint32_t p[4];
+          Elem<T>::dequant(wv[u][t][i], s24, s20, b, p);
+          acc[t] = mfma16x16x32<T>(u32x4_t{p[0], p[1], p[2], p[3]}, xf[i], acc[t]);
+        }
+      }
+    }
+  }
+  if (first) {  // a wave with no chunk (W > chunks) still meets the others at the barrier
+    IMQ_WAIT_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+  }
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) part[wave][t][lane] = acc[t];
+  __syncthreads();
+  if (wave >= TPW || c >= M) return;
+  const int t = wave;
+  f32x4_t sum = part[0][t][lane];
+#pragma unroll
+  for (int i = 1; i < W; ++i) sum += part[i][t][lane];
+  const int f0 = n0 + kRows * t + 4 * h;
+  uint16_t* yr = y + (size_t)c * N;
+  if (vec && f0 + 3 < N) {
+    *reinterpret_cast<uint2*>(yr + f0) =
+        make_uint2(Elem<T>::pack2(sum[0], sum[1]), Elem<T>::pack2(sum[2], sum[3]));
+  } else {
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      if (f0 + v < N) yr[f0 + v] = Elem<T>::out(sum[v]);
+  }
+}
+
 // Waves per workgroup: enough that the device holds about 2048 waves and
 // each wave at most 8 chunks, at most 16 waves and at most half the chunks.
 int skinny_waves(int n, int k) {
@@ -194,10 +336,100 @@ hipError_t launch_w(const uint32_t* w, const uint16_t* s, const uint16_t* b, con
   return hipGetLastError();
 }
 
+// ---- the x-in-LDS multi-tile kernel ----
+
+// Taken for 12 <= M <= 16 with K <= 4096, K % 512 == 0: there x [M, K] is
+// 48-128 KB, which leaves the 16-row kernel one workgroup (four waves) per CU
+// in several rounds; here each workgroup stages x once for up to four row
+// tiles and the grid fits one round.  Measured with the weights from HBM (48
+// rotated copies), [9728 x 2560] M = 16: 11.2 us against 13.7 us.  At M <= 8,
+// and for K = 9728, the 16-row kernel stays faster (8.2 / 8.8 us at M = 4 / 8
+// against 8.7 / 9.5 us).
+constexpr int kLdsMinM = 12;
+constexpr int kLdsMaxK = 4096;
+constexpr int kLdsWaves = 8;
+
+// Largest U compiled for (TPW, W) of the LDS kernel (6 registers per tile and
+// chunk, W / 4 waves per SIMD).
+constexpr int max_u_lds(int tpw, int w) {
+  return w == 16 ? (tpw == 1 ? 8 : tpw == 2 ? 6 : tpw == 3 ? 4 : 3) : 8;
+}
+
+// Bytes of the x tile in LDS: M rows of 2 K bytes plus a 16-byte pad each.
+size_t lds_x_bytes(int k, int m) { return (size_t)m * (2 * (size_t)k + 16); }
+
+struct LdsPlan {
+  int tpw, u;
+  bool ok;
+};
+
+// Tiles per workgroup: the fewest (at most four) that keep the grid within
+// one workgroup per CU.
+LdsPlan plan_lds(int k, int n, int m) {
+  const int chunks = k / kChunkK;
+  const long tiles = (n + kRows - 1) / kRows;
+  int tpw = 4;
+  for (int t = 1; t <= 4; ++t)
+    if ((tiles + t - 1) / t <= 256) {
+      tpw = t;
+      break;
+    }
+  const bool ok = m >= kLdsMinM && k <= kLdsMaxK && k % 512 == 0 &&
+                  lds_x_bytes(k, m) + (size_t)kLdsWaves * tpw * 1024 <= 128 * 1024;
+  const int u = std::max(1, std::min((chunks + kLdsWaves - 1) / kLdsWaves,
+                                     max_u_lds(tpw, kLdsWaves)));
+  return LdsPlan{tpw, u, ok};
+}
+
+template <int T, int TPW, int W, int U>
+hipError_t launch_lds_twu(const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                          const uint16_t* x, uint16_t* y, int k, int n, int m, bool vec,
+                          hipStream_t stream) {
+  if constexpr (U > max_u_lds(TPW, W)) {
+    return hipErrorInvalidValue;
+  } else {
+    const dim3 grid((unsigned)((n + kRows * TPW - 1) / (kRows * TPW))), block(64 * W);
+    hipLaunchKernelGGL((qskinny_lds_kernel<T, TPW, W, U>), grid, block, lds_x_bytes(k, m),
+                       stream, w, s, b, x, y, m, n, k, vec);
+    return hipGetLastError();
+  }
+}
+
+template <int T, int TPW, int W>
+hipError_t launch_lds_tw(const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                         const uint16_t* x, uint16_t* y, int k, int n, int m, int u, bool vec,
+                         hipStream_t stream) {
+  switch (u) {
+    case 1: return launch_lds_twu<T, TPW, W, 1>(w, s, b, x, y, k, n, m, vec, stream);
+    case 2: return launch_lds_twu<T, TPW, W, 2>(w, s, b, x, y, k, n, m, vec, stream);
+    case 3: return launch_lds_twu<T, TPW, W, 3>(w, s, b, x, y, k, n, m, vec, stream);
+    case 4: return launch_lds_twu<T, TPW, W, 4>(w, s, b, x, y, k, n, m, vec, stream);
+    case 5:
+    case 6: return launch_lds_twu<T, TPW, W, 6>(w, s, b, x, y, k, n, m, vec, stream);
+    default: return launch_lds_twu<T, TPW, W, 8>(w, s, b, x, y, k, n, m, vec, stream);
+  }
+}
+
+template <int T, int TPW>
+hipError_t launch_lds_t(const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                        const uint16_t* x, uint16_t* y, int k, int n, int m, const LdsPlan& p,
+                        bool vec, hipStream_t stream) {
+  return launch_lds_tw<T, TPW, kLdsWaves>(w, s, b, x, y, k, n, m, p.u, vec, stream);
+}
+
 template <int T>
 hipError_t launch_t(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
                     uint16_t* y, int k, int n, int m, hipStream_t stream) {
   const bool vec = n % 4 == 0 && ((uintptr_t)y & 7u) == 0;
+  const LdsPlan lp = plan_lds(k, n, m);
+  if (lp.ok) {
+    switch (lp.tpw) {
+      case 1: return launch_lds_t<T, 1>(w, s, b, x, y, k, n, m, lp, vec, stream);
+      case 2: return launch_lds_t<T, 2>(w, s, b, x, y, k, n, m, lp, vec, stream);
+      case 3: return launch_lds_t<T, 3>(w, s, b, x, y, k, n, m, lp, vec, stream);
+      default: return launch_lds_t<T, 4>(w, s, b, x, y, k, n, m, lp, vec, stream);
+    }
+  }
   switch (skinny_waves(n, k)) {
     case 1: return launch_w<T, 1>(w, s, b, x, y, k, n, m, vec, stream);
     case 2: return launch_w<T, 2>(w, s, b, x, y, k, n, m, vec, stream);

@@ -232,14 +232,22 @@ def test_split_k_dispatcher(m, n, k):
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("m,n,k", [(4, 384, 512), (5, 384, 512), (16, 1001, 1024), (13, 17, 128),
-                                   (8, 9728, 2560), (4, 2560, 9728), (16, 2560, 9728), (9, 384, 192)])
+                                   (8, 9728, 2560), (4, 2560, 9728), (5, 2560, 9728),
+                                   (6, 2560, 9728), (16, 2560, 9728), (9, 384, 192),
+                                   (12, 9728, 2560), (16, 9728, 2560), (14, 3000, 4096)])
 def test_few_row_matrix_core_dispatch(dtype, m, n, k):
-    """4 <= M <= 16 through the dispatcher: the weight-streaming kernel (16 rows
-    per workgroup; x staged in LDS when M K 2 <= 64 KiB, else loaded per chunk:
-    M = 4 and 16 at K = 9728 take the second path; N = 1001 and 17 end in a
-    partial row block and take the single-element stores; K = 128 one chunk)
-    or, for K % 128 != 0 (K = 192), the tiled kernel.  Oracle within tolerance, the same bits on a second call,
-    and one-hot rows reproduce the dequantized weights bit for bit."""
+    """4 <= M <= 16 through the dispatcher.  The 16-row weight-streaming kernel
+    stages x in LDS when M K 2, rounded up to whole wave instructions, fits
+    96 KiB: M = 4 and 5 at K = 9728 (80 and exactly 96 KiB) take that path,
+    M = 6 and 16 there (128 KiB and more) load x per chunk into registers.
+    12 <= M <= 16 with K <= 4096 (K % 512 == 0) take the multi-tile kernel
+    with x in LDS: [9728 x 2560] at M = 12 and 16 (three 16-row tiles per
+    workgroup, the last workgroup two), 3000 x 4096 at M = 14 (a partial last
+    tile), 1001 x 1024 at M = 16.  N = 1001 and 17 end in a partial row block
+    and take the single-element stores; K = 128 is one chunk; K % 128 != 0
+    (K = 192) runs the tiled kernel.  Oracle within tolerance, the same bits on
+    a second call, and one-hot rows reproduce the dequantized weights bit for
+    bit."""
     note(f"few-row dispatch {dtype} M={m} N={n} K={k}")
     p = synth.make_problem(m, n, k, seed=23)
     x, w, s, b = synth.to_device(p)
