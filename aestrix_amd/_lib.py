@@ -50,7 +50,7 @@ class Plan(ctypes.Structure):
                 ("workspace_bytes", ctypes.c_size_t)]
 
 
-IMQ_ENTRY_QMM_T, IMQ_ENTRY_QGEMM, IMQ_ENTRY_QGEMV, IMQ_ENTRY_FUSED = 0, 1, 2, 3
+IMQ_ENTRY_QMM_T, IMQ_ENTRY_QGEMM, IMQ_ENTRY_QGEMV, IMQ_ENTRY_FUSED, IMQ_ENTRY_SWIGLU = 0, 1, 2, 3, 4
 KERNEL_NAMES = {0: "qgemv", 1: "few_row", 2: "tile", 3: "tile_reg"}
 
 
@@ -105,6 +105,7 @@ SIGNATURES = {
     "imq_upload": ([_p, _p, _p, _sz, _p], _i),
     "imq_st_upload": ([_p, _p, _s, _i, _p, _sz, _p], _i),
     "imq_load_qlinear": ([_p, _p, _s, _i, ctypes.POINTER(QWeight), _p], _i),
+    "imq_load_qlinear_cat": ([_p, _p, ctypes.POINTER(_s), _i, _i, ctypes.POINTER(QWeight), _p], _i),
     "imq_qweight_free": ([_p, ctypes.POINTER(QWeight)], _i),
     # imq_step.h
     "imq_dit_step_create": ([_p, ctypes.POINTER(DitDims), ctypes.POINTER(QWeight), _i, _i,

@@ -257,6 +257,13 @@ int check_epilogue(imq_ctx* ctx, const char* fn, const uint32_t* w, const void* 
   return bind_device(ctx);
 }
 
+// Whether imq_qmm_swiglu runs the qGEMV's pair mode: few rows, 16-bit T, and
+// the qGEMV's 32-bit offsets (weights under 4 GiB, one x tile under 2 GiB).
+bool swiglu_on_qgemv(int k, int n, int m, imq_dtype dtype) {
+  return m <= imq::kQgemvSwigluMaxM && dtype != IMQ_F32 &&
+         (size_t)n * (size_t)k / 2 < ((size_t)1 << 32) && (size_t)m * k * 2 < ((size_t)1 << 31);
+}
+
 }  // namespace
 
 extern "C" {
@@ -444,6 +451,13 @@ int imq_qmm_plan(imq_ctx* ctx, int entry, int k, int n, int m, imq_dtype dtype, 
         return fail(ctx, IMQ_EUNSUPPORTED, "%s: packed weights of 4 GiB or more", fn);
       *out = imq_plan{IMQ_KERNEL_QGEMV, 0, 1, 0};
       return IMQ_OK;
+    case IMQ_ENTRY_SWIGLU:
+      if (dtype == IMQ_F32) return fail(ctx, IMQ_EUNSUPPORTED, "%s: f32 has no MFMA kernel", fn);
+      if (swiglu_on_qgemv(k, n, m, dtype)) {
+        *out = imq_plan{IMQ_KERNEL_QGEMV, 0, 1, 0};
+        return IMQ_OK;
+      }
+      return tile(true, false);
     case IMQ_ENTRY_QGEMM:
     case IMQ_ENTRY_FUSED:
       if (dtype == IMQ_F32) return fail(ctx, IMQ_EUNSUPPORTED, "%s: f32 has no MFMA kernel", fn);
@@ -542,9 +556,15 @@ int imq_qmm_swiglu(imq_ctx* ctx, const uint32_t* w, const void* scales, const vo
                 "%s: sections gate [%d, +%d) / up [%d, +%d) must lie in the %d weight rows and "
                 "ldy (%d) >= width",
                 fn, gate_row, width, up_row, width, n, ldy);
-  const hipError_t e = imq::launch_qgemm_swiglu(w, scales, biases, x, y, ldy, k, n, m, width,
-                                                gate_row, up_row, in_scale, out_scale, (int)dtype,
-                                                static_cast<hipStream_t>(stream));
+  const auto st = static_cast<hipStream_t>(stream);
+  // Few rows: the qGEMV with the gate and up rows of an output in one lane
+  // group (one launch streams both weight sections).
+  const hipError_t e =
+      swiglu_on_qgemv(k, n, m, dtype)
+          ? imq::launch_qgemv_swiglu(w, scales, biases, x, y, ldy, k, n, m, width, gate_row,
+                                     up_row, in_scale, out_scale, (int)dtype, st)
+          : imq::launch_qgemm_swiglu(w, scales, biases, x, y, ldy, k, n, m, width, gate_row,
+                                     up_row, in_scale, out_scale, (int)dtype, st);
   return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
 }
 

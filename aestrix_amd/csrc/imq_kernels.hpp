@@ -17,6 +17,16 @@ hipError_t launch_dequant(const uint32_t* w, const void* scales, const void* bia
 hipError_t launch_qgemv(const uint32_t* w, const void* scales, const void* biases, const void* x,
                         void* y, int k, int n, int m, int dtype, hipStream_t stream);
 
+// The qGEMV with a gate/up pair of weight rows per output (the SwiGLU stage
+// of launch_qgemm_swiglu, same arguments and result) for 1 <= m <=
+// kQgemvSwigluMaxM, T in {bf16, f16}: the gate and up rows of an output are
+// read by one lane group and combined after the reduction.
+constexpr int kQgemvSwigluMaxM = 4;
+hipError_t launch_qgemv_swiglu(const uint32_t* w, const void* scales, const void* biases,
+                               const void* x, void* y, int ldy, int k, int n, int m, int width,
+                               int gate_row, int up_row, float in_scale, float out_scale,
+                               int dtype, hipStream_t stream);
+
 // fp32 scratch for split-K partial sums.  With too few output tiles to fill
 // the chip, the MFMA kernel splits K, writes each split's partial sums here
 // and a second kernel adds them; a null or short workspace runs unsplit.

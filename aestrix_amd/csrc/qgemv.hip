@@ -22,6 +22,7 @@
 //    multiplied into fp32 accumulators with v_dot2_f32_bf16 / v_dot2_f32_f16
 //    (16-bit T) or fma (f32);
 //  * the G partial sums of a row are combined with DPP adds.
+#include "epilogue.hpp"
 #include "imq_device.hpp"
 #include "imq_kernels.hpp"
 
@@ -102,11 +103,23 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-template <int T, int MR, int G, int U, int R>
+// A gate/up pair of rows per lane group (the SwiGLU mode): output j of row m
+// is y[m][j] (row pitch ldy) = T(g * sigmoid(g) * u * out_scale), g and u the
+// T-rounded products of x row m with weight rows gate_row + j and up_row + j
+// times in_scale -- the qmm followed by dq_silu_mul / dd_swiglu_pitched
+// (Sources/ImarelloDirect/DirectGlueKernels.swift:77-88,
+// DirectDiTKernels.swift:137-157), computed by EpSwiGLU.
+struct GvPair {
+  int gate_row, up_row, width, ldy;
+  float in_scale, out_scale;
+};
+
+template <int T, int MR, int G, int U, int R, bool PAIR>
 __global__ __launch_bounds__(kThreads) void qgemv_kernel(
     const uint32_t* __restrict__ w, const typename Elem<T>::S* __restrict__ scales,
     const typename Elem<T>::S* __restrict__ biases, const typename Elem<T>::S* __restrict__ x,
-    typename Elem<T>::S* __restrict__ y, int K, int N, int M, int kt) {
+    typename Elem<T>::S* __restrict__ y, int K, int N, int M, int kt, const GvPair pr) {
+  static_assert(!PAIR || R == 2, "a gate/up pair is two rows per lane group");
   using E = Elem<T>;
   using X = XTile<T>;
   constexpr int P = X::kP;
@@ -117,6 +130,7 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int gl = lane & (G - 1);
   const int row0 = (blockIdx.x * kWaves + wave) * RPW + (lane / G) * R;
+  const int pj = (blockIdx.x * kWaves + wave) * (64 / G) + lane / G;  // PAIR: output column
   const int gpr = K >> 6;
   if constexpr (MR == 1) M = 1;  // lets the compiler drop the row arithmetic of x
 
@@ -129,7 +143,9 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
   uint32_t woff[R], poff[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const uint32_t rr = (uint32_t)min(row0 + r, N - 1);
+    uint32_t rr = (uint32_t)min(row0 + r, N - 1);
+    if constexpr (PAIR)
+      rr = (uint32_t)min((r == 0 ? pr.gate_row : pr.up_row) + min(pj, pr.width - 1), N - 1);
     woff[r] = rr * (uint32_t)(K / 2);
     poff[r] = rr * (uint32_t)gpr * E::kBytes;
   }
@@ -268,7 +284,14 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[r][m] = group_sum<G>(acc[r][m]);
-  if (gl == G - 1) {
+  if constexpr (PAIR) {
+    if (gl == G - 1 && pj < pr.width) {
+      const EpSwiGLU<T> ep{nullptr, 0, 0, 0, 0, pr.in_scale, pr.out_scale, false};
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (m < M) y[(size_t)m * pr.ldy + pj] = E::out(ep.value2(acc[0][m], acc[1][m]));
+    }
+  } else if (gl == G - 1) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (row0 + r < N) {
@@ -303,13 +326,13 @@ int tile_len(int k, int mr, int g, int eb) {
 // on 9728 x 2560 and 2560 x 9728 at M = 1, 2, 4, 8, 16 picks the fastest G
 // in all ten cases with these caps).
 // IMQ_QGEMV_LANES=16|32|64 overrides.
-Plan make_plan(int k, int n, int mr, int eb) {
+Plan make_plan(int k, int n, int mr, int eb, int r_override = 0) {
   static const int forced = [] {
     const char* e = getenv("IMQ_QGEMV_LANES");
     const int v = e ? atoi(e) : 0;
     return (v == 16 || v == 32 || v == 64) ? v : 0;
   }();
-  const int r = rows_per_lane(mr);
+  const int r = r_override ? r_override : rows_per_lane(mr);
   Plan best{16, 0, 0};
   double best_score = -1.0;
   for (int g = 16; g <= 64; g *= 2) {
@@ -330,65 +353,79 @@ Plan make_plan(int k, int n, int mr, int eb) {
 
 template <int T, int MR, int G, int U>
 hipError_t launch_u(const uint32_t* w, const void* s, const void* b, const void* x, void* y, int k,
-                    int n, int m, int kt, hipStream_t stream) {
+                    int n, int m, int kt, const GvPair* pr, hipStream_t stream) {
   using ST = typename Elem<T>::S;
-  constexpr int R = rows_per_lane(MR);
-  constexpr int rows_per_block = kWaves * (64 / G) * R;
-  const dim3 grid((n + rows_per_block - 1) / rows_per_block);
   // x slots of the longest tile, rounded up to whole 256-slot rounds.
   const size_t pieces = (size_t)m * kt / XTile<T>::kEpp;
   const size_t slots = (pieces + kThreads - 1) / kThreads * kThreads;
-  hipLaunchKernelGGL((qgemv_kernel<T, MR, G, U, R>), grid, dim3(kThreads), slots * 16, stream, w,
-                     static_cast<const ST*>(s), static_cast<const ST*>(b),
-                     static_cast<const ST*>(x), static_cast<ST*>(y), k, n, m, kt);
+  if (pr) {
+    if constexpr (MR <= 4 && T != kF32) {
+      constexpr int kOutsPerBlock = kWaves * (64 / G);
+      const dim3 grid((pr->width + kOutsPerBlock - 1) / kOutsPerBlock);
+      hipLaunchKernelGGL((qgemv_kernel<T, MR, G, U, 2, true>), grid, dim3(kThreads), slots * 16,
+                         stream, w, static_cast<const ST*>(s), static_cast<const ST*>(b),
+                         static_cast<const ST*>(x), static_cast<ST*>(y), k, n, m, kt, *pr);
+      return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+  }
+  constexpr int R = rows_per_lane(MR);
+  constexpr int rows_per_block = kWaves * (64 / G) * R;
+  const dim3 grid((n + rows_per_block - 1) / rows_per_block);
+  hipLaunchKernelGGL((qgemv_kernel<T, MR, G, U, R, false>), grid, dim3(kThreads), slots * 16,
+                     stream, w, static_cast<const ST*>(s), static_cast<const ST*>(b),
+                     static_cast<const ST*>(x), static_cast<ST*>(y), k, n, m, kt, GvPair{});
   return hipGetLastError();
 }
 
 template <int T, int MR, int G>
 hipError_t launch_g(const uint32_t* w, const void* s, const void* b, const void* x, void* y, int k,
-                    int n, int m, const Plan& p, hipStream_t stream) {
+                    int n, int m, const Plan& p, const GvPair* pr, hipStream_t stream) {
   if constexpr (max_chunks(MR) == 8) {
     switch (p.u) {
-      case 1: return launch_u<T, MR, G, 1>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 2: return launch_u<T, MR, G, 2>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 3: return launch_u<T, MR, G, 3>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 4: return launch_u<T, MR, G, 4>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 5: return launch_u<T, MR, G, 5>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 6: return launch_u<T, MR, G, 6>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 7: return launch_u<T, MR, G, 7>(w, s, b, x, y, k, n, m, p.kt, stream);
-      default: return launch_u<T, MR, G, 8>(w, s, b, x, y, k, n, m, p.kt, stream);
+      case 1: return launch_u<T, MR, G, 1>(w, s, b, x, y, k, n, m, p.kt, pr, stream);
+      case 2: return launch_u<T, MR, G, 2>(w, s, b, x, y, k, n, m, p.kt, pr, stream);
+      case 3: return launch_u<T, MR, G, 3>(w, s, b, x, y, k, n, m, p.kt, pr, stream);
+      case 4: return launch_u<T, MR, G, 4>(w, s, b, x, y, k, n, m, p.kt, pr, stream);
+      case 5: return launch_u<T, MR, G, 5>(w, s, b, x, y, k, n, m, p.kt, pr, stream);
+      case 6: return launch_u<T, MR, G, 6>(w, s, b, x, y, k, n, m, p.kt, pr, stream);
+      case 7: return launch_u<T, MR, G, 7>(w, s, b, x, y, k, n, m, p.kt, pr, stream);
+      default: return launch_u<T, MR, G, 8>(w, s, b, x, y, k, n, m, p.kt, pr, stream);
     }
   } else {
     switch (p.u) {
-      case 1: return launch_u<T, MR, G, 1>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 2: return launch_u<T, MR, G, 2>(w, s, b, x, y, k, n, m, p.kt, stream);
-      case 3: return launch_u<T, MR, G, 3>(w, s, b, x, y, k, n, m, p.kt, stream);
-      default: return launch_u<T, MR, G, 4>(w, s, b, x, y, k, n, m, p.kt, stream);
+      case 1: return launch_u<T, MR, G, 1>(w, s, b, x, y, k, n, m, p.kt, pr, stream);
+      case 2: return launch_u<T, MR, G, 2>(w, s, b, x, y, k, n, m, p.kt, pr, stream);
+      case 3: return launch_u<T, MR, G, 3>(w, s, b, x, y, k, n, m, p.kt, pr, stream);
+      default: return launch_u<T, MR, G, 4>(w, s, b, x, y, k, n, m, p.kt, pr, stream);
     }
   }
 }
 
 template <int T, int MR>
 hipError_t launch_m(const uint32_t* w, const void* s, const void* b, const void* x, void* y, int k,
-                    int n, int m, hipStream_t stream) {
-  const Plan p = make_plan(k, n, MR, Elem<T>::kBytes);
+                    int n, int m, const GvPair* pr, hipStream_t stream) {
+  // A pair plans as 2 width rows read two per lane group.
+  const Plan p = pr ? make_plan(k, 2 * pr->width, MR, Elem<T>::kBytes, 2)
+                    : make_plan(k, n, MR, Elem<T>::kBytes);
   switch (p.g) {
-    case 16: return launch_g<T, MR, 16>(w, s, b, x, y, k, n, m, p, stream);
-    case 32: return launch_g<T, MR, 32>(w, s, b, x, y, k, n, m, p, stream);
-    default: return launch_g<T, MR, 64>(w, s, b, x, y, k, n, m, p, stream);
+    case 16: return launch_g<T, MR, 16>(w, s, b, x, y, k, n, m, p, pr, stream);
+    case 32: return launch_g<T, MR, 32>(w, s, b, x, y, k, n, m, p, pr, stream);
+    default: return launch_g<T, MR, 64>(w, s, b, x, y, k, n, m, p, pr, stream);
   }
 }
 
 template <int T>
 hipError_t launch_t(const uint32_t* w, const void* s, const void* b, const void* x, void* y, int k,
-                    int n, int m, hipStream_t stream) {
+                    int n, int m, const GvPair* pr, hipStream_t stream) {
   // M is rounded up to a power of two for the register tile; rows >= M are
   // not stored.
-  if (m <= 1) return launch_m<T, 1>(w, s, b, x, y, k, n, m, stream);
-  if (m <= 2) return launch_m<T, 2>(w, s, b, x, y, k, n, m, stream);
-  if (m <= 4) return launch_m<T, 4>(w, s, b, x, y, k, n, m, stream);
-  if (m <= 8) return launch_m<T, 8>(w, s, b, x, y, k, n, m, stream);
-  if (m <= 16) return launch_m<T, 16>(w, s, b, x, y, k, n, m, stream);
+  if (m <= 1) return launch_m<T, 1>(w, s, b, x, y, k, n, m, pr, stream);
+  if (m <= 2) return launch_m<T, 2>(w, s, b, x, y, k, n, m, pr, stream);
+  if (m <= 4) return launch_m<T, 4>(w, s, b, x, y, k, n, m, pr, stream);
+  if (pr) return hipErrorInvalidValue;
+  if (m <= 8) return launch_m<T, 8>(w, s, b, x, y, k, n, m, nullptr, stream);
+  if (m <= 16) return launch_m<T, 16>(w, s, b, x, y, k, n, m, nullptr, stream);
   return hipErrorInvalidValue;
 }
 
@@ -397,9 +434,22 @@ hipError_t launch_t(const uint32_t* w, const void* s, const void* b, const void*
 hipError_t launch_qgemv(const uint32_t* w, const void* scales, const void* biases, const void* x,
                         void* y, int k, int n, int m, int dtype, hipStream_t stream) {
   switch (dtype) {
-    case kBf16: return launch_t<kBf16>(w, scales, biases, x, y, k, n, m, stream);
-    case kF16: return launch_t<kF16>(w, scales, biases, x, y, k, n, m, stream);
-    case kF32: return launch_t<kF32>(w, scales, biases, x, y, k, n, m, stream);
+    case kBf16: return launch_t<kBf16>(w, scales, biases, x, y, k, n, m, nullptr, stream);
+    case kF16: return launch_t<kF16>(w, scales, biases, x, y, k, n, m, nullptr, stream);
+    case kF32: return launch_t<kF32>(w, scales, biases, x, y, k, n, m, nullptr, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_qgemv_swiglu(const uint32_t* w, const void* scales, const void* biases,
+                               const void* x, void* y, int ldy, int k, int n, int m, int width,
+                               int gate_row, int up_row, float in_scale, float out_scale,
+                               int dtype, hipStream_t stream) {
+  if (m > kQgemvSwigluMaxM) return hipErrorInvalidValue;
+  const GvPair pr{gate_row, up_row, width, ldy, in_scale, out_scale};
+  switch (dtype) {
+    case kBf16: return launch_t<kBf16>(w, scales, biases, x, y, k, n, m, &pr, stream);
+    case kF16: return launch_t<kF16>(w, scales, biases, x, y, k, n, m, &pr, stream);
     default: return hipErrorInvalidValue;
   }
 }

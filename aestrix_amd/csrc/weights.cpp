@@ -749,48 +749,72 @@ int imq_st_upload(imq_ctx* ctx, const imq_st* st, const char* name, int dst_dtyp
                      static_cast<hipStream_t>(stream));
 }
 
-int imq_load_qlinear(imq_ctx* ctx, const imq_st* st, const char* prefix, imq_dtype param_dtype,
-                     imq_qweight* out, imq_stream stream) {
-  const char* fn = "imq_load_qlinear";
+int imq_load_qlinear_cat(imq_ctx* ctx, const imq_st* st, const char* const* prefixes, int count,
+                         imq_dtype param_dtype, imq_qweight* out, imq_stream stream) {
+  const char* fn = "imq_load_qlinear_cat";
   if (!ctx) return fail(nullptr, IMQ_EINVAL, "%s: null context", fn);
-  if (!st || !prefix || !out) return fail(ctx, IMQ_EINVAL, "%s: null argument", fn);
+  if (!st || !prefixes || count <= 0 || !out) return fail(ctx, IMQ_EINVAL, "%s: null argument", fn);
   memset(out, 0, sizeof *out);
   if (param_dtype != IMQ_BF16 && param_dtype != IMQ_F16 && param_dtype != IMQ_F32)
     return fail(ctx, IMQ_EUNSUPPORTED, "%s: dtype %d", fn, (int)param_dtype);
-  const std::string p = prefix;
-  const Tensor* t[3] = {};
+  // Every part: its three tensors, checked; all parts share K and the scale type.
+  struct Part {
+    const Tensor* t[3];
+    int64_t n;
+  };
+  std::vector<Part> parts((size_t)count);
   const char* suffix[3] = {".weight", ".scales", ".biases"};
-  for (int i = 0; i < 3; ++i) {
-    const auto it = st->index.find(p + suffix[i]);
-    if (it == st->index.end())
-      return fail(ctx, IMQ_EINVAL, "missing tensor %s%s", prefix, suffix[i]);
-    t[i] = &st->tensors[it->second];
+  int64_t k = 0, n_total = 0;
+  int src_dtype = -1;
+  for (int pi = 0; pi < count; ++pi) {
+    const char* prefix = prefixes[pi];
+    if (!prefix) return fail(ctx, IMQ_EINVAL, "%s: null prefix %d", fn, pi);
+    const std::string p = prefix;
+    Part& part = parts[(size_t)pi];
+    for (int i = 0; i < 3; ++i) {
+      const auto it = st->index.find(p + suffix[i]);
+      if (it == st->index.end())
+        return fail(ctx, IMQ_EINVAL, "missing tensor %s%s", prefix, suffix[i]);
+      part.t[i] = &st->tensors[it->second];
+    }
+    const Tensor* const* t = part.t;
+    if (t[0]->dtype != IMQ_ST_U32 || t[0]->shape.size() != 2)
+      return fail(ctx, IMQ_EINVAL, "%s: %s.weight must be U32 [N, K/8]", fn, prefix);
+    const int64_t n = t[0]->shape[0];
+    const int64_t kk = t[0]->shape[1] * 8;
+    if (n <= 0 || kk <= 0 || kk % 64 != 0 || n > INT32_MAX || kk > INT32_MAX)
+      return fail(ctx, IMQ_EINVAL, "%s: %s: bad packed shape [%lld, %lld]", fn, prefix,
+                  (long long)n, (long long)t[0]->shape[1]);
+    if (pi == 0) {
+      k = kk;
+      src_dtype = t[1]->dtype;
+    } else if (kk != k) {
+      return fail(ctx, IMQ_EINVAL, "%s: %s has K=%lld, %s has K=%lld", fn, prefix, (long long)kk,
+                  prefixes[0], (long long)k);
+    }
+    for (int i = 1; i < 3; ++i) {
+      if (t[i]->dtype != src_dtype ||
+          (src_dtype != IMQ_ST_BF16 && src_dtype != IMQ_ST_F16 && src_dtype != IMQ_ST_F32))
+        return fail(ctx, IMQ_EINVAL, "%s: %s scales and biases must share BF16, F16 or F32 (and "
+                    "the first projection's type)", fn, prefix);
+      if (t[i]->shape.size() != 2 || t[i]->shape[0] != n || t[i]->shape[1] != k / 64)
+        return fail(ctx, IMQ_EINVAL, "%s: %s%s must be [%lld, %lld]", fn, prefix, suffix[i],
+                    (long long)n, (long long)(k / 64));
+    }
+    part.n = n;
+    n_total += n;
   }
-  if (t[0]->dtype != IMQ_ST_U32 || t[0]->shape.size() != 2)
-    return fail(ctx, IMQ_EINVAL, "%s: %s.weight must be U32 [N, K/8]", fn, prefix);
-  const int64_t n = t[0]->shape[0];
-  const int64_t k = t[0]->shape[1] * 8;
-  if (n <= 0 || k <= 0 || k % 64 != 0 || n > INT32_MAX || k > INT32_MAX)
-    return fail(ctx, IMQ_EINVAL, "%s: %s: bad packed shape [%lld, %lld]", fn, prefix,
-                (long long)n, (long long)t[0]->shape[1]);
-  const int src_dtype = t[1]->dtype;
-  for (int i = 1; i < 3; ++i) {
-    if (t[i]->dtype != src_dtype ||
-        (src_dtype != IMQ_ST_BF16 && src_dtype != IMQ_ST_F16 && src_dtype != IMQ_ST_F32))
-      return fail(ctx, IMQ_EINVAL, "%s: %s scales and biases must share BF16, F16 or F32", fn,
-                  prefix);
-    if (t[i]->shape.size() != 2 || t[i]->shape[0] != n || t[i]->shape[1] != k / 64)
-      return fail(ctx, IMQ_EINVAL, "%s: %s%s must be [%lld, %lld]", fn, prefix, suffix[i],
-                  (long long)n, (long long)(k / 64));
-  }
+  if (n_total > INT32_MAX)
+    return fail(ctx, IMQ_EINVAL, "%s: %lld rows in all", fn, (long long)n_total);
   Conv conv = Conv::kCopy;
   if (!conversion(src_dtype, st_dtype_of(param_dtype), conv))
-    return fail(ctx, IMQ_EUNSUPPORTED, "%s: %s: %s scales to dtype %d", fn, prefix,
-                kDtypes[src_dtype].name, (int)param_dtype);
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: %s scales to dtype %d", fn, kDtypes[src_dtype].name,
+                (int)param_dtype);
   const size_t src_es = kDtypes[src_dtype].size;
   const size_t dst_es = elem_size(param_dtype);
-  const size_t n_params = (size_t)n * (size_t)(k / 64);
-  const size_t w_bytes = t[0]->bytes;
+  const size_t row_w = (size_t)k / 2, row_p = (size_t)(k / 64);
+  const size_t w_bytes = (size_t)n_total * row_w;
+  const size_t n_params = (size_t)n_total * row_p;
   const size_t s_off = align_up(w_bytes, 256);
   const size_t b_off = s_off + align_up(n_params * dst_es, 256);
   const size_t total = b_off + n_params * dst_es;
@@ -799,15 +823,24 @@ int imq_load_qlinear(imq_ctx* ctx, const imq_st* st, const char* prefix, imq_dty
   void* base = nullptr;
   hipError_t e = hipMalloc(&base, total);
   if (e == hipErrorOutOfMemory)
-    return fail(ctx, IMQ_ENOMEM, "%s: %s: %zu bytes: out of device memory", fn, prefix, total);
+    return fail(ctx, IMQ_ENOMEM, "%s: %zu bytes: out of device memory", fn, total);
   if (e != hipSuccess) return hip_fail(ctx, e, fn);
   auto* b8 = static_cast<uint8_t*>(base);
   const auto st_ = static_cast<hipStream_t>(stream);
-  rc = staged_copy(ctx, fn, b8, t[0]->data, w_bytes, 1, 1, Conv::kCopy, st_);
-  if (rc == IMQ_OK)
-    rc = staged_copy(ctx, fn, b8 + s_off, t[1]->data, n_params, src_es, dst_es, conv, st_);
-  if (rc == IMQ_OK)
-    rc = staged_copy(ctx, fn, b8 + b_off, t[2]->data, n_params, src_es, dst_es, conv, st_);
+  size_t row0 = 0;
+  for (const Part& part : parts) {
+    const size_t np = (size_t)part.n * row_p;
+    rc = staged_copy(ctx, fn, b8 + row0 * row_w, part.t[0]->data, part.t[0]->bytes, 1, 1,
+                     Conv::kCopy, st_);
+    if (rc == IMQ_OK)
+      rc = staged_copy(ctx, fn, b8 + s_off + row0 * row_p * dst_es, part.t[1]->data, np, src_es,
+                       dst_es, conv, st_);
+    if (rc == IMQ_OK)
+      rc = staged_copy(ctx, fn, b8 + b_off + row0 * row_p * dst_es, part.t[2]->data, np, src_es,
+                       dst_es, conv, st_);
+    if (rc != IMQ_OK) break;
+    row0 += (size_t)part.n;
+  }
   if (rc != IMQ_OK) {
     (void)hipStreamSynchronize(st_);
     (void)hipFree(base);
@@ -816,11 +849,27 @@ int imq_load_qlinear(imq_ctx* ctx, const imq_st* st, const char* prefix, imq_dty
   out->w = reinterpret_cast<uint32_t*>(b8);
   out->scales = b8 + s_off;
   out->biases = b8 + b_off;
-  out->n = (int)n;
+  out->n = (int)n_total;
   out->k = (int)k;
   out->dtype = param_dtype;
   out->base = base;
   return IMQ_OK;
+}
+
+int imq_load_qlinear(imq_ctx* ctx, const imq_st* st, const char* prefix, imq_dtype param_dtype,
+                     imq_qweight* out, imq_stream stream) {
+  if (!prefix) {
+    if (out) memset(out, 0, sizeof *out);
+    return fail(ctx, IMQ_EINVAL, "imq_load_qlinear: null argument");
+  }
+  const int rc = imq_load_qlinear_cat(ctx, st, &prefix, 1, param_dtype, out, stream);
+  if (rc != IMQ_OK && ctx) {
+    // Report under the entry point the caller used.
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const std::string cat = "imq_load_qlinear_cat";
+    if (ctx->err.compare(0, cat.size(), cat) == 0) ctx->err.replace(0, cat.size(), "imq_load_qlinear");
+  }
+  return rc;
 }
 
 int imq_qweight_free(imq_ctx* ctx, imq_qweight* q) {

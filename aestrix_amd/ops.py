@@ -284,14 +284,16 @@ def qmm_swiglu(x, w, scales, biases, width: int, gate_row: int, up_row: int,
 
 
 _ENTRIES = {"qmm_t": _lib.IMQ_ENTRY_QMM_T, "qgemm": _lib.IMQ_ENTRY_QGEMM,
-            "qgemv": _lib.IMQ_ENTRY_QGEMV, "fused": _lib.IMQ_ENTRY_FUSED}
+            "qgemv": _lib.IMQ_ENTRY_QGEMV, "fused": _lib.IMQ_ENTRY_FUSED,
+            "swiglu": _lib.IMQ_ENTRY_SWIGLU}
 
 
 def qmm_plan(m: int, n: int, k: int, dtype: torch.dtype = torch.bfloat16, entry: str = "qmm_t",
              device=None) -> dict:
     """The kernel, tile height and K split a call of ``entry`` ("qmm_t", "qgemm",
-    "qgemv", or "fused": the fused output stages, n = the weight rows they read)
-    would run for these sizes, without launching anything (``imq_qmm_plan``)."""
+    "qgemv", "fused": the post-scale and gated-residual stages over n weight
+    rows, "swiglu": n = 2 width) would run for these sizes, without launching
+    anything (``imq_qmm_plan``)."""
     _require(entry in _ENTRIES, f"entry must be one of {sorted(_ENTRIES)}")
     ctx = context(device)
     out = _lib.Plan()

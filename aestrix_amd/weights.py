@@ -169,6 +169,20 @@ class SafetensorsSet:
             raise WeightsError(f"{name}: no upload to {target}")
         dev = torch.device("cuda", device_index(device))
         out = torch.empty(t.shape, dtype=target, device=dev)
+        return self.upload_into(name, out, stream)
+
+    def upload_into(self, name: str, out: torch.Tensor,
+                    stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        """Upload the tensor into ``out`` (contiguous, its shape, converted to
+        out's dtype as ``upload`` does) -- e.g. a row range of a larger buffer."""
+        t = self.info(name)
+        target = out.dtype
+        if target not in _TORCH_ST:
+            raise WeightsError(f"{name}: no upload to {target}")
+        if tuple(out.shape) != tuple(t.shape) or not out.is_contiguous() or not out.is_cuda:
+            raise WeightsError(f"{name}: destination must be a contiguous HIP tensor of shape "
+                               f"{t.shape}, got {tuple(out.shape)}")
+        dev = out.device
         ctx = context(dev)
         st = stream if stream is not None else torch.cuda.current_stream(dev)
         dst_st = _TORCH_ST[target]
@@ -201,6 +215,41 @@ def load_qlinear(st: SafetensorsSet, prefix: str, scales: torch.dtype = torch.bf
     s = st.upload(f"{prefix}.scales", scales, device)
     b = st.upload(f"{prefix}.biases", scales, device)
     return Q(w=w, s=s, b=b, n=nn, k=kk)
+
+
+def load_qlinear_cat(st: SafetensorsSet, prefixes: list[str],
+                     scales: torch.dtype = torch.bfloat16, device=None) -> Q:
+    """Projections sharing K as one resident ``Q`` whose rows are theirs in order
+    (q/k/v or gate/up of a text-encoder layer): one call then streams all of
+    their weights in one launch.  Rows [sum(n_0..n_{i-1}), +n_i) are projection i."""
+    if not prefixes:
+        raise WeightsError("no projections to concatenate")
+    metas = []
+    for prefix in prefixes:
+        info = st.info(f"{prefix}.weight")
+        if info.dtype != "U32" or len(info.shape) != 2:
+            raise WeightsError(f"{prefix}.weight must be U32 [N, K/8], got {info.dtype} {info.shape}")
+        nn, kk = info.shape[0], info.shape[1] * 8
+        for suf in ("scales", "biases"):
+            si = st.info(f"{prefix}.{suf}")
+            if si.shape != (nn, kk // 64):
+                raise WeightsError(f"{prefix}.{suf} must be [{nn}, {kk // 64}], got {si.shape}")
+        metas.append((prefix, nn, kk))
+    k = metas[0][2]
+    if any(m[2] != k for m in metas):
+        raise WeightsError(f"projections disagree on K: {[(m[0], m[2]) for m in metas]}")
+    n = sum(m[1] for m in metas)
+    dev = torch.device("cuda", device_index(device))
+    w = torch.empty((n, k // 8), dtype=torch.int32, device=dev)
+    s = torch.empty((n, k // 64), dtype=scales, device=dev)
+    b = torch.empty((n, k // 64), dtype=scales, device=dev)
+    row = 0
+    for prefix, nn, _ in metas:
+        st.upload_into(f"{prefix}.weight", w[row:row + nn])
+        st.upload_into(f"{prefix}.scales", s[row:row + nn])
+        st.upload_into(f"{prefix}.biases", b[row:row + nn])
+        row += nn
+    return Q(w=w, s=s, b=b, n=n, k=k)
 
 
 # ------------------------------------------------------------- key maps

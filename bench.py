@@ -140,6 +140,43 @@ def bench_qgemv(imq, synth, torch, copies: int = 48, ms_list=(1, 4, 16),
     return out
 
 
+def bench_fused_decode(imq, synth, torch, copies: int = 48) -> dict:
+    """Projections that share x at decode sizes as one launch: the text
+    encoder's gate and up ([9728 x 2560] each, rows concatenated) with the
+    SiLU-mul stage (qmm_swiglu; the qGEMV's pair mode at M <= 4), and q/k/v
+    ([4096 + 1024 + 1024 rows x 2560], one plain call), beside the single
+    [9728 x 2560] launch; weights rotated over `copies` copies (from HBM)."""
+    out = {}
+    k, inter = 2560, 9728
+    for tag, n_rows in (("gate_up_swiglu", 2 * inter), ("qkv", 6144)):
+        p = synth.make_problem(4, n_rows, k, seed=7)
+        x, w, s, b = synth.to_device(p)
+        ws = [w.clone() for _ in range(copies)]
+        ss = [s.clone() for _ in range(copies)]
+        bs = [b.clone() for _ in range(copies)]
+        del w, s, b
+        for m in (1, 4):
+            xm = x[:m].contiguous()
+            width = inter if tag == "gate_up_swiglu" else n_rows
+            ys = [torch.empty((m, width), dtype=torch.bfloat16, device="cuda") for _ in range(copies)]
+            if tag == "gate_up_swiglu":
+                launches = [(lambda i=i: imq.qmm_swiglu(xm, ws[i], ss[i], bs[i], inter, 0, inter,
+                                                        out=ys[i])) for i in range(copies)]
+            else:
+                launches = [(lambda i=i: imq.quantized_matmul(xm, ws[i], ss[i], bs[i], out=ys[i]))
+                            for i in range(copies)]
+            ms = time_graph(launches)
+            byts = 2 * m * k + n_rows * k // 2 + 4 * n_rows * k // 64 + 2 * m * width
+            gbs = byts / (ms * 1e-3) / 1e9
+            out[f"{tag}_M{m}_N{n_rows}_K{k}"] = {
+                "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts}
+            log(f"{tag} M={m} N={n_rows} K={k}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
+        del ws, ss, bs
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_qgemv_f32(imq, synth, torch, copies: int = 24) -> dict:
     """The conditioner's M=1 qmm with f32 x, scales, biases and y
     (DirectConditioner.swift:48,75-84): its largest projection [18432x3072]
@@ -492,11 +529,13 @@ def main() -> int:
     extra = {}
     if not args.only_target:
         extra["qgemv"] = bench_qgemv(imq, synth, torch)
+        extra["fused_decode"] = bench_fused_decode(imq, synth, torch)
         extra["qgemv_f32"] = bench_qgemv_f32(imq, synth, torch)
         extra["dequant"] = bench_dequant(imq, synth, torch)
         extra["prescale"] = bench_prescale(imq, torch)
         extra["qgemm_shapes"] = {
-            "M1024_N9216_K3072": bench_qgemm_shape(imq, synth, torch, 1024, 9216, 3072),
+            "M1024_N9216_K3072": bench_qgemm_shape(imq, synth, torch, 1024, 9216, 3072,
+                                                   dispatcher=True),
             "M4608_N27648_K3072": bench_qgemm_shape(imq, synth, torch, 4608, 27648, 3072),
             "M4608_N3072_K9216": bench_qgemm_shape(imq, synth, torch, 4608, 3072, 9216),
         }

@@ -172,8 +172,8 @@ typedef enum imq_entry {
     IMQ_ENTRY_QMM_T = 0,   /* imq_qmm_t and imq_qmm_t_noalloc */
     IMQ_ENTRY_QGEMM = 1,   /* imq_qgemm */
     IMQ_ENTRY_QGEMV = 2,   /* imq_qgemv */
-    IMQ_ENTRY_FUSED = 3    /* imq_qmm_postscale / _gate_add (n = weight rows), imq_qmm_swiglu
-                              (n = 2 * width: the gate and up rows it reads) */
+    IMQ_ENTRY_FUSED = 3,   /* imq_qmm_postscale / _gate_add (n = weight rows) */
+    IMQ_ENTRY_SWIGLU = 4   /* imq_qmm_swiglu (n = 2 * width: the gate and up rows it reads) */
 } imq_entry;
 
 typedef enum imq_kernel {
@@ -229,7 +229,10 @@ int imq_qmm_gate_add(imq_ctx* ctx, const uint32_t* w, const void* scales, const 
                      int n, int m, float scale, int group_size, int bits, imq_dtype dtype,
                      imq_stream stream);
 
-/* SwiGLU over the gate and up sections of one projection W [n, K/8]:
+/* SwiGLU over the gate and up sections of one projection W [n, K/8]
+ * (M <= 4: the qGEMV, the gate and up rows of an output read by one lane
+ * group and combined after the reduction, one launch over both sections;
+ * larger M: the MFMA kernel with the stage in its epilogue):
  * y[i][j] (T, row pitch ldy elements) = T(g * sigmoid(g) * u * out_scale) for
  * j < width, g = float(T(x_i . deq(W)[gate_row + j])) * in_scale, u the same
  * with up_row: dd_swiglu_pitched (DirectDiTKernels.swift:137-157) fused into

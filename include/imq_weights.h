@@ -114,6 +114,15 @@ typedef struct imq_qweight {
  * other conversion (f32 -> f16 or bf16, f16 -> bf16) is IMQ_EUNSUPPORTED. */
 int imq_load_qlinear(imq_ctx* ctx, const imq_st* st, const char* prefix, imq_dtype param_dtype,
                      imq_qweight* out, imq_stream stream);
+
+/* Several projections that share K (and the stored scale type) as one
+ * resident projection whose rows are theirs in the given order: N = the sum
+ * of their N.  One call then covers projections the reference dispatches one
+ * by one on the same input -- q/k/v, gate/up (DirectTEEncoder.swift:384-410,
+ * DirectTEForward.swift:98-106) -- and streams all their weights in one
+ * launch.  Same conversions and errors as imq_load_qlinear. */
+int imq_load_qlinear_cat(imq_ctx* ctx, const imq_st* st, const char* const* prefixes, int count,
+                         imq_dtype param_dtype, imq_qweight* out, imq_stream stream);
 int imq_qweight_free(imq_ctx* ctx, imq_qweight* q);
 
 #ifdef __cplusplus

@@ -263,7 +263,7 @@ def test_swiglu_register_kernel_k192_pitched(dtype):
     m, n, k, width, gate_row, up_row = 130, 600, 192, 200, 17, 300
     note(f"qmm_swiglu (register-staged) {dtype} M={m} width={width} K={k}")
     tdt = torch.float16 if dtype == "f16" else torch.bfloat16
-    assert imq.qmm_plan(m, 2 * width, k, tdt, entry="fused")["kernel"] == "tile_reg"
+    assert imq.qmm_plan(m, 2 * width, k, tdt, entry="swiglu")["kernel"] == "tile_reg"
     p, x, w, s, b = problem(m, n, k, dtype, seed=56)
     buf = torch.full((m, width + 20), 5.0, dtype=tdt, device="cuda")
     imq.qmm_swiglu(x, w, s, b, width, gate_row, up_row, in_scale=16.0, out_scale=1.0 / 16,

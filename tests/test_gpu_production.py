@@ -110,7 +110,7 @@ def test_swiglu_at_production_tile_heights(dtype, case):
     m, n, k, width, gate_row, up_row, tile_rows = case
     note(f"qmm_swiglu {dtype} M={m} N={n} K={k} width={width} gate_row={gate_row} "
          f"up_row={up_row} seed=80")
-    plan = imq.qmm_plan(m, 2 * width, k, TDT[dtype], entry="fused")
+    plan = imq.qmm_plan(m, 2 * width, k, TDT[dtype], entry="swiglu")
     note(f"  plan {plan}")
     assert plan["kernel"] == "tile" and plan["tile_rows"] == tile_rows and plan["splits"] == 1
     # x / 16 with the reference's in/out scales 16 and 1/16 (the f16 protocol
@@ -323,3 +323,28 @@ def test_full_size_denoise_step_sampled_rows(dtype):
     note(f"  {len(img_rows)} image rows: update normwise={normwise:.3g}")
     assert np.all(np.isfinite(eager[dt]))
     assert normwise <= NORMWISE_TOL, normwise
+
+
+# ---------------------------------------- text-encoder MLP-in at decode sizes
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_swiglu_few_rows_on_the_qgemv(dtype, m):
+    """The text encoder's gate and up projections ([9728 x 2560] each, rows
+    concatenated) with dq_silu_mul (DirectGlueKernels.swift:77-88) as one
+    qmm_swiglu call at decode sizes: the qGEMV's pair mode (one launch streams
+    both sections, the gate and up rows of an output read by one lane group).
+    Against the oracle on every row."""
+    inter, k = 9728, 2560
+    note(f"qmm_swiglu (qGEMV pair) {dtype} M={m} width={inter} K={k} seed=86")
+    plan = imq.qmm_plan(m, 2 * inter, k, TDT[dtype], entry="swiglu")
+    assert plan["kernel"] == "qgemv", plan
+    w_h, x, w, s, b = problem(m, 2 * inter, k, dtype, seed=86)
+    y = imq.qmm_swiglu(x, w, s, b, inter, 0, inter)
+    got = t_values(host_bits(y), dtype)
+    xb, sb, bb = host_bits(x), host_bits(s), host_bits(b)
+    g = oracle_qmm(xb, w_h[:inter], sb[:inter], bb[:inter], dtype)
+    u = oracle_qmm(xb, w_h[inter:], sb[inter:], bb[inter:], dtype)
+    want = t_values(round_t(ref.glue_swiglu(g, u, 1.0, 1.0), dtype), dtype)
+    assert_close(got, want, f"swiglu qGEMV pair M={m}")

@@ -196,3 +196,51 @@ def test_dit_key_map_over_two_shards(tmp_path):
                               .float().numpy().astype(np.float16))
         with pytest.raises(WeightsError, match="expected N=3072"):
             weights.load_dit_blocks(st, n_double=1, n_single=0)  # full-size map on a small pack
+
+
+def test_concatenated_projections_c_abi_and_python(tmp_path):
+    """imq_load_qlinear_cat / load_qlinear_cat: q, k, v (K shared, N 96 + 32 +
+    32) as one projection whose rows are theirs in order, scales converted to
+    f16; byte-equal to the parts loaded one by one.  A K mismatch is refused."""
+    note("loader: concatenated projections (C and Python)")
+    k = 512
+    parts = {"q": packed(96, k, seed=51), "k": packed(32, k, seed=52), "v": packed(32, k, seed=53),
+             "odd": packed(32, 256, seed=54)}
+    save_file({f"l.{p}.{key}": v for p, t in parts.items() for key, v in t.items()},
+              str(tmp_path / "0.safetensors"))
+    L = _lib.load()
+    ctx = ops.context()
+    with SafetensorsSet.open_dir(tmp_path) as st:
+        names = (ctypes.c_char_p * 3)(b"l.q", b"l.k", b"l.v")
+        q = _lib.QWeight()
+        _lib.check(L.imq_load_qlinear_cat(ctx, st.handle, names, 3, _lib.IMQ_F16,
+                                          ctypes.byref(q), None), ctx)
+        assert (q.n, q.k, q.dtype) == (160, k, _lib.IMQ_F16)
+        _lib.check(L.imq_stream_sync(ctx, None), ctx)
+        w = np.empty((160, k // 8), np.uint32)
+        s = np.empty((160, k // 64), np.float16)
+        b = np.empty((160, k // 64), np.float16)
+        for dst, src in ((w, q.w), (s, q.scales), (b, q.biases)):
+            _lib.check(L.imq_memcpy_d2h(ctx, dst.ctypes.data_as(ctypes.c_void_p),
+                                        ctypes.c_void_p(src), dst.nbytes, None), ctx)
+        want_w = np.concatenate([parts[p]["weight"].view(torch.int32).numpy().view(np.uint32)
+                                 for p in ("q", "k", "v")])
+        want_s = np.concatenate([parts[p]["scales"].float().numpy().astype(np.float16)
+                                 for p in ("q", "k", "v")])
+        want_b = np.concatenate([parts[p]["biases"].float().numpy().astype(np.float16)
+                                 for p in ("q", "k", "v")])
+        assert np.array_equal(w, want_w) and np.array_equal(s, want_s) and np.array_equal(b, want_b)
+        _lib.check(L.imq_qweight_free(ctx, ctypes.byref(q)), ctx)
+        bad_names = (ctypes.c_char_p * 2)(b"l.q", b"l.odd")
+        bad = _lib.QWeight()
+        assert L.imq_load_qlinear_cat(ctx, st.handle, bad_names, 2, _lib.IMQ_F16,
+                                      ctypes.byref(bad), None) == _lib.IMQ_EINVAL
+        assert b"K=" in L.imq_last_error(ctx)
+        cat = weights.load_qlinear_cat(st, ["l.q", "l.k", "l.v"], torch.float16)
+        torch.cuda.synchronize()
+        assert cat.n == 160 and cat.k == k
+        assert np.array_equal(cat.w.cpu().numpy().view(np.uint32), want_w)
+        assert np.array_equal(cat.s.cpu().numpy(), want_s)
+        assert np.array_equal(cat.b.cpu().numpy(), want_b)
+        with pytest.raises(weights.WeightsError, match="disagree on K"):
+            weights.load_qlinear_cat(st, ["l.q", "l.odd"])
