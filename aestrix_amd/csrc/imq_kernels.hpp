@@ -114,11 +114,11 @@ constexpr int kDispatchGemvMaxM = 4;
 constexpr int kQskinnyMaxM = 16;
 // The M range the regime dispatcher routes to it (bf16 / f16, K % 128 == 0),
 // ahead of the qGEMV.  With the weights coming from HBM (text-encoder MLP
-// shapes, 48 rotated copies), [9728 x 2560]: M = 4 7.8 us against 9.2 us for
-// the qGEMV, M = 8 8.5 us against 13.6 us for the split-K tile kernel, M = 16
-// 14.2 / 14.2 us; [2560 x 9728]: M = 4 11.9 / 13.0 us (qGEMV), M = 5 12.0 /
-// 18.3 us.  At M <= 2 the qGEMV stays faster (M = 1: 5.9 vs 7.6 us).
-constexpr int kDispatchSkinnyMinM = 4;
+// shapes, 48 rotated copies), [9728 x 2560] M = 1 / 2 / 3 / 4: 7.7 / 7.7 /
+// 7.7 / 7.9 us against 5.8 / 6.9 / 8.5 / 8.9 us for the qGEMV; [2560 x 9728]:
+// 11.2 / 11.1 / 11.2 / 11.6 against 6.2 / 8.5 / 12.1 / 13.1 us.  From M = 3
+// this kernel is faster on both.
+constexpr int kDispatchSkinnyMinM = 3;
 constexpr int kDispatchSkinnyMaxM = 16;
 
 // Bytes of the statically allocated split-K scratch of the allocation-free

@@ -118,12 +118,15 @@ __global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restr
                            : u32x4_t{0u, 0u, 0u, 0u};
       }
     }
+    // No branch per chunk (the compiler would sink each chunk's loads into its
+    // branch, behind the products of the chunks before it): a chunk past the
+    // end gets scale and bias 0, so its weights are +0 and add nothing.
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (ch0 + u * W >= chunks) break;  // uniform across the wave
-      const float s = Elem<T>::param(sv[u]);
+      const bool valid = ch0 + u * W < chunks;  // uniform across the wave
+      const float s = valid ? Elem<T>::param(sv[u]) : 0.0f;
       const float s24 = s * 0x1p24f, s20 = s * 0x1p20f;
-      const float b = Elem<T>::param(bv[u]);
+      const float b = valid ? Elem<T>::param(bv[u]) : 0.0f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         uint32_t p[4];
@@ -131,7 +134,7 @@ __global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restr
         u32x4_t xj;
         if constexpr (XLDS) {
           // B fragment read from the staged tile right before its MFMA.
-          const uint32_t ch = (uint32_t)(ch0 + u * W);
+          const uint32_t ch = (uint32_t)min(ch0 + u * W, chunks - 1);
           xj = has_x ? *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(xs) +
                                                           x_off + ch * 256u + j * 16u)
                      : u32x4_t{0u, 0u, 0u, 0u};

@@ -112,7 +112,7 @@ int imq_dequantize(imq_ctx* ctx, const uint32_t* w, const void* scales, const vo
  * DirectDiTStep.qmm (DirectDiTStep.swift:374-406), DirectTELayerSpike.encodeQmm
  * (DirectTELayer.swift:109-128), DirectConditioner.qmm
  * (DirectConditioner.swift:96-117) and MLX quantizedMM(transpose: true)
- * (Sources/ImarelloDiT/AttentionUtils.swift:212-221).  4 <= M <= 16 with
+ * (Sources/ImarelloDiT/AttentionUtils.swift:212-221).  3 <= M <= 16 with
  * K % 128 == 0 runs a weight-streaming matrix-core kernel (16 weight rows per
  * workgroup, K over its waves, no workspace); other M <= 4 the qGEMV kernel;
  * larger M the MFMA qGEMM kernel (f32: the qGEMV kernel, 16 rows at a time).  When the

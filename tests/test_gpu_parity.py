@@ -191,16 +191,19 @@ def test_one_hot_rows_reproduce_dequant_bit_exact(fn_name, m, k):
 
 
 def test_dispatcher_routes_by_m():
-    """M <= 3 is the qGEMV kernel bit for bit; above, the matrix-core kernels
-    (4 <= M <= 16 the weight-streaming one, then the tiled one, whose K may be
-    split by the dispatcher: other fp32 summation orders)."""
+    """M <= 2 is the qGEMV kernel bit for bit; above, the matrix-core kernels
+    (3 <= M <= 16 the weight-streaming one, then the tiled one, whose K may be
+    split by the dispatcher: other fp32 summation orders).  imq_qmm_plan names
+    the same kernels."""
     p = synth.make_problem(17, 384, 512, seed=16)
     x, w, s, b = synth.to_device(p)
-    for m in (1, 3):
+    for m in (1, 2):
         note(f"dispatcher M={m}")
+        assert imq.qmm_plan(m, 384, 512)["kernel"] == "qgemv"
         assert np.array_equal(bits(imq.quantized_matmul(x[:m], w, s, b)),
                               bits(imq.qgemv(x[:m], w, s, b)))
-    for m in (4, 5, 16, 17):
+    for m in (3, 4, 5, 16, 17):
+        assert imq.qmm_plan(m, 384, 512)["kernel"] == ("few_row" if m <= 16 else "tile")
         note(f"dispatcher M={m}")
         y = bits(imq.quantized_matmul(x[:m], w, s, b))
         assert_close(y, cref.qmm_t(p.x[:m], p.w, p.scales, p.biases), f"dispatcher M={m}")
