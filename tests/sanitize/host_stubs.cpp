@@ -1,0 +1,79 @@
+// host_stubs.cpp -- the device-side entry points of libimq for a host-only
+// build of its C++ (capi.cpp, weights.cpp, step.cpp) under AddressSanitizer
+// and UndefinedBehaviorSanitizer on a machine without a GPU.
+//
+// TEST INFRASTRUCTURE ONLY.  The kernels live in .hip translation units that
+// only hipcc compiles; here every launcher reports hipErrorNoDevice and the
+// planners answer as the real ones do for arguments that never reach a
+// launch.  What the sanitized build exercises is the host code: the
+// safetensors/JSON parser and the argument checks of every C entry point.
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "imq_kernels.hpp"
+
+namespace imq {
+
+hipError_t launch_dequant(const uint32_t*, const void*, const void*, void*, int, int, int,
+                          hipStream_t) {
+  return hipErrorNoDevice;
+}
+hipError_t launch_qgemv(const uint32_t*, const void*, const void*, const void*, void*, int, int,
+                        int, int, hipStream_t) {
+  return hipErrorNoDevice;
+}
+hipError_t launch_qgemv_swiglu(const uint32_t*, const void*, const void*, const void*, void*, int,
+                               int, int, int, int, int, int, float, float, int, hipStream_t) {
+  return hipErrorNoDevice;
+}
+hipError_t launch_qgemm(const uint32_t*, const void*, const void*, const void*, void*, int, int,
+                        int, int, hipStream_t, SplitWs) {
+  return hipErrorNoDevice;
+}
+size_t qgemm_split_bytes(int, int, int, bool) { return 0; }
+QgemmPlan qgemm_plan(int k, int n, int m, bool, bool, int) {
+  return QgemmPlan{qgemm_big_supported(k, n, m), 128, 1, 0};
+}
+bool qgemm_big_supported(int k, int n, int m) {
+  return (size_t)m * k * 2 < ((size_t)1 << 31) && (size_t)n * k / 2 < ((size_t)1 << 31) &&
+         k % 256 == 0;
+}
+hipError_t launch_qgemm_postscale(const uint32_t*, const void*, const void*, const void*, float*,
+                                  int, int, int, float, int, hipStream_t, SplitWs) {
+  return hipErrorNoDevice;
+}
+hipError_t launch_qgemm_gate_add(const uint32_t*, const void*, const void*, const void*,
+                                 const float*, const float*, float*, int, int, int, float, int,
+                                 hipStream_t, SplitWs, const float*) {
+  return hipErrorNoDevice;
+}
+hipError_t launch_qgemm_swiglu(const uint32_t*, const void*, const void*, const void*, void*, int,
+                               int, int, int, int, int, int, float, float, int, hipStream_t,
+                               SplitWs) {
+  return hipErrorNoDevice;
+}
+hipError_t launch_prescale(const float*, void*, size_t, float, int, hipStream_t) {
+  return hipErrorNoDevice;
+}
+hipError_t launch_rmsnorm(const float*, const float*, void*, int, int, float, int, hipStream_t,
+                          float) {
+  return hipErrorNoDevice;
+}
+hipError_t launch_fill_f32(float*, float, int, hipStream_t) { return hipErrorNoDevice; }
+hipError_t static_scratch(int, void** out) {
+  *out = nullptr;
+  return hipErrorNoDevice;
+}
+bool qskinny_supported(int k, int n, int m, int dtype) {
+  return m >= 1 && m <= kQskinnyMaxM && n >= 1 && k >= 128 && k % 128 == 0 &&
+         (dtype == 0 || dtype == 1) && (size_t)n * k / 2 < ((size_t)1 << 32) &&
+         (size_t)m * k * 2 < ((size_t)1 << 31);
+}
+hipError_t launch_qskinny(const uint32_t*, const void*, const void*, const void*, void*, int, int,
+                          int, int, hipStream_t) {
+  return hipErrorNoDevice;
+}
+
+}  // namespace imq
