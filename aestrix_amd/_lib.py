@@ -87,6 +87,10 @@ SIGNATURES = {
     "imq_qgemm": (_QMM, _i),
     "imq_cast_prescale": ([_p, _p, _p, _sz, ctypes.c_float, _i, _p], _i),
     "imq_qmm_postscale": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, ctypes.c_float, _i, _i, _i, _p], _i),
+    "imq_dynamic_scale": ([_p, _p, _sz, ctypes.c_float, _p, _p], _i),
+    "imq_cast_prescale_ex": ([_p, _p, _p, _sz, ctypes.c_float, _p, _i, _p], _i),
+    "imq_qmm_postscale_ex": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, ctypes.c_float, _p, _i, _i,
+                              _i, _p], _i),
     "imq_qmm_gate_add": ([_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, ctypes.c_float, _i, _i, _i,
                           _p], _i),
     "imq_qmm_swiglu": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float,

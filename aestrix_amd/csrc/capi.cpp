@@ -515,6 +515,64 @@ int imq_cast_prescale(imq_ctx* ctx, const float* x, void* y, size_t count, float
   return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
 }
 
+int imq_dynamic_scale(imq_ctx* ctx, const float* x, size_t count, float target, float* scale,
+                      imq_stream stream) {
+  const char* fn = "imq_dynamic_scale";
+  if (!ctx) return fail(nullptr, IMQ_EINVAL, "%s: null context", fn);
+  if (!scale || (count > 0 && !x)) return fail(ctx, IMQ_EINVAL, "%s: null device pointer", fn);
+  if (!std::isfinite(target) || target <= 0.0f)
+    return fail(ctx, IMQ_EINVAL, "%s: target %g must be finite and positive", fn, (double)target);
+  if (!aligned(x, 4) || !aligned(scale, 4))
+    return fail(ctx, IMQ_EINVAL, "%s: x and scale must be 4-byte aligned", fn);
+  int rc = bind_device(ctx);
+  if (rc != IMQ_OK) return rc;
+  const hipError_t e =
+      imq::launch_dynamic_scale(x, count, target, scale, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
+}
+
+int imq_cast_prescale_ex(imq_ctx* ctx, const float* x, void* y, size_t count, float scale,
+                         const float* scale_dev, imq_dtype dtype, imq_stream stream) {
+  const char* fn = "imq_cast_prescale_ex";
+  if (!ctx) return fail(nullptr, IMQ_EINVAL, "%s: null context", fn);
+  if (dtype != IMQ_BF16 && dtype != IMQ_F16)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: dtype %d (bf16 and f16 are provided)", fn, (int)dtype);
+  if (!scale_dev && (!std::isfinite(scale) || scale == 0.0f))
+    return fail(ctx, IMQ_EINVAL, "%s: scale %g must be finite and nonzero", fn, (double)scale);
+  if (count == 0) return IMQ_OK;
+  if (!x || !y) return fail(ctx, IMQ_EINVAL, "%s: null device pointer", fn);
+  if (!aligned(x, 4) || !aligned(y, 2) || !aligned(scale_dev, 4))
+    return fail(ctx, IMQ_EINVAL, "%s: x and scale_dev must be 4-byte and y 2-byte aligned", fn);
+  int rc = bind_device(ctx);
+  if (rc != IMQ_OK) return rc;
+  const hipError_t e = imq::launch_prescale(x, y, count, scale, (int)dtype,
+                                            static_cast<hipStream_t>(stream), scale_dev);
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
+}
+
+int imq_qmm_postscale_ex(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                         const void* x, void* y, imq_dtype y_dtype, int k, int n, int m,
+                         float scale, const float* scale_dev, int group_size, int bits,
+                         imq_dtype dtype, imq_stream stream) {
+  const char* fn = "imq_qmm_postscale_ex";
+  int rc = check_epilogue(ctx, fn, w, scales, biases, x, y, k, n, m, group_size, bits, dtype);
+  if (rc != IMQ_OK) return rc;
+  if (y_dtype != IMQ_F32 && y_dtype != IMQ_F16)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: y dtype %d (f32 or f16)", fn, (int)y_dtype);
+  if (y_dtype == IMQ_F16 && dtype != IMQ_F16)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: an f16 result needs the f16 qmm (dtype f16)", fn);
+  if (!aligned(y, y_dtype == IMQ_F32 ? 4 : 2) || !aligned(scale_dev, 4))
+    return fail(ctx, IMQ_EINVAL, "%s: y or scale_dev misaligned", fn);
+  const auto st = static_cast<hipStream_t>(stream);
+  const hipError_t e =
+      y_dtype == IMQ_F32
+          ? imq::launch_qgemm_postscale(w, scales, biases, x, static_cast<float*>(y), k, n, m,
+                                        scale, (int)dtype, st, imq::SplitWs{}, scale_dev)
+          : imq::launch_qgemm_postscale_f16(w, scales, biases, x, y, k, n, m, scale, st,
+                                            scale_dev);
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
+}
+
 int imq_qmm_postscale(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
                       const void* x, float* y, int k, int n, int m, float scale, int group_size,
                       int bits, imq_dtype dtype, imq_stream stream) {

@@ -55,6 +55,8 @@ __device__ __forceinline__ float staged_value(uint32_t bits) {
 
 // y[row][col] = float(T(acc)) * scale, fp32 out: dd_cast_postscale
 // (DirectDiTKernels.swift:199-209), the x16 that undoes the qmm input's /16.
+// With scale_dev set the scale is read from device memory when the kernel
+// runs (the per-tensor dynamic scale).
 template <int T>
 struct EpPostscale {
   static constexpr bool kPair = false;
@@ -63,11 +65,14 @@ struct EpPostscale {
   int ldy;
   float scale;
   bool vec;
+  const float* scale_dev;
   __device__ __forceinline__ float value(float acc) const { return acc; }
+  __device__ __forceinline__ float the_scale() const { return scale_dev ? *scale_dev : scale; }
   __device__ __forceinline__ void emit1(int row, int col, uint16_t v) const {
-    y[(size_t)row * ldy + col] = staged_value<T>(v) * scale;
+    y[(size_t)row * ldy + col] = staged_value<T>(v) * the_scale();
   }
   __device__ __forceinline__ void emit8(int row, int col, uint4 v) const {
+    const float scale = the_scale();
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     float o[8];
 #pragma unroll
@@ -78,6 +83,38 @@ struct EpPostscale {
     float4* d = reinterpret_cast<float4*>(y + (size_t)row * ldy + col);
     d[0] = make_float4(o[0], o[1], o[2], o[3]);
     d[1] = make_float4(o[4], o[5], o[6], o[7]);
+  }
+};
+
+// y[row][col] (f16) = f16(float(f16(acc)) * float(f16(scale))): the
+// post-scale without the f32 upcast (compiledPostScaleF16,
+// Sources/ImarelloDiT/AttentionUtils.swift:166-171, `y * s.asType(.float16)`).
+// The product of two f16 values is exact in f32, so rounding it once to f16
+// is the f16 multiply.  T = f16.
+struct EpPostscaleF16 {
+  static constexpr bool kPair = false;
+  static constexpr bool kPartial = false;
+  uint16_t* y;
+  int ldy;
+  float scale;
+  bool vec;
+  const float* scale_dev;
+  __device__ __forceinline__ float value(float acc) const { return acc; }
+  __device__ __forceinline__ float s16() const {
+    return (float)(_Float16)(scale_dev ? *scale_dev : scale);
+  }
+  __device__ __forceinline__ void emit1(int row, int col, uint16_t v) const {
+    y[(size_t)row * ldy + col] =
+        __builtin_bit_cast(uint16_t, (_Float16)(staged_value<kF16>(v) * s16()));
+  }
+  __device__ __forceinline__ void emit8(int row, int col, uint4 v) const {
+    const float s = s16();
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = pack_f16x2(staged_value<kF16>(w[e] & 0xFFFFu) * s, staged_value<kF16>(w[e] >> 16) * s);
+    *reinterpret_cast<uint4*>(y + (size_t)row * ldy + col) = make_uint4(o[0], o[1], o[2], o[3]);
   }
 };
 

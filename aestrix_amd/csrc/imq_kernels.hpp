@@ -79,7 +79,14 @@ bool qgemm_big_supported(int k, int n, int m);
 //              g = float(T(x . W[gate_row + j])) * in_scale, u likewise with up_row.
 hipError_t launch_qgemm_postscale(const uint32_t* w, const void* scales, const void* biases,
                                   const void* x, float* y, int k, int n, int m, float scale,
-                                  int dtype, hipStream_t stream, SplitWs ws = {});
+                                  int dtype, hipStream_t stream, SplitWs ws = {},
+                                  const float* scale_dev = nullptr);
+// postscale with an f16 result (T = f16 only): y[m][n] (f16) =
+// f16(float(f16(acc)) * float(f16(scale))), the product of two f16 values
+// rounded once (the reference's y * s.asType(.float16)).
+hipError_t launch_qgemm_postscale_f16(const uint32_t* w, const void* scales, const void* biases,
+                                      const void* x, void* y, int k, int n, int m, float scale,
+                                      hipStream_t stream, const float* scale_dev = nullptr);
 hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const void* biases,
                                  const void* x, const float* residual, const float* gate, float* y,
                                  int k, int n, int m, float scale, int dtype, hipStream_t stream,
@@ -89,9 +96,16 @@ hipError_t launch_qgemm_swiglu(const uint32_t* w, const void* scales, const void
                                int gate_row, int up_row, float in_scale, float out_scale, int dtype,
                                hipStream_t stream, SplitWs ws = {});
 
-// y[i] (T) = T(x[i] / scale) for i < count, x fp32; T in {bf16, f16}.
+// y[i] (T) = T(x[i] / scale) for i < count, x fp32; T in {bf16, f16}; with
+// scale_dev the scale is read from device memory when the kernel runs.
 hipError_t launch_prescale(const float* x, void* y, size_t count, float scale, int dtype,
-                           hipStream_t stream);
+                           hipStream_t stream, const float* scale_dev = nullptr);
+
+// *out (device) = max(max_i |x[i]| / target, 1): the per-tensor dynamic scale
+// of the f16 qmm sandwich (three small launches; order independent, so the
+// result is deterministic).
+hipError_t launch_dynamic_scale(const float* x, size_t count, float target, float* out,
+                                hipStream_t stream);
 
 // y[r][c] (T) = x[r][c] * rsqrt(mean(x[r]^2) + eps) * w[c] * out_scale, x fp32
 // [rows, cols]; out_scale a power of two.

@@ -999,20 +999,32 @@ QgemmPlan qgemm_plan(int k, int n, int m, bool fused, bool split, int cus) {
 
 hipError_t launch_qgemm_postscale(const uint32_t* w, const void* scales, const void* biases,
                                   const void* x, float* y, int k, int n, int m, float scale,
-                                  int dtype, hipStream_t stream, SplitWs ws) {
+                                  int dtype, hipStream_t stream, SplitWs ws,
+                                  const float* scale_dev) {
   const auto* s = static_cast<const uint16_t*>(scales);
   const auto* b = static_cast<const uint16_t*>(biases);
   const auto* xx = static_cast<const uint16_t*>(x);
   const bool vec = al16(y) && n % 4 == 0;
   switch (dtype) {
     case kBf16:
-      return launch_big_ep<kBf16>(w, s, b, xx, EpPostscale<kBf16>{y, n, scale, vec}, k, n, m, stream,
-                                  ws);
+      return launch_big_ep<kBf16>(w, s, b, xx, EpPostscale<kBf16>{y, n, scale, vec, scale_dev}, k,
+                                  n, m, stream, ws);
     case kF16:
-      return launch_big_ep<kF16>(w, s, b, xx, EpPostscale<kF16>{y, n, scale, vec}, k, n, m, stream,
-                                 ws);
+      return launch_big_ep<kF16>(w, s, b, xx, EpPostscale<kF16>{y, n, scale, vec, scale_dev}, k,
+                                 n, m, stream, ws);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_qgemm_postscale_f16(const uint32_t* w, const void* scales, const void* biases,
+                                      const void* x, void* y, int k, int n, int m, float scale,
+                                      hipStream_t stream, const float* scale_dev) {
+  auto* yy = static_cast<uint16_t*>(y);
+  const bool vec = al16(y) && n % 8 == 0;
+  return launch_big_ep<kF16>(w, static_cast<const uint16_t*>(scales),
+                             static_cast<const uint16_t*>(biases), static_cast<const uint16_t*>(x),
+                             EpPostscaleF16{yy, n, scale, vec, scale_dev}, k, n, m, stream,
+                             SplitWs{});
 }
 
 hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const void* biases,

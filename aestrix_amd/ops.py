@@ -199,9 +199,12 @@ def _f32_out(out, shape, device, what):
 
 
 def cast_prescale(x: torch.Tensor, scale: float = 16.0, dtype: torch.dtype = torch.float16,
-                  out: torch.Tensor | None = None) -> torch.Tensor:
+                  out: torch.Tensor | None = None,
+                  scale_dev: torch.Tensor | None = None) -> torch.Tensor:
     """T y = T(x / scale) for float32 x (``AttentionUtils.compiledPreScale``,
-    ``Sources/ImarelloDiT/AttentionUtils.swift:155-160``): bit-exact, one HIP kernel."""
+    ``Sources/ImarelloDiT/AttentionUtils.swift:155-160``): bit-exact, one HIP kernel.
+    ``scale_dev`` (a one-element float32 device tensor, e.g. ``dynamic_scale``'s)
+    replaces ``scale`` and is read when the kernel runs."""
     _require(x.is_cuda and x.dtype == torch.float32, "x must be a float32 HIP tensor")
     _require(dtype in (torch.float16, torch.bfloat16), f"dtype {dtype}: float16 or bfloat16")
     x = x if x.is_contiguous() else x.contiguous()
@@ -209,26 +212,63 @@ def cast_prescale(x: torch.Tensor, scale: float = 16.0, dtype: torch.dtype = tor
         out = torch.empty(x.shape, dtype=dtype, device=x.device)
     _require(out.dtype == dtype and out.is_contiguous() and out.shape == x.shape
              and out.device == x.device, f"out must be a contiguous {dtype} tensor shaped like x")
+    sd = _scale_dev(scale_dev, x.device)
     ctx = context(x.device)
     with torch.cuda.device(x.device):
-        st = _lib.load().imq_cast_prescale(ctx, _ptr(x), _ptr(out), x.numel(), float(scale),
-                                           _DTYPES[dtype], _stream(x))
+        st = _lib.load().imq_cast_prescale_ex(ctx, _ptr(x), _ptr(out), x.numel(), float(scale), sd,
+                                              _DTYPES[dtype], _stream(x))
+    _lib.check(st, ctx)
+    return out
+
+
+def _scale_dev(t: torch.Tensor | None, device) -> ctypes.c_void_p:
+    if t is None:
+        return ctypes.c_void_p(0)
+    _require(t.is_cuda and t.device == device and t.dtype == torch.float32 and t.numel() == 1,
+             "scale_dev must be a one-element float32 tensor on x's device")
+    return _ptr(t)
+
+
+def dynamic_scale(x: torch.Tensor, target: float = 64.0,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """One-element float32 device tensor max(amax|x| / target, 1): the per-tensor
+    dynamic scale of ``applyLinearCore`` (``AttentionUtils.swift:173-178,208-210``,
+    ``linearDynamicScaleTarget`` 64), computed on the device without a host sync."""
+    _require(x.is_cuda and x.dtype == torch.float32, "x must be a float32 HIP tensor")
+    x = x if x.is_contiguous() else x.contiguous()
+    if out is None:
+        out = torch.empty(1, dtype=torch.float32, device=x.device)
+    _scale_dev(out, x.device)
+    ctx = context(x.device)
+    with torch.cuda.device(x.device):
+        st = _lib.load().imq_dynamic_scale(ctx, _ptr(x), x.numel(), float(target), _ptr(out),
+                                           _stream(x))
     _lib.check(st, ctx)
     return out
 
 
 def qmm_postscale(x, w, scales, biases, scale: float, group_size: int = GROUP_SIZE,
-                  bits: int = BITS, out=None) -> torch.Tensor:
-    """float32 y = float(T(x . deq(W)^T)) * scale in one kernel (the reference's
-    qmm + dd_cast_postscale, ``DirectDiTKernels.swift:199-209``)."""
+                  bits: int = BITS, out=None, out_dtype: torch.dtype = torch.float32,
+                  scale_dev: torch.Tensor | None = None) -> torch.Tensor:
+    """y = float(T(x . deq(W)^T)) * scale in one kernel (the reference's qmm +
+    dd_cast_postscale, ``DirectDiTKernels.swift:199-209``).  ``out_dtype`` float16
+    keeps the result in f16 without the f32 upcast (``compiledPostScaleF16``,
+    ``AttentionUtils.swift:166-171``: f16(y * f16(scale)), the f16 qmm only);
+    ``scale_dev`` replaces ``scale`` (read when the kernel runs)."""
     n, k, m, lead, x = _epi_args(x, w, scales, biases, group_size, bits)
-    out = _f32_out(out, lead + (n,), x.device, "out")
+    _require(out_dtype in (torch.float32, torch.float16), "out_dtype: float32 or float16")
+    if out is None:
+        out = torch.empty(lead + (n,), dtype=out_dtype, device=x.device)
+    _require(out.dtype == out_dtype and out.is_contiguous() and tuple(out.shape) == lead + (n,),
+             f"out must be a contiguous {out_dtype} tensor of shape {lead + (n,)}")
+    sd = _scale_dev(scale_dev, x.device)
     dtype = _DTYPES.get(x.dtype, -1)
     ctx = context(w.device)
     with torch.cuda.device(w.device):
-        st = _lib.load().imq_qmm_postscale(ctx, _ptr(w), _ptr(scales), _ptr(biases), _ptr(x),
-                                           _ptr(out), k, n, m, float(scale), group_size, bits,
-                                           dtype, _stream(x))
+        st = _lib.load().imq_qmm_postscale_ex(ctx, _ptr(w), _ptr(scales), _ptr(biases), _ptr(x),
+                                              _ptr(out), _DTYPES[out_dtype], k, n, m,
+                                              float(scale), sd, group_size, bits, dtype,
+                                              _stream(x))
     _lib.check(st, ctx)
     return out
 
@@ -354,19 +394,29 @@ class QuantizedLinear:
         return dequantize(self.weight, self.scales, self.biases, self.group_size, self.bits)
 
 
-def apply_linear(linear: QuantizedLinear, x: torch.Tensor, scale: float = 16.0) -> torch.Tensor:
-    """float32 y = linear(x) through the f16 sandwich of ``AttentionUtils.applyLinear`` /
+def apply_linear(linear: QuantizedLinear, x: torch.Tensor, scale: float = 16.0,
+                 output_f16: bool = False, dynamic_target: float | None = None) -> torch.Tensor:
+    """y = linear(x) through the f16 sandwich of ``AttentionUtils.applyLinear`` /
     ``applyLinearCore`` with ``linearF16`` on (``Sources/ImarelloDiT/AttentionUtils.swift:140-150,
-    198-230``): x / scale rounded to f16 (``cast_prescale``), then the f16 qmm and the float32
+    198-230``): x / scale rounded to f16 (``cast_prescale``), then the f16 qmm and the
     x scale rescale in one kernel (``qmm_postscale``).  x is float32 of any leading shape; the
     linear's scales and biases must be float16 (the DiT pack casts them at load,
     ``TransformerWeights.swift:40-54``, exact for that pack; ``load_qlinear(..., IMQ_F16)``
-    does the same).  The static scale (``AttentionTuning.linearF16Scale``, 16) is mirrored;
-    ``linearDynamicScale``'s per-tensor scale is not.  ``linearChunkedSequence``
-    (``:233-261``) runs this in 512-row chunks to bound MLX temporaries; rows are independent,
-    so one launch over all rows gives the same values."""
+    does the same).
+
+    * ``scale``: the static scale (``AttentionTuning.linearF16Scale``, 16);
+    * ``dynamic_target``: the per-tensor dynamic scale instead (``linearDynamicScale``:
+      max(amax|x| / target, 1), ``linearDynamicScaleTarget`` 64), computed on the device;
+    * ``output_f16``: an f16 result without the f32 upcast (``outputF16`` /
+      ``linearF16FullEpilogue``, ``compiledPostScaleF16``), else float32.
+
+    ``linearChunkedSequence`` (``:233-261``) runs this in 512-row chunks to bound MLX
+    temporaries; rows are independent, so one launch over all rows gives the same values
+    (with the dynamic scale, the reference's chunks would each take their own amax)."""
     _require(linear.scales.dtype == torch.float16,
              f"the f16 path needs float16 scales and biases, got {linear.scales.dtype}")
-    x16 = cast_prescale(x, scale, torch.float16)
+    sd = dynamic_scale(x, dynamic_target) if dynamic_target is not None else None
+    x16 = cast_prescale(x, scale, torch.float16, scale_dev=sd)
     return qmm_postscale(x16, linear.weight, linear.scales, linear.biases, scale,
-                         linear.group_size, linear.bits)
+                         linear.group_size, linear.bits,
+                         out_dtype=torch.float16 if output_f16 else torch.float32, scale_dev=sd)

@@ -221,6 +221,27 @@ int imq_qmm_postscale(imq_ctx* ctx, const uint32_t* w, const void* scales, const
                       const void* x, float* y, int k, int n, int m, float scale, int group_size,
                       int bits, imq_dtype dtype, imq_stream stream);
 
+/* The other modes of applyLinearCore's f16 sandwich (AttentionUtils.swift:
+ * 173-178,198-230, AttentionTuning.swift:55-61):
+ *  - the per-tensor dynamic scale (linearDynamicScale): *scale (device fp32)
+ *    = max(max_i |x[i]| / target, 1) over count fp32 elements (compiledDynamicScale;
+ *    target 64 by default there), computed on the device, no host sync; a NaN
+ *    in x gives a NaN scale;
+ *  - the pre-scale cast and the post-scale reading that device scale
+ *    (scale_dev, which overrides scale when not NULL);
+ *  - the post-scale without the f32 upcast (linearF16FullEpilogue,
+ *    compiledPostScaleF16, :166-171): y (f16) = f16(float(f16(acc)) *
+ *    float(f16(scale))), only with the f16 qmm (dtype f16).
+ * imq_qmm_postscale_ex's y_dtype is IMQ_F32 (imq_qmm_postscale) or IMQ_F16. */
+int imq_dynamic_scale(imq_ctx* ctx, const float* x, size_t count, float target, float* scale,
+                      imq_stream stream);
+int imq_cast_prescale_ex(imq_ctx* ctx, const float* x, void* y, size_t count, float scale,
+                         const float* scale_dev, imq_dtype dtype, imq_stream stream);
+int imq_qmm_postscale_ex(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                         const void* x, void* y, imq_dtype y_dtype, int k, int n, int m,
+                         float scale, const float* scale_dev, int group_size, int bits,
+                         imq_dtype dtype, imq_stream stream);
+
 /* y[M, N] (fp32) = residual + gate[n] * float(T(x . deq(W)^T)) * scale: the
  * gated residual dd_gate_add (DirectDiTKernels.swift:211-224).  y may equal
  * residual (in place). */

@@ -175,6 +175,27 @@ def glue_postscale(y_t: np.ndarray, scale: float) -> np.ndarray:
     return (np.asarray(y_t, dtype=np.float32) * np.float32(scale)).astype(np.float32)
 
 
+def glue_postscale_f16(y_f16: np.ndarray, scale: float) -> np.ndarray:
+    """AttentionUtils.compiledPostScaleF16 (Sources/ImarelloDiT/AttentionUtils.swift:166-171):
+    ``y * s.asType(.float16)`` on the f16 qmm output -- the scale rounded to f16,
+    then the f16 product, correctly rounded once (the product of two f16 values
+    is exact in float32).  Returns float16 values."""
+    s16 = np.float32(np.float16(np.float32(scale)))
+    with np.errstate(over="ignore"):
+        return (np.asarray(y_f16, dtype=np.float16).astype(np.float32) * s16).astype(np.float16)
+
+
+def dynamic_scale(x: np.ndarray, target: float) -> np.float32:
+    """AttentionUtils.compiledDynamicScale (AttentionUtils.swift:173-178):
+    ``maximum(abs(x).max() / target, 1)`` in float32 -- the fp32 quotient
+    (correctly rounded), at least 1; a NaN anywhere in x gives NaN.  An empty x
+    has amax 0 and so scale 1."""
+    a = np.abs(np.asarray(x, dtype=np.float32)).ravel()
+    amax = np.float32(0.0) if a.size == 0 else np.float32(np.max(a))
+    q = np.float32(amax / np.float32(target))
+    return q if np.isnan(q) else np.float32(max(q, np.float32(1.0)))
+
+
 def glue_gate_add(y_t: np.ndarray, residual: np.ndarray, gate: np.ndarray,
                   scale: float) -> np.ndarray:
     """dd_gate_add (DirectDiTKernels.swift:211-224): fma(gate[j], float(v) * s, x)."""

@@ -41,7 +41,11 @@ bool qgemm_big_supported(int k, int n, int m) {
          k % 256 == 0;
 }
 hipError_t launch_qgemm_postscale(const uint32_t*, const void*, const void*, const void*, float*,
-                                  int, int, int, float, int, hipStream_t, SplitWs) {
+                                  int, int, int, float, int, hipStream_t, SplitWs, const float*) {
+  return hipErrorNoDevice;
+}
+hipError_t launch_qgemm_postscale_f16(const uint32_t*, const void*, const void*, const void*,
+                                      void*, int, int, int, float, hipStream_t, const float*) {
   return hipErrorNoDevice;
 }
 hipError_t launch_qgemm_gate_add(const uint32_t*, const void*, const void*, const void*,
@@ -54,7 +58,10 @@ hipError_t launch_qgemm_swiglu(const uint32_t*, const void*, const void*, const 
                                SplitWs) {
   return hipErrorNoDevice;
 }
-hipError_t launch_prescale(const float*, void*, size_t, float, int, hipStream_t) {
+hipError_t launch_prescale(const float*, void*, size_t, float, int, hipStream_t, const float*) {
+  return hipErrorNoDevice;
+}
+hipError_t launch_dynamic_scale(const float*, size_t, float, float*, hipStream_t) {
   return hipErrorNoDevice;
 }
 hipError_t launch_rmsnorm(const float*, const float*, void*, int, int, float, int, hipStream_t,

@@ -191,6 +191,134 @@ def test_apply_linear_f16_sandwich(m, n, k):
     assert_close(to_np(y).reshape(m, n), ref.glue_postscale(q, 16.0), "apply_linear")
 
 
+@pytest.mark.parametrize("count", [0, 1, 1000, 3_000_001])
+def test_dynamic_scale_bit_exact(count):
+    """dynamic_scale equals the oracle's max(amax|x| / target, 1) bit for bit: a
+    negative element holding the amax, amax below the target (scale 1), a NaN
+    (NaN), the empty tensor (1); the large case spans many workgroups."""
+    note(f"dynamic_scale count={count}")
+    rng = np.random.default_rng(count + 3)
+    x = (rng.standard_normal(count) * 40).astype(np.float32)
+    if count:
+        x[rng.integers(count)] = -713.25
+    cases = [(x, 64.0), (x, 3.0), (x * np.float32(1e-3), 64.0)]
+    if count:
+        xn = x.copy()
+        xn[count // 2] = np.nan
+        cases.append((xn, 64.0))
+    for xi, target in cases:
+        got = imq.dynamic_scale(torch.from_numpy(xi).cuda(), target).cpu().numpy()
+        want = ref.dynamic_scale(xi, target)
+        assert got.shape == (1,) and got.dtype == np.float32
+        if np.isnan(want):
+            assert np.isnan(got[0])
+        else:
+            assert got[0].view(np.uint32) == want.view(np.uint32), (target, got[0], want)
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 512, 768), (1, 64, 512), (4096, 256, 128)])
+@pytest.mark.parametrize("mode", ["f16_out", "dynamic", "dynamic_f16_out"])
+def test_apply_linear_s4_modes(mode, m, n, k):
+    """applyLinearCore's S4 modes (AttentionUtils.swift:166-178,198-230): the f16
+    result without the f32 upcast, the per-tensor dynamic scale, and both.  The
+    device scale equals the oracle's bit for bit, the prescaled input equals the
+    oracle's (x / s).asType(f16) bit for bit, the f16 result equals
+    f16(y16 * f16(s)) of the library's own f16 qmm bit for bit, apply_linear equals
+    the step-by-step composition bit for bit, and the whole sandwich matches the
+    oracle's within the tolerance."""
+    note(f"apply_linear {mode} M={m} N={n} K={k}")
+    p, x, w, s, b = problem(m, n, k, "f16", seed=61)
+    rng = np.random.default_rng(61)
+    xf_np = (rng.standard_normal((m, k)) * 90).astype(np.float32)
+    xf_np[0, 0] = -1500.0  # amax 1500: dynamic scale 23.4375
+    xf = torch.from_numpy(xf_np).cuda()
+    lin = imq.QuantizedLinear(w, s, b)
+    f16_out = mode.endswith("f16_out")
+    target = 64.0 if mode.startswith("dynamic") else None
+    y = imq.apply_linear(lin, xf, output_f16=f16_out, dynamic_target=target)
+    assert y.dtype == (torch.float16 if f16_out else torch.float32) and tuple(y.shape) == (m, n)
+    if target is None:
+        sc, sd = np.float32(16.0), None
+    else:
+        sd = imq.dynamic_scale(xf, target)
+        sc = ref.dynamic_scale(xf_np, target)
+        assert sd.cpu().numpy()[0] == sc == np.float32(1500.0 / 64)
+    x16 = imq.cast_prescale(xf, 16.0, scale_dev=sd)
+    x16_want = ref.glue_prescale(xf_np, float(sc), "f16")
+    assert np.array_equal(x16.cpu().numpy().view(np.uint16), x16_want.view(np.uint16))
+    composed = imq.qmm_postscale(x16, w, s, b, 16.0, scale_dev=sd,
+                                 out_dtype=torch.float16 if f16_out else torch.float32)
+    assert np.array_equal(to_np(y), to_np(composed))
+    y16 = imq.qgemm(x16, w, s, b).cpu().numpy()  # the library's own f16 qmm
+    if f16_out:
+        got = y.cpu().numpy()
+        assert np.array_equal(got.view(np.uint16), ref.glue_postscale_f16(y16, float(sc)).view(np.uint16))
+    else:
+        assert np.array_equal(to_np(y), ref.glue_postscale(y16.astype(np.float32), float(sc)))
+    q = ref.qmm_t_as(x16_want, p.w, s.cpu().numpy(), b.cpu().numpy(), np.float16)
+    want = ref.glue_postscale_f16(q, float(sc)) if f16_out else ref.glue_postscale(q.astype(np.float32), float(sc))
+    assert_close(to_np(y), want.astype(np.float32), f"apply_linear {mode}")
+
+
+def test_scale_dev_is_read_when_the_kernel_runs():
+    """A graph captured with a device scale replays with the value the tensor
+    holds at replay time, for the prescale and both post-scale results; a
+    captured dynamic_scale recomputes the amax of what x holds at each replay
+    (its accumulator cleared by a kernel, not a memset node)."""
+    m, n, k = 64, 256, 512
+    p, x, w, s, b = problem(m, n, k, "f16", seed=62)
+    xf = x.float() * 40
+    sd = torch.full((1,), 2.0, device="cuda")
+    x16 = torch.empty((m, k), dtype=torch.float16, device="cuda")
+    y32 = torch.empty((m, n), device="cuda")
+    y16 = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    xv = torch.zeros(5000, device="cuda")
+    sd2 = torch.empty(1, device="cuda")
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for _ in range(2):  # warm the launchers outside the capture
+            imq.dynamic_scale(xv, 64.0, out=sd2)
+            imq.cast_prescale(xf, 1.0, out=x16, scale_dev=sd)
+            imq.qmm_postscale(x16, w, s, b, 1.0, out=y32, scale_dev=sd)
+            imq.qmm_postscale(x16, w, s, b, 1.0, out=y16, out_dtype=torch.float16, scale_dev=sd)
+        stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            imq.dynamic_scale(xv, 64.0, out=sd2)
+            imq.cast_prescale(xf, 1.0, out=x16, scale_dev=sd)
+            imq.qmm_postscale(x16, w, s, b, 1.0, out=y32, scale_dev=sd)
+            imq.qmm_postscale(x16, w, s, b, 1.0, out=y16, out_dtype=torch.float16, scale_dev=sd)
+    rng = np.random.default_rng(62)
+    for i, val in enumerate((4.0, 23.4375, 2.0)):
+        xv_np = (rng.standard_normal(5000) * 10 ** i * 30).astype(np.float32)
+        xv.copy_(torch.from_numpy(xv_np))
+        sd.fill_(val)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert sd2.cpu().numpy()[0] == ref.dynamic_scale(xv_np, 64.0), i
+        e16 = imq.cast_prescale(xf, val)
+        assert torch.equal(x16, e16), val
+        assert torch.equal(y32, imq.qmm_postscale(e16, w, s, b, val)), val
+        assert torch.equal(y16, imq.qmm_postscale(e16, w, s, b, val, out_dtype=torch.float16)), val
+
+
+def test_s4_argument_checks():
+    p, x, w, s, b = problem(8, 128, 256, "f16", seed=63)
+    xf = x.float()
+    with pytest.raises(ValueError):
+        imq.dynamic_scale(x)  # float32 only
+    with pytest.raises(imq.ImqInvalid):
+        imq.dynamic_scale(xf, 0.0)
+    with pytest.raises(ValueError):
+        imq.cast_prescale(xf, scale_dev=torch.ones(2, device="cuda"))  # one element
+    with pytest.raises(ValueError):
+        imq.qmm_postscale(x, w, s, b, 1.0, out_dtype=torch.bfloat16)
+    pb, xb, wb, sb, bb = problem(8, 128, 256, "bf16", seed=63)
+    with pytest.raises(imq.ImqUnsupported):
+        imq.qmm_postscale(xb, wb, sb, bb, 1.0, out_dtype=torch.float16)  # f16 result, bf16 qmm
+
+
 def test_prescale_argument_checks():
     x = torch.ones(16, device="cuda")
     with pytest.raises(ValueError):

@@ -632,6 +632,50 @@ def test_glue_prescale_checks_catch_truncation_mutant():
     assert float(ref.bf16_to_f32(trunc_bf16)[1]) != float(bf16[1])
 
 
+def test_glue_postscale_f16_is_the_f16_product():
+    """f16(y * f16(s)): against torch's CPU half multiply (an independent
+    routine), exact scaling by a power of two, the scale's own f16 rounding
+    (1/3 rounds to 0x3555 before the product, checked with rational
+    arithmetic) and overflow to inf."""
+    rng = np.random.default_rng(21)
+    y = (rng.standard_normal(4000) * np.exp2(rng.integers(-20, 12, 4000))).astype(np.float16)
+    for scale in (16.0, 1.0 / 3.0, 4.6875, 1e-3, 300.0):
+        got = ref.glue_postscale_f16(y, scale)
+        assert got.dtype == np.float16
+        want = (torch.from_numpy(y) * torch.tensor(scale, dtype=torch.float32).half()).numpy()
+        assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), scale
+    big = y[np.abs(y) < 2000]
+    assert np.array_equal(ref.glue_postscale_f16(big, 16.0), (big.astype(np.float32) * 16).astype(np.float16))
+    # 5 * f16(1/3) = 5 * 0x3555 = 1706.25 ulps of [1, 2): 1.666015625; 5 * (1/3) in
+    # float32 would round to 1.6669921875
+    got5 = float(ref.glue_postscale_f16(np.float16([5.0]), 1.0 / 3.0)[0])
+    assert got5 == float(_rne_format(5 * Fraction(float(np.float16(1 / 3))), 11, -14, 15)) == 1.666015625
+    # the f32-scale mutant (y * s in float32, then f16) differs at s = 1/3
+    mutant = (y.astype(np.float32) * np.float32(1 / 3)).astype(np.float16)
+    assert not np.array_equal(ref.glue_postscale_f16(y, 1 / 3), mutant)
+    assert np.isinf(ref.glue_postscale_f16(np.float16([60000.0]), 2.0)[0])
+
+
+def test_dynamic_scale_known_answers():
+    """max(amax|x| / target, 1): the amax taken over |x| (a negative element
+    decides here), exact quotients for power-of-two targets, the floor at 1,
+    the fp32 quotient's rounding, NaN propagation and the empty case."""
+    x = np.float32([-300.0, 2.0, 100.0])
+    assert ref.dynamic_scale(x, 64.0) == np.float32(4.6875)  # 300 / 64, exact
+    assert ref.dynamic_scale(x[1:], 64.0) == np.float32(1.5625)  # 100 / 64
+    assert ref.dynamic_scale(np.float32([-10.0, 3.0]), 64.0) == np.float32(1.0)
+    assert ref.dynamic_scale(np.float32([]), 64.0) == np.float32(1.0)
+    assert np.isnan(ref.dynamic_scale(np.float32([1.0, np.nan, 1000.0]), 64.0))
+    assert ref.dynamic_scale(np.float32([np.inf, 1.0]), 64.0) == np.inf
+    # a non-dyadic target: the correctly rounded fp32 quotient of the exact ratio
+    v = np.float32(1000.0)
+    q = ref.dynamic_scale(np.float32([v]), 3.0)
+    assert q == np.float32(float(_rne_format(Fraction(1000, 3), 24, -126, 127)))
+    # mutants: max instead of abs-max; no floor at 1
+    assert np.float32(np.max(x) / 64) != ref.dynamic_scale(x, 64.0)
+    assert np.float32(np.max(np.abs(x[:2])) / 1000) != ref.dynamic_scale(x[:2], 1000.0)
+
+
 # --------------------------------------------------- f16 and the f64 contraction
 
 
