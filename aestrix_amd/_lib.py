@@ -119,6 +119,10 @@ SIGNATURES = {
     "imq_dit_step_set_head": ([_p, ctypes.POINTER(QWeight), ctypes.POINTER(QWeight)], _i),
     "imq_dit_step_denoise": ([_p, _p, _p, _p, ctypes.c_float, _i, _p], _i),
     "imq_dit_step_launches": ([_p], _i),
+    "imq_cond_create": ([_p, _p, _p, _p, _p], _i),
+    "imq_cond_step_conditioning": ([_p, _p, _i, _p, _p, _p], _i),
+    "imq_cond_sinusoid": ([_p, _i, _i, _p], _i),
+    "imq_cond_destroy": ([_p], _i),
     "imq_dit_step_destroy": ([_p], _i),
 }
 

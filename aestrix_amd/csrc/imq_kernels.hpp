@@ -116,6 +116,9 @@ hipError_t launch_rmsnorm(const float* x, const float* w, void* y, int rows, int
 // stream without a host buffer that must outlive the call).
 hipError_t launch_fill_f32(float* p, float v, int n, hipStream_t stream);
 
+// y[i] = x[i] / (1 + exp(-x[i])) for i < n, fp32 (y may be x).
+hipError_t launch_silu_f32(const float* x, float* y, int n, hipStream_t stream);
+
 // Largest M the qGEMV kernel takes.
 constexpr int kQgemvMaxM = 16;
 // Largest bf16 / f16 M the regime dispatcher routes to the qGEMV kernel when

@@ -108,7 +108,25 @@ __global__ __launch_bounds__(kThreads) void fill_f32_kernel(float* __restrict__ 
   if (i < n) p[i] = v;
 }
 
+// y[i] = v / (1 + exp(-v)), v = x[i], fp32: dd_silu_f32 (DirectDiTKernels.swift:176-184)
+// with the device library's expf and an IEEE division.
+__global__ __launch_bounds__(kThreads) void silu_f32_kernel(const float* __restrict__ x,
+                                                            float* __restrict__ y, int n) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) {
+    const float v = x[i];
+    y[i] = v / (1.0f + expf(-v));
+  }
+}
+
 }  // namespace
+
+hipError_t launch_silu_f32(const float* x, float* y, int n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(silu_f32_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, stream, x, y, n);
+  return hipGetLastError();
+}
 
 hipError_t launch_fill_f32(float* p, float v, int n, hipStream_t stream) {
   if (n <= 0) return hipSuccess;

@@ -204,6 +204,33 @@ def bench_qgemv_f32(imq, synth, torch, copies: int = 24) -> dict:
     return out
 
 
+def bench_cond_chain(torch) -> dict:
+    """The DiT's conditioning chain (DirectConditioner.stepConditioning) at FLUX.2
+    klein sizes: dim 3072, sin_dim 256, the four modulation heads concatenated
+    (52224 rows), f32 parameters; all timesteps of a call in one pass (the
+    reference runs six M = 1 dispatches with a blocking wait each per timestep).
+    Device time per call from HIP events, host sinusoid and copy included."""
+    from aestrix_amd.cond import Conditioner, random_conditioner
+
+    l1, l2, heads = random_conditioner(3072, 256, seed=3)
+    cond = Conditioner(l1, l2, heads)
+    byts = sum(q.n * q.k // 2 + 2 * 4 * q.n * (q.k // 64) for q in (l1, l2, heads))
+    out = {"weight_bytes": byts}
+    for count in (1, 4):
+        t = [1000.0 * (i + 1) / count for i in range(count)]
+        temb = torch.empty((count, 3072), device="cuda")
+        hd = torch.empty((count, heads.n), device="cuda")
+        for _ in range(3):
+            cond.run(t, temb, hd)
+        ms = time_events(lambda: cond.run(t, temb, hd), 20)
+        gbs = byts / (ms * 1e-3) / 1e9
+        out[f"timesteps{count}"] = {"us": round(ms * 1e3, 2), "GB/s_weights": round(gbs, 1),
+                                    "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+        log(f"conditioning chain, {count} timesteps: {ms * 1e3:.1f} us ({gbs:.0f} GB/s of weights)")
+    cond.close()
+    return out
+
+
 def bench_dequant(imq, synth, torch, copies: int = 6) -> dict:
     out = {}
     for (n, k) in ((27648, 3072), (3072, 12288)):
@@ -531,6 +558,7 @@ def main() -> int:
         extra["qgemv"] = bench_qgemv(imq, synth, torch)
         extra["fused_decode"] = bench_fused_decode(imq, synth, torch)
         extra["qgemv_f32"] = bench_qgemv_f32(imq, synth, torch)
+        extra["cond_chain"] = bench_cond_chain(torch)
         extra["dequant"] = bench_dequant(imq, synth, torch)
         extra["prescale"] = bench_prescale(imq, torch)
         extra["qgemm_shapes"] = {

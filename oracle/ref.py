@@ -219,3 +219,44 @@ def rmsnorm_rows(x: np.ndarray, w: np.ndarray, eps: float = 1e-5) -> np.ndarray:
     x = np.asarray(x, np.float64)
     inv = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
     return x * inv * np.asarray(w, np.float64)
+
+
+# The conditioning chain of DirectConditioner.stepConditioning
+# (Sources/ImarelloDirect/DirectConditioner.swift:152-213), f32 throughout.
+
+def cond_sinusoid(t: np.ndarray, sin_dim: int) -> np.ndarray:
+    """DirectConditioner.sinusoid (:152-166) for each t: freq_i = expf(-logf(10000)
+    * i / half), arg = t * freq_i, [cosf(arg) | sinf(arg)].  Every float operation
+    rounds to float32 in the reference's order; the transcendental functions are
+    evaluated in float64 and rounded once (correctly rounded float32 results)."""
+    t = np.asarray(t, dtype=np.float32).reshape(-1)
+    half = sin_dim // 2
+    ln = np.float32(np.log(np.float64(10000.0)))
+    i = np.arange(half, dtype=np.float32)
+    e = ((-ln) * i).astype(np.float32) / np.float32(half)
+    freq = np.exp(e.astype(np.float64)).astype(np.float32)
+    arg = (t[:, None] * freq[None, :]).astype(np.float32).astype(np.float64)
+    return np.concatenate([np.cos(arg).astype(np.float32), np.sin(arg).astype(np.float32)], axis=1)
+
+
+def silu_f32(v: np.ndarray) -> np.ndarray:
+    """dd_silu_f32 (DirectDiTKernels.swift:176-184): v / (1 + exp(-v)), evaluated in
+    float64 and rounded once to float32."""
+    vd = np.asarray(v, dtype=np.float32).astype(np.float64)
+    with np.errstate(over="ignore"):
+        return (vd / (1.0 + np.exp(-vd))).astype(np.float32)
+
+
+def cond_chain(t: np.ndarray, l1, l2, heads, head_rows=None):
+    """stepConditioning (:168-213) on the CPU for timesteps t: l1, l2, heads are
+    (w uint32, scales f32, biases f32) triples; returns (temb, heads_out), each
+    qmm the f32 oracle qmm (f32 dequant, float64 accumulation, one rounding).
+    head_rows restricts the heads' output columns to those weight rows."""
+    sin = cond_sinusoid(t, l1[0].shape[1] * 8)
+    t1 = silu_f32(qmm_t_as(sin, *l1, np.float32))
+    temb = qmm_t_as(t1, *l2, np.float32)
+    hw, hs, hb = heads
+    if head_rows is not None:
+        hw, hs, hb = hw[head_rows], hs[head_rows], hb[head_rows]
+    return temb, qmm_t_as(silu_f32(temb), hw, hs, hb, np.float32)
+

@@ -69,6 +69,7 @@ hipError_t launch_rmsnorm(const float*, const float*, void*, int, int, float, in
   return hipErrorNoDevice;
 }
 hipError_t launch_fill_f32(float*, float, int, hipStream_t) { return hipErrorNoDevice; }
+hipError_t launch_silu_f32(const float*, float*, int, hipStream_t) { return hipErrorNoDevice; }
 hipError_t static_scratch(int, void** out) {
   *out = nullptr;
   return hipErrorNoDevice;

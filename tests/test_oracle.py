@@ -676,6 +676,82 @@ def test_dynamic_scale_known_answers():
     assert np.float32(np.max(np.abs(x[:2])) / 1000) != ref.dynamic_scale(x[:2], 1000.0)
 
 
+def test_cond_sinusoid_known_answers():
+    """[cos | sin] of t * 10000^(-i / half): t = 0 gives ones then zeros (a
+    swapped-halves mutant fails), t = 1 gives cos / sin of the frequencies
+    themselves (closed form 10000^(-i/128) in float64, within a few float32
+    ulps of the float operations' rounding), and numpy's float32 functions agree
+    within 4 ulps plus what an ulp of a frequency or of the argument t f moves."""
+    s0 = ref.cond_sinusoid(np.float32([0.0]), 256)[0]
+    assert np.array_equal(s0[:128], np.ones(128, np.float32))
+    assert np.array_equal(s0[128:], np.zeros(128, np.float32))
+    swapped = np.concatenate([s0[128:], s0[:128]])
+    assert not np.array_equal(swapped, s0)
+    s1 = ref.cond_sinusoid(np.float32([1.0]), 256)[0].astype(np.float64)
+    f = 10000.0 ** (-np.arange(128) / 128.0)
+    assert np.max(np.abs(s1[:128] - np.cos(f))) < 4e-7 and np.max(np.abs(s1[128:] - np.sin(f))) < 4e-7
+    # a frequency-index mutant (i / (half - 1)) moves them far more
+    fm = 10000.0 ** (-np.arange(128) / 127.0)
+    assert np.max(np.abs(s1[128:] - np.sin(fm))) > 1e-3
+    t = np.float32([0.0, 1.0, 3.5, 250.0, 999.0])
+    got = ref.cond_sinusoid(t, 256)
+    half = np.float32(128)
+    freq = np.exp((-np.log(np.float32(10000)) * np.arange(128, dtype=np.float32)) / half)
+    arg = t[:, None] * freq[None, :]
+    want = np.concatenate([np.cos(arg), np.sin(arg)], axis=1).astype(np.float32)
+    # numpy's float32 exp may differ from the correctly rounded one by an ulp
+    # of freq, which t multiplies, and its cos / sin by an ulp of the argument:
+    # bound = 4 output ulps + |t| * 2 ulp(freq) + 2 ulp(t f)
+    ulp = np.spacing(np.maximum(np.abs(want), np.float32(2 ** -24)))
+    slack = (np.abs(t[:, None]) * 2 * np.tile(np.spacing(freq), 2)[None, :]
+             + 2 * np.tile(np.spacing(np.abs(arg)), 2))
+    assert np.all(np.abs(got - want) <= 4 * ulp + slack)
+
+
+def test_silu_f32_matches_torch():
+    rng = np.random.default_rng(31)
+    v = np.concatenate([(rng.standard_normal(5000) * 8).astype(np.float32),
+                        np.float32([0.0, -0.0, 1e-30, -90.0, 90.0, -1e4, 1e4])])
+    want = torch.nn.functional.silu(torch.from_numpy(v).double()).float().numpy()
+    assert np.array_equal(ref.silu_f32(v), want)
+    assert ref.silu_f32(np.float32([0.0]))[0] == 0 and ref.silu_f32(np.float32([1e4]))[0] == 1e4
+
+
+def test_cond_chain_against_torch():
+    """The chain's composition against torch float64 on a small model (dim 128,
+    sin_dim 64): torch unpacks the codes with its own shifts, dequantizes in
+    float32 and runs sinusoid -> matmul -> silu -> matmul -> silu -> matmul."""
+    rng = np.random.default_rng(32)
+    dim, sin_dim = 128, 64
+
+    def proj(n, k):
+        w = rng.integers(0, 2 ** 32, (n, k // 8), dtype=np.uint64).astype(np.uint32)
+        s = (np.abs(rng.standard_normal((n, k // 64))) / (4 * np.sqrt(k))).astype(np.float32)
+        b = (-8 * s + rng.standard_normal((n, k // 64)) / (40 * np.sqrt(k))).astype(np.float32)
+        return w, s, b
+
+    l1, l2, hd = proj(dim, sin_dim), proj(dim, dim), proj(17 * dim, dim)
+    t = np.float32([1000.0, 500.0, 37.5])
+    temb, heads = ref.cond_chain(t, l1, l2, hd)
+
+    def deq(p):
+        w, s, b = (torch.from_numpy(a.astype(np.int64) if a.dtype == np.uint32 else a) for a in p)
+        codes = (w[..., None] >> (4 * torch.arange(8))) & 15
+        codes = codes.reshape(w.shape[0], -1).float()
+        return (codes * s.repeat_interleave(64, 1) + b.repeat_interleave(64, 1)).double()
+
+    x = torch.from_numpy(ref.cond_sinusoid(t, sin_dim)).double()
+    silu = torch.nn.functional.silu
+    tt = x @ deq(l1).T
+    tt = silu(tt.float().double()).float().double() @ deq(l2).T
+    want_temb = tt.float()
+    want_heads = (silu(want_temb.double()).float().double() @ deq(hd).T).float()
+    assert np.allclose(temb, want_temb.numpy(), rtol=1e-6, atol=1e-6)
+    assert np.allclose(heads, want_heads.numpy(), rtol=1e-6, atol=1e-6)
+    sub = ref.cond_chain(t, l1, l2, hd, head_rows=slice(100, 200))[1]
+    assert np.array_equal(sub, heads[:, 100:200])
+
+
 # --------------------------------------------------- f16 and the f64 contraction
 
 
