@@ -29,6 +29,7 @@ from .ops import (  # noqa: F401
     qgemm,
     qgemv,
     qmm,
+    qmm_add,
     qmm_gate_add,
     qmm_plan,
     qmm_postscale,

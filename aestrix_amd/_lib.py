@@ -91,6 +91,7 @@ SIGNATURES = {
     "imq_cast_prescale_ex": ([_p, _p, _p, _sz, ctypes.c_float, _p, _i, _p], _i),
     "imq_qmm_postscale_ex": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, ctypes.c_float, _p, _i, _i,
                               _i, _p], _i),
+    "imq_qmm_add": ([_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p], _i),
     "imq_qmm_gate_add": ([_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, ctypes.c_float, _i, _i, _i,
                           _p], _i),
     "imq_qmm_swiglu": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float,
@@ -119,6 +120,11 @@ SIGNATURES = {
     "imq_dit_step_set_head": ([_p, ctypes.POINTER(QWeight), ctypes.POINTER(QWeight)], _i),
     "imq_dit_step_denoise": ([_p, _p, _p, _p, ctypes.c_float, _i, _p], _i),
     "imq_dit_step_launches": ([_p], _i),
+    "imq_te_create": ([_p, _p, _i, _i, ctypes.c_float, _p], _i),
+    "imq_te_attn_in": ([_p, _i, _p, _p, _i, _p], _i),
+    "imq_te_attn_out_mlp": ([_p, _i, _p, _p, _p, _i, _p], _i),
+    "imq_te_dims": ([_p, _p, _p, _p, _p], _i),
+    "imq_te_destroy": ([_p], _i),
     "imq_cond_create": ([_p, _p, _p, _p, _p], _i),
     "imq_cond_step_conditioning": ([_p, _p, _i, _p, _p, _p], _i),
     "imq_cond_sinusoid": ([_p, _i, _i, _p], _i),

@@ -257,11 +257,8 @@ int check_epilogue(imq_ctx* ctx, const char* fn, const uint32_t* w, const void* 
   return bind_device(ctx);
 }
 
-// Whether imq_qmm_swiglu runs the qGEMV's pair mode: few rows, 16-bit T, and
-// the qGEMV's 32-bit offsets (weights under 4 GiB, one x tile under 2 GiB).
 bool swiglu_on_qgemv(int k, int n, int m, imq_dtype dtype) {
-  return m <= imq::kQgemvSwigluMaxM && dtype != IMQ_F32 &&
-         (size_t)n * (size_t)k / 2 < ((size_t)1 << 32) && (size_t)m * k * 2 < ((size_t)1 << 31);
+  return imq::qgemv_swiglu_fits(k, n, m, (int)dtype);
 }
 
 }  // namespace
@@ -581,6 +578,19 @@ int imq_qmm_postscale(imq_ctx* ctx, const uint32_t* w, const void* scales, const
   if (rc != IMQ_OK) return rc;
   if (!aligned(y, 4)) return fail(ctx, IMQ_EINVAL, "%s: y must be 4-byte aligned", fn);
   const hipError_t e = imq::launch_qgemm_postscale(w, scales, biases, x, y, k, n, m, scale,
+                                                   (int)dtype, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
+}
+
+int imq_qmm_add(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                const void* x, const void* residual, void* y, int k, int n, int m, int group_size,
+                int bits, imq_dtype dtype, imq_stream stream) {
+  const char* fn = "imq_qmm_add";
+  int rc = check_epilogue(ctx, fn, w, scales, biases, x, y, k, n, m, group_size, bits, dtype);
+  if (rc != IMQ_OK) return rc;
+  if (!residual) return fail(ctx, IMQ_EINVAL, "%s: null residual", fn);
+  if (!aligned(residual, 2)) return fail(ctx, IMQ_EINVAL, "%s: residual must be 2-byte aligned", fn);
+  const hipError_t e = imq::launch_qgemm_resid_add(w, scales, biases, x, residual, y, k, n, m,
                                                    (int)dtype, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
 }

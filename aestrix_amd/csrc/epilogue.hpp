@@ -118,6 +118,35 @@ struct EpPostscaleF16 {
   }
 };
 
+// y[row][col] = T(float(r[row][col]) + float(T(acc))), T residual stream: the
+// text encoder's dq_add after a qmm (DirectGlueKernels.swift:88-96,
+// DirectTEEncoder.swift:392,411).  y may alias r.
+template <int T>
+struct EpResidAdd {
+  static constexpr bool kPair = false;
+  static constexpr bool kPartial = false;
+  uint16_t* y;
+  const uint16_t* r;
+  int ld;
+  bool vec;
+  __device__ __forceinline__ float value(float acc) const { return acc; }
+  __device__ __forceinline__ void emit1(int row, int col, uint16_t v) const {
+    const size_t i = (size_t)row * ld + col;
+    y[i] = Elem<T>::out(staged_value<T>(r[i]) + staged_value<T>(v));
+  }
+  __device__ __forceinline__ void emit8(int row, int col, uint4 v) const {
+    const size_t i = (size_t)row * ld + col;
+    const uint4 rv = *reinterpret_cast<const uint4*>(r + i);
+    const uint32_t a[4] = {v.x, v.y, v.z, v.w}, b[4] = {rv.x, rv.y, rv.z, rv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = Elem<T>::pack2(staged_value<T>(b[e] & 0xFFFFu) + staged_value<T>(a[e] & 0xFFFFu),
+                            staged_value<T>(b[e] >> 16) + staged_value<T>(a[e] >> 16));
+    *reinterpret_cast<uint4*>(y + i) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+};
+
 // y[row][col] = fma(gate[col], float(T(acc)) * scale, x[row][col]), fp32
 // residual stream: dd_gate_add (DirectDiTKernels.swift:211-224).  y may alias x.
 // With scale_dev set, the scale is read from device memory when the kernel runs

@@ -91,6 +91,11 @@ hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const vo
                                  const void* x, const float* residual, const float* gate, float* y,
                                  int k, int n, int m, float scale, int dtype, hipStream_t stream,
                                  SplitWs ws = {}, const float* scale_dev = nullptr);
+// resid_add: y[m][n] (T) = T(float(resid[m][n]) + float(T(acc))), resid T
+//            (the text encoder's dq_add after its o_proj / down_proj); y may be resid.
+hipError_t launch_qgemm_resid_add(const uint32_t* w, const void* scales, const void* biases,
+                                  const void* x, const void* resid, void* y, int k, int n, int m,
+                                  int dtype, hipStream_t stream, SplitWs ws = {});
 hipError_t launch_qgemm_swiglu(const uint32_t* w, const void* scales, const void* biases,
                                const void* x, void* y, int ldy, int k, int n, int m, int width,
                                int gate_row, int up_row, float in_scale, float out_scale, int dtype,
@@ -116,6 +121,11 @@ hipError_t launch_rmsnorm(const float* x, const float* w, void* y, int rows, int
 // stream without a host buffer that must outlive the call).
 hipError_t launch_fill_f32(float* p, float v, int n, hipStream_t stream);
 
+// y[r][c] (T) = T(x[r][c] * rsqrt(mean(x[r]^2) + eps) * w[c]), x T [rows, cols]
+// (the text encoder's RMSNorm on its T residual stream); T in {bf16, f16}.
+hipError_t launch_rmsnorm_t(const void* x, const float* w, void* y, int rows, int cols, float eps,
+                            int dtype, hipStream_t stream);
+
 // y[i] = x[i] / (1 + exp(-x[i])) for i < n, fp32 (y may be x).
 hipError_t launch_silu_f32(const float* x, float* y, int n, hipStream_t stream);
 
@@ -137,6 +147,14 @@ constexpr int kQskinnyMaxM = 16;
 // this kernel is faster on both.
 constexpr int kDispatchSkinnyMinM = 3;
 constexpr int kDispatchSkinnyMaxM = 16;
+
+// Whether a SwiGLU qmm runs the qGEMV's pair mode: few rows, 16-bit T, and the
+// qGEMV's 32-bit offsets (weights under 4 GiB, one x tile under 2 GiB).
+inline bool qgemv_swiglu_fits(int k, int n, int m, int dtype) {
+  return m <= kQgemvSwigluMaxM && dtype != 2 /* f32 */ &&
+         (size_t)n * (size_t)k / 2 < ((size_t)1 << 32) &&
+         (size_t)m * k * 2 < ((size_t)1 << 31);
+}
 
 // Bytes of the statically allocated split-K scratch of the allocation-free
 // dispatcher (one copy per GPU, scratch.hip).  64 MiB covers the split plans

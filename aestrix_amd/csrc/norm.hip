@@ -108,6 +108,34 @@ __global__ __launch_bounds__(kThreads) void fill_f32_kernel(float* __restrict__ 
   if (i < n) p[i] = v;
 }
 
+// y[r][c] = T(x[r][c] * rsqrt(mean_c(x[r][c]^2) + eps) * w[c]) on a T row
+// (the text encoder's dq_rmsnorm, DirectGlueKernels.swift:14-49: fp32 sum of
+// squares, fp32 weight, the residual stream itself in T).  One workgroup per
+// row; the row is read twice (the second pass from the cache).
+template <int T>
+__global__ __launch_bounds__(kThreads) void rmsnorm_tin_kernel(
+    const typename Elem<T>::S* __restrict__ x, const float* __restrict__ w,
+    typename Elem<T>::S* __restrict__ y, int cols, float eps) {
+  __shared__ float part[kThreads / 64];
+  const typename Elem<T>::S* xr = x + (size_t)blockIdx.x * cols;
+  float acc = 0.f;
+  for (int c = threadIdx.x; c < cols; c += kThreads) {
+    const float v = Elem<T>::param(xr[c]);
+    acc = __builtin_fmaf(v, v, acc);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int i = 0; i < kThreads / 64; ++i) total += part[i];
+  const float inv = __frsqrt_rn(total / (float)cols + eps);
+  typename Elem<T>::S* yr = y + (size_t)blockIdx.x * cols;
+  for (int c = threadIdx.x; c < cols; c += kThreads)
+    yr[c] = Elem<T>::out(Elem<T>::param(xr[c]) * inv * w[c]);
+}
+
 // y[i] = v / (1 + exp(-v)), v = x[i], fp32: dd_silu_f32 (DirectDiTKernels.swift:176-184)
 // with the device library's expf and an IEEE division.
 __global__ __launch_bounds__(kThreads) void silu_f32_kernel(const float* __restrict__ x,
@@ -120,6 +148,24 @@ __global__ __launch_bounds__(kThreads) void silu_f32_kernel(const float* __restr
 }
 
 }  // namespace
+
+hipError_t launch_rmsnorm_t(const void* x, const float* w, void* y, int rows, int cols, float eps,
+                            int dtype, hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  const dim3 grid(rows), block(kThreads);
+  const auto* xx = static_cast<const uint16_t*>(x);
+  auto* yy = static_cast<uint16_t*>(y);
+  switch (dtype) {
+    case kBf16:
+      hipLaunchKernelGGL(rmsnorm_tin_kernel<kBf16>, grid, block, 0, stream, xx, w, yy, cols, eps);
+      break;
+    case kF16:
+      hipLaunchKernelGGL(rmsnorm_tin_kernel<kF16>, grid, block, 0, stream, xx, w, yy, cols, eps);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_silu_f32(const float* x, float* y, int n, hipStream_t stream) {
   if (n <= 0) return hipSuccess;

@@ -1027,6 +1027,26 @@ hipError_t launch_qgemm_postscale_f16(const uint32_t* w, const void* scales, con
                              SplitWs{});
 }
 
+hipError_t launch_qgemm_resid_add(const uint32_t* w, const void* scales, const void* biases,
+                                  const void* x, const void* resid, void* y, int k, int n, int m,
+                                  int dtype, hipStream_t stream, SplitWs ws) {
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* b = static_cast<const uint16_t*>(biases);
+  const auto* xx = static_cast<const uint16_t*>(x);
+  auto* yy = static_cast<uint16_t*>(y);
+  const auto* rr = static_cast<const uint16_t*>(resid);
+  const bool vec = al16(y) && al16(resid) && n % 8 == 0;
+  switch (dtype) {
+    case kBf16:
+      return launch_big_ep<kBf16>(w, s, b, xx, EpResidAdd<kBf16>{yy, rr, n, vec}, k, n, m, stream,
+                                  ws);
+    case kF16:
+      return launch_big_ep<kF16>(w, s, b, xx, EpResidAdd<kF16>{yy, rr, n, vec}, k, n, m, stream,
+                                 ws);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const void* biases,
                                  const void* x, const float* residual, const float* gate, float* y,
                                  int k, int n, int m, float scale, int dtype, hipStream_t stream,

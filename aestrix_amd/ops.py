@@ -294,6 +294,29 @@ def qmm_gate_add(x, w, scales, biases, residual: torch.Tensor, gate: torch.Tenso
     return out
 
 
+def qmm_add(x, w, scales, biases, residual: torch.Tensor, group_size: int = GROUP_SIZE,
+            bits: int = BITS, out=None) -> torch.Tensor:
+    """T y = T(float(residual) + float(T(x . deq(W)^T))) in one kernel: the text
+    encoder's qmm + dq_add (``DirectTEEncoder.swift:390-392,409-411``,
+    ``DirectGlueKernels.swift:88-96``); residual has x's dtype, ``out=residual``
+    updates it in place."""
+    n, k, m, lead, x = _epi_args(x, w, scales, biases, group_size, bits)
+    _require(residual.dtype == x.dtype and residual.is_contiguous()
+             and tuple(residual.shape) == lead + (n,), f"residual must be {x.dtype} [..., N]")
+    if out is None:
+        out = torch.empty(lead + (n,), dtype=x.dtype, device=x.device)
+    _require(out.dtype == x.dtype and out.is_contiguous() and tuple(out.shape) == lead + (n,),
+             f"out must be a contiguous {x.dtype} tensor of shape {lead + (n,)}")
+    dtype = _DTYPES.get(x.dtype, -1)
+    ctx = context(w.device)
+    with torch.cuda.device(w.device):
+        st = _lib.load().imq_qmm_add(ctx, _ptr(w), _ptr(scales), _ptr(biases), _ptr(x),
+                                     _ptr(residual), _ptr(out), k, n, m, group_size, bits, dtype,
+                                     _stream(x))
+    _lib.check(st, ctx)
+    return out
+
+
 def qmm_swiglu(x, w, scales, biases, width: int, gate_row: int, up_row: int,
                in_scale: float = 1.0, out_scale: float = 1.0, group_size: int = GROUP_SIZE,
                bits: int = BITS, out=None) -> torch.Tensor:

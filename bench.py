@@ -231,6 +231,38 @@ def bench_cond_chain(torch) -> dict:
     return out
 
 
+def bench_te_layer(torch) -> dict:
+    """One Qwen3 4B text-encoder layer's quantized-linear work (imq_te: RMSNorm +
+    q/k/v; o_proj + dq_add, RMSNorm, gate/up + dq_silu_mul, down_proj + dq_add)
+    at the padded window L = 512 and the splice regime L = 30
+    (DirectTEEncoder.swift:249-412), bf16, graph-timed over 27 layers."""
+    from aestrix_amd.te import TextEncoderLayers, random_te_layers
+
+    layers = random_te_layers(27, dtype=torch.bfloat16, seed=4)
+    te = TextEncoderLayers(layers, max_rows=512)
+    out = {}
+    flop_per_row = 2.0 * (6144 * 2560 + 2560 * 4096 + 2 * 9728 * 2560 + 2560 * 9728)
+    for rows in (512, 30):
+        x = torch.randn((rows, 2560), device="cuda").bfloat16()
+        attn = torch.randn((rows, 4096), device="cuda").bfloat16()
+        qkv = torch.empty((rows, 6144), dtype=torch.bfloat16, device="cuda")
+        h = [torch.empty_like(x) for _ in range(2)]
+        launches = []
+        for i in range(27):
+            src = x if i == 0 else h[(i - 1) % 2]
+            launches.append(lambda i=i, src=src: te.attn_in(i, src, qkv))
+            launches.append(lambda i=i, src=src: te.attn_out_mlp(i, src, attn, h[i % 2]))
+        ms = time_graph(launches) * len(launches) / 27
+        tf = flop_per_row * rows / (ms * 1e-3) / 1e12
+        out[f"L{rows}"] = {"us_per_layer": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                           "launches_per_layer": 5}
+        log(f"TE layer L={rows}: {ms * 1e3:.1f} us per layer  {tf:.1f} TFLOP/s")
+    te.close()
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_dequant(imq, synth, torch, copies: int = 6) -> dict:
     out = {}
     for (n, k) in ((27648, 3072), (3072, 12288)):
@@ -559,6 +591,7 @@ def main() -> int:
         extra["fused_decode"] = bench_fused_decode(imq, synth, torch)
         extra["qgemv_f32"] = bench_qgemv_f32(imq, synth, torch)
         extra["cond_chain"] = bench_cond_chain(torch)
+        extra["te_layer"] = bench_te_layer(torch)
         extra["dequant"] = bench_dequant(imq, synth, torch)
         extra["prescale"] = bench_prescale(imq, torch)
         extra["qgemm_shapes"] = {

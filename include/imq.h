@@ -242,6 +242,13 @@ int imq_qmm_postscale_ex(imq_ctx* ctx, const uint32_t* w, const void* scales, co
                          float scale, const float* scale_dev, int group_size, int bits,
                          imq_dtype dtype, imq_stream stream);
 
+/* y[M, N] (T) = T(float(residual) + float(T(x . deq(W)^T))), residual T [M, N]:
+ * the text encoder's qmm followed by dq_add (DirectTEEncoder.swift:390-392,
+ * 409-411; DirectGlueKernels.swift:88-96).  y may equal residual. */
+int imq_qmm_add(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                const void* x, const void* residual, void* y, int k, int n, int m, int group_size,
+                int bits, imq_dtype dtype, imq_stream stream);
+
 /* y[M, N] (fp32) = residual + gate[n] * float(T(x . deq(W)^T)) * scale: the
  * gated residual dd_gate_add (DirectDiTKernels.swift:211-224).  y may equal
  * residual (in place). */

@@ -204,6 +204,18 @@ def glue_gate_add(y_t: np.ndarray, residual: np.ndarray, gate: np.ndarray,
     return exact.astype(np.float32)
 
 
+def glue_add_t(y_t: np.ndarray, r_t: np.ndarray, dtype: str) -> np.ndarray:
+    """dq_add (Sources/ImarelloDirect/DirectGlueKernels.swift:88-96) after a qmm:
+    T(float(r) + float(y)) -- the float32 sum of two T values, rounded to T.
+    y_t, r_t are float32 values of T; returns float16 values ("f16") or bf16
+    bits ("bf16")."""
+    s = (np.asarray(r_t, dtype=np.float32) + np.asarray(y_t, dtype=np.float32)).astype(np.float32)
+    if dtype == "f16":
+        with np.errstate(over="ignore"):
+            return s.astype(np.float16)
+    return f32_to_bf16(s)
+
+
 def glue_swiglu(g_t: np.ndarray, u_t: np.ndarray, in_scale: float, out_scale: float) -> np.ndarray:
     """dd_swiglu_pitched (DirectDiTKernels.swift:137-157): g, u = float(.) * inScale;
     g * sigmoid(g) * u * outScale, as float64 (to be rounded to T by the caller)."""

@@ -48,6 +48,13 @@ hipError_t launch_qgemm_postscale_f16(const uint32_t*, const void*, const void*,
                                       void*, int, int, int, float, hipStream_t, const float*) {
   return hipErrorNoDevice;
 }
+hipError_t launch_qgemm_resid_add(const uint32_t*, const void*, const void*, const void*,
+                                  const void*, void*, int, int, int, int, hipStream_t, SplitWs) {
+  return hipErrorNoDevice;
+}
+hipError_t launch_rmsnorm_t(const void*, const float*, void*, int, int, float, int, hipStream_t) {
+  return hipErrorNoDevice;
+}
 hipError_t launch_qgemm_gate_add(const uint32_t*, const void*, const void*, const void*,
                                  const float*, const float*, float*, int, int, int, float, int,
                                  hipStream_t, SplitWs, const float*) {

@@ -752,6 +752,24 @@ def test_cond_chain_against_torch():
     assert np.array_equal(sub, heads[:, 100:200])
 
 
+def test_glue_add_t_matches_torch_half_and_bf16_adds():
+    """T(float(r) + float(y)): torch's CPU bf16 and f16 adds (float arithmetic
+    rounded to the type) are independent implementations of the same step; a
+    mutant that adds in T's precision after rounding each to a coarser type,
+    or that drops the residual, fails."""
+    rng = np.random.default_rng(33)
+    y = (rng.standard_normal(6000) * np.exp2(rng.integers(-12, 12, 6000))).astype(np.float32)
+    r = (rng.standard_normal(6000) * np.exp2(rng.integers(-12, 12, 6000))).astype(np.float32)
+    yb, rb = torch.from_numpy(y).bfloat16(), torch.from_numpy(r).bfloat16()
+    got = ref.glue_add_t(yb.float().numpy(), rb.float().numpy(), "bf16")
+    want = (rb + yb).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+    yh, rh = torch.from_numpy(y).half(), torch.from_numpy(r).half()
+    got16 = ref.glue_add_t(yh.float().numpy(), rh.float().numpy(), "f16")
+    assert np.array_equal(got16.view(np.uint16), (rh + yh).numpy().view(np.uint16))
+    assert not np.array_equal(got, ref.f32_to_bf16(yb.float().numpy()))
+
+
 # --------------------------------------------------- f16 and the f64 contraction
 
 
