@@ -35,4 +35,5 @@ from .ops import (  # noqa: F401
     qmm_postscale,
     qmm_swiglu,
     quantized_matmul,
+    rmsnorm,
 )

@@ -582,6 +582,31 @@ int imq_qmm_postscale(imq_ctx* ctx, const uint32_t* w, const void* scales, const
   return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
 }
 
+int imq_rmsnorm(imq_ctx* ctx, const void* x, imq_dtype x_dtype, const float* w, void* y,
+                imq_dtype y_dtype, int rows, int cols, float eps, imq_stream stream) {
+  const char* fn = "imq_rmsnorm";
+  if (!ctx) return fail(nullptr, IMQ_EINVAL, "%s: null context", fn);
+  if (y_dtype != IMQ_BF16 && y_dtype != IMQ_F16)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: y dtype %d (bf16 or f16)", fn, (int)y_dtype);
+  if (x_dtype != IMQ_F32 && x_dtype != y_dtype)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: x dtype %d (f32, or y's dtype)", fn, (int)x_dtype);
+  if (rows < 0 || cols <= 0) return fail(ctx, IMQ_EINVAL, "%s: rows %d, cols %d", fn, rows, cols);
+  if (!std::isfinite(eps) || eps < 0.f)
+    return fail(ctx, IMQ_EINVAL, "%s: eps %g must be finite and non-negative", fn, (double)eps);
+  if (rows == 0) return IMQ_OK;
+  if (!x || !w || !y) return fail(ctx, IMQ_EINVAL, "%s: null device pointer", fn);
+  if (!aligned(x, elem_size(x_dtype)) || !aligned(w, 4) || !aligned(y, 2))
+    return fail(ctx, IMQ_EINVAL, "%s: x, w or y misaligned for its element type", fn);
+  int rc = bind_device(ctx);
+  if (rc != IMQ_OK) return rc;
+  const auto st = static_cast<hipStream_t>(stream);
+  const hipError_t e =
+      x_dtype == IMQ_F32
+          ? imq::launch_rmsnorm(static_cast<const float*>(x), w, y, rows, cols, eps, (int)y_dtype, st)
+          : imq::launch_rmsnorm_t(x, w, y, rows, cols, eps, (int)y_dtype, st);
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
+}
+
 int imq_qmm_add(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
                 const void* x, const void* residual, void* y, int k, int n, int m, int group_size,
                 int bits, imq_dtype dtype, imq_stream stream) {

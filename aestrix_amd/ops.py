@@ -294,6 +294,33 @@ def qmm_gate_add(x, w, scales, biases, residual: torch.Tensor, gate: torch.Tenso
     return out
 
 
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5,
+            out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Row RMSNorm to T: x * rsqrt(mean(x^2) + eps) * weight with an fp32 sum of
+    squares and fp32 weight; x float32 (the DiT's residual, ``dd_rmsnorm_pitched``,
+    ``DirectDiTKernels.swift:61-99``, eps 1e-5) or T itself (the text encoder's
+    ``dq_rmsnorm``, ``DirectGlueKernels.swift:14-49``, eps 1e-6)."""
+    _require(x.is_cuda and x.dtype in (torch.float32, torch.bfloat16, torch.float16),
+             "x must be a float32, bfloat16 or float16 HIP tensor")
+    out_dtype = out_dtype or (x.dtype if x.dtype != torch.float32 else torch.bfloat16)
+    _require(out_dtype in (torch.bfloat16, torch.float16), "out_dtype: bfloat16 or float16")
+    x = x if x.is_contiguous() else x.contiguous()
+    cols = x.shape[-1]
+    _require(weight.dtype == torch.float32 and weight.is_contiguous() and weight.numel() == cols
+             and weight.device == x.device, f"weight must be float32 [{cols}] on x's device")
+    if out is None:
+        out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    _require(out.dtype == out_dtype and out.is_contiguous() and out.shape == x.shape,
+             f"out must be a contiguous {out_dtype} tensor shaped like x")
+    ctx = context(x.device)
+    with torch.cuda.device(x.device):
+        st = _lib.load().imq_rmsnorm(ctx, _ptr(x), _DTYPES[x.dtype], _ptr(weight), _ptr(out),
+                                     _DTYPES[out_dtype], x.numel() // cols, cols, float(eps),
+                                     _stream(x))
+    _lib.check(st, ctx)
+    return out
+
+
 def qmm_add(x, w, scales, biases, residual: torch.Tensor, group_size: int = GROUP_SIZE,
             bits: int = BITS, out=None) -> torch.Tensor:
     """T y = T(float(residual) + float(T(x . deq(W)^T))) in one kernel: the text

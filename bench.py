@@ -303,6 +303,52 @@ def bench_prescale(imq, torch, copies: int = 4) -> dict:
             "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts}
 
 
+def bench_rmsnorm(imq, torch, copies: int = 4) -> dict:
+    """RMSNorm into a qmm input: the DiT's fp32 residual [4608 x 3072] to f16
+    (6 bytes per element) and the text encoder's bf16 stream [512 x 2560] to bf16
+    (4 bytes per element), buffers rotated past the MALL for the first."""
+    out = {}
+    for tag, (m, k), xdt, ydt, per in (("dit_f32_to_f16", (4608, 3072), torch.float32, torch.float16, 6),
+                                        ("te_bf16", (512, 2560), torch.bfloat16, torch.bfloat16, 4)):
+        xs = [torch.randn((m, k), device="cuda").to(xdt) for _ in range(copies)]
+        ys = [torch.empty((m, k), dtype=ydt, device="cuda") for _ in range(copies)]
+        w = torch.ones(k, device="cuda")
+        launches = [(lambda i=i: imq.rmsnorm(xs[i], w, 1e-5, out_dtype=ydt, out=ys[i]))
+                    for i in range(copies)]
+        ms = time_graph(launches, replays=4)
+        byts = m * k * per + 4 * k
+        gbs = byts / (ms * 1e-3) / 1e9
+        out[tag] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                    "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts}
+        log(f"rmsnorm {tag} [{m}x{k}]: {ms * 1e3:.1f} us  {gbs:.0f} GB/s")
+        del xs, ys
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_x_embedder(imq, synth, torch) -> dict:
+    """The DiT's x_embedder sandwich at 1024^2 (latents [4096 x 128] f32 / 16 to f16,
+    the qmm with K = 128 -- the register-staged tile kernel, K % 256 != 0 -- and
+    the x16 post-scale into f32 [4096 x 3072])."""
+    m, n, k = 4096, 3072, 128
+    p = synth.make_problem(1, n, k, seed=6)
+    _, w, s, b = synth.to_device(p)
+    lin = imq.QuantizedLinear(w, s.half(), b.half())
+    lat = torch.randn((m, k), device="cuda")
+    y = torch.empty((m, n), device="cuda")
+    x16 = torch.empty((m, k), dtype=torch.float16, device="cuda")
+    launches = [lambda: imq.cast_prescale(lat, 16.0, torch.float16, out=x16),
+                lambda: imq.qmm_postscale(x16, lin.weight, lin.scales, lin.biases, 16.0, out=y)]
+    ms = time_graph(launches, replays=10) * 2
+    qmm_ms = time_graph(launches[1:], replays=10)
+    tf = 2.0 * m * n * k / (qmm_ms * 1e-3) / 1e12
+    byts = m * n * 4 + m * k * 2 + n * k // 2
+    log(f"x_embedder sandwich M={m} N={n} K={k}: {ms * 1e3:.1f} us (qmm + post-scale "
+        f"{qmm_ms * 1e3:.1f} us, {tf:.1f} TFLOP/s, {byts / (qmm_ms * 1e-3) / 1e9:.0f} GB/s)")
+    return {"us": round(ms * 1e3, 2), "qmm_postscale_us": round(qmm_ms * 1e3, 2),
+            "TFLOP/s": round(tf, 1), "GB/s": round(byts / (qmm_ms * 1e-3) / 1e9, 1)}
+
+
 def bench_qgemm_shape(imq, synth, torch, m, n, k, reps=10, dispatcher=False) -> dict:
     """One qGEMM shape: imq_qgemm (the tile kernel), or with dispatcher=True
     imq_qmm_t (which may split K for shapes with few output tiles)."""
@@ -507,8 +553,9 @@ def main() -> int:
     ap.add_argument("--only-target", action="store_true",
                     help="time the headline qGEMM only (for profiling runs)")
     ap.add_argument("--only-hbm", action="store_true",
-                    help="run the M=1 qGEMV and dequantize benchmarks and a calibration copy only "
-                         "(for counter runs)")
+                    help="run the HBM-bound and few-row kernels only (M=1 qGEMV, few-row M=4/8/16, "
+                         "dequantize, pre-scale, RMSNorm, the K=128 x_embedder) and a calibration "
+                         "copy (for counter runs)")
     ap.add_argument("--floors", action="store_true",
                     help="run the launch and streaming-read floor kernels only (for profiling runs)")
     ap.add_argument("--only-step", action="store_true",
@@ -536,8 +583,11 @@ def main() -> int:
         bench_dit_step(torch)
         return 0
     if args.only_hbm:
-        bench_qgemv(imq, synth, torch, ms_list=(1,), few_rows=())
+        bench_qgemv(imq, synth, torch, ms_list=(1,), few_rows=(4, 8, 16))
         bench_dequant(imq, synth, torch)
+        bench_prescale(imq, torch)
+        bench_rmsnorm(imq, torch)
+        bench_x_embedder(imq, synth, torch)
         src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
         dst.copy_(src)
@@ -594,6 +644,8 @@ def main() -> int:
         extra["te_layer"] = bench_te_layer(torch)
         extra["dequant"] = bench_dequant(imq, synth, torch)
         extra["prescale"] = bench_prescale(imq, torch)
+        extra["rmsnorm"] = bench_rmsnorm(imq, torch)
+        extra["x_embedder"] = bench_x_embedder(imq, synth, torch)
         extra["qgemm_shapes"] = {
             "M1024_N9216_K3072": bench_qgemm_shape(imq, synth, torch, 1024, 9216, 3072,
                                                    dispatcher=True),
@@ -630,7 +682,10 @@ def main() -> int:
                    "m": m, "n": n, "k": k, "group_size": 64, "bits": 4},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic_from_profiles()},
+                     "traffic": traffic_from_profiles(),
+                     "traffic_source": "profiles/qgemm_target_traffic.md: rocprofv3 --pmc "
+                                       "FETCH_SIZE / WRITE_SIZE of this kernel and shape, scaled "
+                                       "by a 256 MiB copy in the same process (not this run)"},
         "device": {"name": props.name, "cus": props.multi_processor_count,
                    "hip": torch.version.hip},
     }

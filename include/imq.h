@@ -242,6 +242,14 @@ int imq_qmm_postscale_ex(imq_ctx* ctx, const uint32_t* w, const void* scales, co
                          float scale, const float* scale_dev, int group_size, int bits,
                          imq_dtype dtype, imq_stream stream);
 
+/* Row RMSNorm y[r][c] = T(x[r][c] * rsqrt(mean_c(x[r]^2) + eps) * w[c]) (fp32
+ * sum of squares, fp32 weight w [cols]): the DiT's dd_rmsnorm_pitched on its
+ * fp32 residual (x_dtype IMQ_F32, DirectDiTKernels.swift:61-99) and the text
+ * encoder's dq_rmsnorm on its T stream (x_dtype == y_dtype,
+ * DirectGlueKernels.swift:14-49); y_dtype bf16 or f16. */
+int imq_rmsnorm(imq_ctx* ctx, const void* x, imq_dtype x_dtype, const float* w, void* y,
+                imq_dtype y_dtype, int rows, int cols, float eps, imq_stream stream);
+
 /* y[M, N] (T) = T(float(residual) + float(T(x . deq(W)^T))), residual T [M, N]:
  * the text encoder's qmm followed by dq_add (DirectTEEncoder.swift:390-392,
  * 409-411; DirectGlueKernels.swift:88-96).  y may equal residual. */

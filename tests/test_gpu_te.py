@@ -81,6 +81,38 @@ def check(got: np.ndarray, want: np.ndarray, what: str, tol: float = NORMWISE_TO
     assert normwise <= tol, (what, normwise)
 
 
+# --------------------------------------------------------------------- RMSNorm
+
+
+@pytest.mark.parametrize("x_dtype,y_dtype,cols,eps", [
+    (torch.float32, torch.float16, 3072, 1e-5), (torch.float32, torch.bfloat16, 3072, 1e-5),
+    (torch.bfloat16, torch.bfloat16, 2560, 1e-6), (torch.float16, torch.float16, 2560, 1e-6),
+    (torch.float32, torch.bfloat16, 1000, 1e-5), (torch.bfloat16, torch.bfloat16, 1004, 1e-6)])
+def test_rmsnorm(x_dtype, y_dtype, cols, eps):
+    """imq_rmsnorm against the float64 RMSNorm rounded once to T (cols 1004: the
+    T-input kernel's scalar form, the others its 16-byte form): the fp32 sum of
+    squares and rsqrt move a value across a rounding boundary rarely, by one
+    unit in the last place of T (at most 0.5% of the values here, none by more)."""
+    note(f"rmsnorm {x_dtype} -> {y_dtype} cols={cols}")
+    g = torch.Generator(device="cuda").manual_seed(cols)
+    x = (torch.randn((300, cols), device="cuda", generator=g) * 3).to(x_dtype)
+    w = 1.0 + 0.1 * torch.randn(cols, device="cuda", generator=g)
+    y = imq.rmsnorm(x, w, eps, out_dtype=y_dtype)
+    want = to_t(ref.rmsnorm_rows(vals(x).astype(np.float64), vals(w), eps), y_dtype)
+    got = vals(y)
+    if y_dtype == torch.float16:
+        gi = got.astype(np.float16).view(np.int16).astype(np.int64)
+        wi = want.astype(np.float16).view(np.int16).astype(np.int64)
+    else:
+        gi = ref.f32_to_bf16(got).astype(np.int64)
+        wi = ref.f32_to_bf16(want).astype(np.int64)
+    ulps = np.abs(gi - wi)
+    note(f"  equal={np.mean(ulps == 0):.5f} max_ulps={ulps.max()}")
+    assert ulps.max() <= 1 and np.mean(ulps == 0) >= 0.995
+    with pytest.raises(imq.ImqUnsupported):  # a 16-bit x of another type than y
+        imq.rmsnorm(x.half(), w, eps, out_dtype=torch.bfloat16)
+
+
 # ------------------------------------------------------------- qmm + dq_add
 
 
