@@ -47,17 +47,16 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c)
 }
 
 // x staged in LDS when the whole [M, K] tile fits kXLdsMax bytes (rounded up
-// to whole wave instructions, or with 16-byte row pads): one 16-byte DMA per
-// lane and slot instead of four register loads per chunk and lane.  96 KiB
-// against 64: [9728 x 2560] M = 16 14.1 -> 13.3 us, [2560 x 9728] M = 4 12.0
-// -> 11.3 us, the rest equal.
+// to whole wave instructions): one 16-byte DMA per lane and slot instead of
+// four register loads per chunk and lane.  96 KiB against 64: [9728 x 2560]
+// M = 16 14.1 -> 13.3 us, [2560 x 9728] M = 4 12.0 -> 11.3 us, the rest equal.
+// The rows are 2 K bytes apart, so the 16 rows of a B-operand read share a
+// bank group (about 11 conflict cycles per LDS read); rows padded by 16 bytes
+// as in the multi-tile kernel remove that but measured 4-7% slower at M = 4,
+// 5 and 8 (same box, identical outputs): the reads hide under the weight stream.
 constexpr int kXLdsMax = 96 * 1024;
 
-// XMODE: 0 x from memory into registers; 1 x in LDS row-major (rows 2 K bytes
-// apart); 2 x in LDS with rows 2 K + 16 bytes apart (K % 512 == 0: a row is a
-// whole number of 1 KB wave instructions), so the 16 rows of one B-operand
-// read fall in 16 different 16-byte bank groups instead of one.
-template <int T, int W, int U, int XMODE>
+template <int T, int W, int U, bool XLDS>
 __global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restrict__ w,
                                                          const uint16_t* __restrict__ scales,
                                                          const uint16_t* __restrict__ biases,
@@ -65,8 +64,7 @@ __global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restr
                                                          uint16_t* __restrict__ y, int M, int N,
                                                          int K, bool vec) {
   __shared__ f32x4_t part[W][64];
-  constexpr bool XLDS = XMODE != 0;
-  extern __shared__ uint4 xs[];  // XLDS: x[M][K], rows 2 K (XMODE 1) or 2 K + 16 (2) bytes apart
+  extern __shared__ uint4 xs[];  // XLDS: x[M][K] as 16-byte slots, row-major
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, h = lane >> 4;
@@ -81,25 +79,14 @@ __global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restr
   const uint32_t w_off = (uint32_t)row * (uint32_t)(K / 2) + (uint32_t)h * 16u;
   const uint32_t p_off = ((uint32_t)row * (uint32_t)gpr + (uint32_t)(h >> 1)) * 2u;
   const uint32_t x_off = (uint32_t)c * (uint32_t)K * 2u + (uint32_t)h * 64u;
-  const uint32_t xs_off = (uint32_t)c * (uint32_t)(XMODE == 2 ? 2 * K + 16 : 2 * K) + (uint32_t)h * 64u;
   const bool has_x = c < M;
 
-  if constexpr (XMODE == 1) {
+  if constexpr (XLDS) {
     // Slot i * 64 W + 64 wave + lane; lanes past the tile read past x (zeros)
     // into the rounded-up part of the allocation.
     const int slots = M * K / 8, per = 64 * W;
     for (int i = 0; i * per < slots; ++i)
       load_lds16(xr, (uint32_t)(i * per + wave * 64 + lane) * 16u, 0u, xs + i * per + wave * 64);
-    __builtin_amdgcn_sched_barrier(0);
-  } else if constexpr (XMODE == 2) {
-    // One wave instruction per 1 KB piece q of the tile: row m = q / rp, part
-    // q % rp (wave-uniform), to LDS row m at a stride of 2 K + 16 bytes.
-    const int rp = K >> 9, pieces = M * rp;
-    for (int q = wave; q < pieces; q += W) {
-      const int m = q / rp, part = q - m * rp;
-      load_lds16(xr, (uint32_t)lane * 16u, (uint32_t)(m * K * 2 + part * 1024),
-                 reinterpret_cast<char*>(xs) + m * (2 * K + 16) + part * 1024);
-    }
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -153,7 +140,7 @@ __global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restr
           // B fragment read from the staged tile right before its MFMA.
           const uint32_t ch = (uint32_t)min(ch0 + u * W, chunks - 1);
           xj = has_x ? *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(xs) +
-                                                          xs_off + ch * 256u + j * 16u)
+                                                          x_off + ch * 256u + j * 16u)
                      : u32x4_t{0u, 0u, 0u, 0u};
         } else {
           xj = xv[u][j];
@@ -333,25 +320,18 @@ hipError_t launch_w(const uint32_t* w, const uint16_t* s, const uint16_t* b, con
   // Chunks per wave, all loaded before any is computed (one memory round trip).
   const int chunks = k / kChunkK, u = (chunks + W - 1) / W;
   const dim3 grid((unsigned)((n + kRows - 1) / kRows)), block(64 * W);
-  // LDS for the x tile: with K % 512 == 0 rows padded by 16 bytes (whole 1 KB
-  // wave instructions per row); otherwise the slots rounded up to whole
-  // wave-instruction rounds.
+  // LDS for the x tile: the slots rounded up to whole wave-instruction rounds.
   const size_t per = 64 * (size_t)W, slots = (size_t)m * k / 8;
-  const bool padded = k % 512 == 0;
-  const size_t xbytes =
-      padded ? (size_t)m * (2 * (size_t)k + 16) : (slots + per - 1) / per * per * 16;
+  const size_t xbytes = (slots + per - 1) / per * per * 16;
   const bool xlds = xbytes <= (size_t)kXLdsMax;
 #define IMQ_SKINNY(UU)                                                                            \
   do {                                                                                           \
-    if (xlds && padded)                                                                          \
-      hipLaunchKernelGGL((qskinny_kernel<T, W, UU, 2>), grid, block, xbytes, stream, w, s, b, x, \
-                         y, m, n, k, vec);                                                       \
-    else if (xlds)                                                                               \
-      hipLaunchKernelGGL((qskinny_kernel<T, W, UU, 1>), grid, block, xbytes, stream, w, s, b, x, \
-                         y, m, n, k, vec);                                                       \
+    if (xlds)                                                                                    \
+      hipLaunchKernelGGL((qskinny_kernel<T, W, UU, true>), grid, block, xbytes, stream, w, s, b, \
+                         x, y, m, n, k, vec);                                                    \
     else                                                                                         \
-      hipLaunchKernelGGL((qskinny_kernel<T, W, UU, 0>), grid, block, 0, stream, w, s, b, x, y,   \
-                         m, n, k, vec);                                                          \
+      hipLaunchKernelGGL((qskinny_kernel<T, W, UU, false>), grid, block, 0, stream, w, s, b, x,  \
+                         y, m, n, k, vec);                                                       \
   } while (0)
   if (u <= 2) IMQ_SKINNY(2);
   else if (u <= 3) IMQ_SKINNY(3);

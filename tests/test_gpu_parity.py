@@ -240,10 +240,9 @@ def test_split_k_dispatcher(m, n, k):
                                    (12, 9728, 2560), (16, 9728, 2560), (14, 3000, 4096)])
 def test_few_row_matrix_core_dispatch(dtype, m, n, k):
     """4 <= M <= 16 through the dispatcher.  The 16-row weight-streaming kernel
-    stages x in LDS when it fits 96 KiB -- with K % 512 == 0 rows of 2 K + 16
-    bytes (M = 4 and 5 at K = 9728: 76 and 95 KiB, M = 8 at K = 2560), else
-    M K 2 rounded up to whole wave instructions (K = 128 and 192) -- and M = 6 and 16 at K = 9728 (114 KiB and more) load x per chunk into
-    registers.
+    stages x in LDS when M K 2, rounded up to whole wave instructions, fits
+    96 KiB: M = 4 and 5 at K = 9728 (80 and exactly 96 KiB) take that path,
+    M = 6 and 16 there (128 KiB and more) load x per chunk into registers.
     12 <= M <= 16 with K <= 4096 (K % 512 == 0) take the multi-tile kernel
     with x in LDS: [9728 x 2560] at M = 12 and 16 (three 16-row tiles per
     workgroup, the last workgroup two), 3000 x 4096 at M = 14 (a partial last
