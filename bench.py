@@ -313,8 +313,10 @@ def bench_rmsnorm(imq, torch, copies: int = 4) -> dict:
         xs = [torch.randn((m, k), device="cuda").to(xdt) for _ in range(copies)]
         ys = [torch.empty((m, k), dtype=ydt, device="cuda") for _ in range(copies)]
         w = torch.ones(k, device="cuda")
-        launches = [(lambda i=i: imq.rmsnorm(xs[i], w, 1e-5, out_dtype=ydt, out=ys[i]))
-                    for i in range(copies)]
+        # 32 launches per graph: a graph of a few microsecond-long kernels
+        # would otherwise be timed by its own launch latency.
+        launches = [(lambda i=i: imq.rmsnorm(xs[i % copies], w, 1e-5, out_dtype=ydt,
+                                             out=ys[i % copies])) for i in range(32)]
         ms = time_graph(launches, replays=4)
         byts = m * k * per + 4 * k
         gbs = byts / (ms * 1e-3) / 1e9
