@@ -209,7 +209,15 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
   auto st = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
   if (skinny) {
-    e = imq::launch_qskinny(w, s, b, x, y, k, n, m, (int)dtype, st);
+    // The few-row kernel may split K over a workspace (long K, few row tiles).
+    imq::SplitWs ws{};
+    const size_t need = imq::qskinny_split_bytes(k, n, m);
+    if (regime == Regime::kAuto) {
+      ws = split_ws(ctx, st, need);
+    } else if (regime == Regime::kAutoNoAlloc && need > 0 && need <= imq::kStaticScratchBytes) {
+      ws = imq::SplitWs{static_cast<float*>(ctx->static_scratch), need};
+    }
+    e = imq::launch_qskinny(w, s, b, x, y, k, n, m, (int)dtype, st, ws);
   } else if (!gemv) {
     // The dispatcher may split K over a workspace; imq_qgemm is the plain
     // tile kernel (the fused output stages equal it bit for bit).
@@ -463,7 +471,8 @@ int imq_qmm_plan(imq_ctx* ctx, int entry, int k, int n, int m, imq_dtype dtype, 
       const bool gemv = w_fits_gemv && (m <= imq::kDispatchGemvMaxM || dtype == IMQ_F32);
       if (m >= imq::kDispatchSkinnyMinM && m <= imq::kDispatchSkinnyMaxM &&
           imq::qskinny_supported(k, n, m, (int)dtype)) {
-        *out = imq_plan{IMQ_KERNEL_FEW_ROW, 0, 1, 0};
+        const size_t need = imq::qskinny_split_bytes(k, n, m);
+        *out = imq_plan{IMQ_KERNEL_FEW_ROW, 0, need ? imq::qskinny_splits(k, n, m) : 1, need};
         return IMQ_OK;
       }
       if (gemv) {

@@ -169,7 +169,14 @@ hipError_t static_scratch(int device, void** out);
 // k % 128 == 0, T in {bf16, f16}, 32-bit byte offsets.
 bool qskinny_supported(int k, int n, int m, int dtype);
 // y[m][n] = x . deq(W)^T on the matrix cores, 16 weight rows per workgroup.
+// With a workspace of at least qskinny_split_bytes(k, n, m) (nonzero when the
+// row tiles leave CUs idle and K % 512 == 0, m >= 4), K is split over
+// qskinny_splits(k, n, m) workgroup ranges whose fp32 partial sums a second
+// kernel adds in order; without one the unsplit kernels run.
+size_t qskinny_split_bytes(int k, int n, int m);
+int qskinny_splits(int k, int n, int m);
 hipError_t launch_qskinny(const uint32_t* w, const void* scales, const void* biases, const void* x,
-                          void* y, int k, int n, int m, int dtype, hipStream_t stream);
+                          void* y, int k, int n, int m, int dtype, hipStream_t stream,
+                          SplitWs ws = {});
 
 }  // namespace imq

@@ -424,9 +424,269 @@ hipError_t launch_lds_t(const uint32_t* w, const uint16_t* s, const uint16_t* b,
   return launch_lds_tw<T, TPW, kLdsWaves>(w, s, b, x, y, k, n, m, p.u, vec, stream);
 }
 
+// ---- K split: the multi-tile kernel over a range of K, for long K ----
+//
+// Workgroup (g, s) owns TPW 16-row tiles and the K pieces [s per, s per + per)
+// (512 k each, the last range shorter); it stages only its x slice [M, 512
+// per] in LDS (rows 1024 per + 16 bytes apart) and writes fp32 partial sums
+// to ws[s][m][n]; qskinny_reduce_kernel adds the splits in order and rounds
+// to T (deterministic).  For [2560 x 9728] (160 row tiles, x of 16 rows 311
+// KB) the 16-row kernel re-reads all of x from L2 per tile (about 50 MB for
+// 12.5 MB of weights) on 160 workgroups; here each x byte is read once per
+// tile group and split and the grid fills the CUs.
+template <int T, int TPW, int W, int U>
+__global__ __launch_bounds__(64 * W) void qskinny_split_kernel(const uint32_t* __restrict__ w,
+                                                               const uint16_t* __restrict__ scales,
+                                                               const uint16_t* __restrict__ biases,
+                                                               const uint16_t* __restrict__ x,
+                                                               float* __restrict__ ws, int M,
+                                                               int N, int K, int per, bool vec) {
+  constexpr int kWeightLoads = 3 * U * TPW < 63 ? 3 * U * TPW : 63;
+  __shared__ f32x4_t part[W][TPW][64];
+  extern __shared__ uint4 xs[];  // x [M, 512 per], rows 1024 per + 16 bytes apart
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, h = lane >> 4;
+  const int n0 = blockIdx.x * (kRows * TPW);
+  const int gpr = K >> 6;
+  const int p0 = (int)blockIdx.y * per;
+  const int np = min(per, (K >> 9) - p0);  // pieces of 512 k in this range (>= 1)
+  const int chunks = np * 4;
+  const int c0 = p0 * 4;                   // first global chunk of 128 k
+  const int xstride = 1024 * per + 16;
+  const auto wr = make_rsrc(w, (uint32_t)((size_t)N * K / 2));
+  const auto sr = make_rsrc(scales, (uint32_t)((size_t)N * gpr * 2));
+  const auto br = make_rsrc(biases, (uint32_t)((size_t)N * gpr * 2));
+  const auto xr = make_rsrc(x, (uint32_t)((size_t)M * K * 2));
+
+  // 1. The x slice -> LDS, one wave instruction per 1 KB piece (row m = q /
+  //    np, piece q % np, wave-uniform).
+  {
+    const int pieces = M * np;
+    for (int q = wave; q < pieces; q += W) {
+      const int m = q / np, pc = q - m * np;
+      load_lds16(xr, (uint32_t)lane * 16u, (uint32_t)((m * K + (p0 + pc) * 512) * 2),
+                 reinterpret_cast<char*>(xs) + m * xstride + pc * 1024);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  uint32_t w_off[TPW], p_off[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const uint32_t row = (uint32_t)min(n0 + kRows * t + c, N - 1);
+    w_off[t] = row * (uint32_t)(K / 2) + (uint32_t)h * 16u;
+    p_off[t] = (row * (uint32_t)gpr + (uint32_t)(h >> 1)) * 2u;
+  }
+  f32x4_t acc[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int xrow = min(c, M - 1);
+  bool first = true;
+  for (int ch0 = wave; ch0 < chunks; ch0 += W * U) {
+    u32x4_t wv[U][TPW];
+    uint16_t sv[U][TPW], bv[U][TPW];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t ch = (uint32_t)(c0 + min(ch0 + u * W, chunks - 1));
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        wv[u][t] = load_b128(wr, w_off[t], ch * 64u);
+        sv[u][t] = __builtin_amdgcn_raw_buffer_load_b16(sr, p_off[t], ch * 4u, 0);
+        bv[u][t] = __builtin_amdgcn_raw_buffer_load_b16(br, p_off[t], ch * 4u, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (first) {
+      IMQ_WAIT_VMCNT(kWeightLoads);
+      __builtin_amdgcn_s_barrier();
+      first = false;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool valid = ch0 + u * W < chunks;
+      const int j = min(ch0 + u * W, chunks - 1);
+      u32x4_t xf[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xf[i] = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(xs) +
+                                                   xrow * xstride + j * 256 + (4 * h + i) * 16);
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const float sc = valid ? Elem<T>::param(sv[u][t]) : 0.0f;
+        const float s24 = sc * 0x1p24f, s20 = sc * 0x1p20f;
+        const float b = valid ? Elem<T>::param(bv[u][t]) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          uint32_t pq[4];
+          Elem<T>::dequant(wv[u][t][i], s24, s20, b, pq);
+          acc[t] = mfma16x16x32<T>(u32x4_t{pq[0], pq[1], pq[2], pq[3]}, xf[i], acc[t]);
+        }
+      }
+    }
+  }
+  if (first) {
+    IMQ_WAIT_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+  }
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) part[wave][t][lane] = acc[t];
+  __syncthreads();
+  if (wave >= TPW || c >= M) return;
+  const int t = wave;
+  f32x4_t sum = part[0][t][lane];
+#pragma unroll
+  for (int i = 1; i < W; ++i) sum += part[i][t][lane];
+  const int f0 = n0 + kRows * t + 4 * h;
+  float* dst = ws + ((size_t)blockIdx.y * M + c) * N;
+  if (vec && f0 + 3 < N) {
+    *reinterpret_cast<float4*>(dst + f0) = make_float4(sum[0], sum[1], sum[2], sum[3]);
+  } else {
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      if (f0 + v < N) dst[f0 + v] = sum[v];
+  }
+}
+
+// y[i] = T(sum over s of ws[s][i]) for i < count (= M N), splits added in order.
+// y[i] = T(sum over s of ws[s][i]) for i < count (= M N), splits added in
+// order.  VEC (count % 4 == 0, y 8-byte aligned): four outputs per thread,
+// 16-byte partial loads, an 8-byte store; otherwise one output per thread.
+template <int T, bool VEC>
+__global__ __launch_bounds__(256) void qskinny_reduce_kernel(const float* __restrict__ ws,
+                                                             int splits, int count,
+                                                             uint16_t* __restrict__ y) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if constexpr (VEC) {
+    const int i = t * 4;
+    if (i >= count) return;
+    float4 a = *reinterpret_cast<const float4*>(ws + i);
+#pragma unroll 4
+    for (int sp = 1; sp < splits; ++sp) {
+      const float4 v = *reinterpret_cast<const float4*>(ws + (size_t)sp * count + i);
+      a.x += v.x;
+      a.y += v.y;
+      a.z += v.z;
+      a.w += v.w;
+    }
+    *reinterpret_cast<uint2*>(y + i) = make_uint2(Elem<T>::pack2(a.x, a.y), Elem<T>::pack2(a.z, a.w));
+  } else {
+    if (t >= count) return;
+    float a = ws[t];
+#pragma unroll 4
+    for (int sp = 1; sp < splits; ++sp) a += ws[(size_t)sp * count + t];
+    y[t] = Elem<T>::out(a);
+  }
+}
+
+struct SplitPlan {
+  int tpw, per, splits, u;
+  bool ok;
+};
+
+constexpr int kSplitWaves = 8;
+
+// Bytes of the split kernel's x slice in LDS.
+size_t split_x_bytes(int per, int m) { return (size_t)m * (1024 * (size_t)per + 16); }
+
+// Taken where the unsplit kernels stream x per chunk from L2 (x [M, K] past
+// the 96 KiB LDS budget and not the multi-tile kernel's case), M >= 8, and
+// the 16-row workgroups are few (at most 128) or long (K >= 8192).  Measured
+// with the weights from HBM (same box, A/B builds): [2560 x 9728] M = 8 / 12
+// / 16 13.9 / 15.9 / 18.1 -> 13.2 / 13.5 / 13.8 us, [1000 x 4608] M = 12 9.5
+// -> 6.3 us, [1030 x 4608] M = 13 9.6 -> 6.6 us; elsewhere slower: M = 4 and
+// 5 at K = 9728 (x in LDS: 11.7 -> 12.2, 11.9 -> 12.9 us), [2560 x 4096] M =
+// 16 (9.4 -> 10.0), [3072 x 3072] at M = 4 / 8 / 16 (6.3 -> 8.3-8.9 us): there
+// the second launch and the partial sums cost more than the better-filled
+// grid saves.  Among the plans whose x slice fits 64 KB and whose grid fills
+// the CUs: the least estimated L2 traffic (x slices, weights, partial sums).
+SplitPlan plan_split(int k, int n, int m) {
+  SplitPlan best{0, 0, 0, 0, false};
+  if (k % 512 != 0 || k / 512 < 2 || m < 8) return best;
+  const int pieces = k / 512;
+  const long tiles = (n + kRows - 1) / kRows;
+  if (tiles >= 256 || (tiles > 128 && k < 8192)) return best;
+  if ((size_t)m * k * 2 <= (size_t)kXLdsMax || plan_lds(k, n, m).ok) return best;
+  long best_traffic = -1;
+  for (int tpw = 1; tpw <= 4; ++tpw) {
+    const long groups = (tiles + tpw - 1) / tpw;
+    for (int per = 1; per <= pieces; ++per) {
+      const int splits = (pieces + per - 1) / per;
+      if (splits < 2 || groups * splits < 256) continue;
+      if (split_x_bytes(per, m) > 64 * 1024) continue;
+      const long traffic = groups * splits * ((long)m * per * 1024 + (long)tpw * kRows * per * 256) +
+                           (long)splits * m * n * 8;
+      if (best_traffic < 0 || traffic < best_traffic) {
+        best_traffic = traffic;
+        const int chunks = per * 4;
+        const int u = std::max(1, std::min((chunks + kSplitWaves - 1) / kSplitWaves,
+                                           max_u_lds(tpw, kSplitWaves)));
+        best = SplitPlan{tpw, per, splits, u, true};
+      }
+    }
+  }
+  return best;
+}
+
+template <int T, int TPW, int U>
+hipError_t launch_split_tu(const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                           const uint16_t* x, float* ws, int k, int n, int m, const SplitPlan& p,
+                           bool vec, hipStream_t stream) {
+  if constexpr (U > max_u_lds(TPW, kSplitWaves)) {
+    return hipErrorInvalidValue;
+  } else {
+    const dim3 grid((unsigned)((n + kRows * TPW - 1) / (kRows * TPW)), (unsigned)p.splits);
+    hipLaunchKernelGGL((qskinny_split_kernel<T, TPW, kSplitWaves, U>), grid, dim3(64 * kSplitWaves),
+                       split_x_bytes(p.per, m), stream, w, s, b, x, ws, m, n, k, p.per, vec);
+    return hipGetLastError();
+  }
+}
+
+template <int T, int TPW>
+hipError_t launch_split_t(const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                          const uint16_t* x, float* ws, int k, int n, int m, const SplitPlan& p,
+                          bool vec, hipStream_t stream) {
+  switch (p.u) {
+    case 1: return launch_split_tu<T, TPW, 1>(w, s, b, x, ws, k, n, m, p, vec, stream);
+    case 2: return launch_split_tu<T, TPW, 2>(w, s, b, x, ws, k, n, m, p, vec, stream);
+    case 3: return launch_split_tu<T, TPW, 3>(w, s, b, x, ws, k, n, m, p, vec, stream);
+    case 4: return launch_split_tu<T, TPW, 4>(w, s, b, x, ws, k, n, m, p, vec, stream);
+    case 5:
+    case 6: return launch_split_tu<T, TPW, 6>(w, s, b, x, ws, k, n, m, p, vec, stream);
+    default: return launch_split_tu<T, TPW, 8>(w, s, b, x, ws, k, n, m, p, vec, stream);
+  }
+}
+
+template <int T>
+hipError_t launch_split(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
+                        uint16_t* y, float* ws, int k, int n, int m, const SplitPlan& p,
+                        hipStream_t stream) {
+  const bool vec = n % 4 == 0 && ((uintptr_t)ws & 15u) == 0;
+  hipError_t e;
+  switch (p.tpw) {
+    case 1: e = launch_split_t<T, 1>(w, s, b, x, ws, k, n, m, p, vec, stream); break;
+    case 2: e = launch_split_t<T, 2>(w, s, b, x, ws, k, n, m, p, vec, stream); break;
+    case 3: e = launch_split_t<T, 3>(w, s, b, x, ws, k, n, m, p, vec, stream); break;
+    default: e = launch_split_t<T, 4>(w, s, b, x, ws, k, n, m, p, vec, stream); break;
+  }
+  if (e != hipSuccess) return e;
+  const int count = m * n;
+  if (count % 4 == 0 && ((uintptr_t)y & 7u) == 0)
+    hipLaunchKernelGGL((qskinny_reduce_kernel<T, true>), dim3((unsigned)((count / 4 + 255) / 256)),
+                       dim3(256), 0, stream, ws, p.splits, count, y);
+  else
+    hipLaunchKernelGGL((qskinny_reduce_kernel<T, false>), dim3((unsigned)((count + 255) / 256)),
+                       dim3(256), 0, stream, ws, p.splits, count, y);
+  return hipGetLastError();
+}
+
 template <int T>
 hipError_t launch_t(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
-                    uint16_t* y, int k, int n, int m, hipStream_t stream) {
+                    uint16_t* y, int k, int n, int m, hipStream_t stream, SplitWs ws) {
+  const SplitPlan sp = plan_split(k, n, m);
+  if (sp.ok && ws.p && ws.bytes >= (size_t)sp.splits * m * n * sizeof(float))
+    return launch_split<T>(w, s, b, x, y, ws.p, k, n, m, sp, stream);
   const bool vec = n % 4 == 0 && ((uintptr_t)y & 7u) == 0;
   const LdsPlan lp = plan_lds(k, n, m);
   if (lp.ok) {
@@ -454,15 +714,25 @@ bool qskinny_supported(int k, int n, int m, int dtype) {
          (size_t)m * k * 2 < ((size_t)1 << 31);
 }
 
+size_t qskinny_split_bytes(int k, int n, int m) {
+  const SplitPlan sp = plan_split(k, n, m);
+  return sp.ok ? (size_t)sp.splits * m * n * sizeof(float) : 0;
+}
+
+int qskinny_splits(int k, int n, int m) {
+  const SplitPlan sp = plan_split(k, n, m);
+  return sp.ok ? sp.splits : 1;
+}
+
 hipError_t launch_qskinny(const uint32_t* w, const void* scales, const void* biases, const void* x,
-                          void* y, int k, int n, int m, int dtype, hipStream_t stream) {
+                          void* y, int k, int n, int m, int dtype, hipStream_t stream, SplitWs ws) {
   if (!qskinny_supported(k, n, m, dtype)) return hipErrorInvalidValue;
   const auto* s = static_cast<const uint16_t*>(scales);
   const auto* b = static_cast<const uint16_t*>(biases);
   const auto* xx = static_cast<const uint16_t*>(x);
   auto* yy = static_cast<uint16_t*>(y);
-  if (dtype == kBf16) return launch_t<kBf16>(w, s, b, xx, yy, k, n, m, stream);
-  return launch_t<kF16>(w, s, b, xx, yy, k, n, m, stream);
+  if (dtype == kBf16) return launch_t<kBf16>(w, s, b, xx, yy, k, n, m, stream, ws);
+  return launch_t<kF16>(w, s, b, xx, yy, k, n, m, stream, ws);
 }
 
 }  // namespace imq

@@ -48,7 +48,7 @@ hipError_t plain_qmm(const imq_te* te, const imq_qweight& q, const void* x, void
   const int dt = (int)te->dtype;
   if (rows >= imq::kDispatchSkinnyMinM && rows <= imq::kDispatchSkinnyMaxM &&
       imq::qskinny_supported(q.k, q.n, rows, dt))
-    return imq::launch_qskinny(q.w, q.scales, q.biases, x, y, q.k, q.n, rows, dt, st);
+    return imq::launch_qskinny(q.w, q.scales, q.biases, x, y, q.k, q.n, rows, dt, st, te->split);
   if (rows <= imq::kDispatchGemvMaxM)
     return imq::launch_qgemv(q.w, q.scales, q.biases, x, y, q.k, q.n, rows, dt, st);
   return imq::launch_qgemm(q.w, q.scales, q.biases, x, y, q.k, q.n, rows, dt, st, te->split);
@@ -115,6 +115,8 @@ int imq_te_create(imq_ctx* ctx, const imq_te_layer_weights* layers, int n_layers
   size_t ws = 0;
   for (int rows = 1; rows <= max_rows; ++rows) {
     ws = std::max(ws, imq::qgemm_split_bytes(hidden, l0.qkv.n, rows, false));
+    if (rows <= imq::kDispatchSkinnyMaxM)
+      ws = std::max(ws, imq::qskinny_split_bytes(hidden, l0.qkv.n, rows));
     ws = std::max(ws, imq::qgemm_split_bytes(nq, hidden, rows, true));
     ws = std::max(ws, imq::qgemm_split_bytes(hidden, 2 * inter, rows, true));
     ws = std::max(ws, imq::qgemm_split_bytes(inter, hidden, rows, true));

@@ -86,8 +86,10 @@ bool qskinny_supported(int k, int n, int m, int dtype) {
          (dtype == 0 || dtype == 1) && (size_t)n * k / 2 < ((size_t)1 << 32) &&
          (size_t)m * k * 2 < ((size_t)1 << 31);
 }
+size_t qskinny_split_bytes(int, int, int) { return 0; }
+int qskinny_splits(int, int, int) { return 1; }
 hipError_t launch_qskinny(const uint32_t*, const void*, const void*, const void*, void*, int, int,
-                          int, int, hipStream_t) {
+                          int, int, hipStream_t, SplitWs) {
   return hipErrorNoDevice;
 }
 

@@ -233,11 +233,27 @@ def test_split_k_dispatcher(m, n, k):
     assert np.array_equal(yo, bits(imq.dequantize(w, s, b))[:, cols].T)
 
 
+@pytest.mark.parametrize("m,n,k,splits", [(16, 2560, 9728, 10), (12, 2560, 9728, 10),
+                                          (12, 1000, 4608, 9), (8, 2560, 9728, 10),
+                                          (6, 2560, 9728, 1), (4, 2560, 9728, 1), (16, 2560, 4096, 1),
+                                          (16, 9728, 2560, 1), (3, 2560, 9728, 1)])
+def test_few_row_split_plan(m, n, k, splits):
+    """imq_qmm_plan reports the few-row kernel's K split and its workspace: taken
+    from M = 8 where x streams from L2 and the 16-row workgroups are few or
+    long ([2560 x 9728], 1000 x 4608), not below M = 8, not at K = 4096 with
+    160 tiles, not for [9728 x 2560] (608 tiles)."""
+    plan = imq.qmm_plan(m, n, k, torch.bfloat16)
+    assert plan["kernel"] == "few_row", plan
+    assert plan["splits"] == splits, plan
+    assert plan["workspace_bytes"] == (splits * m * n * 4 if splits > 1 else 0), plan
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("m,n,k", [(4, 384, 512), (5, 384, 512), (16, 1001, 1024), (13, 17, 128),
                                    (8, 9728, 2560), (4, 2560, 9728), (5, 2560, 9728),
-                                   (6, 2560, 9728), (16, 2560, 9728), (9, 384, 192),
-                                   (12, 9728, 2560), (16, 9728, 2560), (14, 3000, 4096)])
+                                   (6, 2560, 9728), (8, 2560, 9728), (16, 2560, 9728),
+                                   (9, 384, 192), (12, 9728, 2560), (16, 9728, 2560),
+                                   (14, 3000, 4096), (12, 1000, 4608), (13, 1030, 4608)])
 def test_few_row_matrix_core_dispatch(dtype, m, n, k):
     """4 <= M <= 16 through the dispatcher.  The 16-row weight-streaming kernel
     stages x in LDS when M K 2, rounded up to whole wave instructions, fits
@@ -248,9 +264,13 @@ def test_few_row_matrix_core_dispatch(dtype, m, n, k):
     workgroup, the last workgroup two), 3000 x 4096 at M = 14 (a partial last
     tile), 1001 x 1024 at M = 16.  N = 1001 and 17 end in a partial row block
     and take the single-element stores; K = 128 is one chunk; K % 128 != 0
-    (K = 192) runs the tiled kernel.  Oracle within tolerance, the same bits on
+    (K = 192) runs the tiled kernel.  From M = 8, where x would stream from L2
+    and the 16-row workgroups are few or long, K is split over workgroups (fp32
+    partial sums added in order by a second kernel): [2560 x 9728] at M = 8 and
+    16, 1000 x 4608 at M = 12, 1030 x 4608 at M = 13 (N % 4 != 0: the
+    single-element partial stores and reduction).  Oracle within tolerance, the same bits on
     a second call, and one-hot rows reproduce the dequantized weights bit for
-    bit."""
+    bit (a one-hot row has one nonzero product in one split)."""
     note(f"few-row dispatch {dtype} M={m} N={n} K={k}")
     p = synth.make_problem(m, n, k, seed=23)
     x, w, s, b = synth.to_device(p)
