@@ -25,6 +25,7 @@ from .ops import (  # noqa: F401
     cast_prescale,
     context,
     dequantize,
+    dequantize_rows,
     dynamic_scale,
     qgemm,
     qgemv,

@@ -91,6 +91,7 @@ SIGNATURES = {
     "imq_cast_prescale_ex": ([_p, _p, _p, _sz, ctypes.c_float, _p, _i, _p], _i),
     "imq_qmm_postscale_ex": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, ctypes.c_float, _p, _i, _i,
                               _i, _p], _i),
+    "imq_dequantize_rows": ([_p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _p], _i),
     "imq_rmsnorm": ([_p, _p, _i, _p, _p, _i, _i, _i, ctypes.c_float, _p], _i),
     "imq_qmm_add": ([_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p], _i),
     "imq_qmm_gate_add": ([_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, ctypes.c_float, _i, _i, _i,

@@ -385,6 +385,39 @@ int imq_memcpy_d2h(imq_ctx* ctx, void* dst, const void* src, size_t bytes, imq_s
   return copy(ctx, "imq_memcpy_d2h", dst, src, bytes, hipMemcpyDeviceToHost, stream);
 }
 
+int imq_dequantize_rows(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                        const int32_t* rows, int count, void* out, int k, int n, int group_size,
+                        int bits, imq_dtype dtype, imq_stream stream) {
+  const char* fn = "imq_dequantize_rows";
+  if (!ctx) return fail(nullptr, IMQ_EINVAL, "%s: null context", fn);
+  if (group_size != 64)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: group_size %d (only 64 is provided)", fn, group_size);
+  if (bits != 4) return fail(ctx, IMQ_EUNSUPPORTED, "%s: bits %d (only 4 is provided)", fn, bits);
+  if (dtype != IMQ_BF16 && dtype != IMQ_F16 && dtype != IMQ_F32)
+    return fail(ctx, IMQ_EUNSUPPORTED, "%s: dtype %d (bf16, f16 and f32 are provided)", fn,
+                (int)dtype);
+  if (k <= 0 || n <= 0 || count < 0)
+    return fail(ctx, IMQ_EINVAL, "%s: shape K=%d N=%d count=%d", fn, k, n, count);
+  if (k % 64 != 0)
+    return fail(ctx, IMQ_EINVAL, "%s: K=%d is not a multiple of the group size 64", fn, k);
+  if ((size_t)count * (size_t)(k / 8) >= ((size_t)1 << 32))
+    return fail(ctx, IMQ_EINVAL, "%s: count %d x K %d past the kernel's 32-bit word index", fn,
+                count, k);
+  if (count == 0) return IMQ_OK;
+  if (!w || !scales || !biases || !rows || !out)
+    return fail(ctx, IMQ_EINVAL, "%s: null device pointer", fn);
+  const size_t es = elem_size(dtype);
+  if (!aligned(w, 4) || !aligned(rows, 4) || !aligned(out, 16) || !aligned(scales, es) ||
+      !aligned(biases, es))
+    return fail(ctx, IMQ_EINVAL, "%s: misaligned pointer (w, rows 4; out 16; scales, biases %zu)",
+                fn, es);
+  int rc = bind_device(ctx);
+  if (rc != IMQ_OK) return rc;
+  const hipError_t e = imq::launch_dequant_rows(w, scales, biases, rows, count, out, k, n,
+                                                (int)dtype, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
+}
+
 int imq_dequantize(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
                    void* out, int k, int n, int group_size, int bits, imq_dtype dtype,
                    imq_stream stream) {

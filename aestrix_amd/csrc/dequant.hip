@@ -106,6 +106,55 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint32_t* __res
   }
 }
 
+// Rows gathered by index (DirectTEEncoder.embedRow, :106-123, for a batch of
+// token ids): output row r is deq(W[rows[r]]); ids are clamped to [0, n) so a
+// bad id never reads outside W.  One thread per packed word, as above.
+template <typename Out>
+__global__ __launch_bounds__(kThreads) void dequant_rows_kernel(
+    const uint32_t* __restrict__ w, const typename Out::S* __restrict__ scales,
+    const typename Out::S* __restrict__ biases, const int32_t* __restrict__ rows,
+    u32x4_t* __restrict__ out, uint32_t total_words, uint32_t wpr, int n) {
+  const uint32_t o = blockIdx.x * (uint32_t)kThreads + threadIdx.x;
+  if (o >= total_words) return;
+  const uint32_t r = o / wpr, j = o - r * wpr;
+  const int id = min(max(rows[r], 0), n - 1);
+  const size_t wi = (size_t)id * wpr + j;
+  const uint32_t word = __builtin_nontemporal_load(w + wi);
+  const float s = Out::load(scales[wi >> 3]);
+  const float b = Out::load(biases[wi >> 3]);
+  const uint32_t lo = word & 0x0F0F0F0Fu;
+  const uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;
+  if constexpr (Out::kWordBytes == 16) {
+    uint32_t v[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+      v[p] = Out::pack(affine(s, (float)((lo >> (8 * p)) & 0xFFu), b),
+                       affine(s, (float)((hi >> (8 * p)) & 0xFFu), b));
+    out[o] = u32x4_t{v[0], v[1], v[2], v[3]};
+  } else {
+    uint32_t v[8];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      v[2 * p] = __float_as_uint(affine(s, (float)((lo >> (8 * p)) & 0xFFu), b));
+      v[2 * p + 1] = __float_as_uint(affine(s, (float)((hi >> (8 * p)) & 0xFFu), b));
+    }
+    out[2 * o] = u32x4_t{v[0], v[1], v[2], v[3]};
+    out[2 * o + 1] = u32x4_t{v[4], v[5], v[6], v[7]};
+  }
+}
+
+template <typename Out>
+hipError_t launch_rows_out(const uint32_t* w, const void* scales, const void* biases,
+                           const int32_t* rows, int count, void* out, int k, int n,
+                           hipStream_t stream) {
+  using S = typename Out::S;
+  const uint32_t wpr = (uint32_t)(k / 8), total = (uint32_t)count * wpr;
+  hipLaunchKernelGGL(dequant_rows_kernel<Out>, dim3((total + kThreads - 1) / kThreads),
+                     dim3(kThreads), 0, stream, w, static_cast<const S*>(scales),
+                     static_cast<const S*>(biases), rows, static_cast<u32x4_t*>(out), total, wpr, n);
+  return hipGetLastError();
+}
+
 template <typename Out>
 hipError_t launch_out(const uint32_t* w, const void* scales, const void* biases, void* out,
                       int64_t total, hipStream_t stream) {
@@ -126,6 +175,18 @@ hipError_t launch_out(const uint32_t* w, const void* scales, const void* biases,
 }
 
 }  // namespace
+
+hipError_t launch_dequant_rows(const uint32_t* w, const void* scales, const void* biases,
+                               const int32_t* rows, int count, void* out, int k, int n, int dtype,
+                               hipStream_t stream) {
+  if (count <= 0) return hipSuccess;
+  switch (dtype) {
+    case kBf16: return launch_rows_out<Bf16Out>(w, scales, biases, rows, count, out, k, n, stream);
+    case kF16: return launch_rows_out<F16Out>(w, scales, biases, rows, count, out, k, n, stream);
+    case kF32: return launch_rows_out<F32Out>(w, scales, biases, rows, count, out, k, n, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 hipError_t launch_dequant(const uint32_t* w, const void* scales, const void* biases, void* out,
                           int k, int n, int dtype, hipStream_t stream) {

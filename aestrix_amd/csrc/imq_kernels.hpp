@@ -13,6 +13,12 @@ namespace imq {
 hipError_t launch_dequant(const uint32_t* w, const void* scales, const void* biases, void* out,
                           int k, int n, int dtype, hipStream_t stream);
 
+// out[r][k] = deq(W)[clamp(rows[r], 0, n - 1)][k] for r < count (rows on the
+// device): the embedding rows of a batch of token ids.  count * k / 8 < 2^32.
+hipError_t launch_dequant_rows(const uint32_t* w, const void* scales, const void* biases,
+                               const int32_t* rows, int count, void* out, int k, int n, int dtype,
+                               hipStream_t stream);
+
 // y[m][n] = x . deq(W)^T for 1 <= m <= 16, T in {bf16, f16, f32}; no MFMA.
 hipError_t launch_qgemv(const uint32_t* w, const void* scales, const void* biases, const void* x,
                         void* y, int k, int n, int m, int dtype, hipStream_t stream);

@@ -294,6 +294,31 @@ def qmm_gate_add(x, w, scales, biases, residual: torch.Tensor, gate: torch.Tenso
     return out
 
 
+def dequantize_rows(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                    rows: torch.Tensor, group_size: int = GROUP_SIZE, bits: int = BITS,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """deq(W)[rows] [len(rows), K] in the scales' dtype: ``DirectTEEncoder.embedRow``
+    (``DirectTEEncoder.swift:106-123``) for a batch of token ids, one launch.
+    Ids are checked against [0, N) here (the kernel clamps them)."""
+    n, k = _check_weight(w, scales, biases, group_size, bits)
+    _require(rows.dim() == 1 and rows.dtype in (torch.int32, torch.int64), "rows: 1-D integer ids")
+    if rows.numel():
+        lo, hi = int(rows.min()), int(rows.max())
+        _require(0 <= lo and hi < n, f"ids must lie in [0, {n}), got [{lo}, {hi}]")
+    ids = rows.to(device=w.device, dtype=torch.int32).contiguous()
+    if out is None:
+        out = torch.empty((ids.numel(), k), dtype=scales.dtype, device=w.device)
+    _require(out.dtype == scales.dtype and out.is_contiguous() and tuple(out.shape) == (ids.numel(), k),
+             f"out must be a contiguous {scales.dtype} [{ids.numel()}, {k}] tensor")
+    ctx = context(w.device)
+    with torch.cuda.device(w.device):
+        st = _lib.load().imq_dequantize_rows(ctx, _ptr(w), _ptr(scales), _ptr(biases), _ptr(ids),
+                                             ids.numel(), _ptr(out), k, n, group_size, bits,
+                                             _DTYPES[scales.dtype], _stream(ids))
+    _lib.check(st, ctx)
+    return out
+
+
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5,
             out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """Row RMSNorm to T: x * rsqrt(mean(x^2) + eps) * weight with an fp32 sum of

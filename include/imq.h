@@ -107,6 +107,15 @@ int imq_dequantize(imq_ctx* ctx, const uint32_t* w, const void* scales, const vo
                    void* out, int k, int n, int group_size, int bits, imq_dtype dtype,
                    imq_stream stream);
 
+/* out[i, K] (T) = deq(W)[rows[i]] for i < count: DirectTEEncoder.embedRow
+ * (DirectTEEncoder.swift:106-123) for a batch of token ids in one launch, the
+ * same bits as imq_dequantize's rows.  rows: int32 [count] in device memory;
+ * an id outside [0, N) reads row clamp(id, 0, N - 1) (the ids are the
+ * caller's to validate; no read leaves W). */
+int imq_dequantize_rows(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
+                        const int32_t* rows, int count, void* out, int k, int n, int group_size,
+                        int bits, imq_dtype dtype, imq_stream stream);
+
 /* y[M, N] = x[M, K] . deq(W)^T -- the regime dispatcher.  Replaces the
  * dispatch of `affine_qmm_t_{T}_gs_64_b_4_alN_true_batch_0` in
  * DirectDiTStep.qmm (DirectDiTStep.swift:374-406), DirectTELayerSpike.encodeQmm

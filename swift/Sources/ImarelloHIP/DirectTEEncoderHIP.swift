@@ -12,7 +12,7 @@ public protocol TEAttentionCore: AnyObject {
 /// `DirectTEEncoder` (Sources/ImarelloDirect/DirectTEEncoder.swift) over include/imq_te.h:
 /// the layers `DirectTEForward.loadLayers` uploads (DirectTEForward.swift:97-138, raw
 /// bf16 parameters, q/k/v and gate/up concatenated), the embedding rows
-/// (`embedRow`, :106-123, on the device by imq_dequantize), and
+/// (`embedRow`, :106-123, on the device by imq_dequantize_rows), and
 /// `encode` / `encodeRealOnly` (:249-360) as the 27-layer loop with the
 /// hidden-state taps after layers 9, 18 and 27 (DirectTEForward.swift:20).
 public final class DirectTEEncoderHIP {
@@ -26,7 +26,7 @@ public final class DirectTEEncoderHIP {
     public let ctx: HIPContext
     var layers: [[ProjectionQ]] = []  // qkv, o, gate_up, down
     var norms: [(DeviceBuffer, DeviceBuffer)] = []
-    let embed: ProjectionQ
+    let embedTable: ProjectionQ
     let plan: OpaquePointer
     let x, y, qkv, attnO: DeviceBuffer
 
@@ -51,7 +51,7 @@ public final class DirectTEEncoderHIP {
                 norm_in: nIn.ptr.assumingMemoryBound(to: Float.self),
                 norm_post: nPost.ptr.assumingMemoryBound(to: Float.self)))
         }
-        embed = try ProjectionQ(ctx, st, "embed_tokens", dtype: IMQ_BF16)
+        embedTable = try ProjectionQ(ctx, st, "embed_tokens", dtype: IMQ_BF16)
         var h: OpaquePointer?
         try ctx.check(imq_te_create(ctx.ctx, &weights, Int32(weights.count), Int32(Self.maxLen), 1e-6, &h))
         plan = h!
@@ -63,19 +63,19 @@ public final class DirectTEEncoderHIP {
 
     deinit { imq_te_destroy(plan) }
 
-    /// `embedRow` for each token: the dequantized embedding row (bf16,
-    /// RNE(s q + b), bit-exact with the reference's CPU form) into row `pos`.
+    /// `embedRow` for every token in one launch: the dequantized embedding rows
+    /// (bf16, RNE(s q + b), bit-exact with the reference's CPU form) into x.
     func embed(tokens: [Int32]) throws {
-        let q = embed.q
-        let k = Int(q.k)
-        for (pos, t) in tokens.enumerated() {
-            let row = Int(t)
-            let w = q.w + row * (k / 8)
-            let s = q.scales + row * (k / 64) * 2
-            let b = q.biases + row * (k / 64) * 2
-            try ctx.check(imq_dequantize(ctx.ctx, w, s, b, x.at(pos * k * 2), q.k, 1, 64, 4, IMQ_BF16,
-                                         ctx.stream))
+        let q = embedTable.q
+        guard tokens.allSatisfy({ $0 >= 0 && $0 < q.n }) else {
+            throw HIPError.shape("token id outside [0, \(q.n))")
         }
+        let ids = try DeviceBuffer(ctx, copying: tokens)
+        try ctx.check(imq_dequantize_rows(ctx.ctx, q.w, q.scales, q.biases,
+                                          ids.ptr.assumingMemoryBound(to: Int32.self),
+                                          Int32(tokens.count), x.ptr, q.k, q.n, 64, 4, IMQ_BF16,
+                                          ctx.stream))
+        try ctx.sync()  // ids is released on return
     }
 
     /// The layer loop of `encode` / `encodeRealOnly` over `tokens` (the

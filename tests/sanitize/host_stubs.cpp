@@ -88,6 +88,10 @@ bool qskinny_supported(int k, int n, int m, int dtype) {
 }
 size_t qskinny_split_bytes(int, int, int) { return 0; }
 int qskinny_splits(int, int, int) { return 1; }
+hipError_t launch_dequant_rows(const uint32_t*, const void*, const void*, const int32_t*, int,
+                               void*, int, int, int, hipStream_t) {
+  return hipErrorNoDevice;
+}
 hipError_t launch_qskinny(const uint32_t*, const void*, const void*, const void*, void*, int, int,
                           int, int, hipStream_t, SplitWs) {
   return hipErrorNoDevice;

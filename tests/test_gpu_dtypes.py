@@ -23,7 +23,7 @@ import pytest
 import torch
 
 import aestrix_amd as imq
-from aestrix_amd import _lib
+from aestrix_amd import _lib, synth
 from oracle import ref
 
 pytestmark = pytest.mark.gpu
@@ -137,3 +137,33 @@ def test_one_hot_rows_reproduce_dequant_bit_exact(dtype, fn_name, m):
     deq = host(imq.dequantize(dev(w), dev(s), dev(b)))
     assert np.array_equal(y, deq[:, cols].T)
     assert np.array_equal(deq, ref.dequantize_as(w, s, b, dtype))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_dequantize_rows_equals_dequantize(dtype):
+    """imq_dequantize_rows (embedRow for a batch of ids, DirectTEEncoder.swift:106-123):
+    the rows of imq_dequantize bit for bit, ids repeated and at both ends, an
+    empty batch; ids out of range are refused on the host and clamped by the
+    kernel when passed straight to the C ABI."""
+    p = synth.make_problem(1, 1000, 2560, seed=81)
+    _, w, s, b = synth.to_device(p)
+    s, b = s.to(dtype), b.to(dtype)
+    full = imq.dequantize(w, s, b)
+    ids = torch.tensor([5, 0, 999, 5, 17, 998, 0, 512], dtype=torch.int32, device="cuda")
+    got = imq.dequantize_rows(w, s, b, ids)
+    torch.cuda.synchronize()
+    assert torch.equal(got, full[ids.long()])
+    assert imq.dequantize_rows(w, s, b, ids[:0]).shape == (0, 2560)
+    with pytest.raises(ValueError, match="ids"):
+        imq.dequantize_rows(w, s, b, torch.tensor([3, 1000], device="cuda"))
+    # straight to the C ABI: -7 reads row 0, 1003 reads row 999
+    from aestrix_amd import _lib, ops
+    bad = torch.tensor([-7, 1003, 4], dtype=torch.int32, device="cuda")
+    out = torch.empty((3, 2560), dtype=dtype, device="cuda")
+    ctx = ops.context(w.device)
+    st = _lib.load().imq_dequantize_rows(ctx, ops._ptr(w), ops._ptr(s), ops._ptr(b), ops._ptr(bad), 3,
+                                         ops._ptr(out), 2560, 1000, 64, 4, ops._DTYPES[dtype],
+                                         ops._stream(out))
+    _lib.check(st, ctx)
+    torch.cuda.synchronize()
+    assert torch.equal(out, full[torch.tensor([0, 999, 4], device="cuda")])
