@@ -847,7 +847,10 @@ hipError_t launch_reduce(const SplitWs& ws, int splits, int m, int ncols, int ld
 // split_steps * (MT + 1.5) plus 12 for its prologue and output; a split adds
 // the workspace traffic of its reduction (8 bytes per output and split, at
 // about 1.4 MB per unit) plus 3 for the extra launch.  Splits are taken only
-// when the tiles leave CUs idle.
+// when the tiles leave CUs idle.  160-row tiles exist for row counts that
+// leave a round of 192-row tiles part empty: 1024 x 9216 at K = 3072 is 252
+// tiles in one round instead of 216 (58.4 -> 57.0 us), 2048 x 9216 is 468
+// tiles in two rounds instead of 396 in two (115.0 -> 105.6 us).
 struct BigPlan {
   int mt, splits, split_steps;
 };
@@ -857,7 +860,7 @@ BigPlan pick_big_plan(int m, int n, int k, int cus, bool small, bool split) {
   const int steps = k / (64 * kBigKG);
   BigPlan best{8, 1, steps};
   double best_cost = 1e30;
-  for (int mt : {8, 7, 6, 4, 2, 1}) {
+  for (int mt : {8, 7, 6, 5, 4, 2, 1}) {
     const long tiles = (long)((m + 32 * mt - 1) / (32 * mt)) * tiles_n;
     const int max_splits = split && tiles < cus ? std::max(1, steps / 2) : 1;
     for (int sp = 1; sp <= max_splits; ++sp) {
@@ -920,6 +923,7 @@ hipError_t launch_big_mt(int mt, const uint32_t* w, const uint16_t* scales, cons
       if constexpr (kSmall) return launch_big<T, 2>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
       return hipErrorInvalidValue;
     case 4: return launch_big<T, 4>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
+    case 5: return launch_big<T, 5>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
     case 6: return launch_big<T, 6>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
     case 7: return launch_big<T, 7>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
     default: return launch_big<T, 8>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);

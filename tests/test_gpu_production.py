@@ -98,10 +98,12 @@ def sample_rows(m: int, count: int) -> np.ndarray:
 
 # (M, N weight rows, K, width, gate_row, up_row, tile rows): the single block's
 # to_qkv_mlp_proj MLP half (J = 4608), the double blocks' ff.linear_in over the
-# image rows (4096) and ff_context.linear_in over the text rows (512).
+# image rows (4096) and ff_context.linear_in over the text rows (512); 1024
+# rows of a 9216-row pair take 160-row tiles (7 x 36 = 252 tiles, one round).
 SWIGLU = [(4608, 27648, 3072, 9216, 9216, 18432, 224),
           (4096, 18432, 3072, 9216, 0, 9216, 256),
-          (512, 18432, 3072, 9216, 0, 9216, 192)]
+          (512, 18432, 3072, 9216, 0, 9216, 192),
+          (1024, 9216, 3072, 4608, 0, 4608, 160)]
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
@@ -130,8 +132,9 @@ def test_swiglu_at_production_tile_heights(dtype, case):
 
 
 # (M, N, K, tile rows): the single block's to_out (K = 12288) over J = 4608
-# rows and the double blocks' ff.linear_out (K = 9216) over the image rows.
-GATE_ADD = [(4608, 3072, 12288, 224), (4096, 3072, 9216, 224)]
+# rows and the double blocks' ff.linear_out (K = 9216) over the image rows;
+# 1024 x 9216 at K = 3072 takes 160-row tiles.
+GATE_ADD = [(4608, 3072, 12288, 224), (4096, 3072, 9216, 224), (1024, 9216, 3072, 160)]
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
@@ -157,8 +160,10 @@ def test_gate_add_at_production_tile_heights(dtype, case):
 
 
 # (M, N, K, tile rows, splits): the double blocks' Q/K/V over image rows and
-# text rows, and the image rows' MLP-in width as a plain store (256-row tiles).
-PLAIN = [(4096, 3072, 3072, 224, 1), (512, 3072, 3072, 32, 1), (4096, 18432, 3072, 256, 1)]
+# text rows, the image rows' MLP-in width as a plain store (256-row tiles), and
+# the 1024-row MLP-in qGEMM (160-row tiles: 252 tiles in one round on 256 CUs).
+PLAIN = [(4096, 3072, 3072, 224, 1), (512, 3072, 3072, 32, 1), (4096, 18432, 3072, 256, 1),
+         (1024, 9216, 3072, 160, 1)]
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
