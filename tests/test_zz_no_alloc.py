@@ -92,7 +92,8 @@ def test_noalloc_matches_qmm_t_on_two_calls(dtype, first, second):
 
 
 def test_noalloc_refuses_a_plan_past_the_static_scratch():
-    m, n, k = 1536, 6144, 16384
+    # 224-row tiles, K split three ways: 3 x 1536 x 6144 fp32 partial sums (108 MiB).
+    m, n, k = 1536, 6144, 32768
     need = split_bytes(m, n, k)
     note(f"noalloc M={m} N={n} K={k}: plan needs {need} bytes")
     assert need > STATIC_SCRATCH_BYTES
