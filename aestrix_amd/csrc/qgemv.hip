@@ -324,7 +324,10 @@ int tile_len(int k, int mr, int g, int eb) {
 // counting at most 4096 for M <= 4, 2048 for M <= 8 and 1024 above: beyond
 // those counts more waves stopped paying for idle lanes (a sweep of every G
 // on 9728 x 2560 and 2560 x 9728 at M = 1, 2, 4, 8, 16 picks the fastest G
-// in all ten cases with these caps).
+// in all ten cases with these caps).  Candidates are tried 32, 64, 16, so a
+// tie goes to 32 lanes: M = 1 [18432 x 3072] scores 16 and 32 alike and runs
+// in 8.6 us at 32 against 9.0 at 16 (weights from HBM; [9728 x 2560] 5.6 /
+// 6.1 / 7.2 us at 32 / 16 / 64).
 // IMQ_QGEMV_LANES=16|32|64 overrides.
 Plan make_plan(int k, int n, int mr, int eb, int r_override = 0) {
   static const int forced = [] {
@@ -335,7 +338,7 @@ Plan make_plan(int k, int n, int mr, int eb, int r_override = 0) {
   const int r = r_override ? r_override : rows_per_lane(mr);
   Plan best{16, 0, 0};
   double best_score = -1.0;
-  for (int g = 16; g <= 64; g *= 2) {
+  for (int g : {32, 64, 16}) {
     if (forced && g != forced) continue;
     const int kt = tile_len(k, mr, g, eb);
     const int tch = kt / 32;
