@@ -286,7 +286,16 @@ __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_
 // fixed for the whole K loop and the K-step advance is a scalar offset, so a
 // load costs no vector ALU work) into a 2-stage LDS ring.  Packed weights need
 // no sharing between waves (each wave owns its columns), so they are loaded
-// straight into registers.  Both are loaded one step ahead.  Scales and biases
+// straight into registers.  Both are loaded one step ahead.  A weight load
+// reads 16 rows x the step's 64 bytes (lane L: row L % 16, bytes 16 (L / 16)),
+// 16 cache lines per instruction; two of them (rows 0-15 and 16-31 of a
+// column tile) are turned into the 32-row MFMA operand layout by one
+// v_permlane16_swap per dword (the 16-lane rows 1, 3 of the first trade places
+// with rows 0, 2 of the second): lane (r32, h) then holds row r32's bytes
+// [32 h, 32 h + 16) in the first register and [32 h + 16, 32 h + 32) in the
+// second, i.e. all 64 codes of group h of the step.  Loaded directly in that
+// layout, one instruction touched 32 rows x 32 bytes (32 lines) and the
+// weights took about as many memory-pipeline cycles as the activations.  Scales and biases
 // are loaded four groups at a time (8 bytes of a row per load, one block of
 // two steps ahead): a lane's per-group 2-byte loads touch one cache line per
 // row each and cost more memory-pipeline time than the weights and
@@ -333,7 +342,8 @@ template <int MT>
 struct BigSrc {
   __amdgpu_buffer_rsrc_t xr, wr, sr, br;
   uint32_t a_off[BigCfg<MT>::kA];  // byte offsets of this thread's activation slots
-  uint32_t w_off[2];  // byte offsets of this lane's 16 weight bytes, per column tile
+  uint32_t w_off[2][kBigKG];  // byte offsets of this lane's 16 weight bytes, per column
+                              // tile and 16-row half
   uint32_t p_off[2];  // byte offsets of this lane's scale / bias row, per column tile
 };
 
@@ -351,10 +361,11 @@ __device__ __forceinline__ uint2 load_param_block(__amdgpu_buffer_rsrc_t rs, uin
   return __builtin_bit_cast(uint2, v);
 }
 
-// Scale or bias of position j (0..3) of a block.
-__device__ __forceinline__ uint32_t param_at(uint2 blk, int j) {
-  const uint32_t w = (j < 2) ? blk.x : blk.y;
-  return (j & 1) ? (w >> 16) : (w & 0xFFFFu);
+// Scale or bias of position J0 + h (J0 = 0 or 2, h = 0 or 1) of a block.
+template <int J0>
+__device__ __forceinline__ uint32_t param_at(uint2 blk, int h) {
+  const uint32_t w = (J0 < 2) ? blk.x : blk.y;
+  return (w >> (16 * h)) & 0xFFFFu;
 }
 
 // Dequant parameters of one group for the two column tiles: s * 2^24 and
@@ -363,16 +374,16 @@ struct GroupParams {
   float s24[2], s20[2], b[2];
 };
 
-template <int T>
+template <int T, int J0>
 __device__ __forceinline__ GroupParams group_params(const uint2 (&sblk)[2], const uint2 (&bblk)[2],
-                                                    int j) {
+                                                    int h) {
   GroupParams p;
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    const float sv = Elem<T>::param((typename Elem<T>::S)param_at(sblk[nt], j));
+    const float sv = Elem<T>::param((typename Elem<T>::S)param_at<J0>(sblk[nt], h));
     p.s24[nt] = sv * 0x1p24f;
     p.s20[nt] = sv * 0x1p20f;
-    p.b[nt] = Elem<T>::param((typename Elem<T>::S)param_at(bblk[nt], j));
+    p.b[nt] = Elem<T>::param((typename Elem<T>::S)param_at<J0>(bblk[nt], h));
   }
   return p;
 }
@@ -386,15 +397,30 @@ __device__ __forceinline__ constexpr int a_split(int p) {
   return p * BigCfg<MT>::kA / kIssuePts;
 }
 
-// Weight loads of step gs into register set ST.
+// Weight loads of step gs into register set ST: per column tile the rows
+// 0-15 (i = 0) and 16-31 (i = 1), 64 bytes each.
 template <int MT, int ST>
 __device__ __forceinline__ void big_issue_w(uint32_t gs, const BigSrc<MT>& src,
                                             u32x4_t (&wr)[2][2][kBigKG]) {
 #pragma unroll
-  for (int q = 0; q < kBigKG; ++q)
+  for (int i = 0; i < kBigKG; ++i)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)
-      wr[ST][nt][q] = load_b128(src.wr, src.w_off[nt], (gs * kBigKG + q) * 32u);
+      wr[ST][nt][i] = load_b128(src.wr, src.w_off[nt][i], gs * 64u);
+}
+
+// The landed weight registers of a step into MFMA operand layout (see the
+// kernel's comment): afterwards wr[nt][0] holds words 0-3 and wr[nt][1]
+// words 4-7 of the lane's group.
+__device__ __forceinline__ void big_swap_w(u32x4_t (&wr)[2][kBigKG]) {
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const auto r = __builtin_amdgcn_permlane16_swap(wr[nt][0][j], wr[nt][1][j], false, false);
+      wr[nt][0][j] = r[0];
+      wr[nt][1][j] = r[1];
+    }
 }
 
 // Activation loads [a_split(p), a_split(p + 1)) of step gs into stage ST.
@@ -408,10 +434,9 @@ __device__ __forceinline__ void big_issue_a(int p, uint32_t gs, const BigRing& r
       load_lds16(src.xr, src.a_off[i], gs * (128u * kBigKG), ab + i * kThreads);
 }
 
-// LDS reads and weight dequant of k-slice t of a step into buffer B.  In
-// group q = t / 4, slice kk = t % 4, lane (r32, h) holds k = 64 q + 32 h +
-// 8 kk .. +8 of its activation row and of its weight row (word kk of its 16
-// bytes of the group), so the two operands agree.
+// LDS reads and weight dequant of k-slice t of a step into buffer B: lane
+// (r32, h) holds k = 64 h + 8 t .. +8 of its activation row and of its weight
+// row (word t of its group h), so the two operands agree.
 template <int T, int MT, int B>
 __device__ __forceinline__ void big_operands(int t, const uint4* at, const u32x4_t (&wr)[2][kBigKG],
                                              const GroupParams& gp, BigFrags<MT>& f, int arow0,
@@ -420,7 +445,7 @@ __device__ __forceinline__ void big_operands(int t, const uint4* at, const u32x4
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
     f.a[B][mt] = __builtin_bit_cast(
-        u32x4_t, at[a_slot_kg<kBigKG>(arow0 + mt * 32 + r32, 8 * q + 4 * h + kk)]);
+        u32x4_t, at[a_slot_kg<kBigKG>(arow0 + mt * 32 + r32, 8 * h + t)]);
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const u32x4_t wv = wr[nt][q];
@@ -457,7 +482,8 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
   __builtin_amdgcn_sched_barrier(0);
 
   const uint4* at = ring.a[ST];
-  GroupParams gp = group_params<T>(sblk[SLOT], bblk[SLOT], J0);
+  big_swap_w(wr[ST]);
+  const GroupParams gp = group_params<T, J0>(sblk[SLOT], bblk[SLOT], h);
   big_operands<T, MT, 0>(0, at, wr[ST], gp, f, arow0, r32, h);
   if constexpr (S % 2 == 0) {
     // The next block (steps g+2, g+3) goes to the other slot.
@@ -492,7 +518,6 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
 #pragma unroll
   for (int t = 0; t + 1 < kBigSlices; ++t) {
     __builtin_amdgcn_sched_barrier(0);
-    if (((t + 1) & 3) == 0) gp = group_params<T>(sblk[SLOT], bblk[SLOT], J0 + ((t + 1) >> 2));
     if (t + 1 < kIssuePts) big_issue_a<MT, ST ^ 1>(t + 1, gs1, ring, src, wave);
     if (t & 1) {
       big_operands<T, MT, 0>(t + 1, at, wr[ST], gp, f, arow0, r32, h);
@@ -650,14 +675,20 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     src.a_off[i] = (gr * (uint32_t)K + (uint32_t)c * 8u) * 2u;
   }
   // In MFMA operand layout lane (r32, h) of column tile nt owns weight row
-  // ncol0 + 32 nt + r32 and bytes [16 h, 16 h + 16) of each group.
+  // ncol0 + 32 nt + r32 (its scales and biases); its loads read row
+  // ncol0 + 32 nt + 16 i + lane % 16, bytes [16 (lane / 16), +16) of the step.
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     int wrow = ncol0 + nt * 32 + r32;
     if constexpr (EP::kPair) wrow = (nt == 0 ? ep.gate_row : ep.up_row) + min(pcol0 + r32, ep.width - 1);
-    const int gr = min(wrow, N - 1);
-    src.w_off[nt] = (uint32_t)gr * (uint32_t)(K / 2) + (uint32_t)h * 16u;
-    src.p_off[nt] = (uint32_t)gr * (uint32_t)gpr * 2u;
+    src.p_off[nt] = (uint32_t)min(wrow, N - 1) * (uint32_t)gpr * 2u;
+#pragma unroll
+    for (int i = 0; i < kBigKG; ++i) {
+      const int c = 16 * i + (lane & 15);
+      int lrow = ncol0 + nt * 32 + c;
+      if constexpr (EP::kPair) lrow = (nt == 0 ? ep.gate_row : ep.up_row) + min(pcol0 + c, ep.width - 1);
+      src.w_off[nt][i] = (uint32_t)min(lrow, N - 1) * (uint32_t)(K / 2) + (uint32_t)(lane >> 4) * 16u;
+    }
   }
 
   f32x16_t acc[MT][2];
