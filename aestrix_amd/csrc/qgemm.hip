@@ -295,11 +295,12 @@ __global__ __launch_bounds__(kThreads, (MT * NT * 16 > 128) ? 1 : 2) void qgemm_
 // [32 h, 32 h + 16) in the first register and [32 h + 16, 32 h + 32) in the
 // second, i.e. all 64 codes of group h of the step.  Loaded directly in that
 // layout, one instruction touched 32 rows x 32 bytes (32 lines) and the
-// weights took about as many memory-pipeline cycles as the activations.  Scales and biases
-// are loaded four groups at a time (8 bytes of a row per load, one block of
-// two steps ahead): a lane's per-group 2-byte loads touch one cache line per
-// row each and cost more memory-pipeline time than the weights and
-// activations together.  The K loop is unrolled by four steps so that the
+// weights took about as many memory-pipeline cycles as the activations.
+// Scales and biases are loaded eight groups at a time (16 bytes of a row per
+// load, the four steps of an unrolled iteration, one iteration ahead): a
+// lane's per-group 2-byte loads touch one cache line per row each and cost
+// more memory-pipeline time than the weights and activations together, and 8
+// bytes per two steps still cost 2-5% against none at all.  The K loop is unrolled by four steps so that the
 // ring stage, the weight registers, the scale-block slot and the group's
 // position in its block are compile-time constants: the compiler can prove
 // that loads in flight into the other stage do not alias this stage's reads
@@ -354,17 +355,20 @@ struct BigFrags {
   u32x4_t b[2][2];
 };
 
-// Four consecutive scales (or biases) of a row, groups 4b .. 4b+3.
-__device__ __forceinline__ uint2 load_param_block(__amdgpu_buffer_rsrc_t rs, uint32_t voff,
-                                                  uint32_t b) {
-  const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, b * 8u, 0);
-  return __builtin_bit_cast(uint2, v);
+// Eight consecutive scales (or biases) of a row: groups 2 g .. 2 g + 7, the
+// four K-steps from step g (a 4-byte aligned offset).  The prefetch after a
+// split's last block is clamped to two steps before its end and reads 8 bytes
+// past it (the next row's, or zeros past the buffer; never used).
+__device__ __forceinline__ uint4 load_param_block(__amdgpu_buffer_rsrc_t rs, uint32_t voff,
+                                                  uint32_t g) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, g * 4u, 0);
+  return __builtin_bit_cast(uint4, v);
 }
 
-// Scale or bias of position J0 + h (J0 = 0 or 2, h = 0 or 1) of a block.
-template <int J0>
-__device__ __forceinline__ uint32_t param_at(uint2 blk, int h) {
-  const uint32_t w = (J0 < 2) ? blk.x : blk.y;
+// Scale or bias of group h of step S (0..3) of a block.
+template <int S>
+__device__ __forceinline__ uint32_t param_at(uint4 blk, int h) {
+  const uint32_t w = S == 0 ? blk.x : S == 1 ? blk.y : S == 2 ? blk.z : blk.w;
   return (w >> (16 * h)) & 0xFFFFu;
 }
 
@@ -374,16 +378,16 @@ struct GroupParams {
   float s24[2], s20[2], b[2];
 };
 
-template <int T, int J0>
-__device__ __forceinline__ GroupParams group_params(const uint2 (&sblk)[2], const uint2 (&bblk)[2],
+template <int T, int S>
+__device__ __forceinline__ GroupParams group_params(const uint4 (&sblk)[2], const uint4 (&bblk)[2],
                                                     int h) {
   GroupParams p;
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    const float sv = Elem<T>::param((typename Elem<T>::S)param_at<J0>(sblk[nt], h));
+    const float sv = Elem<T>::param((typename Elem<T>::S)param_at<S>(sblk[nt], h));
     p.s24[nt] = sv * 0x1p24f;
     p.s20[nt] = sv * 0x1p20f;
-    p.b[nt] = Elem<T>::param((typename Elem<T>::S)param_at<J0>(bblk[nt], h));
+    p.b[nt] = Elem<T>::param((typename Elem<T>::S)param_at<S>(bblk[nt], h));
   }
   return p;
 }
@@ -464,17 +468,15 @@ __device__ __forceinline__ void big_mfmas(const BigFrags<MT>& f, f32x16_t (&acc)
     for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma32<T>(f.a[B][mt], f.b[B][nt], acc[mt][nt]);
 }
 
-// One K-step.  S = g % kBigUnroll: stage and weight registers S % 2, scale
-// block slot S / 2, first group at position 2 (S % 2) of its block.
+// One K-step.  S = g % kBigUnroll: stage and weight registers S % 2, dword S
+// of the scale / bias blocks in slot 0 (slot 1: the next four steps').
 template <int T, int MT, int S>
 __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
-                                         const BigSrc<MT>& src, uint2 (&sblk)[2][2],
-                                         uint2 (&bblk)[2][2], u32x4_t (&wr)[2][2][kBigKG],
+                                         const BigSrc<MT>& src, uint4 (&sblk)[2][2],
+                                         uint4 (&bblk)[2][2], u32x4_t (&wr)[2][2][kBigKG],
                                          BigFrags<MT>& f, f32x16_t (&acc)[MT][2], int wave,
                                          int arow0, int r32, int h) {
   constexpr int ST = S % 2;
-  constexpr int SLOT = S / 2;
-  constexpr int J0 = (S % 2) * kBigKG;
   constexpr int kMfma = 2 * MT;
   IMQ_WAIT_VM_LGKM_0();
   __builtin_amdgcn_sched_barrier(0);
@@ -483,16 +485,16 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
 
   const uint4* at = ring.a[ST];
   big_swap_w(wr[ST]);
-  const GroupParams gp = group_params<T, J0>(sblk[SLOT], bblk[SLOT], h);
+  const GroupParams gp = group_params<T, S>(sblk[0], bblk[0], h);
   big_operands<T, MT, 0>(0, at, wr[ST], gp, f, arow0, r32, h);
-  if constexpr (S % 2 == 0) {
-    // The next block (steps g+2, g+3) goes to the other slot.
-    const int blocks = steps * kBigKG / 4;
-    const uint32_t nb = (uint32_t)min(g * kBigKG / 4 + 1, blocks - 1);
+  if constexpr (S == 0) {
+    // The next block (steps g+4 .. g+7) goes to slot 1; the K loop moves it to
+    // slot 0 after step g+3.
+    const uint32_t nb = (uint32_t)min(g + 4, steps - 2);
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      sblk[SLOT ^ 1][nt] = load_param_block(src.sr, src.p_off[nt], nb);
-      bblk[SLOT ^ 1][nt] = load_param_block(src.br, src.p_off[nt], nb);
+      sblk[1][nt] = load_param_block(src.sr, src.p_off[nt], nb);
+      bblk[1][nt] = load_param_block(src.br, src.p_off[nt], nb);
     }
   }
   const uint32_t gs1 = (uint32_t)min(g + 1, steps - 1);
@@ -502,7 +504,7 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
   {
     // LDS reads first, then each deferred MFMA followed by a share of the
     // loads and of slice 0's dequant.
-    constexpr int kVmem = 2 * kBigKG + a_split<MT>(1) + (S % 2 == 0 ? 4 : 0);
+    constexpr int kVmem = 2 * kBigKG + a_split<MT>(1) + (S == 0 ? 4 : 0);
     constexpr int kVmemPer = (kVmem + kMfma - 1) / kMfma;
     constexpr int kValuPer = (2 * 17 + 8 + kMfma - 1) / kMfma;
 #pragma unroll
@@ -701,12 +703,12 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
 
   // Prologue: the first scale block, the loads of step 0, and zero operands
   // for the first step's deferred MFMAs (they add nothing).
-  uint2 sblk[2][2], bblk[2][2];
+  uint4 sblk[2][2], bblk[2][2];
   u32x4_t wr[2][2][kBigKG];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    sblk[0][nt] = load_param_block(src.sr, src.p_off[nt], (uint32_t)(g0 * kBigKG / 4));
-    bblk[0][nt] = load_param_block(src.br, src.p_off[nt], (uint32_t)(g0 * kBigKG / 4));
+    sblk[0][nt] = load_param_block(src.sr, src.p_off[nt], (uint32_t)g0);
+    bblk[0][nt] = load_param_block(src.br, src.p_off[nt], (uint32_t)g0);
   }
   big_issue_w<MT, 0>((uint32_t)g0, src, wr);
 #pragma unroll
@@ -717,15 +719,19 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) f.b[1][nt] = u32x4_t{0u, 0u, 0u, 0u};
 
-  // g1 - g0 is even: full unrolls, then possibly one block.  The ring stage
-  // and scale slot count from g0 (a block start); loads past g1 are clamped
-  // to g1 - 1.
+  // g1 - g0 is even: full unrolls, then possibly two steps.  The ring stage
+  // and scale blocks count from g0; loads past g1 are clamped to g1 - 1.
   int g = g0;
   for (; g + kBigUnroll <= g1; g += kBigUnroll) {
     big_step<T, MT, 0>(g, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
     big_step<T, MT, 1>(g + 1, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
     big_step<T, MT, 2>(g + 2, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
     big_step<T, MT, 3>(g + 3, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      sblk[0][nt] = sblk[1][nt];
+      bblk[0][nt] = bblk[1][nt];
+    }
   }
   if (g < g1) {
     big_step<T, MT, 0>(g, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
