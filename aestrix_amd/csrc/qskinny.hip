@@ -307,6 +307,152 @@ __global__ __launch_bounds__(64 * W) void qskinny_lds_kernel(const uint32_t* __r
   }
 }
 
+// ---------------------------------------------------------------------------
+// M <= 8, x in LDS, K % 512 == 0: eight weight rows x 128 bytes per load.
+//
+// Over a span of 256 k the B operand's 16 columns carry (token t, K half p)
+// as j = 2 t + p: lane (c, h) of A holds weight row r = c / 2 of an octet of
+// the tile, k = 128 (c % 2) + 32 h + 8 s .. +8 of the span in k-slice s; lane
+// (j, h) of B holds x[t][128 p + 32 h + 8 s .. +8].  Output (2 r + p, 2 t + p')
+// is half p of row r against half p' of token t; the blocks with p = p',
+// added, are row r's dot product with token t over the span (the others are
+// never used).  A wave instruction then reads 8 rows x 128 contiguous bytes
+// (8 cache lines; the 16-row kernel's read 16 rows x 64 bytes), with the same
+// number of loads and MFMAs per weight byte.  W is even: wave w takes octet
+// w % 2 and the spans w / 2, w / 2 + W / 2, ... (as many as the 16-row kernel
+// gives a wave chunks; its x fragment serves one octet).
+//
+// Octet o's row r is tile row 4 (r / 2) + 2 o + r % 2: once the p = p' pairs
+// are added (a DPP swap of adjacent lanes) lane (j, g) of a wave of octet o
+// holds features 4 g + 2 o, 4 g + 2 o + 1 of token j / 2; the reduction over
+// the waves gives it features 4 g .. 4 g + 3, stored as 8 bytes.
+//
+// x in LDS: row t's 16-byte piece q (k = 8 q) at t K / 8 + (q ^ (2 t + bit 4
+// of q) % 16), so the 16 lanes of a B read (tokens t, halves p, one h and s)
+// hit 16 different 16-byte bank groups (rows are K / 8 pieces apart, a
+// multiple of 16).  One DMA instruction stages 64 pieces of a row: the XOR
+// stays inside 16-piece blocks, so it still reads 1 KB of x contiguously.
+__device__ __forceinline__ float swap_adjacent(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF,
+                                                            0xF, true));  // quad_perm 1,0,3,2
+}
+
+template <int T, int W, int U>
+__global__ __launch_bounds__(64 * W) void qskinny_half_kernel(const uint32_t* __restrict__ w,
+                                                              const uint16_t* __restrict__ scales,
+                                                              const uint16_t* __restrict__ biases,
+                                                              const uint16_t* __restrict__ x,
+                                                              uint16_t* __restrict__ y, int M,
+                                                              int N, int K, bool vec) {
+  static_assert(W % 2 == 0, "waves pair up over the two octets");
+  constexpr int kStride = W / 2;  // span stride of a wave
+  __shared__ float2 part[W][64];
+  extern __shared__ uint4 xs[];  // x [M, K], pieces XOR-placed within 16-piece blocks
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int o = wave & 1;
+  const int c = lane & 15, h = lane >> 4;
+  const int n0 = blockIdx.x * kRows;
+  const int gpr = K >> 6;
+  const int spans = K >> 8;
+  const int row_pieces = K >> 3;
+  const auto wr = make_rsrc(w, (uint32_t)((size_t)N * K / 2));
+  const auto sr = make_rsrc(scales, (uint32_t)((size_t)N * gpr * 2));
+  const auto br = make_rsrc(biases, (uint32_t)((size_t)N * gpr * 2));
+  const auto xr = make_rsrc(x, (uint32_t)((size_t)M * K * 2));
+
+  // 1. x -> LDS: instruction e stages pieces [64 i, 64 i + 64) of row t.
+  {
+    const int per_row = K >> 9;
+    for (int e = wave; e < M * per_row; e += W) {
+      const int t = e / per_row, i = e - t * per_row;
+      const int u = 64 * i + lane;
+      const int q = u ^ ((2 * t + ((u >> 4) & 1)) & 15);
+      load_lds16(xr, (uint32_t)(t * K + 8 * q) * 2u, 0u, xs + t * row_pieces + 64 * i);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // A operand: octet o, tile row 4 (c / 4) + 2 o + (c / 2) % 2, bytes 64 (c % 2) + 16 h of
+  // each 128-byte span; group 2 (c % 2) + h / 2 of the span's four.
+  const uint32_t row = (uint32_t)min(n0 + 4 * (c >> 2) + 2 * o + ((c >> 1) & 1), N - 1);
+  const uint32_t w_off = row * (uint32_t)(K / 2) + (uint32_t)(c & 1) * 64u + (uint32_t)h * 16u;
+  const uint32_t p_off = (row * (uint32_t)gpr + 2u * (uint32_t)(c & 1) + (uint32_t)(h >> 1)) * 2u;
+  // B operand: token min(c / 2, M - 1) (columns past M are never stored), half c % 2.
+  const int t = min(c >> 1, M - 1);
+  const int sw = 2 * t + (c & 1);
+  const uint32_t xb = (uint32_t)(t * row_pieces + 16 * (c & 1)) * 16u;
+  uint32_t xo[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) xo[s] = xb + (uint32_t)(((4 * h + s) ^ sw) * 16);
+
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int sp0 = wave >> 1; sp0 < spans; sp0 += kStride * U) {
+    u32x4_t wv[U];
+    uint16_t sv[U], bv[U];
+    // Spans past the end are clamped to the last one and dropped.
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t sp = (uint32_t)min(sp0 + u * kStride, spans - 1);
+      wv[u] = load_b128(wr, w_off + sp * 128u, 0);
+      sv[u] = __builtin_amdgcn_raw_buffer_load_b16(sr, p_off + sp * 8u, 0, 0);
+      bv[u] = __builtin_amdgcn_raw_buffer_load_b16(br, p_off + sp * 8u, 0, 0);
+    }
+    // x is in LDS once this wave's DMA loads (issued before the 3 U loads
+    // above) have landed and every wave has passed the barrier; every wave
+    // has a first pass (W / 2 <= spans).
+    __builtin_amdgcn_sched_barrier(0);
+    if (sp0 == (wave >> 1)) {
+      IMQ_WAIT_VMCNT(3 * U);
+      __builtin_amdgcn_s_barrier();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool valid = sp0 + u * kStride < spans;  // uniform across the wave
+      const uint32_t sp = (uint32_t)min(sp0 + u * kStride, spans - 1);
+      const float sc = valid ? Elem<T>::param(sv[u]) : 0.0f;
+      const float s24 = sc * 0x1p24f, s20 = sc * 0x1p20f;
+      const float bb = valid ? Elem<T>::param(bv[u]) : 0.0f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        uint32_t p[4];
+        Elem<T>::dequant(wv[u][s], s24, s20, bb, p);
+        const u32x4_t xj = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(xs) +
+                                                             xo[s] + sp * 512u);
+        acc = mfma16x16x32<T>(u32x4_t{p[0], p[1], p[2], p[3]}, xj, acc);
+      }
+    }
+  }
+  // Lane (j, g) holds rows 4 g + v of column j: its half j % 2 is in v = j % 2
+  // (octet row 2 g) and v = 2 + j % 2 (octet row 2 g + 1).
+  const bool odd = (c & 1) != 0;
+  float v0 = odd ? acc[1] : acc[0];
+  float v1 = odd ? acc[3] : acc[2];
+  v0 += swap_adjacent(v0);
+  v1 += swap_adjacent(v1);
+  part[wave][lane] = make_float2(v0, v1);
+  __syncthreads();
+  if (wave != 0 || odd || (c >> 1) >= M) return;
+  float sum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    const float2 v = part[i][lane];
+    sum[2 * (i & 1)] += v.x;
+    sum[2 * (i & 1) + 1] += v.y;
+  }
+  const int f0 = n0 + 4 * h;
+  uint16_t* yr = y + (size_t)(c >> 1) * N;
+  if (vec && f0 + 3 < N) {
+    *reinterpret_cast<uint2*>(yr + f0) =
+        make_uint2(Elem<T>::pack2(sum[0], sum[1]), Elem<T>::pack2(sum[2], sum[3]));
+  } else {
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      if (f0 + v < N) yr[f0 + v] = Elem<T>::out(sum[v]);
+  }
+}
+
 // Waves per workgroup: enough that the device holds about 2048 waves and
 // each wave at most 8 chunks, at most 16 waves and at most half the chunks.
 int skinny_waves(int n, int k) {
@@ -327,6 +473,24 @@ hipError_t launch_w(const uint32_t* w, const uint16_t* s, const uint16_t* b, con
   const size_t per = 64 * (size_t)W, slots = (size_t)m * k / 8;
   const size_t xbytes = (slots + per - 1) / per * per * 16;
   const bool xlds = xbytes <= (size_t)kXLdsMax;
+  if constexpr (W % 2 == 0) {
+    if (xlds && m <= 8 && k % 512 == 0) {
+      // Units of 8 rows x 256 k, as many per wave as chunks: W / 2 <= k / 256,
+      // as 2 W <= chunks.
+      const size_t hbytes = (size_t)m * k * 2;
+#define IMQ_HALF(UU)                                                                             \
+  hipLaunchKernelGGL((qskinny_half_kernel<T, W, UU>), grid, block, hbytes, stream, w, s, b, x, y, \
+                     m, n, k, vec)
+      if (u <= 2) IMQ_HALF(2);
+      else if (u <= 3) IMQ_HALF(3);
+      else if (u <= 4) IMQ_HALF(4);
+      else if (u <= 5) IMQ_HALF(5);
+      else if (u <= 6) IMQ_HALF(6);
+      else IMQ_HALF(8);
+#undef IMQ_HALF
+      return hipGetLastError();
+    }
+  }
 #define IMQ_SKINNY(UU)                                                                            \
   do {                                                                                           \
     if (xlds)                                                                                    \
