@@ -253,12 +253,18 @@ def test_few_row_split_plan(m, n, k, splits):
                                    (8, 9728, 2560), (4, 2560, 9728), (5, 2560, 9728),
                                    (6, 2560, 9728), (8, 2560, 9728), (16, 2560, 9728),
                                    (9, 384, 192), (12, 9728, 2560), (16, 9728, 2560),
-                                   (14, 3000, 4096), (12, 1000, 4608), (13, 1030, 4608)])
+                                   (14, 3000, 4096), (12, 1000, 4608), (13, 1030, 4608),
+                                   (3, 1001, 1024), (7, 1030, 2560), (8, 17, 512)])
 def test_few_row_matrix_core_dispatch(dtype, m, n, k):
-    """4 <= M <= 16 through the dispatcher.  The 16-row weight-streaming kernel
+    """3 <= M <= 16 through the dispatcher.  The 16-row weight-streaming kernel
     stages x in LDS when M K 2, rounded up to whole wave instructions, fits
     96 KiB: M = 4 and 5 at K = 9728 (80 and exactly 96 KiB) take that path,
     M = 6 and 16 there (128 KiB and more) load x per chunk into registers.
+    With x in LDS, M <= 8 and K % 512 == 0 its 8-row-load form runs (B
+    columns = token and K half): 384 x 512 at M = 4, 5, [9728 x 2560] at M = 8,
+    [2560 x 9728] at M = 4, 5, 1001 x 1024 at M = 3 and 17 x 512 at M = 8
+    (partial row tiles; K = 512 is one span per wave pair), 1030 x 2560 at
+    M = 7 (N % 4 != 0: single-element stores).
     12 <= M <= 16 with K <= 4096 (K % 512 == 0) take the multi-tile kernel
     with x in LDS: [9728 x 2560] at M = 12 and 16 (three 16-row tiles per
     workgroup, the last workgroup two), 3000 x 4096 at M = 14 (a partial last
