@@ -46,6 +46,12 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c)
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
+// The value of the adjacent lane (lane ^ 1), by DPP.
+__device__ __forceinline__ float swap_adjacent(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF,
+                                                            0xF, true));  // quad_perm 1,0,3,2
+}
+
 // x staged in LDS when the whole [M, K] tile fits kXLdsMax bytes (rounded up
 // to whole wave instructions): one 16-byte DMA per lane and slot instead of
 // four register loads per chunk and lane.  96 KiB against 64: [9728 x 2560]
@@ -180,6 +186,7 @@ __global__ __launch_bounds__(64 * W) void qskinny_kernel(const uint32_t* __restr
 // them.  Activation bytes cross the memory pipeline once per workgroup
 // instead of once per wave and chunk.
 //
+// qskinny_lds_kernel (one tile per workgroup): loads read 16 rows x 64 bytes.
 // LDS x layout: row m at byte m (2 K + 16), its 16-byte pieces in order: the 16
 // lanes (c, 0..15) of one B-operand read group (rows c, the same piece) hit 16
 // different 16-byte bank groups.
@@ -307,6 +314,183 @@ __global__ __launch_bounds__(64 * W) void qskinny_lds_kernel(const uint32_t* __r
   }
 }
 
+// qskinny_lds8_kernel (two or more tiles per workgroup): loads read 8 weight
+// rows x 128 bytes, as in qskinny_half_kernel (below).  Over a span of 256 k
+// the B operand's columns carry (token, K half) as j = 2 t' + p, A lane (c, h)
+// holds row c / 2 of an octet of a tile at k = 128 (c % 2) + 32 h + 8 s, and
+// the blocks with p = p' are the halves of a row's dot product with a token.
+// With 12-16 tokens there are two token groups (tokens 8 g + t'): two MFMAs
+// and two B fragments per A fragment, which pay where a B fragment serves two
+// or more tiles (A/B against the 16-row-load form: [9728 x 2560] M = 12 / 16
+// 10.6 / 10.8 -> 10.0 / 10.3 us at three tiles, [6144 x 2560] M = 13 -5% at
+// two; 4-6% slower at one tile).  W is even: wave w takes octet w % 2 of every
+// tile over spans w / 2, w / 2 + W / 2, ... (as many units as it had chunks).
+//
+// LDS x layout: row m's 16-byte piece q at m K / 8 + (q ^ (2 (m % 8) + bit 4 of
+// q) % 16): the 16 lanes of a B read (tokens 8 g + t', halves p) hit 16
+// different 16-byte bank groups.
+// The x staging waits (s_waitcnt vmcnt with the weight loads' count left
+// outstanding, then a raw barrier) while the weights are still in flight.
+template <int T, int TPW, int W, int U>
+__global__ __launch_bounds__(64 * W) void qskinny_lds8_kernel(const uint32_t* __restrict__ w,
+                                                             const uint16_t* __restrict__ scales,
+                                                             const uint16_t* __restrict__ biases,
+                                                             const uint16_t* __restrict__ x,
+                                                             uint16_t* __restrict__ y, int M,
+                                                             int N, int K, bool vec) {
+  static_assert(W % 2 == 0, "waves pair up over the two octets of a tile");
+  constexpr int kStride = W / 2;  // span stride of a wave
+  constexpr int kWeightLoads = 3 * U * TPW < 63 ? 3 * U * TPW : 63;
+  __shared__ float2 part[W][TPW][2][64];
+  extern __shared__ uint4 xs[];  // x [M, K], pieces XOR-placed within 16-piece blocks
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int o = wave & 1;
+  const int c = lane & 15, h = lane >> 4;
+  const int n0 = blockIdx.x * (kRows * TPW);
+  const int gpr = K >> 6;
+  const int spans = K >> 8;
+  const int row_pieces = K >> 3;
+  const auto wr = make_rsrc(w, (uint32_t)((size_t)N * K / 2));
+  const auto sr = make_rsrc(scales, (uint32_t)((size_t)N * gpr * 2));
+  const auto br = make_rsrc(biases, (uint32_t)((size_t)N * gpr * 2));
+  const auto xr = make_rsrc(x, (uint32_t)((size_t)M * K * 2));
+
+  // 1. x -> LDS: instruction e stages pieces [64 i, 64 i + 64) of row m (1 KB
+  //    of x, read contiguously: the XOR stays inside 16-piece blocks).
+  {
+    const int per_row = K >> 9;
+    for (int e = wave; e < M * per_row; e += W) {
+      const int m = e / per_row, i = e - m * per_row;
+      const int u = 64 * i + lane;
+      const int q = u ^ ((2 * (m & 7) + ((u >> 4) & 1)) & 15);
+      load_lds16(xr, (uint32_t)(m * K + 8 * q) * 2u, 0u, xs + m * row_pieces + 64 * i);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. This wave's weight, scale and bias fragments: octet o of tile t, tile
+  //    row 4 (c / 4) + 2 o + (c / 2) % 2.
+  uint32_t w_off[TPW], p_off[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const uint32_t row =
+        (uint32_t)min(n0 + kRows * t + 4 * (c >> 2) + 2 * o + ((c >> 1) & 1), N - 1);
+    w_off[t] = row * (uint32_t)(K / 2) + (uint32_t)(c & 1) * 64u + (uint32_t)h * 16u;
+    p_off[t] = (row * (uint32_t)gpr + 2u * (uint32_t)(c & 1) + (uint32_t)(h >> 1)) * 2u;
+  }
+  // B operand of token group g: row min(8 g + c / 2, M - 1) (columns past M are
+  // never stored), half c % 2.
+  uint32_t xo[2][4];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int m = min(8 * g + (c >> 1), M - 1);
+    const int sw = 2 * (m & 7) + (c & 1);
+    const uint32_t xb = (uint32_t)(m * row_pieces + 16 * (c & 1)) * 16u;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xo[g][s] = xb + (uint32_t)(((4 * h + s) ^ sw) * 16);
+  }
+  f32x4_t acc[TPW][2];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) acc[t][0] = acc[t][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  bool first = true;
+  for (int sp0 = wave >> 1; sp0 < spans; sp0 += kStride * U) {
+    u32x4_t wv[U][TPW];
+    uint16_t sv[U][TPW], bv[U][TPW];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t sp = (uint32_t)min(sp0 + u * kStride, spans - 1);
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        wv[u][t] = load_b128(wr, w_off[t], sp * 128u);
+        sv[u][t] = __builtin_amdgcn_raw_buffer_load_b16(sr, p_off[t], sp * 8u, 0);
+        bv[u][t] = __builtin_amdgcn_raw_buffer_load_b16(br, p_off[t], sp * 8u, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (first) {
+      // The x loads (issued first) have landed once at most the 3 U TPW
+      // weight-side loads are outstanding (the counter tracks at most 63: with
+      // more, the oldest had retired before the last could issue); after the
+      // barrier every wave's have.
+      IMQ_WAIT_VMCNT(kWeightLoads);
+      __builtin_amdgcn_s_barrier();
+      first = false;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // A span past the end gets scale and bias 0 (weights +0): no branch, so
+    // its loads stay above.
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool valid = sp0 + u * kStride < spans;
+      const uint32_t sp = (uint32_t)min(sp0 + u * kStride, spans - 1);
+      u32x4_t xf[2][4];
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          xf[g][s] = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(xs) +
+                                                       xo[g][s] + sp * 512u);
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const float sc = valid ? Elem<T>::param(sv[u][t]) : 0.0f;
+        const float s24 = sc * 0x1p24f, s20 = sc * 0x1p20f;
+        const float b = valid ? Elem<T>::param(bv[u][t]) : 0.0f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          uint32_t p[4];
+          Elem<T>::dequant(wv[u][t][s], s24, s20, b, p);
+          const u32x4_t a = u32x4_t{p[0], p[1], p[2], p[3]};
+          acc[t][0] = mfma16x16x32<T>(a, xf[0][s], acc[t][0]);
+          acc[t][1] = mfma16x16x32<T>(a, xf[1][s], acc[t][1]);
+        }
+      }
+    }
+  }
+  if (first) {  // a wave with no span (W / 2 > spans) still meets the others at the barrier
+    IMQ_WAIT_VMCNT(0);
+    __builtin_amdgcn_s_barrier();
+  }
+  // Lane (j, g') holds rows 4 g' + v of column j: its half j % 2 is in v = j % 2
+  // (octet row 2 g') and v = 2 + j % 2 (octet row 2 g' + 1).
+  const bool odd = (c & 1) != 0;
+#pragma unroll
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      float v0 = odd ? acc[t][g][1] : acc[t][g][0];
+      float v1 = odd ? acc[t][g][3] : acc[t][g][2];
+      v0 += swap_adjacent(v0);
+      v1 += swap_adjacent(v1);
+      part[wave][t][g][lane] = make_float2(v0, v1);
+    }
+  __syncthreads();
+  if (wave >= TPW || odd) return;
+  const int t = wave;
+  const int f0 = n0 + kRows * t + 4 * h;
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int m = 8 * g + (c >> 1);
+    if (m >= M) continue;
+    float sum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      const float2 v = part[i][t][g][lane];
+      sum[2 * (i & 1)] += v.x;
+      sum[2 * (i & 1) + 1] += v.y;
+    }
+    uint16_t* yr = y + (size_t)m * N;
+    if (vec && f0 + 3 < N) {
+      *reinterpret_cast<uint2*>(yr + f0) =
+          make_uint2(Elem<T>::pack2(sum[0], sum[1]), Elem<T>::pack2(sum[2], sum[3]));
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (f0 + v < N) yr[f0 + v] = Elem<T>::out(sum[v]);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // M <= 8, x in LDS, K % 512 == 0: eight weight rows x 128 bytes per load.
 //
@@ -332,11 +516,6 @@ __global__ __launch_bounds__(64 * W) void qskinny_lds_kernel(const uint32_t* __r
 // hit 16 different 16-byte bank groups (rows are K / 8 pieces apart, a
 // multiple of 16).  One DMA instruction stages 64 pieces of a row: the XOR
 // stays inside 16-piece blocks, so it still reads 1 KB of x contiguously.
-__device__ __forceinline__ float swap_adjacent(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF,
-                                                            0xF, true));  // quad_perm 1,0,3,2
-}
-
 template <int T, int W, int U>
 __global__ __launch_bounds__(64 * W) void qskinny_half_kernel(const uint32_t* __restrict__ w,
                                                               const uint16_t* __restrict__ scales,
@@ -524,13 +703,17 @@ constexpr int kLdsMaxK = 4096;
 constexpr int kLdsWaves = 8;
 
 // Largest U compiled for (TPW, W) of the LDS kernel (6 registers per tile and
-// chunk, W / 4 waves per SIMD).
+// span, W / 4 waves per SIMD; with eight waves four tiles x 8 spans would spill,
+// and K <= kLdsMaxK gives a wave at most 4 spans anyway).
 constexpr int max_u_lds(int tpw, int w) {
-  return w == 16 ? (tpw == 1 ? 8 : tpw == 2 ? 6 : tpw == 3 ? 4 : 3) : 8;
+  return w == 16 ? (tpw == 1 ? 8 : tpw == 2 ? 6 : tpw == 3 ? 4 : 3) : (tpw == 4 ? 6 : 8);
 }
 
-// Bytes of the x tile in LDS: M rows of 2 K bytes plus a 16-byte pad each.
-size_t lds_x_bytes(int k, int m) { return (size_t)m * (2 * (size_t)k + 16); }
+// Bytes of the x tile in LDS: M rows of 2 K bytes, plus a 16-byte pad each for
+// the one-tile kernel.
+size_t lds_x_bytes(int k, int m, int tpw) {
+  return (size_t)m * (2 * (size_t)k + (tpw == 1 ? 16 : 0));
+}
 
 struct LdsPlan {
   int tpw, u;
@@ -549,7 +732,7 @@ LdsPlan plan_lds(int k, int n, int m) {
       break;
     }
   const bool ok = m >= kLdsMinM && k <= kLdsMaxK && k % 512 == 0 &&
-                  lds_x_bytes(k, m) + (size_t)kLdsWaves * tpw * 1024 <= 128 * 1024;
+                  lds_x_bytes(k, m, tpw) + (size_t)kLdsWaves * tpw * 1024 <= 128 * 1024;
   const int u = std::max(1, std::min((chunks + kLdsWaves - 1) / kLdsWaves,
                                      max_u_lds(tpw, kLdsWaves)));
   return LdsPlan{tpw, u, ok};
@@ -563,8 +746,12 @@ hipError_t launch_lds_twu(const uint32_t* w, const uint16_t* s, const uint16_t* 
     return hipErrorInvalidValue;
   } else {
     const dim3 grid((unsigned)((n + kRows * TPW - 1) / (kRows * TPW))), block(64 * W);
-    hipLaunchKernelGGL((qskinny_lds_kernel<T, TPW, W, U>), grid, block, lds_x_bytes(k, m),
-                       stream, w, s, b, x, y, m, n, k, vec);
+    if constexpr (TPW == 1)
+      hipLaunchKernelGGL((qskinny_lds_kernel<T, TPW, W, U>), grid, block, lds_x_bytes(k, m, TPW),
+                         stream, w, s, b, x, y, m, n, k, vec);
+    else
+      hipLaunchKernelGGL((qskinny_lds8_kernel<T, TPW, W, U>), grid, block, lds_x_bytes(k, m, TPW),
+                         stream, w, s, b, x, y, m, n, k, vec);
     return hipGetLastError();
   }
 }
