@@ -784,7 +784,13 @@ hipError_t launch_lds_t(const uint32_t* w, const uint16_t* s, const uint16_t* b,
 // (512 k each, the last range shorter); it stages only its x slice [M, 512
 // per] in LDS (rows 1024 per + 16 bytes apart) and writes fp32 partial sums
 // to ws[s][m][n]; qskinny_reduce_kernel adds the splits in order and rounds
-// to T (deterministic).  For [2560 x 9728] (160 row tiles, x of 16 rows 311
+// to T (deterministic).  The second launch costs about 2.9 us per call
+// ([2560 x 9728] M = 16: 13.7 us, 10.8 without it), but adding the splits in
+// the last-arriving workgroup of each tile group (arrival counters, no
+// waiting) measured slower in every form tried: device-scope fences in every
+// workgroup (each writes back and invalidates its XCD's L2) 84 us,
+// agent-scope atomic stores and loads of the partial sums 19 us, atomic
+// stores with one acquire fence in the last workgroup 16.8 us.  For [2560 x 9728] (160 row tiles, x of 16 rows 311
 // KB) the 16-row kernel re-reads all of x from L2 per tile (about 50 MB for
 // 12.5 MB of weights) on 160 workgroups; here each x byte is read once per
 // tile group and split and the grid fills the CUs.
@@ -903,7 +909,6 @@ __global__ __launch_bounds__(64 * W) void qskinny_split_kernel(const uint32_t* _
   }
 }
 
-// y[i] = T(sum over s of ws[s][i]) for i < count (= M N), splits added in order.
 // y[i] = T(sum over s of ws[s][i]) for i < count (= M N), splits added in
 // order.  VEC (count % 4 == 0, y 8-byte aligned): four outputs per thread,
 // 16-byte partial loads, an 8-byte store; otherwise one output per thread.

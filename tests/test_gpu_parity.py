@@ -248,6 +248,49 @@ def test_few_row_split_plan(m, n, k, splits):
     assert plan["workspace_bytes"] == (splits * m * n * 4 if splits > 1 else 0), plan
 
 
+@pytest.mark.gpu
+def test_few_row_split_repeated_and_replayed():
+    """The few-row K split (partial sums in the stream's workspace, added by a
+    second kernel) on four shapes with different tile groups and splits,
+    alternating on one stream many times, then inside a captured graph
+    replayed several times with the zeroed outputs and eager calls in between:
+    every result equals the first call's bits."""
+    shapes = [(16, 2560, 9728), (12, 1000, 4608), (8, 2560, 9728), (13, 1030, 4608)]
+    probs = []
+    for i, (m, n, k) in enumerate(shapes):
+        assert imq.qmm_plan(m, n, k, torch.bfloat16)["splits"] > 1
+        p = synth.make_problem(m, n, k, seed=40 + i)
+        x, w, s_, b = synth.to_device(p)
+        probs.append((x, w, s_, b, imq.quantized_matmul(x, w, s_, b)))
+    torch.cuda.synchronize()
+    want = [bits(y) for *_, y in probs]
+    for rep in range(6):
+        for i, (x, w, s_, b, _) in enumerate(probs):
+            y = imq.quantized_matmul(x, w, s_, b)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(y), want[i]), f"eager call {rep} of shape {shapes[i]}"
+    stream = torch.cuda.Stream()
+    outs = [torch.empty_like(y) for *_, y in probs]
+    with torch.cuda.stream(stream):
+        for i, (x, w, s_, b, _) in enumerate(probs):  # the stream's workspace, outside capture
+            imq.quantized_matmul(x, w, s_, b, out=outs[i])
+    stream.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i, (x, w, s_, b, _) in enumerate(probs):
+            imq.quantized_matmul(x, w, s_, b, out=outs[i])
+    for rep in range(4):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, o in enumerate(outs):
+            assert np.array_equal(bits(o), want[i]), f"replay {rep} of shape {shapes[i]}"
+        x, w, s_, b, _ = probs[0]
+        assert np.array_equal(bits(imq.quantized_matmul(x, w, s_, b)), want[0])
+        torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("m,n,k", [(4, 384, 512), (5, 384, 512), (16, 1001, 1024), (13, 17, 128),
                                    (8, 9728, 2560), (4, 2560, 9728), (5, 2560, 9728),
