@@ -136,6 +136,23 @@ def bench_qgemv(imq, synth, torch, copies: int = 48, ms_list=(1, 4, 16),
                         "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts}
             log(f"{tag} M={m} N={n} K={k}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
         del ws, ss, bs
+        # The floor one launch of this size reaches: a device copy moving the
+        # M=1 call's bytes (half read, half written), rotated the same way.
+        byts = qmm_bytes(1, n, k)
+        words = byts // 8
+        src = [torch.empty(words, dtype=torch.int32, device="cuda") for _ in range(copies)]
+        dst = [torch.empty(words, dtype=torch.int32, device="cuda") for _ in range(copies)]
+        launches = [(lambda i=i: dst[i].copy_(src[i])) for i in range(copies)]
+        ms = time_graph(launches)
+        gbs = 8 * words / (ms * 1e-3) / 1e9
+        qg = out[f"M1_N{n}_K{k}"] if 1 in ms_list else None
+        out[f"copy_floor_N{n}_K{k}"] = {
+            "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "bytes": 8 * words,
+            "qgemv_M1_vs_copy": round(ms * 1e3 / qg["us"], 3) if qg else None}
+        log(f"device copy of the M=1 bytes ({8 * words} B moved): {ms * 1e3:.2f} us  "
+            f"{gbs:.0f} GB/s" + (f"  (qGEMV M=1 at {ms * 1e3 / qg['us']:.2f} of its rate)"
+                                  if qg else ""))
+        del src, dst
         torch.cuda.empty_cache()
     return out
 
