@@ -111,7 +111,7 @@ def time_graph(launches, replays: int = 5) -> float:
 
 
 def bench_qgemv(imq, synth, torch, copies: int = 48, ms_list=(1, 4, 16),
-                few_rows=(8, 16)) -> dict:
+                few_rows=(4, 8, 16)) -> dict:
     """The qGEMV at M in ms_list, and the regime dispatcher at M in few_rows (the
     weight-streaming matrix-core kernel), weights rotated over `copies` copies."""
     out = {}
