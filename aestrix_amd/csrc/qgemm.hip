@@ -826,20 +826,37 @@ __global__ __launch_bounds__(256) void reduce_ep_kernel(const float* __restrict_
   float a[8], u[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) a[e] = u[e] = 0.f;
-  for (int sp = 0; sp < splits; ++sp) {
-    const float* pr = ws + sp * stride + (size_t)row * ldp + c0;
-    if (vload) {
-      const float4 p0 = reinterpret_cast<const float4*>(pr)[0];
-      const float4 p1 = reinterpret_cast<const float4*>(pr)[1];
-      a[0] += p0.x; a[1] += p0.y; a[2] += p0.z; a[3] += p0.w;
-      a[4] += p1.x; a[5] += p1.y; a[6] += p1.z; a[7] += p1.w;
-      if constexpr (EP::kPair) {
-        const float4 q0 = reinterpret_cast<const float4*>(pr + ep.width)[0];
-        const float4 q1 = reinterpret_cast<const float4*>(pr + ep.width)[1];
-        u[0] += q0.x; u[1] += q0.y; u[2] += q0.z; u[3] += q0.w;
-        u[4] += q1.x; u[5] += q1.y; u[6] += q1.z; u[7] += q1.w;
+  if (vload) {
+    // The loads of kBatch splits go out before the first add (indices past
+    // the last split repeat it and are not added): one memory round trip per
+    // batch instead of one per split.
+    constexpr int kBatch = EP::kPair ? 4 : 8;
+    for (int s0 = 0; s0 < splits; s0 += kBatch) {
+      float4 p[kBatch][2], q[kBatch][2];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const float* pr = ws + (size_t)min(s0 + j, splits - 1) * stride + (size_t)row * ldp + c0;
+        p[j][0] = reinterpret_cast<const float4*>(pr)[0];
+        p[j][1] = reinterpret_cast<const float4*>(pr)[1];
+        if constexpr (EP::kPair) {
+          q[j][0] = reinterpret_cast<const float4*>(pr + ep.width)[0];
+          q[j][1] = reinterpret_cast<const float4*>(pr + ep.width)[1];
+        }
       }
-    } else {
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        if (s0 + j >= splits) break;
+        a[0] += p[j][0].x; a[1] += p[j][0].y; a[2] += p[j][0].z; a[3] += p[j][0].w;
+        a[4] += p[j][1].x; a[5] += p[j][1].y; a[6] += p[j][1].z; a[7] += p[j][1].w;
+        if constexpr (EP::kPair) {
+          u[0] += q[j][0].x; u[1] += q[j][0].y; u[2] += q[j][0].z; u[3] += q[j][0].w;
+          u[4] += q[j][1].x; u[5] += q[j][1].y; u[6] += q[j][1].z; u[7] += q[j][1].w;
+        }
+      }
+    }
+  } else {
+    for (int sp = 0; sp < splits; ++sp) {
+      const float* pr = ws + sp * stride + (size_t)row * ldp + c0;
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         if (c0 + e < ncols) {
