@@ -103,7 +103,7 @@ int imq_cond_create(imq_ctx* ctx, const imq_qweight* time_l1, const imq_qweight*
   int rc = bind_device(ctx);
   if (rc != IMQ_OK) return rc;
   auto* c = new (std::nothrow) imq_cond;
-  if (!c) return fail(ctx, IMQ_EHIP, "%s: out of host memory", fn);
+  if (!c) return fail(ctx, IMQ_ENOMEM, "%s: out of host memory", fn);
   c->ctx = ctx;
   c->l1 = *time_l1;
   c->l2 = *time_l2;

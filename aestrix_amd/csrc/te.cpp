@@ -100,7 +100,7 @@ int imq_te_create(imq_ctx* ctx, const imq_te_layer_weights* layers, int n_layers
   int rc = bind_device(ctx);
   if (rc != IMQ_OK) return rc;
   auto* te = new (std::nothrow) imq_te;
-  if (!te) return fail(ctx, IMQ_EHIP, "%s: out of host memory", fn);
+  if (!te) return fail(ctx, IMQ_ENOMEM, "%s: out of host memory", fn);
   te->ctx = ctx;
   te->layers.assign(layers, layers + n_layers);
   te->hidden = hidden;
