@@ -154,11 +154,17 @@ hipError_t encode(imq_dit_step* st, hipStream_t s) {
     const imq_qweight* W = &st->w[(size_t)12 * d.n_double + 2 * b];
     const float* g = st->gates + ((size_t)4 * d.n_double + b) * dim;
     ok(imq::launch_rmsnorm(st->X, st->norm_w, st->nX, J, dim, kEps, T, s));
-    ok(imq::launch_qgemm(W[0].w, W[0].scales, W[0].biases, st->nX, st->QKV, dim, 3 * dim, J, T, s,
-                         st->split));
+    // The Q/K/V rows (side stream) and the SwiGLU rows (main stream) of
+    // to_qkv_mlp_proj read the same input and write different buffers: run
+    // side by side, each one's part-empty last tile round fills with the
+    // other's tiles.
+    fork();
+    ok(imq::launch_qgemm(W[0].w, W[0].scales, W[0].biases, st->nX, st->QKV, dim, 3 * dim, J, T, t,
+                         st->split_txt));
     ok(imq::launch_qgemm_swiglu(W[0].w, W[0].scales, W[0].biases, st->nX, st->C + (size_t)dim * es,
                                 cw, dim, 3 * dim + 2 * ffi, J, ffi, 3 * dim, 3 * dim + ffi, 1.0f,
                                 1.0f, T, s, st->split));
+    join();
     ok(imq::launch_qgemm_gate_add(W[1].w, W[1].scales, W[1].biases, st->C, st->X, g, st->X, cw, dim,
                                   J, 1.0f, T, s, st->split));
   }
