@@ -712,6 +712,10 @@ def main() -> int:
     if qgemv := extra.get("qgemv"):
         result["qgemv_headline"] = {"shape": "M=1 [9728x2560]",
                                     **qgemv["M1_N9728_K2560"]}
+        if floor := qgemv.get("copy_floor_N9728_K2560"):
+            # A device copy moving the same bytes in one launch, same run.
+            result["qgemv_headline"]["copy_floor_GB/s"] = floor["GB/s"]
+            result["qgemv_headline"]["frac_of_copy_floor"] = floor["qgemv_M1_vs_copy"]
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(synth)
