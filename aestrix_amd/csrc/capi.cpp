@@ -204,20 +204,26 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
   const bool automatic = regime == Regime::kAuto || regime == Regime::kAutoNoAlloc;
   const bool gemv = regime == Regime::kGemv ||
                     (automatic && w_fits_gemv && (m <= imq::kDispatchGemvMaxM || dtype == IMQ_F32));
-  const bool skinny = automatic && m >= imq::kDispatchSkinnyMinM &&
-                      m <= imq::kDispatchSkinnyMaxM && imq::qskinny_supported(k, n, m, (int)dtype);
+  const bool few = automatic && m >= imq::kDispatchSkinnyMinM && m <= imq::kQskinnyMaxM &&
+                   imq::qskinny_supported(k, n, m, (int)dtype);
   auto st = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
-  if (skinny) {
-    // The few-row kernel may split K over a workspace (long K, few row tiles).
-    imq::SplitWs ws{};
+  // The few-row kernel may split K over a workspace (long K, few row tiles);
+  // past kDispatchSkinnyMaxM rows it runs only that way, and only with the
+  // workspace in hand (otherwise the tile kernel takes the call).
+  imq::SplitWs sws{};
+  bool skinny = false;
+  if (few) {
     const size_t need = imq::qskinny_split_bytes(k, n, m);
     if (regime == Regime::kAuto) {
-      ws = split_ws(ctx, st, need);
+      sws = split_ws(ctx, st, need);
     } else if (regime == Regime::kAutoNoAlloc && need > 0 && need <= imq::kStaticScratchBytes) {
-      ws = imq::SplitWs{static_cast<float*>(ctx->static_scratch), need};
+      sws = imq::SplitWs{static_cast<float*>(ctx->static_scratch), need};
     }
-    e = imq::launch_qskinny(w, s, b, x, y, k, n, m, (int)dtype, st, ws);
+    skinny = m <= imq::kDispatchSkinnyMaxM || (need > 0 && sws.p && sws.bytes >= need);
+  }
+  if (skinny) {
+    e = imq::launch_qskinny(w, s, b, x, y, k, n, m, (int)dtype, st, sws);
   } else if (!gemv) {
     // The dispatcher may split K over a workspace; imq_qgemm is the plain
     // tile kernel (the fused output stages equal it bit for bit).
@@ -502,9 +508,11 @@ int imq_qmm_plan(imq_ctx* ctx, int entry, int k, int n, int m, imq_dtype dtype, 
       return tile(entry == IMQ_ENTRY_FUSED, false);
     case IMQ_ENTRY_QMM_T: {
       const bool gemv = w_fits_gemv && (m <= imq::kDispatchGemvMaxM || dtype == IMQ_F32);
-      if (m >= imq::kDispatchSkinnyMinM && m <= imq::kDispatchSkinnyMaxM &&
-          imq::qskinny_supported(k, n, m, (int)dtype)) {
-        const size_t need = imq::qskinny_split_bytes(k, n, m);
+      const size_t few_need = imq::qskinny_supported(k, n, m, (int)dtype)
+                                  ? imq::qskinny_split_bytes(k, n, m) : 0;
+      if (m >= imq::kDispatchSkinnyMinM && imq::qskinny_supported(k, n, m, (int)dtype) &&
+          (m <= imq::kDispatchSkinnyMaxM || few_need > 0)) {
+        const size_t need = few_need;
         *out = imq_plan{IMQ_KERNEL_FEW_ROW, 0, need ? imq::qskinny_splits(k, n, m) : 1, need};
         return IMQ_OK;
       }

@@ -143,8 +143,10 @@ constexpr int kQgemvMaxM = 16;
 // growing with M.
 constexpr int kDispatchGemvMaxM = 4;
 
-// Largest M the weight-streaming MFMA kernel (qskinny.hip) takes.
-constexpr int kQskinnyMaxM = 16;
+// Largest M the weight-streaming MFMA kernel (qskinny.hip) takes: up to 16
+// rows every form of it, 17 to 32 rows its K split (two token groups per
+// weight fragment) where it plans one.
+constexpr int kQskinnyMaxM = 32;
 // The M range the regime dispatcher routes to it (bf16 / f16, K % 128 == 0),
 // ahead of the qGEMV.  With the weights coming from HBM (text-encoder MLP
 // shapes, 48 rotated copies), [9728 x 2560] M = 1 / 2 / 3 / 4: 7.7 / 7.7 /
@@ -171,18 +173,28 @@ constexpr size_t kStaticScratchBytes = (size_t)64 << 20;
 // up with hipGetSymbolAddress on the first call for a device.
 hipError_t static_scratch(int device, void** out);
 
-// Whether the weight-streaming kernel takes this call: 1 <= m <= 16,
-// k % 128 == 0, T in {bf16, f16}, 32-bit byte offsets.
+// Whether the weight-streaming kernel takes this call: 1 <= m <= 32,
+// k % 128 == 0, T in {bf16, f16}, 32-bit byte offsets (past 16 rows only with
+// its K split, below).
 bool qskinny_supported(int k, int n, int m, int dtype);
 // y[m][n] = x . deq(W)^T on the matrix cores, 16 weight rows per workgroup.
-// With a workspace of at least qskinny_split_bytes(k, n, m) (nonzero when the
-// row tiles leave CUs idle and K % 512 == 0, m >= 4), K is split over
+// With a workspace of at least qskinny_split_bytes(k, n, m) (nonzero when
+// K % 512 == 0, 8 <= m <= 32 and the row tiles are few or long: fewer than
+// 256, and up to 16 rows also when x does not fit LDS), K is split over
 // qskinny_splits(k, n, m) workgroup ranges whose fp32 partial sums a second
-// kernel adds in order; without one the unsplit kernels run.
+// kernel adds in order; without one the unsplit kernels run (m <= 16, else
+// hipErrorInvalidValue).
 size_t qskinny_split_bytes(int k, int n, int m);
 int qskinny_splits(int k, int n, int m);
 hipError_t launch_qskinny(const uint32_t* w, const void* scales, const void* biases, const void* x,
                           void* y, int k, int n, int m, int dtype, hipStream_t stream,
                           SplitWs ws = {});
+// The K split with the residual add of launch_qgemm_resid_add in its second
+// kernel: y = T(float(resid) + float(T(x . deq(W)^T))), y may be resid.  Only
+// where qskinny_split_bytes(k, n, m) > 0 and ws holds that many bytes
+// (hipErrorInvalidValue otherwise).
+hipError_t launch_qskinny_resid_add(const uint32_t* w, const void* scales, const void* biases,
+                                    const void* x, const void* resid, void* y, int k, int n, int m,
+                                    int dtype, hipStream_t stream, SplitWs ws);
 
 }  // namespace imq

@@ -27,6 +27,7 @@
 // for all of them (see plan_lds).
 #include <algorithm>
 
+#include "epilogue.hpp"
 #include "imq_device.hpp"
 #include "imq_kernels.hpp"
 
@@ -781,6 +782,8 @@ hipError_t launch_lds_t(const uint32_t* w, const uint16_t* s, const uint16_t* b,
 // ---- K split: the multi-tile kernel over a range of K, for long K ----
 //
 // Workgroup (g, s) owns TPW 16-row tiles and the K pieces [s per, s per + per)
+// for TG groups of 16 tokens (M <= 16 TG tokens; each dequantized weight
+// fragment feeds one MFMA per group)
 // (512 k each, the last range shorter); it stages only its x slice [M, 512
 // per] in LDS (rows 1024 per + 16 bytes apart) and writes fp32 partial sums
 // to ws[s][m][n]; qskinny_reduce_kernel adds the splits in order and rounds
@@ -794,7 +797,7 @@ hipError_t launch_lds_t(const uint32_t* w, const uint16_t* s, const uint16_t* b,
 // KB) the 16-row kernel re-reads all of x from L2 per tile (about 50 MB for
 // 12.5 MB of weights) on 160 workgroups; here each x byte is read once per
 // tile group and split and the grid fills the CUs.
-template <int T, int TPW, int W, int U>
+template <int T, int TPW, int W, int U, int TG>
 __global__ __launch_bounds__(64 * W) void qskinny_split_kernel(const uint32_t* __restrict__ w,
                                                                const uint16_t* __restrict__ scales,
                                                                const uint16_t* __restrict__ biases,
@@ -802,7 +805,7 @@ __global__ __launch_bounds__(64 * W) void qskinny_split_kernel(const uint32_t* _
                                                                float* __restrict__ ws, int M,
                                                                int N, int K, int per, bool vec) {
   constexpr int kWeightLoads = 3 * U * TPW < 63 ? 3 * U * TPW : 63;
-  __shared__ f32x4_t part[W][TPW][64];
+  __shared__ f32x4_t part[W][TPW][TG][64];
   extern __shared__ uint4 xs[];  // x [M, 512 per], rows 1024 per + 16 bytes apart
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -838,10 +841,16 @@ __global__ __launch_bounds__(64 * W) void qskinny_split_kernel(const uint32_t* _
     w_off[t] = row * (uint32_t)(K / 2) + (uint32_t)h * 16u;
     p_off[t] = (row * (uint32_t)gpr + (uint32_t)(h >> 1)) * 2u;
   }
-  f32x4_t acc[TPW];
+  f32x4_t acc[TPW][TG];
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int xrow = min(c, M - 1);
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int g = 0; g < TG; ++g) acc[t][g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // B operand of token group g (16 tokens): row min(16 g + c, M - 1); columns
+  // past M are never stored.
+  int xrow[TG];
+#pragma unroll
+  for (int g = 0; g < TG; ++g) xrow[g] = min(16 * g + c, M - 1);
   bool first = true;
   for (int ch0 = wave; ch0 < chunks; ch0 += W * U) {
     u32x4_t wv[U][TPW];
@@ -867,11 +876,13 @@ __global__ __launch_bounds__(64 * W) void qskinny_split_kernel(const uint32_t* _
     for (int u = 0; u < U; ++u) {
       const bool valid = ch0 + u * W < chunks;
       const int j = min(ch0 + u * W, chunks - 1);
-      u32x4_t xf[4];
+      u32x4_t xf[TG][4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        xf[i] = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(xs) +
-                                                   xrow * xstride + j * 256 + (4 * h + i) * 16);
+      for (int g = 0; g < TG; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          xf[g][i] = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(xs) +
+                                                      xrow[g] * xstride + j * 256 + (4 * h + i) * 16);
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const float sc = valid ? Elem<T>::param(sv[u][t]) : 0.0f;
@@ -881,7 +892,9 @@ __global__ __launch_bounds__(64 * W) void qskinny_split_kernel(const uint32_t* _
         for (int i = 0; i < 4; ++i) {
           uint32_t pq[4];
           Elem<T>::dequant(wv[u][t][i], s24, s20, b, pq);
-          acc[t] = mfma16x16x32<T>(u32x4_t{pq[0], pq[1], pq[2], pq[3]}, xf[i], acc[t]);
+          const u32x4_t a = u32x4_t{pq[0], pq[1], pq[2], pq[3]};
+#pragma unroll
+          for (int g = 0; g < TG; ++g) acc[t][g] = mfma16x16x32<T>(a, xf[g][i], acc[t][g]);
         }
       }
     }
@@ -891,31 +904,40 @@ __global__ __launch_bounds__(64 * W) void qskinny_split_kernel(const uint32_t* _
     __builtin_amdgcn_s_barrier();
   }
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) part[wave][t][lane] = acc[t];
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int g = 0; g < TG; ++g) part[wave][t][g][lane] = acc[t][g];
   __syncthreads();
-  if (wave >= TPW || c >= M) return;
+  if (wave >= TPW) return;
   const int t = wave;
-  f32x4_t sum = part[0][t][lane];
-#pragma unroll
-  for (int i = 1; i < W; ++i) sum += part[i][t][lane];
   const int f0 = n0 + kRows * t + 4 * h;
-  float* dst = ws + ((size_t)blockIdx.y * M + c) * N;
-  if (vec && f0 + 3 < N) {
-    *reinterpret_cast<float4*>(dst + f0) = make_float4(sum[0], sum[1], sum[2], sum[3]);
-  } else {
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
-      if (f0 + v < N) dst[f0 + v] = sum[v];
+  for (int g = 0; g < TG; ++g) {
+    const int m = 16 * g + c;
+    if (m >= M) continue;
+    f32x4_t sum = part[0][t][g][lane];
+#pragma unroll
+    for (int i = 1; i < W; ++i) sum += part[i][t][g][lane];
+    float* dst = ws + ((size_t)blockIdx.y * M + m) * N;
+    if (vec && f0 + 3 < N) {
+      *reinterpret_cast<float4*>(dst + f0) = make_float4(sum[0], sum[1], sum[2], sum[3]);
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (f0 + v < N) dst[f0 + v] = sum[v];
+    }
   }
 }
 
 // y[i] = T(sum over s of ws[s][i]) for i < count (= M N), splits added in
-// order.  VEC (count % 4 == 0, y 8-byte aligned): four outputs per thread,
-// 16-byte partial loads, an 8-byte store; otherwise one output per thread.
-template <int T, bool VEC>
+// order; with RES, y[i] = T(float(r[i]) + float(T(sum))), the text encoder's
+// dq_add after the qmm (EpResidAdd's arithmetic; y may be r).  VEC (count % 4
+// == 0, y and r 8-byte aligned): four outputs per thread, 16-byte partial
+// loads, an 8-byte store; otherwise one output per thread.
+template <int T, bool VEC, bool RES>
 __global__ __launch_bounds__(256) void qskinny_reduce_kernel(const float* __restrict__ ws,
                                                              int splits, int count,
-                                                             uint16_t* __restrict__ y) {
+                                                             const uint16_t* r, uint16_t* y) {
   const int t = blockIdx.x * 256 + threadIdx.x;
   if constexpr (VEC) {
     const int i = t * 4;
@@ -929,12 +951,20 @@ __global__ __launch_bounds__(256) void qskinny_reduce_kernel(const float* __rest
       a.z += v.z;
       a.w += v.w;
     }
+    if constexpr (RES) {
+      const uint2 rv = *reinterpret_cast<const uint2*>(r + i);
+      a.x = staged_value<T>(rv.x & 0xFFFFu) + round_to(a.x, T);
+      a.y = staged_value<T>(rv.x >> 16) + round_to(a.y, T);
+      a.z = staged_value<T>(rv.y & 0xFFFFu) + round_to(a.z, T);
+      a.w = staged_value<T>(rv.y >> 16) + round_to(a.w, T);
+    }
     *reinterpret_cast<uint2*>(y + i) = make_uint2(Elem<T>::pack2(a.x, a.y), Elem<T>::pack2(a.z, a.w));
   } else {
     if (t >= count) return;
     float a = ws[t];
 #pragma unroll 4
     for (int sp = 1; sp < splits; ++sp) a += ws[(size_t)sp * count + t];
+    if constexpr (RES) a = staged_value<T>(r[t]) + round_to(a, T);
     y[t] = Elem<T>::out(a);
   }
 }
@@ -958,22 +988,36 @@ size_t split_x_bytes(int per, int m) { return (size_t)m * (1024 * (size_t)per + 
 // 5 at K = 9728 (x in LDS: 11.7 -> 12.2, 11.9 -> 12.9 us), [2560 x 4096] M =
 // 16 (9.4 -> 10.0), [3072 x 3072] at M = 4 / 8 / 16 (6.3 -> 8.3-8.9 us): there
 // the second launch and the partial sums cost more than the better-filled
-// grid saves.  Among the plans whose x slice fits 64 KB and whose grid fills
-// the CUs: the least estimated L2 traffic (x slices, weights, partial sums).
+// grid saves.  17 to 32 rows (two token groups per weight fragment) take it
+// wherever the row tiles are fewer than 256, against the tile kernel's 32-row
+// tiles and their split K (same box, A/B builds, M = 30 unless stated):
+// [2560 x 9728] 19.1 -> 17.0 us (M = 17 18.0 -> 15.9), [2560 x 4096] 14.7 ->
+// 13.2, [2560 x 2560] 11.4 -> 8.0, [1000 x 4608] 13.6 -> 7.2, [3072 x 3072]
+// 12.7 -> 12.4, M = 24 [1024 x 2560] 10.5 -> 5.8.  Among the plans whose x
+// slice fits 64 KB (80 KB for two token groups) and whose grid fills the CUs:
+// the least estimated L2 traffic (x slices, weights, partial sums).
 SplitPlan plan_split(int k, int n, int m) {
   SplitPlan best{0, 0, 0, 0, false};
-  if (k % 512 != 0 || k / 512 < 2 || m < 8) return best;
+  if (k % 512 != 0 || k / 512 < 2 || m < 8 || m > 2 * kRows) return best;
   const int pieces = k / 512;
   const long tiles = (n + kRows - 1) / kRows;
-  if (tiles >= 256 || (tiles > 128 && k < 8192)) return best;
-  if ((size_t)m * k * 2 <= (size_t)kXLdsMax || plan_lds(k, n, m).ok) return best;
+  if (tiles >= 256) return best;
+  // Up to 16 rows the unsplit kernels are the alternative; past 16 rows (two
+  // token groups, this kernel only) the tile kernel is.
+  if (m <= kRows) {
+    if (tiles > 128 && k < 8192) return best;
+    if ((size_t)m * k * 2 <= (size_t)kXLdsMax || plan_lds(k, n, m).ok) return best;
+  }
   long best_traffic = -1;
   for (int tpw = 1; tpw <= 4; ++tpw) {
     const long groups = (tiles + tpw - 1) / tpw;
     for (int per = 1; per <= pieces; ++per) {
       const int splits = (pieces + per - 1) / per;
       if (splits < 2 || groups * splits < 256) continue;
-      if (split_x_bytes(per, m) > 64 * 1024) continue;
+      // x slice budget: 64 KB beside the 32 KB of per-wave sums of one token
+      // group; 80 KB beside the 64 KB of two (32 rows then still take two
+      // 512-k pieces per split).
+      if (split_x_bytes(per, m) > (m > kRows ? 80 : 64) * 1024) continue;
       const long traffic = groups * splits * ((long)m * per * 1024 + (long)tpw * kRows * per * 256) +
                            (long)splits * m * n * 8;
       if (best_traffic < 0 || traffic < best_traffic) {
@@ -996,8 +1040,14 @@ hipError_t launch_split_tu(const uint32_t* w, const uint16_t* s, const uint16_t*
     return hipErrorInvalidValue;
   } else {
     const dim3 grid((unsigned)((n + kRows * TPW - 1) / (kRows * TPW)), (unsigned)p.splits);
-    hipLaunchKernelGGL((qskinny_split_kernel<T, TPW, kSplitWaves, U>), grid, dim3(64 * kSplitWaves),
-                       split_x_bytes(p.per, m), stream, w, s, b, x, ws, m, n, k, p.per, vec);
+    if (m > kRows)
+      hipLaunchKernelGGL((qskinny_split_kernel<T, TPW, kSplitWaves, U, 2>), grid,
+                         dim3(64 * kSplitWaves), split_x_bytes(p.per, m), stream, w, s, b, x, ws,
+                         m, n, k, p.per, vec);
+    else
+      hipLaunchKernelGGL((qskinny_split_kernel<T, TPW, kSplitWaves, U, 1>), grid,
+                         dim3(64 * kSplitWaves), split_x_bytes(p.per, m), stream, w, s, b, x, ws,
+                         m, n, k, p.per, vec);
     return hipGetLastError();
   }
 }
@@ -1019,8 +1069,8 @@ hipError_t launch_split_t(const uint32_t* w, const uint16_t* s, const uint16_t* 
 
 template <int T>
 hipError_t launch_split(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
-                        uint16_t* y, float* ws, int k, int n, int m, const SplitPlan& p,
-                        hipStream_t stream) {
+                        const uint16_t* resid, uint16_t* y, float* ws, int k, int n, int m,
+                        const SplitPlan& p, hipStream_t stream) {
   const bool vec = n % 4 == 0 && ((uintptr_t)ws & 15u) == 0;
   hipError_t e;
   switch (p.tpw) {
@@ -1031,12 +1081,23 @@ hipError_t launch_split(const uint32_t* w, const uint16_t* s, const uint16_t* b,
   }
   if (e != hipSuccess) return e;
   const int count = m * n;
-  if (count % 4 == 0 && ((uintptr_t)y & 7u) == 0)
-    hipLaunchKernelGGL((qskinny_reduce_kernel<T, true>), dim3((unsigned)((count / 4 + 255) / 256)),
-                       dim3(256), 0, stream, ws, p.splits, count, y);
-  else
-    hipLaunchKernelGGL((qskinny_reduce_kernel<T, false>), dim3((unsigned)((count + 255) / 256)),
-                       dim3(256), 0, stream, ws, p.splits, count, y);
+  const bool rvec = count % 4 == 0 && ((uintptr_t)y & 7u) == 0 && ((uintptr_t)resid & 7u) == 0;
+  const dim3 grid((unsigned)(((rvec ? count / 4 : count) + 255) / 256));
+  if (resid) {
+    if (rvec)
+      hipLaunchKernelGGL((qskinny_reduce_kernel<T, true, true>), grid, dim3(256), 0, stream, ws,
+                         p.splits, count, resid, y);
+    else
+      hipLaunchKernelGGL((qskinny_reduce_kernel<T, false, true>), grid, dim3(256), 0, stream, ws,
+                         p.splits, count, resid, y);
+  } else {
+    if (rvec)
+      hipLaunchKernelGGL((qskinny_reduce_kernel<T, true, false>), grid, dim3(256), 0, stream, ws,
+                         p.splits, count, nullptr, y);
+    else
+      hipLaunchKernelGGL((qskinny_reduce_kernel<T, false, false>), grid, dim3(256), 0, stream, ws,
+                         p.splits, count, nullptr, y);
+  }
   return hipGetLastError();
 }
 
@@ -1045,7 +1106,8 @@ hipError_t launch_t(const uint32_t* w, const uint16_t* s, const uint16_t* b, con
                     uint16_t* y, int k, int n, int m, hipStream_t stream, SplitWs ws) {
   const SplitPlan sp = plan_split(k, n, m);
   if (sp.ok && ws.p && ws.bytes >= (size_t)sp.splits * m * n * sizeof(float))
-    return launch_split<T>(w, s, b, x, y, ws.p, k, n, m, sp, stream);
+    return launch_split<T>(w, s, b, x, nullptr, y, ws.p, k, n, m, sp, stream);
+  if (m > kRows) return hipErrorInvalidValue;  // past 16 rows only the K split runs
   const bool vec = n % 4 == 0 && ((uintptr_t)y & 7u) == 0;
   const LdsPlan lp = plan_lds(k, n, m);
   if (lp.ok) {
@@ -1071,6 +1133,22 @@ bool qskinny_supported(int k, int n, int m, int dtype) {
   return m >= 1 && m <= kQskinnyMaxM && n >= 1 && k >= kChunkK && k % kChunkK == 0 &&
          (dtype == kBf16 || dtype == kF16) && (size_t)n * k / 2 < ((size_t)1 << 32) &&
          (size_t)m * k * 2 < ((size_t)1 << 31);
+}
+
+hipError_t launch_qskinny_resid_add(const uint32_t* w, const void* scales, const void* biases,
+                                    const void* x, const void* resid, void* y, int k, int n, int m,
+                                    int dtype, hipStream_t stream, SplitWs ws) {
+  if (!qskinny_supported(k, n, m, dtype)) return hipErrorInvalidValue;
+  const SplitPlan sp = plan_split(k, n, m);
+  if (!sp.ok || !ws.p || ws.bytes < (size_t)sp.splits * m * n * sizeof(float))
+    return hipErrorInvalidValue;
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* b = static_cast<const uint16_t*>(biases);
+  const auto* xx = static_cast<const uint16_t*>(x);
+  const auto* rr = static_cast<const uint16_t*>(resid);
+  auto* yy = static_cast<uint16_t*>(y);
+  if (dtype == kBf16) return launch_split<kBf16>(w, s, b, xx, rr, yy, ws.p, k, n, m, sp, stream);
+  return launch_split<kF16>(w, s, b, xx, rr, yy, ws.p, k, n, m, sp, stream);
 }
 
 size_t qskinny_split_bytes(int k, int n, int m) {

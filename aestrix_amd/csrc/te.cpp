@@ -41,13 +41,23 @@ bool weight_ok(const imq_qweight& q, imq_dtype dtype) {
          (size_t)q.n * (size_t)q.k / 2 < ((size_t)1 << 32);
 }
 
+// Whether the few-row kernel's K split takes this projection past 16 rows
+// (its plan exists and the plan's workspace holds its partial sums).
+bool few_row_split(const imq_te* te, const imq_qweight& q, int rows) {
+  const int dt = (int)te->dtype;
+  if (rows <= imq::kDispatchSkinnyMaxM || !imq::qskinny_supported(q.k, q.n, rows, dt)) return false;
+  const size_t need = imq::qskinny_split_bytes(q.k, q.n, rows);
+  return need > 0 && te->split.p && te->split.bytes >= need;
+}
+
 // The regime dispatcher's choice for a plain projection (imq_qmm_t's, with
 // the plan's workspace).
 hipError_t plain_qmm(const imq_te* te, const imq_qweight& q, const void* x, void* y, int rows,
                      hipStream_t st) {
   const int dt = (int)te->dtype;
-  if (rows >= imq::kDispatchSkinnyMinM && rows <= imq::kDispatchSkinnyMaxM &&
-      imq::qskinny_supported(q.k, q.n, rows, dt))
+  if ((rows >= imq::kDispatchSkinnyMinM && rows <= imq::kDispatchSkinnyMaxM &&
+       imq::qskinny_supported(q.k, q.n, rows, dt)) ||
+      few_row_split(te, q, rows))
     return imq::launch_qskinny(q.w, q.scales, q.biases, x, y, q.k, q.n, rows, dt, st, te->split);
   if (rows <= imq::kDispatchGemvMaxM)
     return imq::launch_qgemv(q.w, q.scales, q.biases, x, y, q.k, q.n, rows, dt, st);
@@ -115,8 +125,11 @@ int imq_te_create(imq_ctx* ctx, const imq_te_layer_weights* layers, int n_layers
   size_t ws = 0;
   for (int rows = 1; rows <= max_rows; ++rows) {
     ws = std::max(ws, imq::qgemm_split_bytes(hidden, l0.qkv.n, rows, false));
-    if (rows <= imq::kDispatchSkinnyMaxM)
+    if (rows <= imq::kQskinnyMaxM) {
       ws = std::max(ws, imq::qskinny_split_bytes(hidden, l0.qkv.n, rows));
+      ws = std::max(ws, imq::qskinny_split_bytes(nq, hidden, rows));
+      ws = std::max(ws, imq::qskinny_split_bytes(inter, hidden, rows));
+    }
     ws = std::max(ws, imq::qgemm_split_bytes(nq, hidden, rows, true));
     ws = std::max(ws, imq::qgemm_split_bytes(hidden, 2 * inter, rows, true));
     ws = std::max(ws, imq::qgemm_split_bytes(inter, hidden, rows, true));
@@ -174,8 +187,13 @@ int imq_te_attn_out_mlp(imq_te* te, int layer, const void* x, const void* attn_o
   const auto st = static_cast<hipStream_t>(stream);
   const int dt = (int)te->dtype;
   const int h = te->hidden, in = te->inter;
-  hipError_t e = imq::launch_qgemm_resid_add(l.o.w, l.o.scales, l.o.biases, attn_o, x, te->r,
-                                             te->nq, h, rows, dt, st, te->split);
+  // o_proj and down_proj with dq_add: past 16 rows the few-row kernel's K
+  // split where it takes the shape, else the tile kernel.
+  hipError_t e = few_row_split(te, l.o, rows)
+                     ? imq::launch_qskinny_resid_add(l.o.w, l.o.scales, l.o.biases, attn_o, x,
+                                                     te->r, te->nq, h, rows, dt, st, te->split)
+                     : imq::launch_qgemm_resid_add(l.o.w, l.o.scales, l.o.biases, attn_o, x, te->r,
+                                                   te->nq, h, rows, dt, st, te->split);
   if (e == hipSuccess) e = imq::launch_rmsnorm_t(te->r, l.norm_post, te->h1, rows, h, te->eps, dt, st);
   if (e == hipSuccess) {
     const imq_qweight& g = l.gate_up;
@@ -186,8 +204,11 @@ int imq_te_attn_out_mlp(imq_te* te, int layer, const void* x, const void* attn_o
                                        in, 0, in, 1.0f, 1.0f, dt, st, te->split);
   }
   if (e == hipSuccess)
-    e = imq::launch_qgemm_resid_add(l.down.w, l.down.scales, l.down.biases, te->m, te->r, y, in, h,
-                                    rows, dt, st, te->split);
+    e = few_row_split(te, l.down, rows)
+            ? imq::launch_qskinny_resid_add(l.down.w, l.down.scales, l.down.biases, te->m, te->r, y,
+                                            in, h, rows, dt, st, te->split)
+            : imq::launch_qgemm_resid_add(l.down.w, l.down.scales, l.down.biases, te->m, te->r, y,
+                                          in, h, rows, dt, st, te->split);
   return e == hipSuccess ? IMQ_OK : hip_fail(te->ctx, e, fn);
 }
 

@@ -96,5 +96,9 @@ hipError_t launch_qskinny(const uint32_t*, const void*, const void*, const void*
                           int, int, hipStream_t, SplitWs) {
   return hipErrorNoDevice;
 }
+hipError_t launch_qskinny_resid_add(const uint32_t*, const void*, const void*, const void*,
+                                    const void*, void*, int, int, int, int, hipStream_t, SplitWs) {
+  return hipErrorNoDevice;
+}
 
 }  // namespace imq

@@ -248,6 +248,26 @@ def test_few_row_split_plan(m, n, k, splits):
     assert plan["workspace_bytes"] == (splits * m * n * 4 if splits > 1 else 0), plan
 
 
+@pytest.mark.parametrize("m,n,k,splits", [(17, 2560, 9728, 10), (30, 2560, 9728, 10),
+                                          (32, 2560, 9728, 10), (30, 2560, 4096, 8),
+                                          (24, 1024, 2560, 5), (24, 1030, 4608, 9),
+                                          (30, 9728, 2560, 0), (30, 2560, 1024, 2),
+                                          (33, 2560, 9728, 0), (20, 2560, 2560, 5),
+                                          (24, 2560, 3840, 0), (20, 17, 1024, 0)])
+def test_few_row_split_past_16_rows_plan(m, n, k, splits):
+    """17 to 32 rows take the few-row kernel's K split (two token groups per
+    weight fragment) where it plans one: fewer than 256 row tiles, K % 512 ==
+    0 with at least two 512-k pieces, and enough (tile group, split) work
+    units to fill the CUs.  The others here (splits 0) run the tile kernel:
+    608 row tiles, 33 rows, K = 3840, two row tiles at K = 1024."""
+    plan = imq.qmm_plan(m, n, k, torch.bfloat16)
+    if splits:
+        assert plan["kernel"] == "few_row" and plan["splits"] == splits, plan
+        assert plan["workspace_bytes"] == splits * m * n * 4, plan
+    else:
+        assert plan["kernel"] == "tile", plan
+
+
 @pytest.mark.gpu
 def test_few_row_split_repeated_and_replayed():
     """The few-row K split (partial sums in the stream's workspace, added by a
@@ -255,7 +275,8 @@ def test_few_row_split_repeated_and_replayed():
     alternating on one stream many times, then inside a captured graph
     replayed several times with the zeroed outputs and eager calls in between:
     every result equals the first call's bits."""
-    shapes = [(16, 2560, 9728), (12, 1000, 4608), (8, 2560, 9728), (13, 1030, 4608)]
+    shapes = [(16, 2560, 9728), (12, 1000, 4608), (8, 2560, 9728), (13, 1030, 4608),
+              (30, 2560, 9728), (25, 1030, 4608)]
     probs = []
     for i, (m, n, k) in enumerate(shapes):
         assert imq.qmm_plan(m, n, k, torch.bfloat16)["splits"] > 1
@@ -297,7 +318,9 @@ def test_few_row_split_repeated_and_replayed():
                                    (6, 2560, 9728), (8, 2560, 9728), (16, 2560, 9728),
                                    (9, 384, 192), (12, 9728, 2560), (16, 9728, 2560),
                                    (14, 3000, 4096), (12, 1000, 4608), (13, 1030, 4608),
-                                   (3, 1001, 1024), (7, 1030, 2560), (8, 17, 512)])
+                                   (3, 1001, 1024), (7, 1030, 2560), (8, 17, 512),
+                                   (17, 2560, 9728), (30, 2560, 4096), (32, 2560, 9728),
+                                   (24, 1030, 4608), (30, 1000, 4608), (20, 520, 9728)])
 def test_few_row_matrix_core_dispatch(dtype, m, n, k):
     """3 <= M <= 16 through the dispatcher.  The 16-row weight-streaming kernel
     stages x in LDS when M K 2, rounded up to whole wave instructions, fits
@@ -317,7 +340,10 @@ def test_few_row_matrix_core_dispatch(dtype, m, n, k):
     and the 16-row workgroups are few or long, K is split over workgroups (fp32
     partial sums added in order by a second kernel): [2560 x 9728] at M = 8 and
     16, 1000 x 4608 at M = 12, 1030 x 4608 at M = 13 (N % 4 != 0: the
-    single-element partial stores and reduction).  Oracle within tolerance, the same bits on
+    single-element partial stores and reduction).  17 to 32 rows run only that
+    split, with two token groups: [2560 x 9728] at M = 17 (the second group one
+    token) and 32, 2560 x 4096 at M = 30, 1030 x 4608 at M = 24, 1000 x 4608 at
+    M = 30, 520 x 9728 at M = 20 (a partial last row tile).  Oracle within tolerance, the same bits on
     a second call, and one-hot rows reproduce the dequantized weights bit for
     bit (a one-hot row has one nonzero product in one split)."""
     note(f"few-row dispatch {dtype} M={m} N={n} K={k}")
