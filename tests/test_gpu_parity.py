@@ -234,7 +234,8 @@ def test_split_k_dispatcher(m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k,splits", [(16, 2560, 9728, 10), (12, 2560, 9728, 10),
-                                          (12, 1000, 4608, 9), (8, 2560, 9728, 10),
+                                          (12, 1000, 4608, 5), (8, 2560, 9728, 10),
+                                          (16, 1024, 9728, 10), (13, 1030, 4608, 5),
                                           (6, 2560, 9728, 1), (4, 2560, 9728, 1), (16, 2560, 4096, 1),
                                           (16, 9728, 2560, 1), (3, 2560, 9728, 1)])
 def test_few_row_split_plan(m, n, k, splits):
@@ -249,17 +250,19 @@ def test_few_row_split_plan(m, n, k, splits):
 
 
 @pytest.mark.parametrize("m,n,k,splits", [(17, 2560, 9728, 10), (30, 2560, 9728, 10),
-                                          (32, 2560, 9728, 10), (30, 2560, 4096, 8),
-                                          (24, 1024, 2560, 5), (24, 1030, 4608, 9),
+                                          (32, 2560, 9728, 10), (30, 2560, 4096, 4),
+                                          (24, 1024, 2560, 3), (24, 1030, 4608, 5),
                                           (30, 9728, 2560, 0), (30, 2560, 1024, 2),
-                                          (33, 2560, 9728, 0), (20, 2560, 2560, 5),
-                                          (24, 2560, 3840, 0), (20, 17, 1024, 0)])
+                                          (33, 2560, 9728, 0), (20, 2560, 2560, 3),
+                                          (30, 3072, 3072, 3), (24, 2560, 3840, 0),
+                                          (20, 17, 1024, 2)])
 def test_few_row_split_past_16_rows_plan(m, n, k, splits):
     """17 to 32 rows take the few-row kernel's K split (two token groups per
-    weight fragment) where it plans one: fewer than 256 row tiles, K % 512 ==
-    0 with at least two 512-k pieces, and enough (tile group, split) work
-    units to fill the CUs.  The others here (splits 0) run the tile kernel:
-    608 row tiles, 33 rows, K = 3840, two row tiles at K = 1024."""
+    weight fragment) where it plans one: fewer than 256 row tiles and K % 512
+    == 0 with at least two 512-k pieces; the splits are those of the plan
+    with the least wave work on the busiest CU (two pieces per split where
+    the x slice allows it).  The others here (splits 0) run the tile kernel:
+    608 row tiles, 33 rows, K = 3840."""
     plan = imq.qmm_plan(m, n, k, torch.bfloat16)
     if splits:
         assert plan["kernel"] == "few_row" and plan["splits"] == splits, plan
