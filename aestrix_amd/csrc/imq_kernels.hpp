@@ -179,8 +179,9 @@ hipError_t static_scratch(int device, void** out);
 bool qskinny_supported(int k, int n, int m, int dtype);
 // y[m][n] = x . deq(W)^T on the matrix cores, 16 weight rows per workgroup.
 // With a workspace of at least qskinny_split_bytes(k, n, m) (nonzero when
-// K % 512 == 0, 8 <= m <= 32 and the row tiles are few or long: fewer than
-// 256, and up to 16 rows also when x does not fit LDS), K is split over
+// K % 512 == 0 and 6 <= m <= 32: up to 16 rows where x does not fit LDS or
+// the multi-tile kernel would take two rounds of the CUs, past 16 rows where
+// the row tiles are fewer than 256), K is split over
 // qskinny_splits(k, n, m) workgroup ranges whose fp32 partial sums a second
 // kernel adds in order; without one the unsplit kernels run (m <= 16, else
 // hipErrorInvalidValue).

@@ -975,14 +975,20 @@ struct SplitPlan {
 };
 
 constexpr int kSplitWaves = 8;
+// Fewest rows for the K split: at M <= 5 all of x fits LDS up to K = 9728
+// and the unsplit kernels stay faster ([2560 x 9728] M = 4: 10.2 us unsplit,
+// 10.2 us for the best split plan).
+constexpr int kSplitMinM = 6;
 
 // Bytes of the split kernel's x slice in LDS.
 size_t split_x_bytes(int per, int m) { return (size_t)m * (1024 * (size_t)per + 16); }
 
-// Taken where the unsplit kernels stream x per chunk from L2 (x [M, K] past
-// the 96 KiB LDS budget and not the multi-tile kernel's case), M >= 8, and
-// the 16-row workgroups are few (at most 128) or long (K >= 8192).  Measured
-// with the weights from HBM (same box, A/B builds): [2560 x 9728] M = 8 / 12
+// Taken, from M = 6, where the unsplit kernels would stream x per chunk from
+// L2 (x [M, K] past the 96 KiB LDS budget and not the multi-tile kernel's
+// case), and where it saves more than a quarter of the multi-tile kernel's
+// wave work (the plan rule below).  Its first planner (M >= 8, at most 128
+// row tiles or K >= 8192, least L2 traffic), measured with the weights from
+// HBM (same box, A/B builds): [2560 x 9728] M = 8 / 12
 // / 16 13.9 / 15.9 / 18.1 -> 13.2 / 13.5 / 13.8 us, [1000 x 4608] M = 12 9.5
 // -> 6.3 us, [1030 x 4608] M = 13 9.6 -> 6.6 us; elsewhere slower: M = 4 and
 // 5 at K = 9728 (x in LDS: 11.7 -> 12.2, 11.9 -> 12.9 us), [2560 x 4096] M =
@@ -1009,15 +1015,24 @@ size_t split_x_bytes(int per, int m) { return (size_t)m * (1024 * (size_t)per + 
 // [1024 x 9728] M = 16 10.1 -> 8.2 us.
 SplitPlan plan_split(int k, int n, int m) {
   SplitPlan best{0, 0, 0, 0, false};
-  if (k % 512 != 0 || k / 512 < 2 || m < 8 || m > 2 * kRows) return best;
+  if (k % 512 != 0 || k / 512 < 2 || m < kSplitMinM || m > 2 * kRows) return best;
   const int pieces = k / 512;
   const long tiles = (n + kRows - 1) / kRows;
-  if (tiles >= 256) return best;
-  // Up to 16 rows the unsplit kernels are the alternative; past 16 rows (two
-  // token groups, this kernel only) the tile kernel is.
+  // Up to 16 rows the unsplit kernels are the alternative: the multi-tile
+  // kernel where it plans (compared by the same wave work below), otherwise
+  // the kernels with all of x in LDS; past 16 rows (two token groups, this
+  // kernel only) the tile kernel is, from 256 row tiles on.
+  long lds_work = -1;
   if (m <= kRows) {
-    if (tiles > 128 && k < 8192) return best;
-    if ((size_t)m * k * 2 <= (size_t)kXLdsMax || plan_lds(k, n, m).ok) return best;
+    const LdsPlan lp = plan_lds(k, n, m);
+    if (lp.ok) {
+      const long groups = (tiles + lp.tpw - 1) / lp.tpw;
+      lds_work = (groups + 255) / 256 * ((k / kChunkK + kLdsWaves - 1) / kLdsWaves) * lp.tpw;
+    } else if ((size_t)m * k * 2 <= (size_t)kXLdsMax) {
+      return best;
+    }
+  } else if (tiles >= 256) {
+    return best;
   }
   const int tg = m > kRows ? 2 : 1;
   long best_work = -1;
@@ -1040,6 +1055,11 @@ SplitPlan plan_split(int k, int n, int m) {
       }
     }
   }
+  // Against the multi-tile kernel the split (a second launch, partial sums)
+  // must save more than a quarter of the wave work: [19456 x 2560] M = 12 /
+  // 16 (15 against 24) 21.6 / 22.4 -> 15.3 / 16.6 us; [2560 x 4096] M = 13
+  // (3 against 4) ran 7.2 us on the multi-tile kernel and 8.3 split.
+  if (lds_work >= 0 && best.ok && best_work * 4 >= lds_work * 3) best.ok = false;
   return best;
 }
 

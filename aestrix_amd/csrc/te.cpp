@@ -41,11 +41,13 @@ bool weight_ok(const imq_qweight& q, imq_dtype dtype) {
          (size_t)q.n * (size_t)q.k / 2 < ((size_t)1 << 32);
 }
 
-// Whether the few-row kernel's K split takes this projection past 16 rows
-// (its plan exists and the plan's workspace holds its partial sums).
+// Whether the few-row kernel's K split takes this projection (its plan
+// exists, from 6 rows, and the plan's workspace holds its partial sums): past
+// 16 rows in place of the tile kernel, and for the o / down projections with
+// their residual add at any row count it plans for.
 bool few_row_split(const imq_te* te, const imq_qweight& q, int rows) {
   const int dt = (int)te->dtype;
-  if (rows <= imq::kDispatchSkinnyMaxM || !imq::qskinny_supported(q.k, q.n, rows, dt)) return false;
+  if (rows < imq::kDispatchSkinnyMinM || !imq::qskinny_supported(q.k, q.n, rows, dt)) return false;
   const size_t need = imq::qskinny_split_bytes(q.k, q.n, rows);
   return need > 0 && te->split.p && te->split.bytes >= need;
 }

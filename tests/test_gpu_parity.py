@@ -236,13 +236,20 @@ def test_split_k_dispatcher(m, n, k):
 @pytest.mark.parametrize("m,n,k,splits", [(16, 2560, 9728, 10), (12, 2560, 9728, 10),
                                           (12, 1000, 4608, 5), (8, 2560, 9728, 10),
                                           (16, 1024, 9728, 10), (13, 1030, 4608, 5),
-                                          (6, 2560, 9728, 1), (4, 2560, 9728, 1), (16, 2560, 4096, 1),
-                                          (16, 9728, 2560, 1), (3, 2560, 9728, 1)])
+                                          (6, 2560, 9728, 10), (16, 2560, 4096, 4),
+                                          (16, 19456, 2560, 3), (16, 4096, 9728, 10),
+                                          (5, 2560, 9728, 1), (4, 2560, 9728, 1),
+                                          (16, 9728, 2560, 1), (16, 6144, 2560, 1),
+                                          (12, 12288, 2560, 1), (13, 2560, 4096, 1),
+                                          (3, 2560, 9728, 1)])
 def test_few_row_split_plan(m, n, k, splits):
-    """imq_qmm_plan reports the few-row kernel's K split and its workspace: taken
-    from M = 8 where x streams from L2 and the 16-row workgroups are few or
-    long ([2560 x 9728], 1000 x 4608), not below M = 8, not at K = 4096 with
-    160 tiles, not for [9728 x 2560] (608 tiles)."""
+    """imq_qmm_plan reports the few-row kernel's K split and its workspace:
+    taken from M = 6 where x does not fit LDS ([2560 x 9728], [1000 x 4608],
+    [2560 x 4096] at M = 16), and where it saves a quarter of the multi-tile
+    kernel's wave work ([19456 x 2560] M = 16: two rounds of 304 workgroups
+    of four tiles); not at M <= 5, nor where the multi-tile kernel fills the
+    CUs in one round ([9728 x 2560], [6144 x 2560], [12288 x 2560], [2560 x
+    4096] at M = 13)."""
     plan = imq.qmm_plan(m, n, k, torch.bfloat16)
     assert plan["kernel"] == "few_row", plan
     assert plan["splits"] == splits, plan
