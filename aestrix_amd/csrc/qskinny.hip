@@ -634,12 +634,19 @@ __global__ __launch_bounds__(64 * W) void qskinny_half_kernel(const uint32_t* __
 }
 
 // Waves per workgroup: enough that the device holds about 2048 waves and
-// each wave at most 8 chunks, at most 16 waves and at most half the chunks.
+// each wave at most 8 chunks, at most 16 waves and at most half the chunks;
+// but 8 where that leaves a wave at most 4 chunks.  16 waves of 1-2 chunks
+// each lost to 8 waves of 3-4 (same box, weights from HBM): [3072 x 3072] M
+// = 4 / 8 5.7 / 6.0 -> 5.0 / 5.2 us (16 waves over 24 chunks leave a quarter
+// of the slots idle), [2560 x 4096] M = 4 / 8 5.9 / 6.4 -> 5.8 / 6.2 us; at
+// K = 9728 (76 chunks) 16 waves stay far ahead (9.9 against 12.5 us).
 int skinny_waves(int n, int k) {
   const long blocks = (n + kRows - 1) / kRows;
   const int chunks = k / kChunkK;
   int wv = 1;
-  while (wv < 16 && (blocks * wv < 2048 || chunks > 8 * wv) && wv * 2 <= chunks) wv *= 2;
+  while (wv < 16 && (blocks * wv < 2048 || chunks > 8 * wv) && wv * 2 <= chunks &&
+         !(wv == 8 && chunks <= 4 * wv))
+    wv *= 2;
   return wv;
 }
 
@@ -1019,14 +1026,16 @@ SplitPlan plan_split(int k, int n, int m) {
   const int pieces = k / 512;
   const long tiles = (n + kRows - 1) / kRows;
   // Up to 16 rows the unsplit kernels are the alternative: the multi-tile
-  // kernel where it plans (compared by the same wave work below), otherwise
-  // the kernels with all of x in LDS; past 16 rows (two token groups, this
-  // kernel only) the tile kernel is, from 256 row tiles on.
+  // kernel where it plans (in one round of the CUs it stays; in more it is
+  // compared by the same wave work below), otherwise the kernels with all of
+  // x in LDS; past 16 rows (two token groups, this kernel only) the tile
+  // kernel is, from 256 row tiles on.
   long lds_work = -1;
   if (m <= kRows) {
     const LdsPlan lp = plan_lds(k, n, m);
     if (lp.ok) {
       const long groups = (tiles + lp.tpw - 1) / lp.tpw;
+      if (groups <= 256) return best;
       lds_work = (groups + 255) / 256 * ((k / kChunkK + kLdsWaves - 1) / kLdsWaves) * lp.tpw;
     } else if ((size_t)m * k * 2 <= (size_t)kXLdsMax) {
       return best;
@@ -1055,10 +1064,12 @@ SplitPlan plan_split(int k, int n, int m) {
       }
     }
   }
-  // Against the multi-tile kernel the split (a second launch, partial sums)
-  // must save more than a quarter of the wave work: [19456 x 2560] M = 12 /
-  // 16 (15 against 24) 21.6 / 22.4 -> 15.3 / 16.6 us; [2560 x 4096] M = 13
-  // (3 against 4) ran 7.2 us on the multi-tile kernel and 8.3 split.
+  // Against the multi-tile kernel in two or more rounds the split (a second
+  // launch, partial sums) must save more than a quarter of the wave work:
+  // [19456 x 2560] M = 12 / 16 (15 against 24) 21.6 / 22.4 -> 15.3 / 16.6 us.
+  // In one round the second launch costs more than the split saves:
+  // [2560 x 4096] M = 13 7.2 -> 8.3 us, [2560 x 2560] M = 12 4.7 -> 6.1,
+  // [1024 x 2560] M = 12 4.6 -> 5.3 us when split.
   if (lds_work >= 0 && best.ok && best_work * 4 >= lds_work * 3) best.ok = false;
   return best;
 }

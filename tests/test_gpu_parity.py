@@ -241,15 +241,16 @@ def test_split_k_dispatcher(m, n, k):
                                           (5, 2560, 9728, 1), (4, 2560, 9728, 1),
                                           (16, 9728, 2560, 1), (16, 6144, 2560, 1),
                                           (12, 12288, 2560, 1), (13, 2560, 4096, 1),
+                                          (12, 2560, 2560, 1), (12, 1024, 2560, 1),
                                           (3, 2560, 9728, 1)])
 def test_few_row_split_plan(m, n, k, splits):
     """imq_qmm_plan reports the few-row kernel's K split and its workspace:
     taken from M = 6 where x does not fit LDS ([2560 x 9728], [1000 x 4608],
     [2560 x 4096] at M = 16), and where it saves a quarter of the multi-tile
     kernel's wave work ([19456 x 2560] M = 16: two rounds of 304 workgroups
-    of four tiles); not at M <= 5, nor where the multi-tile kernel fills the
-    CUs in one round ([9728 x 2560], [6144 x 2560], [12288 x 2560], [2560 x
-    4096] at M = 13)."""
+    of four tiles); not at M <= 5, nor where the multi-tile kernel fits one
+    round of the CUs ([9728 x 2560], [6144 x 2560], [12288 x 2560], [2560 x
+    4096] at M = 13, [2560 x 2560] and [1024 x 2560] at M = 12)."""
     plan = imq.qmm_plan(m, n, k, torch.bfloat16)
     assert plan["kernel"] == "few_row", plan
     assert plan["splits"] == splits, plan
