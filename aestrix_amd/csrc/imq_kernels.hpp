@@ -181,7 +181,7 @@ bool qskinny_supported(int k, int n, int m, int dtype);
 // With a workspace of at least qskinny_split_bytes(k, n, m) (nonzero when
 // K % 512 == 0 and 6 <= m <= 32: up to 16 rows where x does not fit LDS or
 // the multi-tile kernel would take two rounds of the CUs, past 16 rows where
-// the row tiles are fewer than 256), K is split over
+// the row tiles are fewer than 512), K is split over
 // qskinny_splits(k, n, m) workgroup ranges whose fp32 partial sums a second
 // kernel adds in order; without one the unsplit kernels run (m <= 16, else
 // hipErrorInvalidValue).

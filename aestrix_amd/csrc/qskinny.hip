@@ -1002,7 +1002,7 @@ size_t split_x_bytes(int per, int m) { return (size_t)m * (1024 * (size_t)per + 
 // 16 (9.4 -> 10.0), [3072 x 3072] at M = 4 / 8 / 16 (6.3 -> 8.3-8.9 us): there
 // the second launch and the partial sums cost more than the better-filled
 // grid saves.  17 to 32 rows (two token groups per weight fragment) take it
-// wherever the row tiles are fewer than 256, against the tile kernel's 32-row
+// wherever the row tiles are fewer than 256 (now 512), against the tile kernel's 32-row
 // tiles and their split K (same box, A/B builds, M = 30 unless stated):
 // [2560 x 9728] 19.1 -> 17.0 us (M = 17 18.0 -> 15.9), [2560 x 4096] 14.7 ->
 // 13.2, [2560 x 2560] 11.4 -> 8.0, [1000 x 4608] 13.6 -> 7.2, [3072 x 3072]
@@ -1029,7 +1029,11 @@ SplitPlan plan_split(int k, int n, int m) {
   // kernel where it plans (in one round of the CUs it stays; in more it is
   // compared by the same wave work below), otherwise the kernels with all of
   // x in LDS; past 16 rows (two token groups, this kernel only) the tile
-  // kernel is, from 256 row tiles on.
+  // kernel is, from 512 row tiles on: M = 30 / 24 / 17 [6144 x 2560] 13.3 /
+  // 13.5 / 12.7 -> 12.8 / 12.1 / 10.1 us, [4096 x 2560] M = 30 12.6 -> 9.5
+  // split; [9728 x 2560] M = 30 / 20 15.0 / 13.8 on the tile kernel against
+  // 15.8 / 14.8 for the planned split, [19456 x 2560] M = 30 18.3 against 23
+  // or more for any split.
   long lds_work = -1;
   if (m <= kRows) {
     const LdsPlan lp = plan_lds(k, n, m);
@@ -1040,7 +1044,7 @@ SplitPlan plan_split(int k, int n, int m) {
     } else if ((size_t)m * k * 2 <= (size_t)kXLdsMax) {
       return best;
     }
-  } else if (tiles >= 256) {
+  } else if (tiles >= 512) {
     return best;
   }
   const int tg = m > kRows ? 2 : 1;

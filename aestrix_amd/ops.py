@@ -160,7 +160,7 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     """y[..., N] = x[..., K] . deq(W)^T (MLX quantizedMM with transpose=true).
 
     3 <= M <= 16 rows with K % 128 == 0 run the few-row matrix-core kernel
-    (17 <= M <= 32 its K split, where fewer than 256 row tiles allow it),
+    (17 <= M <= 32 its K split, where fewer than 512 row tiles allow it),
     other M <= 4 (and f32) the qGEMV kernel, larger M the MFMA qGEMM kernel,
     with K split over a per-stream workspace when its output tiles are too few
     to fill the GPU (deterministic; another fp32 summation order than qgemm)."""

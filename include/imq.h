@@ -125,7 +125,7 @@ int imq_dequantize_rows(imq_ctx* ctx, const uint32_t* w, const void* scales, con
  * K % 128 == 0 runs a weight-streaming matrix-core kernel (16 weight rows per
  * workgroup, K over its waves; from M = 6, where x does not fit LDS or the
  * row tiles are many, K split over the workspace below; 17 <= M <= 32 that
- * split only, where the row tiles are fewer than 256); other M <= 4 the
+ * split only, where the row tiles are fewer than 512); other M <= 4 the
  * qGEMV kernel;
  * larger M the MFMA qGEMM kernel (f32: the qGEMV kernel, 16 rows at a time).  When the
  * output tiles are too few to fill the GPU, the qGEMM splits

@@ -263,14 +263,16 @@ def test_few_row_split_plan(m, n, k, splits):
                                           (30, 9728, 2560, 0), (30, 2560, 1024, 2),
                                           (33, 2560, 9728, 0), (20, 2560, 2560, 3),
                                           (30, 3072, 3072, 3), (24, 2560, 3840, 0),
-                                          (20, 17, 1024, 2)])
+                                          (20, 17, 1024, 2), (30, 6144, 2560, 3),
+                                          (17, 6144, 2560, 3), (30, 4096, 2560, 3),
+                                          (20, 9728, 2560, 0), (30, 19456, 2560, 0)])
 def test_few_row_split_past_16_rows_plan(m, n, k, splits):
     """17 to 32 rows take the few-row kernel's K split (two token groups per
-    weight fragment) where it plans one: fewer than 256 row tiles and K % 512
+    weight fragment) where it plans one: fewer than 512 row tiles and K % 512
     == 0 with at least two 512-k pieces; the splits are those of the plan
     with the least wave work on the busiest CU (two pieces per split where
     the x slice allows it).  The others here (splits 0) run the tile kernel:
-    608 row tiles, 33 rows, K = 3840."""
+    608 and 1216 row tiles, 33 rows, K = 3840."""
     plan = imq.qmm_plan(m, n, k, torch.bfloat16)
     if splits:
         assert plan["kernel"] == "few_row" and plan["splits"] == splits, plan
