@@ -197,5 +197,17 @@ hipError_t launch_qskinny(const uint32_t* w, const void* scales, const void* bia
 hipError_t launch_qskinny_resid_add(const uint32_t* w, const void* scales, const void* biases,
                                     const void* x, const void* resid, void* y, int k, int n, int m,
                                     int dtype, hipStream_t stream, SplitWs ws);
+// The same, followed in the split sum's own launch by the row RMSNorm of its
+// result: y as above, then h = T(y * rsqrt(mean_n(y^2) + eps) * norm_w)
+// (launch_rmsnorm_t's arithmetic) -- the text encoder's o projection, dq_add
+// and post-attention RMSNorm in two launches.  Where the _fits predicate holds
+// (the split as above, N % 8 == 0, N <= 8192, 16-byte aligned operands);
+// hipErrorInvalidValue otherwise, before any launch.
+bool qskinny_resid_add_norm_fits(int k, int n, int m, int dtype, const void* resid,
+                                 const void* y, const float* norm_w, const void* h, SplitWs ws);
+hipError_t launch_qskinny_resid_add_norm(const uint32_t* w, const void* scales,
+                                         const void* biases, const void* x, const void* resid,
+                                         void* y, const float* norm_w, void* h, float eps, int k,
+                                         int n, int m, int dtype, hipStream_t stream, SplitWs ws);
 
 }  // namespace imq

@@ -976,6 +976,90 @@ __global__ __launch_bounds__(256) void qskinny_reduce_kernel(const float* __rest
   }
 }
 
+// One row m per workgroup: r = T(float(resid) + float(T(sum over s of
+// ws[s][m][:]))) as qskinny_reduce_kernel's RES form, stored to y, then the
+// row's RMSNorm h = T(r * rsqrt(mean(r^2) + eps) * nw) with the arithmetic of
+// the T-input RMSNorm kernel (thread i takes the 8-value pieces i, i + 256,
+// ..., the same fma order, wave and workgroup sums): the text encoder's
+// o projection, dq_add and the RMSNorm before the MLP in one launch instead
+// of two.  N % 8 == 0, N <= 2048 V, 16-byte aligned rows; y may be resid.
+template <int T, int V>
+__global__ __launch_bounds__(256) void qskinny_reduce_norm_kernel(
+    const float* __restrict__ ws, int splits, int count, int N, const uint16_t* r, uint16_t* y,
+    const float* __restrict__ nw, uint16_t* __restrict__ h, float eps) {
+  __shared__ float part[4];
+  const int n8 = N >> 3;
+  const size_t row = (size_t)blockIdx.x * N;
+  uint4 v[V];
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int idx = threadIdx.x + i * 256;
+    v[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (idx < n8) {
+      const size_t o = row + 8 * (size_t)idx;
+      float4 a0 = *reinterpret_cast<const float4*>(ws + o);
+      float4 a1 = *reinterpret_cast<const float4*>(ws + o + 4);
+      for (int sp = 1; sp < splits; ++sp) {
+        const float4 p0 = *reinterpret_cast<const float4*>(ws + (size_t)sp * count + o);
+        const float4 p1 = *reinterpret_cast<const float4*>(ws + (size_t)sp * count + o + 4);
+        a0.x += p0.x;
+        a0.y += p0.y;
+        a0.z += p0.z;
+        a0.w += p0.w;
+        a1.x += p1.x;
+        a1.y += p1.y;
+        a1.z += p1.z;
+        a1.w += p1.w;
+      }
+      const uint4 rv = *reinterpret_cast<const uint4*>(r + o);
+      const float f[8] = {staged_value<T>(rv.x & 0xFFFFu) + round_to(a0.x, T),
+                          staged_value<T>(rv.x >> 16) + round_to(a0.y, T),
+                          staged_value<T>(rv.y & 0xFFFFu) + round_to(a0.z, T),
+                          staged_value<T>(rv.y >> 16) + round_to(a0.w, T),
+                          staged_value<T>(rv.z & 0xFFFFu) + round_to(a1.x, T),
+                          staged_value<T>(rv.z >> 16) + round_to(a1.y, T),
+                          staged_value<T>(rv.w & 0xFFFFu) + round_to(a1.z, T),
+                          staged_value<T>(rv.w >> 16) + round_to(a1.w, T)};
+      v[i] = make_uint4(Elem<T>::pack2(f[0], f[1]), Elem<T>::pack2(f[2], f[3]),
+                        Elem<T>::pack2(f[4], f[5]), Elem<T>::pack2(f[6], f[7]));
+      *reinterpret_cast<uint4*>(y + o) = v[i];
+    }
+    const uint32_t q[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = Elem<T>::param((uint16_t)(q[e] & 0xFFFFu));
+      const float hi = Elem<T>::param((uint16_t)(q[e] >> 16));
+      acc = __builtin_fmaf(lo, lo, acc);
+      acc = __builtin_fmaf(hi, hi, acc);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) total += part[i];
+  const float inv = __frsqrt_rn(total / (float)N + eps);
+  const float4* wr = reinterpret_cast<const float4*>(nw);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int idx = threadIdx.x + i * 256;
+    if (idx < n8) {
+      const float4 w0 = wr[2 * idx], w1 = wr[2 * idx + 1];
+      const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      const uint32_t q[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = Elem<T>::pack2(Elem<T>::param((uint16_t)(q[e] & 0xFFFFu)) * inv * ww[2 * e],
+                              Elem<T>::param((uint16_t)(q[e] >> 16)) * inv * ww[2 * e + 1]);
+      *reinterpret_cast<uint4*>(h + row + 8 * (size_t)idx) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
 struct SplitPlan {
   int tpw, per, splits, u;
   bool ok;
@@ -1113,10 +1197,19 @@ hipError_t launch_split_t(const uint32_t* w, const uint16_t* s, const uint16_t* 
   }
 }
 
+// Rows of the fused split sum + residual + RMSNorm: N % 8 == 0, at most 8192
+// columns, 16-byte aligned rows and partial sums.
+bool norm_fits(int n, const void* resid, const void* y, const float* nw, const void* h,
+               const float* ws) {
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  return n % 8 == 0 && n <= 2048 * 4 && a16(resid) && a16(y) && a16(nw) && a16(h) && a16(ws);
+}
+
 template <int T>
 hipError_t launch_split(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
                         const uint16_t* resid, uint16_t* y, float* ws, int k, int n, int m,
-                        const SplitPlan& p, hipStream_t stream) {
+                        const SplitPlan& p, hipStream_t stream, const float* nw = nullptr,
+                        uint16_t* h = nullptr, float eps = 0.f) {
   const bool vec = n % 4 == 0 && ((uintptr_t)ws & 15u) == 0;
   hipError_t e;
   switch (p.tpw) {
@@ -1127,6 +1220,19 @@ hipError_t launch_split(const uint32_t* w, const uint16_t* s, const uint16_t* b,
   }
   if (e != hipSuccess) return e;
   const int count = m * n;
+  if (nw) {
+    const int v = (n / 8 + 255) / 256;
+    if (v <= 1)
+      hipLaunchKernelGGL((qskinny_reduce_norm_kernel<T, 1>), dim3(m), dim3(256), 0, stream, ws,
+                         p.splits, count, n, resid, y, nw, h, eps);
+    else if (v == 2)
+      hipLaunchKernelGGL((qskinny_reduce_norm_kernel<T, 2>), dim3(m), dim3(256), 0, stream, ws,
+                         p.splits, count, n, resid, y, nw, h, eps);
+    else
+      hipLaunchKernelGGL((qskinny_reduce_norm_kernel<T, 4>), dim3(m), dim3(256), 0, stream, ws,
+                         p.splits, count, n, resid, y, nw, h, eps);
+    return hipGetLastError();
+  }
   const bool rvec = count % 4 == 0 && ((uintptr_t)y & 7u) == 0 && ((uintptr_t)resid & 7u) == 0;
   const dim3 grid((unsigned)(((rvec ? count / 4 : count) + 255) / 256));
   if (resid) {
@@ -1195,6 +1301,32 @@ hipError_t launch_qskinny_resid_add(const uint32_t* w, const void* scales, const
   auto* yy = static_cast<uint16_t*>(y);
   if (dtype == kBf16) return launch_split<kBf16>(w, s, b, xx, rr, yy, ws.p, k, n, m, sp, stream);
   return launch_split<kF16>(w, s, b, xx, rr, yy, ws.p, k, n, m, sp, stream);
+}
+
+bool qskinny_resid_add_norm_fits(int k, int n, int m, int dtype, const void* resid,
+                                 const void* y, const float* norm_w, const void* h, SplitWs ws) {
+  if (!qskinny_supported(k, n, m, dtype)) return false;
+  const SplitPlan sp = plan_split(k, n, m);
+  return sp.ok && ws.p && ws.bytes >= (size_t)sp.splits * m * n * sizeof(float) &&
+         norm_fits(n, resid, y, norm_w, h, ws.p);
+}
+
+hipError_t launch_qskinny_resid_add_norm(const uint32_t* w, const void* scales,
+                                         const void* biases, const void* x, const void* resid,
+                                         void* y, const float* norm_w, void* h, float eps, int k,
+                                         int n, int m, int dtype, hipStream_t stream, SplitWs ws) {
+  if (!qskinny_resid_add_norm_fits(k, n, m, dtype, resid, y, norm_w, h, ws))
+    return hipErrorInvalidValue;
+  const SplitPlan sp = plan_split(k, n, m);
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* b = static_cast<const uint16_t*>(biases);
+  const auto* xx = static_cast<const uint16_t*>(x);
+  const auto* rr = static_cast<const uint16_t*>(resid);
+  auto* yy = static_cast<uint16_t*>(y);
+  auto* hh = static_cast<uint16_t*>(h);
+  if (dtype == kBf16)
+    return launch_split<kBf16>(w, s, b, xx, rr, yy, ws.p, k, n, m, sp, stream, norm_w, hh, eps);
+  return launch_split<kF16>(w, s, b, xx, rr, yy, ws.p, k, n, m, sp, stream, norm_w, hh, eps);
 }
 
 size_t qskinny_split_bytes(int k, int n, int m) {

@@ -189,14 +189,25 @@ int imq_te_attn_out_mlp(imq_te* te, int layer, const void* x, const void* attn_o
   const auto st = static_cast<hipStream_t>(stream);
   const int dt = (int)te->dtype;
   const int h = te->hidden, in = te->inter;
-  // o_proj and down_proj with dq_add: past 16 rows the few-row kernel's K
-  // split where it takes the shape, else the tile kernel.
-  hipError_t e = few_row_split(te, l.o, rows)
-                     ? imq::launch_qskinny_resid_add(l.o.w, l.o.scales, l.o.biases, attn_o, x,
-                                                     te->r, te->nq, h, rows, dt, st, te->split)
-                     : imq::launch_qgemm_resid_add(l.o.w, l.o.scales, l.o.biases, attn_o, x, te->r,
-                                                   te->nq, h, rows, dt, st, te->split);
-  if (e == hipSuccess) e = imq::launch_rmsnorm_t(te->r, l.norm_post, te->h1, rows, h, te->eps, dt, st);
+  // o_proj and down_proj with dq_add: the few-row kernel's K split where it
+  // takes the shape (for o_proj with the RMSNorm after it in its split-sum
+  // kernel, one launch fewer), else the tile kernel.
+  hipError_t e;
+  if (few_row_split(te, l.o, rows) &&
+      imq::qskinny_resid_add_norm_fits(te->nq, h, rows, dt, x, te->r, l.norm_post, te->h1,
+                                       te->split)) {
+    e = imq::launch_qskinny_resid_add_norm(l.o.w, l.o.scales, l.o.biases, attn_o, x, te->r,
+                                           l.norm_post, te->h1, te->eps, te->nq, h, rows, dt, st,
+                                           te->split);
+  } else {
+    e = few_row_split(te, l.o, rows)
+            ? imq::launch_qskinny_resid_add(l.o.w, l.o.scales, l.o.biases, attn_o, x, te->r,
+                                            te->nq, h, rows, dt, st, te->split)
+            : imq::launch_qgemm_resid_add(l.o.w, l.o.scales, l.o.biases, attn_o, x, te->r, te->nq,
+                                          h, rows, dt, st, te->split);
+    if (e == hipSuccess)
+      e = imq::launch_rmsnorm_t(te->r, l.norm_post, te->h1, rows, h, te->eps, dt, st);
+  }
   if (e == hipSuccess) {
     const imq_qweight& g = l.gate_up;
     e = imq::qgemv_swiglu_fits(g.k, g.n, rows, dt)

@@ -100,5 +100,14 @@ hipError_t launch_qskinny_resid_add(const uint32_t*, const void*, const void*, c
                                     const void*, void*, int, int, int, int, hipStream_t, SplitWs) {
   return hipErrorNoDevice;
 }
+bool qskinny_resid_add_norm_fits(int, int, int, int, const void*, const void*, const float*,
+                                 const void*, SplitWs) {
+  return false;
+}
+hipError_t launch_qskinny_resid_add_norm(const uint32_t*, const void*, const void*, const void*,
+                                         const void*, void*, const float*, void*, float, int, int,
+                                         int, int, hipStream_t, SplitWs) {
+  return hipErrorNoDevice;
+}
 
 }  // namespace imq
