@@ -192,8 +192,11 @@ hipError_t launch_qskinny(const uint32_t* w, const void* scales, const void* bia
                           SplitWs ws = {});
 // The K split with the residual add of launch_qgemm_resid_add in its second
 // kernel: y = T(float(resid) + float(T(x . deq(W)^T))), y may be resid.  Only
-// where qskinny_split_bytes(k, n, m) > 0 and ws holds that many bytes
-// (hipErrorInvalidValue otherwise).
+// where qskinny_resid_split_bytes(k, n, m) > 0 and ws holds that many bytes
+// (hipErrorInvalidValue otherwise).  Its plan is the K split's own from 3
+// rows, also where a plain product would run unsplit (no unsplit kernel has
+// the residual add; the tile kernel's form is the alternative).
+size_t qskinny_resid_split_bytes(int k, int n, int m);
 hipError_t launch_qskinny_resid_add(const uint32_t* w, const void* scales, const void* biases,
                                     const void* x, const void* resid, void* y, int k, int n, int m,
                                     int dtype, hipStream_t stream, SplitWs ws);

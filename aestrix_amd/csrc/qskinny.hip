@@ -1104,9 +1104,12 @@ size_t split_x_bytes(int per, int m) { return (size_t)m * (1024 * (size_t)per + 
 // / 16 13.2 / 13.5 / 13.7 -> 11.1 / 11.6 / 12.5 us, M = 30 [2560 x 4096]
 // 13.3 -> 9.2, [3072 x 3072] 12.3 -> 8.5, [2560 x 2560] 7.9 -> 6.8,
 // [1024 x 9728] M = 16 10.1 -> 8.2 us.
-SplitPlan plan_split(int k, int n, int m) {
+// resid: for the residual-add form, which the unsplit kernels do not have
+// (the tile kernel is its alternative): from 3 rows, and where the unsplit
+// kernels would be preferred for a plain product.
+SplitPlan plan_split(int k, int n, int m, bool resid = false) {
   SplitPlan best{0, 0, 0, 0, false};
-  if (k % 512 != 0 || k / 512 < 2 || m < kSplitMinM || m > 2 * kRows) return best;
+  if (k % 512 != 0 || k / 512 < 2 || m < (resid ? 3 : kSplitMinM) || m > 2 * kRows) return best;
   const int pieces = k / 512;
   const long tiles = (n + kRows - 1) / kRows;
   // Up to 16 rows the unsplit kernels are the alternative: the multi-tile
@@ -1119,7 +1122,7 @@ SplitPlan plan_split(int k, int n, int m) {
   // 15.8 / 14.8 for the planned split, [19456 x 2560] M = 30 18.3 against 23
   // or more for any split.
   long lds_work = -1;
-  if (m <= kRows) {
+  if (m <= kRows && !resid) {
     const LdsPlan lp = plan_lds(k, n, m);
     if (lp.ok) {
       const long groups = (tiles + lp.tpw - 1) / lp.tpw;
@@ -1128,7 +1131,7 @@ SplitPlan plan_split(int k, int n, int m) {
     } else if ((size_t)m * k * 2 <= (size_t)kXLdsMax) {
       return best;
     }
-  } else if (tiles >= 512) {
+  } else if (m > kRows && tiles >= 512) {
     return best;
   }
   const int tg = m > kRows ? 2 : 1;
@@ -1291,7 +1294,7 @@ hipError_t launch_qskinny_resid_add(const uint32_t* w, const void* scales, const
                                     const void* x, const void* resid, void* y, int k, int n, int m,
                                     int dtype, hipStream_t stream, SplitWs ws) {
   if (!qskinny_supported(k, n, m, dtype)) return hipErrorInvalidValue;
-  const SplitPlan sp = plan_split(k, n, m);
+  const SplitPlan sp = plan_split(k, n, m, true);
   if (!sp.ok || !ws.p || ws.bytes < (size_t)sp.splits * m * n * sizeof(float))
     return hipErrorInvalidValue;
   const auto* s = static_cast<const uint16_t*>(scales);
@@ -1306,7 +1309,7 @@ hipError_t launch_qskinny_resid_add(const uint32_t* w, const void* scales, const
 bool qskinny_resid_add_norm_fits(int k, int n, int m, int dtype, const void* resid,
                                  const void* y, const float* norm_w, const void* h, SplitWs ws) {
   if (!qskinny_supported(k, n, m, dtype)) return false;
-  const SplitPlan sp = plan_split(k, n, m);
+  const SplitPlan sp = plan_split(k, n, m, true);
   return sp.ok && ws.p && ws.bytes >= (size_t)sp.splits * m * n * sizeof(float) &&
          norm_fits(n, resid, y, norm_w, h, ws.p);
 }
@@ -1317,7 +1320,7 @@ hipError_t launch_qskinny_resid_add_norm(const uint32_t* w, const void* scales,
                                          int n, int m, int dtype, hipStream_t stream, SplitWs ws) {
   if (!qskinny_resid_add_norm_fits(k, n, m, dtype, resid, y, norm_w, h, ws))
     return hipErrorInvalidValue;
-  const SplitPlan sp = plan_split(k, n, m);
+  const SplitPlan sp = plan_split(k, n, m, true);
   const auto* s = static_cast<const uint16_t*>(scales);
   const auto* b = static_cast<const uint16_t*>(biases);
   const auto* xx = static_cast<const uint16_t*>(x);
@@ -1331,6 +1334,11 @@ hipError_t launch_qskinny_resid_add_norm(const uint32_t* w, const void* scales,
 
 size_t qskinny_split_bytes(int k, int n, int m) {
   const SplitPlan sp = plan_split(k, n, m);
+  return sp.ok ? (size_t)sp.splits * m * n * sizeof(float) : 0;
+}
+
+size_t qskinny_resid_split_bytes(int k, int n, int m) {
+  const SplitPlan sp = plan_split(k, n, m, true);
   return sp.ok ? (size_t)sp.splits * m * n * sizeof(float) : 0;
 }
 

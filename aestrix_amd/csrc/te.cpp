@@ -41,14 +41,23 @@ bool weight_ok(const imq_qweight& q, imq_dtype dtype) {
          (size_t)q.n * (size_t)q.k / 2 < ((size_t)1 << 32);
 }
 
-// Whether the few-row kernel's K split takes this projection (its plan
-// exists, from 6 rows, and the plan's workspace holds its partial sums): past
-// 16 rows in place of the tile kernel, and for the o / down projections with
-// their residual add at any row count it plans for.
+// Whether the few-row kernel's K split takes this plain projection (its plan
+// exists, from 6 rows, and the plan's workspace holds its partial sums); past
+// 16 rows in place of the tile kernel.
 bool few_row_split(const imq_te* te, const imq_qweight& q, int rows) {
   const int dt = (int)te->dtype;
   if (rows < imq::kDispatchSkinnyMinM || !imq::qskinny_supported(q.k, q.n, rows, dt)) return false;
   const size_t need = imq::qskinny_split_bytes(q.k, q.n, rows);
+  return need > 0 && te->split.p && te->split.bytes >= need;
+}
+
+// The same for the residual-add form of the o / down projections, whose
+// alternative is the tile kernel's at any row count (its plan exists from 3
+// rows).
+bool resid_split(const imq_te* te, const imq_qweight& q, int rows) {
+  const int dt = (int)te->dtype;
+  if (rows < imq::kDispatchSkinnyMinM || !imq::qskinny_supported(q.k, q.n, rows, dt)) return false;
+  const size_t need = imq::qskinny_resid_split_bytes(q.k, q.n, rows);
   return need > 0 && te->split.p && te->split.bytes >= need;
 }
 
@@ -129,8 +138,8 @@ int imq_te_create(imq_ctx* ctx, const imq_te_layer_weights* layers, int n_layers
     ws = std::max(ws, imq::qgemm_split_bytes(hidden, l0.qkv.n, rows, false));
     if (rows <= imq::kQskinnyMaxM) {
       ws = std::max(ws, imq::qskinny_split_bytes(hidden, l0.qkv.n, rows));
-      ws = std::max(ws, imq::qskinny_split_bytes(nq, hidden, rows));
-      ws = std::max(ws, imq::qskinny_split_bytes(inter, hidden, rows));
+      ws = std::max(ws, imq::qskinny_resid_split_bytes(nq, hidden, rows));
+      ws = std::max(ws, imq::qskinny_resid_split_bytes(inter, hidden, rows));
     }
     ws = std::max(ws, imq::qgemm_split_bytes(nq, hidden, rows, true));
     ws = std::max(ws, imq::qgemm_split_bytes(hidden, 2 * inter, rows, true));
@@ -193,14 +202,14 @@ int imq_te_attn_out_mlp(imq_te* te, int layer, const void* x, const void* attn_o
   // takes the shape (for o_proj with the RMSNorm after it in its split-sum
   // kernel, one launch fewer), else the tile kernel.
   hipError_t e;
-  if (few_row_split(te, l.o, rows) &&
+  if (resid_split(te, l.o, rows) &&
       imq::qskinny_resid_add_norm_fits(te->nq, h, rows, dt, x, te->r, l.norm_post, te->h1,
                                        te->split)) {
     e = imq::launch_qskinny_resid_add_norm(l.o.w, l.o.scales, l.o.biases, attn_o, x, te->r,
                                            l.norm_post, te->h1, te->eps, te->nq, h, rows, dt, st,
                                            te->split);
   } else {
-    e = few_row_split(te, l.o, rows)
+    e = resid_split(te, l.o, rows)
             ? imq::launch_qskinny_resid_add(l.o.w, l.o.scales, l.o.biases, attn_o, x, te->r,
                                             te->nq, h, rows, dt, st, te->split)
             : imq::launch_qgemm_resid_add(l.o.w, l.o.scales, l.o.biases, attn_o, x, te->r, te->nq,
@@ -217,7 +226,7 @@ int imq_te_attn_out_mlp(imq_te* te, int layer, const void* x, const void* attn_o
                                        in, 0, in, 1.0f, 1.0f, dt, st, te->split);
   }
   if (e == hipSuccess)
-    e = few_row_split(te, l.down, rows)
+    e = resid_split(te, l.down, rows)
             ? imq::launch_qskinny_resid_add(l.down.w, l.down.scales, l.down.biases, te->m, te->r, y,
                                             in, h, rows, dt, st, te->split)
             : imq::launch_qgemm_resid_add(l.down.w, l.down.scales, l.down.biases, te->m, te->r, y,

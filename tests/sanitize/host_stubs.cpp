@@ -87,6 +87,7 @@ bool qskinny_supported(int k, int n, int m, int dtype) {
          (size_t)m * k * 2 < ((size_t)1 << 31);
 }
 size_t qskinny_split_bytes(int, int, int) { return 0; }
+size_t qskinny_resid_split_bytes(int, int, int) { return 0; }
 int qskinny_splits(int, int, int) { return 1; }
 hipError_t launch_dequant_rows(const uint32_t*, const void*, const void*, const int32_t*, int,
                                void*, int, int, int, hipStream_t) {
