@@ -197,6 +197,21 @@ hipError_t launch_qskinny(const uint32_t* w, const void* scales, const void* bia
 // rows, also where a plain product would run unsplit (no unsplit kernel has
 // the residual add; the tile kernel's form is the alternative).
 size_t qskinny_resid_split_bytes(int k, int n, int m);
+// y[m][j] = EpSwiGLU(gate sum j, up sum j) for j < width over a pair weight of
+// n = 2 width rows (gate rows [0, width), up rows [width, n)): the few-row
+// kernel's K split, its fp32 partial sums summed by the tile kernel's
+// split-sum kernel with the SwiGLU stage (launch_reduce_swiglu).  Its plan is
+// the residual form's (qskinny_resid_split_bytes(k, n, m) > 0, and ws holds
+// that many bytes); hipErrorInvalidValue otherwise, before any launch.
+hipError_t launch_qskinny_swiglu(const uint32_t* w, const void* scales, const void* biases,
+                                 const void* x, void* y, int ldy, int k, int n, int m, int width,
+                                 float in_scale, float out_scale, int dtype, hipStream_t stream,
+                                 SplitWs ws);
+// The SwiGLU output stage over fp32 partial sums ws[split][row][2 width]
+// (gate sums at [0, width), up sums at [width, 2 width)): the tile kernel's
+// split-sum kernel with EpSwiGLU, in split order.
+hipError_t launch_reduce_swiglu(const float* ws, int splits, int m, int width, void* y, int ldy,
+                                float in_scale, float out_scale, int dtype, hipStream_t stream);
 hipError_t launch_qskinny_resid_add(const uint32_t* w, const void* scales, const void* biases,
                                     const void* x, const void* resid, void* y, int k, int n, int m,
                                     int dtype, hipStream_t stream, SplitWs ws);

@@ -1131,6 +1131,24 @@ hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const vo
   }
 }
 
+hipError_t launch_reduce_swiglu(const float* ws, int splits, int m, int width, void* y, int ldy,
+                                float in_scale, float out_scale, int dtype, hipStream_t stream) {
+  auto* yy = static_cast<uint16_t*>(y);
+  const bool vec = al16(y) && ldy % 8 == 0;
+  const SplitWs sw{const_cast<float*>(ws), 0, 0};
+  switch (dtype) {
+    case kBf16:
+      return launch_reduce<kBf16>(
+          sw, splits, m, width, 2 * width,
+          EpSwiGLU<kBf16>{yy, ldy, width, 0, width, in_scale, out_scale, vec}, stream);
+    case kF16:
+      return launch_reduce<kF16>(
+          sw, splits, m, width, 2 * width,
+          EpSwiGLU<kF16>{yy, ldy, width, 0, width, in_scale, out_scale, vec}, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t launch_qgemm_swiglu(const uint32_t* w, const void* scales, const void* biases,
                                const void* x, void* y, int ldy, int k, int n, int m, int width,
                                int gate_row, int up_row, float in_scale, float out_scale, int dtype,

@@ -1208,19 +1208,26 @@ bool norm_fits(int n, const void* resid, const void* y, const float* nw, const v
   return n % 8 == 0 && n <= 2048 * 4 && a16(resid) && a16(y) && a16(nw) && a16(h) && a16(ws);
 }
 
+// The split kernel alone: fp32 partial sums ws[split][m][n].
+template <int T>
+hipError_t launch_split_partials(const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                                 const uint16_t* x, float* ws, int k, int n, int m,
+                                 const SplitPlan& p, hipStream_t stream) {
+  const bool vec = n % 4 == 0 && ((uintptr_t)ws & 15u) == 0;
+  switch (p.tpw) {
+    case 1: return launch_split_t<T, 1>(w, s, b, x, ws, k, n, m, p, vec, stream);
+    case 2: return launch_split_t<T, 2>(w, s, b, x, ws, k, n, m, p, vec, stream);
+    case 3: return launch_split_t<T, 3>(w, s, b, x, ws, k, n, m, p, vec, stream);
+    default: return launch_split_t<T, 4>(w, s, b, x, ws, k, n, m, p, vec, stream);
+  }
+}
+
 template <int T>
 hipError_t launch_split(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
                         const uint16_t* resid, uint16_t* y, float* ws, int k, int n, int m,
                         const SplitPlan& p, hipStream_t stream, const float* nw = nullptr,
                         uint16_t* h = nullptr, float eps = 0.f) {
-  const bool vec = n % 4 == 0 && ((uintptr_t)ws & 15u) == 0;
-  hipError_t e;
-  switch (p.tpw) {
-    case 1: e = launch_split_t<T, 1>(w, s, b, x, ws, k, n, m, p, vec, stream); break;
-    case 2: e = launch_split_t<T, 2>(w, s, b, x, ws, k, n, m, p, vec, stream); break;
-    case 3: e = launch_split_t<T, 3>(w, s, b, x, ws, k, n, m, p, vec, stream); break;
-    default: e = launch_split_t<T, 4>(w, s, b, x, ws, k, n, m, p, vec, stream); break;
-  }
+  const hipError_t e = launch_split_partials<T>(w, s, b, x, ws, k, n, m, p, stream);
   if (e != hipSuccess) return e;
   const int count = m * n;
   if (nw) {
@@ -1335,6 +1342,26 @@ hipError_t launch_qskinny_resid_add_norm(const uint32_t* w, const void* scales,
 size_t qskinny_split_bytes(int k, int n, int m) {
   const SplitPlan sp = plan_split(k, n, m);
   return sp.ok ? (size_t)sp.splits * m * n * sizeof(float) : 0;
+}
+
+hipError_t launch_qskinny_swiglu(const uint32_t* w, const void* scales, const void* biases,
+                                 const void* x, void* y, int ldy, int k, int n, int m, int width,
+                                 float in_scale, float out_scale, int dtype, hipStream_t stream,
+                                 SplitWs ws) {
+  if (!qskinny_supported(k, n, m, dtype) || n != 2 * width || ldy < width)
+    return hipErrorInvalidValue;
+  const SplitPlan sp = plan_split(k, n, m, true);
+  if (!sp.ok || !ws.p || ws.bytes < (size_t)sp.splits * m * n * sizeof(float))
+    return hipErrorInvalidValue;
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* b = static_cast<const uint16_t*>(biases);
+  const auto* xx = static_cast<const uint16_t*>(x);
+  const hipError_t e =
+      dtype == kBf16 ? launch_split_partials<kBf16>(w, s, b, xx, ws.p, k, n, m, sp, stream)
+                     : launch_split_partials<kF16>(w, s, b, xx, ws.p, k, n, m, sp, stream);
+  if (e != hipSuccess) return e;
+  return launch_reduce_swiglu(ws.p, sp.splits, m, width, y, ldy, in_scale, out_scale, dtype,
+                              stream);
 }
 
 size_t qskinny_resid_split_bytes(int k, int n, int m) {

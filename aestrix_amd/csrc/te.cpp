@@ -51,9 +51,9 @@ bool few_row_split(const imq_te* te, const imq_qweight& q, int rows) {
   return need > 0 && te->split.p && te->split.bytes >= need;
 }
 
-// The same for the residual-add form of the o / down projections, whose
-// alternative is the tile kernel's at any row count (its plan exists from 3
-// rows).
+// The same for the residual-add form of the o / down projections and the
+// SwiGLU form of gate/up, whose alternative is the tile kernel's at any row
+// count (their plan exists from 3 rows).
 bool resid_split(const imq_te* te, const imq_qweight& q, int rows) {
   const int dt = (int)te->dtype;
   if (rows < imq::kDispatchSkinnyMinM || !imq::qskinny_supported(q.k, q.n, rows, dt)) return false;
@@ -140,6 +140,7 @@ int imq_te_create(imq_ctx* ctx, const imq_te_layer_weights* layers, int n_layers
       ws = std::max(ws, imq::qskinny_split_bytes(hidden, l0.qkv.n, rows));
       ws = std::max(ws, imq::qskinny_resid_split_bytes(nq, hidden, rows));
       ws = std::max(ws, imq::qskinny_resid_split_bytes(inter, hidden, rows));
+      ws = std::max(ws, imq::qskinny_resid_split_bytes(hidden, 2 * inter, rows));
     }
     ws = std::max(ws, imq::qgemm_split_bytes(nq, hidden, rows, true));
     ws = std::max(ws, imq::qgemm_split_bytes(hidden, 2 * inter, rows, true));
@@ -219,11 +220,18 @@ int imq_te_attn_out_mlp(imq_te* te, int layer, const void* x, const void* attn_o
   }
   if (e == hipSuccess) {
     const imq_qweight& g = l.gate_up;
-    e = imq::qgemv_swiglu_fits(g.k, g.n, rows, dt)
-            ? imq::launch_qgemv_swiglu(g.w, g.scales, g.biases, te->h1, te->m, in, g.k, g.n, rows,
-                                       in, 0, in, 1.0f, 1.0f, dt, st)
-            : imq::launch_qgemm_swiglu(g.w, g.scales, g.biases, te->h1, te->m, in, g.k, g.n, rows,
-                                       in, 0, in, 1.0f, 1.0f, dt, st, te->split);
+    // gate/up with dq_silu_mul: the qGEMV's pair mode at few rows, then the
+    // few-row kernel's K split with the SwiGLU stage in its split sum where
+    // it plans, else the tile kernel.
+    if (imq::qgemv_swiglu_fits(g.k, g.n, rows, dt))
+      e = imq::launch_qgemv_swiglu(g.w, g.scales, g.biases, te->h1, te->m, in, g.k, g.n, rows, in,
+                                   0, in, 1.0f, 1.0f, dt, st);
+    else if (g.n == 2 * in && resid_split(te, g, rows))
+      e = imq::launch_qskinny_swiglu(g.w, g.scales, g.biases, te->h1, te->m, in, g.k, g.n, rows,
+                                     in, 1.0f, 1.0f, dt, st, te->split);
+    else
+      e = imq::launch_qgemm_swiglu(g.w, g.scales, g.biases, te->h1, te->m, in, g.k, g.n, rows, in,
+                                   0, in, 1.0f, 1.0f, dt, st, te->split);
   }
   if (e == hipSuccess)
     e = resid_split(te, l.down, rows)

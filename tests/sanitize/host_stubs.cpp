@@ -88,6 +88,15 @@ bool qskinny_supported(int k, int n, int m, int dtype) {
 }
 size_t qskinny_split_bytes(int, int, int) { return 0; }
 size_t qskinny_resid_split_bytes(int, int, int) { return 0; }
+hipError_t launch_qskinny_swiglu(const uint32_t*, const void*, const void*, const void*, void*,
+                                 int, int, int, int, int, float, float, int, hipStream_t,
+                                 SplitWs) {
+  return hipErrorNoDevice;
+}
+hipError_t launch_reduce_swiglu(const float*, int, int, int, void*, int, float, float, int,
+                                hipStream_t) {
+  return hipErrorNoDevice;
+}
 int qskinny_splits(int, int, int) { return 1; }
 hipError_t launch_dequant_rows(const uint32_t*, const void*, const void*, const int32_t*, int,
                                void*, int, int, int, hipStream_t) {
