@@ -248,18 +248,18 @@ def bench_cond_chain(torch) -> dict:
     return out
 
 
-def bench_te_layer(torch) -> dict:
+def bench_te_layer(torch, rows_list=(512, 30, 16, 8, 4)) -> dict:
     """One Qwen3 4B text-encoder layer's quantized-linear work (imq_te: RMSNorm +
     q/k/v; o_proj + dq_add, RMSNorm, gate/up + dq_silu_mul, down_proj + dq_add)
-    at the padded window L = 512 and the splice regime L = 30
-    (DirectTEEncoder.swift:249-412), bf16, graph-timed over 27 layers."""
+    at the padded window L = 512, the splice regime L = 30 and a few shorter
+    windows (DirectTEEncoder.swift:249-412), bf16, graph-timed over 27 layers."""
     from aestrix_amd.te import TextEncoderLayers, random_te_layers
 
     layers = random_te_layers(27, dtype=torch.bfloat16, seed=4)
     te = TextEncoderLayers(layers, max_rows=512)
     out = {}
     flop_per_row = 2.0 * (6144 * 2560 + 2560 * 4096 + 2 * 9728 * 2560 + 2560 * 9728)
-    for rows in (512, 30):
+    for rows in rows_list:
         x = torch.randn((rows, 2560), device="cuda").bfloat16()
         attn = torch.randn((rows, 4096), device="cuda").bfloat16()
         qkv = torch.empty((rows, 6144), dtype=torch.bfloat16, device="cuda")
@@ -271,8 +271,7 @@ def bench_te_layer(torch) -> dict:
             launches.append(lambda i=i, src=src: te.attn_out_mlp(i, src, attn, h[i % 2]))
         ms = time_graph(launches) * len(launches) / 27
         tf = flop_per_row * rows / (ms * 1e-3) / 1e12
-        out[f"L{rows}"] = {"us_per_layer": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
-                           "launches_per_layer": 5}
+        out[f"L{rows}"] = {"us_per_layer": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1)}
         log(f"TE layer L={rows}: {ms * 1e3:.1f} us per layer  {tf:.1f} TFLOP/s")
     te.close()
     del layers
@@ -579,6 +578,8 @@ def main() -> int:
                     help="run the launch and streaming-read floor kernels only (for profiling runs)")
     ap.add_argument("--only-step", action="store_true",
                     help="run the whole DiT step benchmark only (for profiling runs)")
+    ap.add_argument("--only-te", action="store_true",
+                    help="run the text-encoder layer benchmark only (for profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} requested, but this path runs on one GPU "
@@ -600,6 +601,9 @@ def main() -> int:
     props = torch.cuda.get_device_properties(0)
     if args.only_step:
         bench_dit_step(torch)
+        return 0
+    if args.only_te:
+        bench_te_layer(torch)
         return 0
     if args.only_hbm:
         bench_qgemv(imq, synth, torch, ms_list=(1,), few_rows=(4, 8, 16))
