@@ -17,7 +17,10 @@
  *                         y = T(r + T(m . Wdown^T))                       (fused dq_add)
  *
  * 5 launches instead of the reference's 12 for the same quantized work; the
- * q/k/v and gate/up weights stream in one launch each.  T is the layers'
+ * q/k/v and gate/up weights stream in one launch each.  At few rows a
+ * projection may take a K split, whose second (summing) launch carries the
+ * fused stage (dq_add, dq_silu_mul) and, for o_proj, the RMSNorm after it.
+ * T is the layers'
  * dtype (bf16, the reference's raw TE pack, or f16); x, y, qkv, attn_o are T
  * row-major, rows = tokens.  Calls are asynchronous on the given stream; the
  * plan's scratch makes calls on one plan one at a time.
