@@ -193,8 +193,8 @@ hipError_t launch_qskinny(const uint32_t* w, const void* scales, const void* bia
 // The K split with the residual add of launch_qgemm_resid_add in its second
 // kernel: y = T(float(resid) + float(T(x . deq(W)^T))), y may be resid.  Only
 // where qskinny_resid_split_bytes(k, n, m) > 0 and ws holds that many bytes
-// (hipErrorInvalidValue otherwise).  Its plan is the K split's own from 3
-// rows, also where a plain product would run unsplit (no unsplit kernel has
+// (hipErrorInvalidValue otherwise).  Its plan is the K split's own from 1
+// row, also where a plain product would run unsplit (no unsplit kernel has
 // the residual add; the tile kernel's form is the alternative).
 size_t qskinny_resid_split_bytes(int k, int n, int m);
 // y[m][j] = EpSwiGLU(gate sum j, up sum j) for j < width over a pair weight of
@@ -212,6 +212,10 @@ hipError_t launch_qskinny_swiglu(const uint32_t* w, const void* scales, const vo
 // split-sum kernel with EpSwiGLU, in split order.
 hipError_t launch_reduce_swiglu(const float* ws, int splits, int m, int width, void* y, int ldy,
                                 float in_scale, float out_scale, int dtype, hipStream_t stream);
+// y[row][j] = T(silu(g) * u) (EpSwiGLU's arithmetic) from a T product gu
+// [rows, ld] with g at column j and u at width + j.
+hipError_t launch_swiglu_t(const void* gu, int ld, int rows, int width, void* y, int ldy,
+                           float in_scale, float out_scale, int dtype, hipStream_t stream);
 hipError_t launch_qskinny_resid_add(const uint32_t* w, const void* scales, const void* biases,
                                     const void* x, const void* resid, void* y, int k, int n, int m,
                                     int dtype, hipStream_t stream, SplitWs ws);

@@ -1131,6 +1131,42 @@ hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const vo
   }
 }
 
+namespace {
+
+// y[row][j] = T(EpSwiGLU(g, u)) from a T product [rows, 2 width] (gate at
+// column j, up at width + j): the fused stage's arithmetic on values already
+// rounded to T (its round_to is then exact).
+template <int T>
+__global__ __launch_bounds__(256) void swiglu_t_kernel(const uint16_t* __restrict__ gu, int ld,
+                                                       int rows, const EpSwiGLU<T> ep) {
+  const long t = (long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long)rows * ep.width) return;
+  const int row = (int)(t / ep.width), j = (int)(t % ep.width);
+  const uint16_t* r = gu + (size_t)row * ld;
+  ep.emit1(row, j, Elem<T>::out(ep.value2(Elem<T>::param(r[j]), Elem<T>::param(r[ep.width + j]))));
+}
+
+}  // namespace
+
+hipError_t launch_swiglu_t(const void* gu, int ld, int rows, int width, void* y, int ldy,
+                           float in_scale, float out_scale, int dtype, hipStream_t stream) {
+  if (rows <= 0 || width <= 0) return hipSuccess;
+  const auto* g = static_cast<const uint16_t*>(gu);
+  auto* yy = static_cast<uint16_t*>(y);
+  const dim3 grid((unsigned)(((long)rows * width + 255) / 256));
+  switch (dtype) {
+    case kBf16:
+      hipLaunchKernelGGL((swiglu_t_kernel<kBf16>), grid, dim3(256), 0, stream, g, ld, rows,
+                         EpSwiGLU<kBf16>{yy, ldy, width, 0, width, in_scale, out_scale, false});
+      return hipGetLastError();
+    case kF16:
+      hipLaunchKernelGGL((swiglu_t_kernel<kF16>), grid, dim3(256), 0, stream, g, ld, rows,
+                         EpSwiGLU<kF16>{yy, ldy, width, 0, width, in_scale, out_scale, false});
+      return hipGetLastError();
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t launch_reduce_swiglu(const float* ws, int splits, int m, int width, void* y, int ldy,
                                 float in_scale, float out_scale, int dtype, hipStream_t stream) {
   auto* yy = static_cast<uint16_t*>(y);

@@ -1105,11 +1105,11 @@ size_t split_x_bytes(int per, int m) { return (size_t)m * (1024 * (size_t)per + 
 // 13.3 -> 9.2, [3072 x 3072] 12.3 -> 8.5, [2560 x 2560] 7.9 -> 6.8,
 // [1024 x 9728] M = 16 10.1 -> 8.2 us.
 // resid: for the residual-add form, which the unsplit kernels do not have
-// (the tile kernel is its alternative): from 3 rows, and where the unsplit
+// (the tile kernel is its alternative): from 1 row, and where the unsplit
 // kernels would be preferred for a plain product.
 SplitPlan plan_split(int k, int n, int m, bool resid = false) {
   SplitPlan best{0, 0, 0, 0, false};
-  if (k % 512 != 0 || k / 512 < 2 || m < (resid ? 3 : kSplitMinM) || m > 2 * kRows) return best;
+  if (k % 512 != 0 || k / 512 < 2 || m < (resid ? 1 : kSplitMinM) || m > 2 * kRows) return best;
   const int pieces = k / 512;
   const long tiles = (n + kRows - 1) / kRows;
   // Up to 16 rows the unsplit kernels are the alternative: the multi-tile

@@ -53,10 +53,10 @@ bool few_row_split(const imq_te* te, const imq_qweight& q, int rows) {
 
 // The same for the residual-add form of the o / down projections and the
 // SwiGLU form of gate/up, whose alternative is the tile kernel's at any row
-// count (their plan exists from 3 rows).
+// count (their plan exists from 1 row).
 bool resid_split(const imq_te* te, const imq_qweight& q, int rows) {
   const int dt = (int)te->dtype;
-  if (rows < imq::kDispatchSkinnyMinM || !imq::qskinny_supported(q.k, q.n, rows, dt)) return false;
+  if (!imq::qskinny_supported(q.k, q.n, rows, dt)) return false;
   const size_t need = imq::qskinny_resid_split_bytes(q.k, q.n, rows);
   return need > 0 && te->split.p && te->split.bytes >= need;
 }
@@ -223,7 +223,17 @@ int imq_te_attn_out_mlp(imq_te* te, int layer, const void* x, const void* attn_o
     // gate/up with dq_silu_mul: the qGEMV's pair mode at few rows, then the
     // few-row kernel's K split with the SwiGLU stage in its split sum where
     // it plans, else the tile kernel.
-    if (imq::qgemv_swiglu_fits(g.k, g.n, rows, dt))
+    if (rows >= imq::kDispatchSkinnyMinM && imq::qgemv_swiglu_fits(g.k, g.n, rows, dt) &&
+        g.n == 2 * in && imq::qskinny_supported(g.k, g.n, rows, dt) &&
+        imq::qskinny_split_bytes(g.k, g.n, rows) == 0 && te->split.p &&
+        te->split.bytes >= (size_t)rows * g.n * 2) {
+      // 3-4 rows: the few-row kernel's T product [rows, 2 inter] into the
+      // split workspace (free until down_proj), then the SwiGLU stage.
+      e = imq::launch_qskinny(g.w, g.scales, g.biases, te->h1, te->split.p, g.k, g.n, rows, dt, st,
+                              imq::SplitWs{});
+      if (e == hipSuccess)
+        e = imq::launch_swiglu_t(te->split.p, g.n, rows, in, te->m, in, 1.0f, 1.0f, dt, st);
+    } else if (imq::qgemv_swiglu_fits(g.k, g.n, rows, dt))
       e = imq::launch_qgemv_swiglu(g.w, g.scales, g.biases, te->h1, te->m, in, g.k, g.n, rows, in,
                                    0, in, 1.0f, 1.0f, dt, st);
     else if (g.n == 2 * in && resid_split(te, g, rows))

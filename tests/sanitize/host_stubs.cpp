@@ -97,6 +97,10 @@ hipError_t launch_reduce_swiglu(const float*, int, int, int, void*, int, float, 
                                 hipStream_t) {
   return hipErrorNoDevice;
 }
+hipError_t launch_swiglu_t(const void*, int, int, int, void*, int, float, float, int,
+                           hipStream_t) {
+  return hipErrorNoDevice;
+}
 int qskinny_splits(int, int, int) { return 1; }
 hipError_t launch_dequant_rows(const uint32_t*, const void*, const void*, const int32_t*, int,
                                void*, int, int, int, hipStream_t) {
