@@ -102,6 +102,11 @@ hipError_t launch_qgemm_gate_add(const uint32_t* w, const void* scales, const vo
 hipError_t launch_qgemm_resid_add(const uint32_t* w, const void* scales, const void* biases,
                                   const void* x, const void* resid, void* y, int k, int n, int m,
                                   int dtype, hipStream_t stream, SplitWs ws = {});
+// The qGEMV with the residual add in its store, m <= 4, 16-bit T:
+// y = T(float(resid) + float(T(x . deq(W)^T))) (EpResidAdd's arithmetic).
+hipError_t launch_qgemv_resid_add(const uint32_t* w, const void* scales, const void* biases,
+                                  const void* x, const void* resid, void* y, int k, int n, int m,
+                                  int dtype, hipStream_t stream);
 hipError_t launch_qgemm_swiglu(const uint32_t* w, const void* scales, const void* biases,
                                const void* x, void* y, int ldy, int k, int n, int m, int width,
                                int gate_row, int up_row, float in_scale, float out_scale, int dtype,

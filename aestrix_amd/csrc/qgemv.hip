@@ -109,10 +109,15 @@ __device__ __forceinline__ float group_sum(float v) {
 // times in_scale -- the qmm followed by dq_silu_mul / dd_swiglu_pitched
 // (Sources/ImarelloDirect/DirectGlueKernels.swift:77-88,
 // DirectDiTKernels.swift:137-157), computed by EpSwiGLU.
+// width 0: no pair; then a non-null resid makes the plain store
+// y = T(float(resid) + float(T(acc))) (EpResidAdd's arithmetic, 16-bit T).
 struct GvPair {
   int gate_row, up_row, width, ldy;
   float in_scale, out_scale;
+  const void* resid = nullptr;
 };
+
+bool is_pair(const GvPair* pr) { return pr && pr->width > 0; }
 
 template <int T, int MR, int G, int U, int R, bool PAIR>
 __global__ __launch_bounds__(kThreads) void qgemv_kernel(
@@ -292,12 +297,21 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
         if (m < M) y[(size_t)m * pr.ldy + pj] = E::out(ep.value2(acc[0][m], acc[1][m]));
     }
   } else if (gl == G - 1) {
+    const auto* rs = static_cast<const typename E::S*>(pr.resid);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (row0 + r < N) {
 #pragma unroll
-        for (int m = 0; m < MR; ++m)
-          if (m < M) y[(size_t)m * N + row0 + r] = E::out(acc[r][m]);
+        for (int m = 0; m < MR; ++m) {
+          if (m < M) {
+            const size_t i = (size_t)m * N + row0 + r;
+            float v = acc[r][m];
+            if constexpr (T != kF32) {
+              if (rs) v = staged_value<T>(rs[i]) + round_to(v, T);
+            }
+            y[i] = E::out(v);
+          }
+        }
       }
     }
   }
@@ -361,7 +375,7 @@ hipError_t launch_u(const uint32_t* w, const void* s, const void* b, const void*
   // x slots of the longest tile, rounded up to whole 256-slot rounds.
   const size_t pieces = (size_t)m * kt / XTile<T>::kEpp;
   const size_t slots = (pieces + kThreads - 1) / kThreads * kThreads;
-  if (pr) {
+  if (is_pair(pr)) {
     if constexpr (MR <= 4 && T != kF32) {
       constexpr int kOutsPerBlock = kWaves * (64 / G);
       const dim3 grid((pr->width + kOutsPerBlock - 1) / kOutsPerBlock);
@@ -377,7 +391,8 @@ hipError_t launch_u(const uint32_t* w, const void* s, const void* b, const void*
   const dim3 grid((n + rows_per_block - 1) / rows_per_block);
   hipLaunchKernelGGL((qgemv_kernel<T, MR, G, U, R, false>), grid, dim3(kThreads), slots * 16,
                      stream, w, static_cast<const ST*>(s), static_cast<const ST*>(b),
-                     static_cast<const ST*>(x), static_cast<ST*>(y), k, n, m, kt, GvPair{});
+                     static_cast<const ST*>(x), static_cast<ST*>(y), k, n, m, kt,
+                     pr ? *pr : GvPair{});
   return hipGetLastError();
 }
 
@@ -409,8 +424,8 @@ template <int T, int MR>
 hipError_t launch_m(const uint32_t* w, const void* s, const void* b, const void* x, void* y, int k,
                     int n, int m, const GvPair* pr, hipStream_t stream) {
   // A pair plans as 2 width rows read two per lane group.
-  const Plan p = pr ? make_plan(k, 2 * pr->width, MR, Elem<T>::kBytes, 2)
-                    : make_plan(k, n, MR, Elem<T>::kBytes);
+  const Plan p = is_pair(pr) ? make_plan(k, 2 * pr->width, MR, Elem<T>::kBytes, 2)
+                             : make_plan(k, n, MR, Elem<T>::kBytes);
   switch (p.g) {
     case 16: return launch_g<T, MR, 16>(w, s, b, x, y, k, n, m, p, pr, stream);
     case 32: return launch_g<T, MR, 32>(w, s, b, x, y, k, n, m, p, pr, stream);
@@ -426,7 +441,7 @@ hipError_t launch_t(const uint32_t* w, const void* s, const void* b, const void*
   if (m <= 1) return launch_m<T, 1>(w, s, b, x, y, k, n, m, pr, stream);
   if (m <= 2) return launch_m<T, 2>(w, s, b, x, y, k, n, m, pr, stream);
   if (m <= 4) return launch_m<T, 4>(w, s, b, x, y, k, n, m, pr, stream);
-  if (pr) return hipErrorInvalidValue;
+  if (pr) return hipErrorInvalidValue;  // pair and residual forms: m <= 4
   if (m <= 8) return launch_m<T, 8>(w, s, b, x, y, k, n, m, nullptr, stream);
   if (m <= 16) return launch_m<T, 16>(w, s, b, x, y, k, n, m, nullptr, stream);
   return hipErrorInvalidValue;
@@ -440,6 +455,19 @@ hipError_t launch_qgemv(const uint32_t* w, const void* scales, const void* biase
     case kBf16: return launch_t<kBf16>(w, scales, biases, x, y, k, n, m, nullptr, stream);
     case kF16: return launch_t<kF16>(w, scales, biases, x, y, k, n, m, nullptr, stream);
     case kF32: return launch_t<kF32>(w, scales, biases, x, y, k, n, m, nullptr, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_qgemv_resid_add(const uint32_t* w, const void* scales, const void* biases,
+                                  const void* x, const void* resid, void* y, int k, int n, int m,
+                                  int dtype, hipStream_t stream) {
+  if (m > 4 || !resid) return hipErrorInvalidValue;
+  GvPair pr{0, 0, 0, 0, 1.0f, 1.0f};
+  pr.resid = resid;
+  switch (dtype) {
+    case kBf16: return launch_t<kBf16>(w, scales, biases, x, y, k, n, m, &pr, stream);
+    case kF16: return launch_t<kF16>(w, scales, biases, x, y, k, n, m, &pr, stream);
     default: return hipErrorInvalidValue;
   }
 }

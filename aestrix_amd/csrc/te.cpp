@@ -203,7 +203,13 @@ int imq_te_attn_out_mlp(imq_te* te, int layer, const void* x, const void* attn_o
   // takes the shape (for o_proj with the RMSNorm after it in its split-sum
   // kernel, one launch fewer), else the tile kernel.
   hipError_t e;
-  if (resid_split(te, l.o, rows) &&
+  if (rows <= imq::kDispatchGemvMaxM) {
+    // 1-2 rows: the qGEMV with the residual add in its store, then RMSNorm.
+    e = imq::launch_qgemv_resid_add(l.o.w, l.o.scales, l.o.biases, attn_o, x, te->r, te->nq, h,
+                                    rows, dt, st);
+    if (e == hipSuccess)
+      e = imq::launch_rmsnorm_t(te->r, l.norm_post, te->h1, rows, h, te->eps, dt, st);
+  } else if (resid_split(te, l.o, rows) &&
       imq::qskinny_resid_add_norm_fits(te->nq, h, rows, dt, x, te->r, l.norm_post, te->h1,
                                        te->split)) {
     e = imq::launch_qskinny_resid_add_norm(l.o.w, l.o.scales, l.o.biases, attn_o, x, te->r,
@@ -244,7 +250,10 @@ int imq_te_attn_out_mlp(imq_te* te, int layer, const void* x, const void* attn_o
                                    0, in, 1.0f, 1.0f, dt, st, te->split);
   }
   if (e == hipSuccess)
-    e = resid_split(te, l.down, rows)
+    e = rows <= imq::kDispatchGemvMaxM
+            ? imq::launch_qgemv_resid_add(l.down.w, l.down.scales, l.down.biases, te->m, te->r, y,
+                                          in, h, rows, dt, st)
+        : resid_split(te, l.down, rows)
             ? imq::launch_qskinny_resid_add(l.down.w, l.down.scales, l.down.biases, te->m, te->r, y,
                                             in, h, rows, dt, st, te->split)
             : imq::launch_qgemm_resid_add(l.down.w, l.down.scales, l.down.biases, te->m, te->r, y,

@@ -28,6 +28,10 @@ hipError_t launch_qgemv_swiglu(const uint32_t*, const void*, const void*, const 
                                int, int, int, int, int, int, float, float, int, hipStream_t) {
   return hipErrorNoDevice;
 }
+hipError_t launch_qgemv_resid_add(const uint32_t*, const void*, const void*, const void*,
+                                  const void*, void*, int, int, int, int, hipStream_t) {
+  return hipErrorNoDevice;
+}
 hipError_t launch_qgemm(const uint32_t*, const void*, const void*, const void*, void*, int, int,
                         int, int, hipStream_t, SplitWs) {
   return hipErrorNoDevice;
