@@ -51,6 +51,12 @@ bool few_row_split(const imq_te* te, const imq_qweight& q, int rows) {
   return need > 0 && te->split.p && te->split.bytes >= need;
 }
 
+// Rows up to which the o / down projections run the qGEMV with the residual
+// add in its store (layer at L = 1 / 2 29.3 / 36.1 us against 38.3 / 41.1 on
+// the K split); from 3 rows the split is ahead (the qGEMV's dot products
+// grow with the rows: down at L = 4 14.1 us on it).
+constexpr int kGemvResidMaxRows = 2;
+
 // The same for the residual-add form of the o / down projections and the
 // SwiGLU form of gate/up, whose alternative is the tile kernel's at any row
 // count (their plan exists from 1 row).
@@ -203,7 +209,7 @@ int imq_te_attn_out_mlp(imq_te* te, int layer, const void* x, const void* attn_o
   // takes the shape (for o_proj with the RMSNorm after it in its split-sum
   // kernel, one launch fewer), else the tile kernel.
   hipError_t e;
-  if (rows <= imq::kDispatchGemvMaxM) {
+  if (rows <= kGemvResidMaxRows) {
     // 1-2 rows: the qGEMV with the residual add in its store, then RMSNorm.
     e = imq::launch_qgemv_resid_add(l.o.w, l.o.scales, l.o.biases, attn_o, x, te->r, te->nq, h,
                                     rows, dt, st);
@@ -250,7 +256,7 @@ int imq_te_attn_out_mlp(imq_te* te, int layer, const void* x, const void* attn_o
                                    0, in, 1.0f, 1.0f, dt, st, te->split);
   }
   if (e == hipSuccess)
-    e = rows <= imq::kDispatchGemvMaxM
+    e = rows <= kGemvResidMaxRows
             ? imq::launch_qgemv_resid_add(l.down.w, l.down.scales, l.down.biases, te->m, te->r, y,
                                           in, h, rows, dt, st)
         : resid_split(te, l.down, rows)

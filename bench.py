@@ -248,7 +248,7 @@ def bench_cond_chain(torch) -> dict:
     return out
 
 
-def bench_te_layer(torch, rows_list=(512, 30, 16, 8, 4)) -> dict:
+def bench_te_layer(torch, rows_list=(512, 30, 16, 8, 4, 1)) -> dict:
     """One Qwen3 4B text-encoder layer's quantized-linear work (imq_te: RMSNorm +
     q/k/v; o_proj + dq_add, RMSNorm, gate/up + dq_silu_mul, down_proj + dq_add)
     at the padded window L = 512, the splice regime L = 30 and a few shorter
