@@ -148,8 +148,18 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_tin_vec_kernel(
   __shared__ float part[kThreads / 64];
   const int n8 = cols >> 3;
   const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)blockIdx.x * cols);
+  const float4* wr = reinterpret_cast<const float4*>(w);
   uint4 v[V];
+  float4 wv[V][2];  // the weights load beside the row, not after the sum
   float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int idx = threadIdx.x + i * kThreads;
+    if (idx < n8) {
+      wv[i][0] = wr[2 * idx];
+      wv[i][1] = wr[2 * idx + 1];
+    }
+  }
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int idx = threadIdx.x + i * kThreads;
@@ -171,13 +181,12 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_tin_vec_kernel(
 #pragma unroll
   for (int i = 0; i < kThreads / 64; ++i) total += part[i];
   const float inv = __frsqrt_rn(total / (float)cols + eps);
-  const float4* wr = reinterpret_cast<const float4*>(w);
   uint4* yr = reinterpret_cast<uint4*>(y + (size_t)blockIdx.x * cols);
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int idx = threadIdx.x + i * kThreads;
     if (idx < n8) {
-      const float4 w0 = wr[2 * idx], w1 = wr[2 * idx + 1];
+      const float4 w0 = wv[i][0], w1 = wv[i][1];
       const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
       const uint32_t q[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
       uint32_t o[4];

@@ -990,7 +990,17 @@ __global__ __launch_bounds__(256) void qskinny_reduce_norm_kernel(
   __shared__ float part[4];
   const int n8 = N >> 3;
   const size_t row = (size_t)blockIdx.x * N;
+  const float4* wr = reinterpret_cast<const float4*>(nw);
   uint4 v[V];
+  float4 wv[V][2];  // the norm weights load beside the sums, not after them
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int idx = threadIdx.x + i * 256;
+    if (idx < n8) {
+      wv[i][0] = wr[2 * idx];
+      wv[i][1] = wr[2 * idx + 1];
+    }
+  }
   float acc = 0.f;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
@@ -1042,12 +1052,11 @@ __global__ __launch_bounds__(256) void qskinny_reduce_norm_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i) total += part[i];
   const float inv = __frsqrt_rn(total / (float)N + eps);
-  const float4* wr = reinterpret_cast<const float4*>(nw);
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int idx = threadIdx.x + i * 256;
     if (idx < n8) {
-      const float4 w0 = wr[2 * idx], w1 = wr[2 * idx + 1];
+      const float4 w0 = wv[i][0], w1 = wv[i][1];
       const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
       const uint32_t q[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
       uint32_t o[4];
