@@ -161,7 +161,7 @@ def oracle_attn_out_mlp(x: np.ndarray, attn_o: np.ndarray, l, tdt) -> np.ndarray
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("rows", [512, 30, 16, 8, 4, 1])
+@pytest.mark.parametrize("rows", [512, 30, 17, 16, 8, 4, 3, 2, 1])
 def test_layer_halves_match_oracle(dtype, rows):
     note(f"TE layer halves {dtype} rows={rows} (hidden 2560, qkv 6144, inter 9728)")
     layers = random_te_layers(1, dtype=dtype, seed=71)
