@@ -181,6 +181,37 @@ imq::SplitWs split_ws(imq_ctx* ctx, hipStream_t st, size_t need) {
   return {static_cast<float*>(p), need};
 }
 
+// Orders an allocation-free call that uses the static scratch after the
+// previous such call on the same GPU, whatever stream or thread made it, so
+// that eager calls never share the scratch in flight.  Not under stream
+// capture: a captured call's graph replays are ordered by their caller.
+class ScratchOrder {
+ public:
+  ~ScratchOrder() { (void)release(); }
+  hipError_t acquire(int device, hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(st, &cs);
+    if (e != hipSuccess || cs != hipStreamCaptureStatusNone) return e;
+    e = imq::scratch_acquire(device, st);
+    if (e == hipSuccess) {
+      device_ = device;
+      st_ = st;
+      held_ = true;
+    }
+    return e;
+  }
+  hipError_t release() {
+    if (!held_) return hipSuccess;
+    held_ = false;
+    return imq::scratch_release(device_, st_);
+  }
+
+ private:
+  int device_ = -1;
+  hipStream_t st_ = nullptr;
+  bool held_ = false;
+};
+
 int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, const void* s,
             const void* b, const void* x, void* y, int k, int n, int m, int group_size, int bits,
             imq_dtype dtype, imq_stream stream) {
@@ -217,12 +248,23 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
     const size_t need = imq::qskinny_split_bytes(k, n, m);
     if (regime == Regime::kAuto) {
       sws = split_ws(ctx, st, need);
-    } else if (regime == Regime::kAutoNoAlloc && need > 0 && need <= imq::kStaticScratchBytes) {
+    } else if (regime == Regime::kAutoNoAlloc && need > 0) {
+      // imq_qmm_t would split here; running unsplit (or on the tile kernel)
+      // would change the bits, so a plan the static scratch cannot hold is
+      // refused, as on the tile path below.
+      if (need > imq::kStaticScratchBytes)
+        return fail(ctx, IMQ_EINVAL,
+                    "%s: M=%d N=%d K=%d needs %zu bytes of split-K scratch; the static scratch "
+                    "holds %zu (imq_qmm_t takes this shape)",
+                    fn, m, n, k, need, imq::kStaticScratchBytes);
       sws = imq::SplitWs{static_cast<float*>(ctx->static_scratch), need};
     }
     skinny = m <= imq::kDispatchSkinnyMaxM || (need > 0 && sws.p && sws.bytes >= need);
   }
+  ScratchOrder order;
   if (skinny) {
+    if (regime == Regime::kAutoNoAlloc && sws.p && (e = order.acquire(ctx->device, st)) != hipSuccess)
+      return hip_fail(ctx, e, fn);
     e = imq::launch_qskinny(w, s, b, x, y, k, n, m, (int)dtype, st, sws);
   } else if (!gemv) {
     // The dispatcher may split K over a workspace; imq_qgemm is the plain
@@ -238,6 +280,7 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
                     "holds %zu (imq_qmm_t takes this shape)",
                     fn, m, n, k, need, imq::kStaticScratchBytes);
       if (need > 0) ws = imq::SplitWs{static_cast<float*>(ctx->static_scratch), need};
+      if (ws.p && (e = order.acquire(ctx->device, st)) != hipSuccess) return hip_fail(ctx, e, fn);
     }
     e = imq::launch_qgemm(w, s, b, x, y, k, n, m, (int)dtype, st, ws);
   } else {
@@ -250,6 +293,8 @@ int run_qmm(imq_ctx* ctx, const char* fn, Regime regime, const uint32_t* w, cons
                             (int)dtype, st);
     }
   }
+  const hipError_t eo = order.release();
+  if (e == hipSuccess) e = eo;
   return e == hipSuccess ? IMQ_OK : hip_fail(ctx, e, fn);
 }
 

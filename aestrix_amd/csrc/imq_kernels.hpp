@@ -177,6 +177,14 @@ constexpr size_t kStaticScratchBytes = (size_t)64 << 20;
 // Device address of that scratch on `device`, which must be current; looked
 // up with hipGetSymbolAddress on the first call for a device.
 hipError_t static_scratch(int device, void** out);
+// Orders the calls that use that scratch on one device: scratch_acquire
+// locks the device's order and makes `stream` wait for the previous such
+// call (an event recorded on whatever stream it ran on); scratch_release
+// records this call's event on `stream` and unlocks.  Outside stream capture
+// only (a capturing caller orders its graph replays itself).  The event is
+// created by static_scratch, at set-up, so these allocate nothing.
+hipError_t scratch_acquire(int device, hipStream_t stream);
+hipError_t scratch_release(int device, hipStream_t stream);
 
 // Whether the weight-streaming kernel takes this call: 1 <= m <= 32,
 // k % 128 == 0, T in {bf16, f16}, 32-bit byte offsets (past 16 rows only with

@@ -887,7 +887,10 @@ hipError_t launch_reduce(const SplitWs& ws, int splits, int m, int ncols, int ld
                          hipStream_t stream) {
   const long threads = (long)m * ((ncols + 7) / 8);
   const dim3 grid((unsigned)((threads + 255) / 256));
-  const bool vload = ldp % 4 == 0 && ncols % 8 == 0;
+  // 16-byte partial loads: ws 16-byte aligned and every row / pair offset a
+  // multiple of four floats.
+  bool vload = ldp % 4 == 0 && ncols % 8 == 0 && ((uintptr_t)ws.p & 15u) == 0;
+  if constexpr (EP::kPair) vload = vload && ep.width % 4 == 0;
   hipLaunchKernelGGL((reduce_ep_kernel<T, EP>), grid, dim3(256), 0, stream, ws.p, splits, m, ncols,
                      ldp, vload, ep);
   return hipGetLastError();

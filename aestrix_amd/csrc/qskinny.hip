@@ -1252,7 +1252,10 @@ hipError_t launch_split(const uint32_t* w, const uint16_t* s, const uint16_t* b,
                          p.splits, count, n, resid, y, nw, h, eps);
     return hipGetLastError();
   }
-  const bool rvec = count % 4 == 0 && ((uintptr_t)y & 7u) == 0 && ((uintptr_t)resid & 7u) == 0;
+  // The vector form loads float4 partials at ws + split * count + i (i % 4 == 0)
+  // and stores four T values: ws 16-byte and y / resid 8-byte aligned.
+  const bool rvec = count % 4 == 0 && ((uintptr_t)ws & 15u) == 0 && ((uintptr_t)y & 7u) == 0 &&
+                    ((uintptr_t)resid & 7u) == 0;
   const dim3 grid((unsigned)(((rvec ? count / 4 : count) + 255) / 256));
   if (resid) {
     if (rvec)

@@ -151,10 +151,13 @@ int imq_qmm_t(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* b
  * partial sum a call reads it has written first, so nothing needs clearing.
  * A shape whose plan needs more scratch than that returns IMQ_EINVAL (the
  * largest plans of the text-encoder, conditioner and DiT shapes up to
- * M = 2048 fit).  All calls on one GPU share the one scratch: calls that
- * overlap in time on that GPU (several streams, several contexts, several
- * threads, or a graph replay beside another call) race and may return wrong
- * results; order them on one stream. */
+ * M = 2048 fit), also where imq_qmm_t would run the few-row kernel's K split.
+ * All calls on one GPU share the one scratch.  Eager calls that use it are
+ * ordered on the device by the library (each waits, by an event and without
+ * blocking the host, for the previous one on that GPU, whatever its stream,
+ * context or thread).  Calls made under stream capture are not: a graph
+ * replay that overlaps another call using the scratch on that GPU races and
+ * may return wrong results; order such replays on one stream. */
 int imq_qmm_t_noalloc(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
                       const void* x, void* y, int k, int n, int m, int group_size, int bits,
                       imq_dtype dtype, imq_stream stream);
@@ -205,7 +208,11 @@ typedef struct imq_plan {
 
 /* The plan of a call of `entry` with these sizes and dtype on ctx's device,
  * without launching anything; the same argument checks as the entry point on
- * the sizes (IMQ_EINVAL / IMQ_EUNSUPPORTED). */
+ * the sizes (IMQ_EINVAL / IMQ_EUNSUPPORTED).  For IMQ_ENTRY_QMM_T it is the
+ * plan with its split-K workspace in hand: imq_qmm_t_noalloc runs it or
+ * returns IMQ_EINVAL, and imq_qmm_t runs it except under stream capture on a
+ * stream whose workspace is still smaller than workspace_bytes, where it runs
+ * the same kernel family unsplit (or, at 17-32 rows, the tile kernel). */
 int imq_qmm_plan(imq_ctx* ctx, int entry, int k, int n, int m, imq_dtype dtype, imq_plan* out);
 
 /* ---- fused output stages ------------------------------------------------

@@ -85,6 +85,8 @@ hipError_t static_scratch(int, void** out) {
   *out = nullptr;
   return hipErrorNoDevice;
 }
+hipError_t scratch_acquire(int, hipStream_t) { return hipErrorNoDevice; }
+hipError_t scratch_release(int, hipStream_t) { return hipErrorNoDevice; }
 bool qskinny_supported(int k, int n, int m, int dtype) {
   return m >= 1 && m <= kQskinnyMaxM && n >= 1 && k >= 128 && k % 128 == 0 &&
          (dtype == 0 || dtype == 1) && (size_t)n * k / 2 < ((size_t)1 << 32) &&
