@@ -105,6 +105,55 @@ def test_noalloc_refuses_a_plan_past_the_static_scratch():
         noalloc(x, w, s, s, y)
 
 
+def test_noalloc_refuses_a_few_row_split_past_the_static_scratch():
+    """At 16 rows the few-row kernel splits K when x does not fit LDS; with
+    enough weight rows its partial sums outgrow the static scratch.  imq_qmm_t
+    runs that split plan; the allocation-free entry point refuses the call
+    rather than run a different plan (different bits)."""
+    m, k = 16, 8192
+    for n in (131072, 262144, 524288):
+        plan = imq.qmm_plan(m, n, k)
+        note(f"few-row plan M={m} N={n} K={k}: {plan}")
+        if plan["kernel"] == "few_row" and plan["workspace_bytes"] > STATIC_SCRATCH_BYTES:
+            break
+    else:
+        pytest.fail("no few-row split plan past the static scratch among the shapes tried")
+    x = torch.zeros((m, k), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros((n, k // 8), dtype=torch.int32, device="cuda")
+    s = torch.zeros((n, k // 64), dtype=torch.bfloat16, device="cuda")
+    y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(_lib.ImqInvalid, match="static scratch"):
+        noalloc(x, w, s, s, y)
+    del x, w, s, y
+    torch.cuda.empty_cache()
+
+
+def test_noalloc_calls_on_two_streams_are_ordered():
+    """Eager calls on different streams share the one scratch; the library
+    orders them on the GPU, so back-to-back calls on two streams (no host sync
+    between) both return imq_qmm_t's bits."""
+    # Split-K tile plans and few-row K splits (the shapes of the pairs above).
+    shapes = [(512, 2560, 9728), (40, 1000, 2560), (16, 2560, 9728), (32, 9728, 2560)]
+    probs = [problem(m, n, k, seed=80 + i, dtype="bf16") for i, (m, n, k) in enumerate(shapes)]
+    for m, n, k in shapes:
+        assert split_bytes(m, n, k) > 0, (m, n, k)
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    ys = []
+    for rep in range(3):
+        for i, ((m, n, k), (x, w, s, b)) in enumerate(zip(shapes, probs)):
+            y = torch.full((m, n), 5.0, dtype=torch.bfloat16, device="cuda")
+            streams[i % 2].wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(streams[i % 2]):
+                noalloc(x, w, s, b, y)
+            ys.append((i, y))
+    torch.cuda.synchronize()
+    for i, y in ys:
+        x, w, s, b = probs[i]
+        assert torch.equal(y, imq.quantized_matmul(x, w, s, b)), f"shape {shapes[i]}"
+
+
 def test_noalloc_under_graph_capture():
     """Captured on a fresh stream (where imq_qmm_t would have no workspace and
     would run unsplit), the entry point keeps its split plan; replays with
