@@ -5,10 +5,20 @@ TFLOP/s at M=4608, K=3072, N=18432 (the DiT MLP-in projection at 1024^2,
 bf16 activations, 4-bit group-64 weights); one "step" is one qGEMM launch
 over that synthetic batch, inputs resident in HBM.  The same line carries:
 
-* roofline   -- the qGEMM against the dense bf16 MFMA peak (2.5 PFLOP/s);
+* roofline   -- the qGEMM against the dense bf16 MFMA peak (2.5 PFLOP/s, quoted
+                at a 2400 MHz engine clock), and against that peak scaled to
+                the engine clock the GPU held while the headline ran;
+* device     -- engine / memory clock, board power, power cap and junction
+                temperature from the GPU's sysfs node: idle, averaged over the
+                loaded headline, and after it;
+* dense_bf16_reference -- the vendor dense GEMM (hipBLASLt via torch.matmul)
+                on the headline shape with the weights already bf16, same box,
+                with the clock and power it ran at (a reference point only);
 * qgemv      -- M=1/4/16 on the text-encoder MLP shapes [9728x2560] and
                 [2560x9728], GB/s of algorithmic bytes against 8 TB/s, with the
-                weights rotated over enough copies to miss the 256 MB MALL;
+                weights rotated over enough copies to miss the 256 MB MALL
+                (a captured graph of 48 launches), and one launch alone after
+                a 512 MiB read that evicts every cache (single_us);
 * qgemv_f32  -- the conditioner's M=1 f32 qmm ([18432x3072], [3072x256]), GB/s;
 * dequant    -- the two projections of a DiT single-stream block, GB/s;
 * prescale   -- the f16 sandwich's pre-scale cast (x / 16 to f16) on [4608x3072] float32, GB/s;
@@ -29,9 +39,10 @@ over that synthetic batch, inputs resident in HBM.  The same line carries:
 
 Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 100] [--no-cpu-baseline]
 
-Before its W warmup steps the headline runs untimed launches for 0.5 s, so
-the clock and power state have settled whatever W is (short warm-ups landed
-inside the transient of the first tens of ms of sustained MFMA load).
+Before its W warmup steps the headline runs untimed launches for 1 s, so
+the clock and power state have settled whatever W is: under a sustained dense
+MFMA load the board reaches its power cap and the engine clock settles well
+below its 2400 MHz maximum within about 0.7 s.
 """
 
 from __future__ import annotations
@@ -46,7 +57,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "4-bit qGEMM TFLOP/s (% MFMA peak) at M=4608; qGEMV GB/s (% HBM) at M=1"
-PREWARM_S = 0.5  # untimed launches before the warmup steps of the headline
+PREWARM_S = 1.0  # untimed launches before the warmup steps of the headline
+STEADY_S = 0.5   # the clock / power readings averaged: the pre-warm's last STEADY_S + the timed steps
+MAX_SCLK_MHZ = 2400.0  # the engine clock the dense MFMA peak is quoted at
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 TARGET = (4608, 18432, 3072)  # M, N, K
@@ -79,6 +92,130 @@ def time_events(fn, reps: int) -> float:
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / reps
+
+
+class GpuState:
+    """The GPU's engine clock, memory clock, board power, power cap and
+    temperatures, read from its amdgpu sysfs node (found by the PCI address
+    torch reports).  The power and clock readings are the firmware's running
+    averages, refreshed every few ms; a reading that fails is left out."""
+
+    def __init__(self, torch):
+        props = torch.cuda.get_device_properties(0)
+        self.dev = (f"/sys/bus/pci/devices/{props.pci_domain_id:04x}:{props.pci_bus_id:02x}:"
+                    f"{props.pci_device_id:02x}.0")
+        hw = os.path.join(self.dev, "hwmon")
+        names = sorted(os.listdir(hw)) if os.path.isdir(hw) else []
+        self.hwmon = os.path.join(hw, names[0]) if names else None
+
+    @staticmethod
+    def _read(path):
+        try:
+            with open(path) as f:
+                return f.read()
+        except OSError:
+            return None
+
+    def _level(self, name):
+        """MHz of the current level of pp_dpm_<name> (the line marked '*')."""
+        txt = self._read(os.path.join(self.dev, name))
+        for line in (txt or "").splitlines():
+            if line.rstrip().endswith("*"):
+                try:
+                    return int(line.split(":")[1].strip().lower().split("mhz")[0])
+                except (IndexError, ValueError):
+                    return None
+        return None
+
+    def _hw(self, name, scale):
+        if not self.hwmon:
+            return None
+        txt = self._read(os.path.join(self.hwmon, name))
+        try:
+            return round(int(txt) / scale, 1) if txt else None
+        except ValueError:
+            return None
+
+    def snapshot(self) -> dict:
+        snap = {"sclk_mhz": self._level("pp_dpm_sclk"), "mclk_mhz": self._level("pp_dpm_mclk"),
+                "power_w": self._hw("power1_input", 1e6) or self._hw("power1_average", 1e6),
+                "power_cap_w": self._hw("power1_cap", 1e6),
+                "temp_junction_c": self._hw("temp2_input", 1e3),
+                "temp_mem_c": self._hw("temp3_input", 1e3)}
+        return {k: v for k, v in snap.items() if v is not None}
+
+
+class StateSampler:
+    """Samples GpuState every ~20 ms on a host thread while work runs;
+    summary(since) averages the samples taken after `since` seconds."""
+
+    def __init__(self, state: GpuState):
+        import threading
+
+        self.state = state
+        self.samples = []
+        self._stop = threading.Event()
+        self._t0 = time.perf_counter()
+        self._th = threading.Thread(target=self._run, daemon=True)
+
+    def _run(self):
+        while not self._stop.is_set():
+            self.samples.append((time.perf_counter() - self._t0, self.state.snapshot()))
+            self._stop.wait(0.02)
+
+    def __enter__(self):
+        self._th.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        self._th.join()
+
+    def elapsed(self) -> float:
+        return time.perf_counter() - self._t0
+
+    def summary(self, since: float = 0.0) -> dict:
+        rows = [snap for t, snap in self.samples if t >= since]
+        out = {"samples": len(rows)}
+
+        def vals(key):
+            return [r[key] for r in rows if key in r]
+
+        if v := vals("sclk_mhz"):
+            out.update(sclk_mhz=round(sum(v) / len(v), 1), sclk_min_mhz=min(v),
+                       sclk_max_mhz=max(v))
+        if v := vals("power_w"):
+            out.update(power_w=round(sum(v) / len(v), 1), power_max_w=max(v))
+        if v := vals("temp_junction_c"):
+            out.update(temp_junction_max_c=max(v))
+        return out
+
+
+def time_single(fn_list, flush, reps: int = 24) -> float:
+    """Median milliseconds of ONE launch: before each, `flush` overwrites a
+    buffer larger than the 256 MB MALL (so the launch reads its operands from
+    HBM), then HIP events on torch's current stream bracket fn_list[i] alone."""
+    import torch
+
+    times = []
+    for r in range(reps):
+        flush()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn_list[r % len(fn_list)]()
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end))
+    times.sort()
+    return times[len(times) // 2]
+
+
+def mall_flush(torch):
+    """A function that reads 512 MiB (twice the MALL) and so leaves no
+    operand of the next launch in any cache."""
+    buf = torch.ones(128 << 20, dtype=torch.int32, device="cuda")
+    return lambda: buf.amax()
 
 
 def time_graph(launches, replays: int = 5) -> float:
@@ -115,6 +252,7 @@ def bench_qgemv(imq, synth, torch, copies: int = 48, ms_list=(1, 4, 16),
     """The qGEMV at M in ms_list, and the regime dispatcher at M in few_rows (the
     weight-streaming matrix-core kernel), weights rotated over `copies` copies."""
     out = {}
+    flush = mall_flush(torch)
     for (n, k) in ((9728, 2560), (2560, 9728)):
         p = synth.make_problem(16, n, k, seed=0)
         x, w, s, b = synth.to_device(p)
@@ -129,12 +267,16 @@ def bench_qgemv(imq, synth, torch, copies: int = 48, ms_list=(1, 4, 16),
             launches = [(lambda i=i, fn=fn: fn(xm, ws[i], ss[i], bs[i], out=ys[i]))
                         for i in range(copies)]
             ms = time_graph(launches)
+            one = time_single(launches, flush)
             byts = qmm_bytes(m, n, k)
             gbs = byts / (ms * 1e-3) / 1e9
             key = f"M{m}_N{n}_K{k}" if tag == "qgemv" else f"qmm_t_M{m}_N{n}_K{k}"
             out[key] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
-                        "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts}
-            log(f"{tag} M={m} N={n} K={k}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s")
+                        "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts,
+                        "single_us": round(one * 1e3, 3),
+                        "single_GB/s": round(byts / (one * 1e-3) / 1e9, 1)}
+            log(f"{tag} M={m} N={n} K={k}: {ms * 1e3:.2f} us  {gbs:.0f} GB/s "
+                f"(one cold launch: {one * 1e3:.2f} us)")
         del ws, ss, bs
         # The floor one launch of this size reaches: a device copy moving the
         # M=1 call's bytes (half read, half written), rotated the same way.
@@ -144,14 +286,18 @@ def bench_qgemv(imq, synth, torch, copies: int = 48, ms_list=(1, 4, 16),
         dst = [torch.empty(words, dtype=torch.int32, device="cuda") for _ in range(copies)]
         launches = [(lambda i=i: dst[i].copy_(src[i])) for i in range(copies)]
         ms = time_graph(launches)
+        one = time_single(launches, flush)
         gbs = 8 * words / (ms * 1e-3) / 1e9
         qg = out[f"M1_N{n}_K{k}"] if 1 in ms_list else None
         out[f"copy_floor_N{n}_K{k}"] = {
             "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "bytes": 8 * words,
-            "qgemv_M1_vs_copy": round(ms * 1e3 / qg["us"], 3) if qg else None}
+            "single_us": round(one * 1e3, 3),
+            "qgemv_M1_vs_copy": round(ms * 1e3 / qg["us"], 3) if qg else None,
+            "qgemv_M1_vs_copy_single": round(one * 1e3 / qg["single_us"], 3) if qg else None}
         log(f"device copy of the M=1 bytes ({8 * words} B moved): {ms * 1e3:.2f} us  "
-            f"{gbs:.0f} GB/s" + (f"  (qGEMV M=1 at {ms * 1e3 / qg['us']:.2f} of its rate)"
-                                  if qg else ""))
+            f"{gbs:.0f} GB/s, one cold launch {one * 1e3:.2f} us"
+            + (f"  (qGEMV M=1 at {ms * 1e3 / qg['us']:.2f} of its rate, "
+               f"{one * 1e3 / qg['single_us']:.2f} single)" if qg else ""))
         del src, dst
         torch.cuda.empty_cache()
     return out
@@ -281,6 +427,7 @@ def bench_te_layer(torch, rows_list=(512, 30, 16, 8, 4, 1)) -> dict:
 
 def bench_dequant(imq, synth, torch, copies: int = 6) -> dict:
     out = {}
+    flush = mall_flush(torch)
     for (n, k) in ((27648, 3072), (3072, 12288)):
         p = synth.make_problem(0, n, k, seed=1)
         _, w, s, b = synth.to_device(p)
@@ -291,11 +438,15 @@ def bench_dequant(imq, synth, torch, copies: int = 6) -> dict:
         launches = [(lambda i=i: imq.dequantize(ws[i], ss[i], bs[i], out=os_[i]))
                     for i in range(copies)]
         ms = time_graph(launches, replays=4)
+        one = time_single(launches, flush, reps=12)
         byts = dequant_bytes(n, k)
         gbs = byts / (ms * 1e-3) / 1e9
         out[f"N{n}_K{k}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
-                             "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts}
-        log(f"dequant N={n} K={k}: {ms * 1e3:.1f} us  {gbs:.0f} GB/s")
+                             "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": byts,
+                             "single_us": round(one * 1e3, 2),
+                             "single_GB/s": round(byts / (one * 1e-3) / 1e9, 1)}
+        log(f"dequant N={n} K={k}: {ms * 1e3:.1f} us  {gbs:.0f} GB/s "
+            f"(one cold launch: {one * 1e3:.1f} us)")
         del ws, ss, bs, os_
         torch.cuda.empty_cache()
     return out
@@ -365,6 +516,36 @@ def bench_x_embedder(imq, synth, torch) -> dict:
         f"{qmm_ms * 1e3:.1f} us, {tf:.1f} TFLOP/s, {byts / (qmm_ms * 1e-3) / 1e9:.0f} GB/s)")
     return {"us": round(ms * 1e3, 2), "qmm_postscale_us": round(qmm_ms * 1e3, 2),
             "TFLOP/s": round(tf, 1), "GB/s": round(byts / (qmm_ms * 1e-3) / 1e9, 1)}
+
+
+def bench_dense_bf16(torch, imq, x, w, s, b, gpu: GpuState, steps: int = 20) -> dict:
+    """A reference point on the same box, not part of the product: the vendor
+    dense GEMM (hipBLASLt through torch.matmul) on the headline shape with the
+    weights already dequantized to bf16 (4x the weight bytes, no dequant work),
+    timed like the headline, with the clock and power it runs at."""
+    m, k = x.shape
+    n = w.shape[0]
+    wt = imq.dequantize(w, s, b).t().contiguous()  # [K, N] bf16
+    y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    with StateSampler(gpu) as smp:
+        t_pre = time.perf_counter()
+        while time.perf_counter() - t_pre < PREWARM_S:
+            for _ in range(20):
+                torch.matmul(x, wt, out=y)
+            torch.cuda.synchronize()
+        steady_from = smp.elapsed() - STEADY_S
+        ms = time_events(lambda: torch.matmul(x, wt, out=y), steps)
+    loaded = smp.summary(since=steady_from)
+    tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    log(f"dense bf16 reference (torch.matmul, hipBLASLt) M={m} N={n} K={k}: {ms:.4f} ms  "
+        f"{tf:.1f} TFLOP/s  loaded: {loaded}")
+    del wt, y
+    out = {"what": "torch.matmul (hipBLASLt) on the dequantized bf16 weights, same shape and box",
+           "ms": round(ms, 5), "TFLOP/s": round(tf, 1),
+           "frac_mfma": round(tf / PEAK_BF16_TFLOPS, 4), "loaded": loaded}
+    if sclk := loaded.get("sclk_mhz"):
+        out["frac_at_loaded_clock"] = round(tf / (PEAK_BF16_TFLOPS * sclk / MAX_SCLK_MHZ), 4)
+    return out
 
 
 def bench_qgemm_shape(imq, synth, torch, m, n, k, reps=10, dispatcher=False) -> dict:
@@ -623,29 +804,40 @@ def main() -> int:
     p = synth.make_problem(m, n, k, seed=0)
     x, w, s, b = synth.to_device(p)
     y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-    # Untimed pre-warm until PREWARM_S of wall time has passed (the GPU leaves
-    # its idle clock and power state), then the W warmup steps.
-    t_pre = time.perf_counter()
-    while time.perf_counter() - t_pre < PREWARM_S:
-        for _ in range(20):
+    gpu = GpuState(torch)
+    idle = gpu.snapshot()
+    with StateSampler(gpu) as smp:
+        # Untimed pre-warm until PREWARM_S of wall time has passed (the GPU
+        # leaves its idle clock and settles at its loaded clock and power),
+        # then the W warmup steps.
+        t_pre = time.perf_counter()
+        while time.perf_counter() - t_pre < PREWARM_S:
+            for _ in range(20):
+                imq.quantized_matmul(x, w, s, b, out=y)
+            torch.cuda.synchronize()
+        steady_from = smp.elapsed() - STEADY_S
+        for _ in range(args.warmup):
             imq.quantized_matmul(x, w, s, b, out=y)
         torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        imq.quantized_matmul(x, w, s, b, out=y)
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    start.record()
-    for _ in range(args.steps):
-        imq.quantized_matmul(x, w, s, b, out=y)
-    end.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record()
+        for _ in range(args.steps):
+            imq.quantized_matmul(x, w, s, b, out=y)
+        end.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    loaded = smp.summary(since=steady_from)
+    after = gpu.snapshot()
     ms = start.elapsed_time(end) / args.steps
     flop = 2.0 * m * n * k
     tflops = flop / (ms * 1e-3) / 1e12
-    log(f"target qgemm: {ms:.4f} ms/step  {tflops:.1f} TFLOP/s  (host wall {wall:.3f} s)")
+    log(f"target qgemm: {ms:.4f} ms/step  {tflops:.1f} TFLOP/s  (host wall {wall:.3f} s); "
+        f"loaded: {loaded}")
+    dense = None
+    if not args.only_target:
+        dense = bench_dense_bf16(torch, imq, x, w, s, b, gpu)
     del x, w, s, b, y
     torch.cuda.empty_cache()
     if args.only_target:
@@ -710,8 +902,18 @@ def main() -> int:
                                        "FETCH_SIZE / WRITE_SIZE of this kernel and shape, scaled "
                                        "by a 256 MiB copy in the same process (not this run)"},
         "device": {"name": props.name, "cus": props.multi_processor_count,
-                   "hip": torch.version.hip},
+                   "hip": torch.version.hip, "idle": idle, "headline_loaded": loaded,
+                   "after_headline": after},
     }
+    if sclk := loaded.get("sclk_mhz"):
+        # The peak is quoted at MAX_SCLK_MHZ; under the board's power cap the
+        # engine clock of a sustained dense MFMA load settles lower.
+        peak_at_clock = PEAK_BF16_TFLOPS * sclk / MAX_SCLK_MHZ
+        result["roofline"]["loaded_sclk_mhz"] = sclk
+        result["roofline"]["peak_at_loaded_clock"] = round(peak_at_clock, 1)
+        result["roofline"]["frac_at_loaded_clock"] = round(tflops / peak_at_clock, 4)
+    if dense:
+        result["dense_bf16_reference"] = dense
     result.update(extra)
     if qgemv := extra.get("qgemv"):
         result["qgemv_headline"] = {"shape": "M=1 [9728x2560]",
@@ -720,6 +922,8 @@ def main() -> int:
             # A device copy moving the same bytes in one launch, same run.
             result["qgemv_headline"]["copy_floor_GB/s"] = floor["GB/s"]
             result["qgemv_headline"]["frac_of_copy_floor"] = floor["qgemv_M1_vs_copy"]
+            result["qgemv_headline"]["copy_floor_single_us"] = floor["single_us"]
+            result["qgemv_headline"]["single_frac_of_copy_floor"] = floor["qgemv_M1_vs_copy_single"]
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(synth)
