@@ -79,6 +79,7 @@ SIGNATURES = {
     "imq_free": ([_p, _p], _i),
     "imq_memcpy_h2d": ([_p, _p, _p, _sz, _p], _i),
     "imq_memcpy_d2h": ([_p, _p, _p, _sz, _p], _i),
+    "imq_memcpy_d2d": ([_p, _p, _p, _sz, _p], _i),
     "imq_dequantize": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "imq_qmm_t": (_QMM, _i),
     "imq_qmm_t_noalloc": (_QMM, _i),
@@ -122,6 +123,13 @@ SIGNATURES = {
     "imq_dit_step_set_head": ([_p, ctypes.POINTER(QWeight), ctypes.POINTER(QWeight)], _i),
     "imq_dit_step_denoise": ([_p, _p, _p, _p, ctypes.c_float, _i, _p], _i),
     "imq_dit_step_launches": ([_p], _i),
+    "imq_dit_double_attn_in": ([_p, _i, _p, _p, _p, _p, _p, _p], _i),
+    "imq_dit_double_attn_out": ([_p, _i, _p, _p, _p], _i),
+    "imq_dit_double_mlp": ([_p, _i, _p, _p, _p], _i),
+    "imq_dit_single_attn_in": ([_p, _i, _p, _p, _p, _p, _p], _i),
+    "imq_dit_single_attn_out": ([_p, _i, _p, _p, _p], _i),
+    "imq_dit_head_embed": ([_p, _p, _p, _p], _i),
+    "imq_dit_head_out": ([_p, _p, _p, _p, _p, ctypes.c_float, _p], _i),
     "imq_te_create": ([_p, _p, _i, _i, ctypes.c_float, _p], _i),
     "imq_te_attn_in": ([_p, _i, _p, _p, _i, _p], _i),
     "imq_te_attn_out_mlp": ([_p, _i, _p, _p, _p, _i, _p], _i),

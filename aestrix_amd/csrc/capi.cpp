@@ -436,6 +436,10 @@ int imq_memcpy_d2h(imq_ctx* ctx, void* dst, const void* src, size_t bytes, imq_s
   return copy(ctx, "imq_memcpy_d2h", dst, src, bytes, hipMemcpyDeviceToHost, stream);
 }
 
+int imq_memcpy_d2d(imq_ctx* ctx, void* dst, const void* src, size_t bytes, imq_stream stream) {
+  return copy(ctx, "imq_memcpy_d2d", dst, src, bytes, hipMemcpyDeviceToDevice, stream);
+}
+
 int imq_dequantize_rows(imq_ctx* ctx, const uint32_t* w, const void* scales, const void* biases,
                         const int32_t* rows, int count, void* out, int k, int n, int group_size,
                         int bits, imq_dtype dtype, imq_stream stream) {

@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <initializer_list>
 #include <new>
 #include <vector>
 
@@ -75,130 +76,221 @@ constexpr float kEps = 1e-5f;  // DirectDiTStep.swift:416
 
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
-// Launch every kernel of the blocks on stream s (st->launches counts them).
-hipError_t encode(imq_dit_step* st, hipStream_t s) {
-  const imq_dit_dims& d = st->d;
-  const int J = d.l_txt + d.l_img;
-  const int dim = d.dim, ffi = d.ff_inner;
-  const int T = (int)st->dtype;
-  const size_t es = 2;
+// The block halves share this launch bookkeeping: every kernel launched
+// counts in st->launches, the first failing call's error is kept, and the
+// text rows' chain (on st->side) forks from and joins back into stream s.
+struct Enc {
+  imq_dit_step* st;
+  hipStream_t s;
   hipError_t e = hipSuccess;
-  auto ok = [&](hipError_t r) {
+  void ok(hipError_t r) {
     ++st->launches;
     if (e == hipSuccess) e = r;
-  };
-  auto sync = [&](hipError_t r) {
+  }
+  void sync(hipError_t r) {
     if (e == hipSuccess) e = r;
-  };
-  // The text rows' chain (on st->side) depends on the main stream up to here.
-  auto fork = [&]() {
+  }
+  void fork() {
     sync(hipEventRecord(st->ev_fork, s));
     sync(hipStreamWaitEvent(st->side, st->ev_fork, 0));
-  };
-  auto join = [&]() {
+  }
+  void join() {
     sync(hipEventRecord(st->ev_join, st->side));
     sync(hipStreamWaitEvent(s, st->ev_join, 0));
-  };
-  auto rows = [&](char* base, int row0, int width) { return base + (size_t)row0 * width * es; };
-  hipStream_t t = st->side;
+  }
   // The image and text chains each plan their tiles for their share of the
   // CUs, so that both fit side by side in one tile round: at 4096 + 512 rows
   // and dim 3072, 192 + 24 tiles of 256 rows on 256 CUs instead of the 228
   // tiles of 224 rows the image rows take alone.  The SwiGLU projections keep
   // the whole device (1152 tiles, 4.5 rounds): the text rows fill the last.
-  imq::SplitWs wi = st->split, wt = st->split_txt;
-  wi.cus = st->cus_img;
-  wt.cus = st->cus_txt;
-  float* Xt = st->X;
-  float* Xi = st->X + (size_t)d.l_txt * dim;
-  for (int b = 0; b < d.n_double; ++b) {
-    const imq_qweight* W = &st->w[(size_t)12 * b];
-    const float* g = st->gates + (size_t)4 * b * dim;
-    ok(imq::launch_rmsnorm(st->X, st->norm_w, st->nX, J, dim, kEps, T, s));
-    char* nXt = rows(st->nX, 0, dim);
-    char* nXi = rows(st->nX, d.l_txt, dim);
-    char* outs[3] = {st->Q, st->K, st->V};
-    // Image rows (4096 at 1024^2) on s and text rows (512) on t at the same
-    // time: an image-row projection leaves CUs idle in its last tile round
-    // and a text-row one never fills the GPU.  The two chains touch disjoint
-    // rows of every buffer and have their own split-K workspaces.
-    fork();
-    for (int q = 0; q < 3; ++q)
-      ok(imq::launch_qgemm(W[q].w, W[q].scales, W[q].biases, nXi, rows(outs[q], d.l_txt, dim), dim,
-                           dim, d.l_img, T, s, wi));
-    // to_out / to_add_out on the V rows (the attention output's stand-in).
-    ok(imq::launch_qgemm_gate_add(W[6].w, W[6].scales, W[6].biases, rows(st->V, d.l_txt, dim), Xi,
-                                  g, Xi, dim, dim, d.l_img, 1.0f, T, s, wi));
-    for (int q = 0; q < 3; ++q)
-      ok(imq::launch_qgemm(W[3 + q].w, W[3 + q].scales, W[3 + q].biases, nXt, rows(outs[q], 0, dim),
-                           dim, dim, d.l_txt, T, t, wt));
-    ok(imq::launch_qgemm_gate_add(W[7].w, W[7].scales, W[7].biases, rows(st->V, 0, dim), Xt,
-                                  g + dim, Xt, dim, dim, d.l_txt, 1.0f, T, t, wt));
-    join();
-    ok(imq::launch_rmsnorm(st->X, st->norm_w, st->nX, J, dim, kEps, T, s));
-    fork();
-    ok(imq::launch_qgemm_swiglu(W[8].w, W[8].scales, W[8].biases, nXi, rows(st->SW, d.l_txt, ffi),
-                                ffi, dim, 2 * ffi, d.l_img, ffi, 0, ffi, 1.0f, 1.0f, T, s,
-                                st->split));
-    ok(imq::launch_qgemm_gate_add(W[9].w, W[9].scales, W[9].biases, rows(st->SW, d.l_txt, ffi), Xi,
-                                  g + 2 * dim, Xi, ffi, dim, d.l_img, 1.0f, T, s, wi));
-    ok(imq::launch_qgemm_swiglu(W[10].w, W[10].scales, W[10].biases, nXt, rows(st->SW, 0, ffi), ffi,
-                                dim, 2 * ffi, d.l_txt, ffi, 0, ffi, 1.0f, 1.0f, T, t,
-                                st->split_txt));
-    ok(imq::launch_qgemm_gate_add(W[11].w, W[11].scales, W[11].biases, rows(st->SW, 0, ffi), Xt,
-                                  g + 3 * dim, Xt, ffi, dim, d.l_txt, 1.0f, T, t, wt));
-    join();
+  imq::SplitWs wi() const {
+    imq::SplitWs w = st->split;
+    w.cus = st->cus_img;
+    return w;
   }
-  const int cw = dim + ffi;
-  for (int b = 0; b < d.n_single; ++b) {
-    const imq_qweight* W = &st->w[(size_t)12 * d.n_double + 2 * b];
-    const float* g = st->gates + ((size_t)4 * d.n_double + b) * dim;
-    ok(imq::launch_rmsnorm(st->X, st->norm_w, st->nX, J, dim, kEps, T, s));
-    // The Q/K/V rows (side stream) and the SwiGLU rows (main stream) of
-    // to_qkv_mlp_proj read the same input and write different buffers: run
-    // side by side, each one's part-empty last tile round fills with the
-    // other's tiles.
-    fork();
-    ok(imq::launch_qgemm(W[0].w, W[0].scales, W[0].biases, st->nX, st->QKV, dim, 3 * dim, J, T, t,
-                         st->split_txt));
-    ok(imq::launch_qgemm_swiglu(W[0].w, W[0].scales, W[0].biases, st->nX, st->C + (size_t)dim * es,
-                                cw, dim, 3 * dim + 2 * ffi, J, ffi, 3 * dim, 3 * dim + ffi, 1.0f,
-                                1.0f, T, s, st->split));
-    join();
-    ok(imq::launch_qgemm_gate_add(W[1].w, W[1].scales, W[1].biases, st->C, st->X, g, st->X, cw, dim,
-                                  J, 1.0f, T, s, st->split));
+  imq::SplitWs wt() const {
+    imq::SplitWs w = st->split_txt;
+    w.cus = st->cus_txt;
+    return w;
   }
-  return e;
+  static const char* rows(const void* base, int row0, int width) {
+    return static_cast<const char*>(base) + (size_t)row0 * width * 2;
+  }
+  static char* rows(void* base, int row0, int width) {
+    return static_cast<char*>(base) + (size_t)row0 * width * 2;
+  }
+  // The normalized block input: nx when the caller gives one, else the
+  // plan's stand-in for the reference's lnMod, RMSNorm(x) into st->nX.
+  const void* norm(const float* x, const void* nx) {
+    if (nx) return nx;
+    const imq_dit_dims& d = st->d;
+    ok(imq::launch_rmsnorm(x, st->norm_w, st->nX, d.l_txt + d.l_img, d.dim, kEps, (int)st->dtype,
+                           s));
+    return st->nX;
+  }
+};
+
+// Double block b before attention (encodeDouble's projections up to the
+// attention, DirectDiTStep.swift:549-563): q, k, v of the text rows (add_q,
+// add_k, add_v) and of the image rows (to_q, to_k, to_v) from the normalized
+// input.  Image rows (4096 at 1024^2) on s and text rows (512) on the side
+// stream at the same time: an image-row projection leaves CUs idle in its
+// last tile round and a text-row one never fills the GPU.  The two chains
+// touch disjoint rows of every buffer and have their own split-K workspaces.
+void double_attn_in(Enc& c, int b, const float* x, const void* nx, void* q, void* k, void* v) {
+  imq_dit_step* st = c.st;
+  const imq_dit_dims& d = st->d;
+  const int dim = d.dim, T = (int)st->dtype;
+  const imq_qweight* W = &st->w[(size_t)12 * b];
+  const void* n = c.norm(x, nx);
+  void* outs[3] = {q, k, v};
+  c.fork();
+  for (int i = 0; i < 3; ++i)
+    c.ok(imq::launch_qgemm(W[i].w, W[i].scales, W[i].biases, Enc::rows(n, d.l_txt, dim),
+                           Enc::rows(outs[i], d.l_txt, dim), dim, dim, d.l_img, T, c.s, c.wi()));
+  for (int i = 0; i < 3; ++i)
+    c.ok(imq::launch_qgemm(W[3 + i].w, W[3 + i].scales, W[3 + i].biases, n, outs[i], dim, dim,
+                           d.l_txt, T, st->side, c.wt()));
+  c.join();
 }
 
-// One denoise step (encodeDenoiseStep, DirectDiTStep.swift:908-971) on stream
-// s, the inputs already in the plan's buffers: lat16 = T(lat_in / 16), the
-// image rows of X = float(T(lat16 . x_embedder^T)) * 16 (cast ÷16, qmm,
-// cast ×16: :917-941), the blocks, then the head: nH = T(RMSNorm(image rows) /
-// 16) (the stand-in for lnMod "out", whose AdaLN modulation is outside the
-// quantized-linear path), and lat_out = lat_in + float(T(nH . proj_out^T)) *
-// 16 dt (proj_out and the Euler gate-add with gate ones, :947-965), the scale
-// read from st->euler when the kernel runs.
-hipError_t encode_denoise(imq_dit_step* st, hipStream_t s) {
+// Double block b after attention (:568-571): the image rows' to_out and the
+// text rows' to_add_out on the attention output, each with its gated
+// residual add into x.
+void double_attn_out(Enc& c, int b, const void* attn, float* x) {
+  imq_dit_step* st = c.st;
   const imq_dit_dims& d = st->d;
-  const int T = (int)st->dtype;
-  const int C = st->lat_ch;
-  float* Xi = st->X + (size_t)d.l_txt * d.dim;
-  hipError_t e = hipSuccess;
-  auto ok = [&](hipError_t r) {
-    ++st->launches;
-    if (e == hipSuccess) e = r;
-  };
-  ok(imq::launch_prescale(st->lat_in, st->lat16, (size_t)d.l_img * C, 16.0f, T, s));
-  ok(imq::launch_qgemm_postscale(st->x_emb.w, st->x_emb.scales, st->x_emb.biases, st->lat16, Xi,
-                                 C, d.dim, d.l_img, 16.0f, T, s));
-  const hipError_t eb = encode(st, s);
-  if (e == hipSuccess) e = eb;
-  ok(imq::launch_rmsnorm(Xi, st->norm_w, st->nH, d.l_img, d.dim, kEps, T, s, 1.0f / 16.0f));
-  ok(imq::launch_qgemm_gate_add(st->proj_out.w, st->proj_out.scales, st->proj_out.biases, st->nH,
-                                st->lat_in, st->ones, st->lat_out, d.dim, C, d.l_img, 0.0f, T, s,
-                                st->split_head, st->euler));
-  return e;
+  const int dim = d.dim, T = (int)st->dtype;
+  const imq_qweight* W = &st->w[(size_t)12 * b];
+  const float* g = st->gates + (size_t)4 * b * dim;
+  float* Xt = x;
+  float* Xi = x + (size_t)d.l_txt * dim;
+  c.fork();
+  c.ok(imq::launch_qgemm_gate_add(W[6].w, W[6].scales, W[6].biases, Enc::rows(attn, d.l_txt, dim),
+                                  Xi, g, Xi, dim, dim, d.l_img, 1.0f, T, c.s, c.wi()));
+  c.ok(imq::launch_qgemm_gate_add(W[7].w, W[7].scales, W[7].biases, attn, Xt, g + dim, Xt, dim,
+                                  dim, d.l_txt, 1.0f, T, st->side, c.wt()));
+  c.join();
+}
+
+// Double block b's MLPs (:572-587): SwiGLU(nx . linear_in^T) then
+// linear_out with the gated residual add, image rows (ff) and text rows
+// (ff_context) side by side.
+void double_mlp(Enc& c, int b, const void* nx, float* x) {
+  imq_dit_step* st = c.st;
+  const imq_dit_dims& d = st->d;
+  const int dim = d.dim, ffi = d.ff_inner, T = (int)st->dtype;
+  const imq_qweight* W = &st->w[(size_t)12 * b];
+  const float* g = st->gates + (size_t)4 * b * dim;
+  float* Xt = x;
+  float* Xi = x + (size_t)d.l_txt * dim;
+  const void* n = c.norm(x, nx);
+  c.fork();
+  c.ok(imq::launch_qgemm_swiglu(W[8].w, W[8].scales, W[8].biases, Enc::rows(n, d.l_txt, dim),
+                                Enc::rows(st->SW, d.l_txt, ffi), ffi, dim, 2 * ffi, d.l_img, ffi, 0,
+                                ffi, 1.0f, 1.0f, T, c.s, st->split));
+  c.ok(imq::launch_qgemm_gate_add(W[9].w, W[9].scales, W[9].biases,
+                                  Enc::rows(st->SW, d.l_txt, ffi), Xi, g + 2 * dim, Xi, ffi, dim,
+                                  d.l_img, 1.0f, T, c.s, c.wi()));
+  c.ok(imq::launch_qgemm_swiglu(W[10].w, W[10].scales, W[10].biases, n, st->SW, ffi, dim, 2 * ffi,
+                                d.l_txt, ffi, 0, ffi, 1.0f, 1.0f, T, st->side, st->split_txt));
+  c.ok(imq::launch_qgemm_gate_add(W[11].w, W[11].scales, W[11].biases, st->SW, Xt, g + 3 * dim, Xt,
+                                  ffi, dim, d.l_txt, 1.0f, T, st->side, c.wt()));
+  c.join();
+}
+
+// Single block b before attention (encodeSingle up to the attention,
+// :593-611): the Q/K/V rows of to_qkv_mlp_proj into qkv and its SwiGLU rows
+// into columns [dim, dim + ff_inner) of concat.  Both read the same input and
+// write different buffers, so they run side by side (Q/K/V on the side
+// stream): each one's part-empty last tile round fills with the other's tiles.
+void single_attn_in(Enc& c, int b, const float* x, const void* nx, void* qkv, void* concat) {
+  imq_dit_step* st = c.st;
+  const imq_dit_dims& d = st->d;
+  const int J = d.l_txt + d.l_img, dim = d.dim, ffi = d.ff_inner, T = (int)st->dtype;
+  const int cw = dim + ffi;
+  const imq_qweight* W = &st->w[(size_t)12 * d.n_double + 2 * b];
+  const void* n = c.norm(x, nx);
+  c.fork();
+  c.ok(imq::launch_qgemm(W[0].w, W[0].scales, W[0].biases, n, qkv, dim, 3 * dim, J, T, st->side,
+                         st->split_txt));
+  c.ok(imq::launch_qgemm_swiglu(W[0].w, W[0].scales, W[0].biases, n,
+                                static_cast<char*>(concat) + (size_t)dim * 2, cw, dim,
+                                3 * dim + 2 * ffi, J, ffi, 3 * dim, 3 * dim + ffi, 1.0f, 1.0f, T,
+                                c.s, st->split));
+  c.join();
+}
+
+// Single block b after attention (:616-617): to_out over [attention | MLP]
+// with the gated residual add into x.
+void single_attn_out(Enc& c, int b, const void* concat, float* x) {
+  imq_dit_step* st = c.st;
+  const imq_dit_dims& d = st->d;
+  const int J = d.l_txt + d.l_img, dim = d.dim, ffi = d.ff_inner, T = (int)st->dtype;
+  const imq_qweight* W = &st->w[(size_t)12 * d.n_double + 2 * b];
+  const float* g = st->gates + ((size_t)4 * d.n_double + b) * dim;
+  c.ok(imq::launch_qgemm_gate_add(W[1].w, W[1].scales, W[1].biases, concat, x, g, x, dim + ffi,
+                                  dim, J, 1.0f, T, c.s, st->split));
+}
+
+// Launch every kernel of the blocks on stream s over the plan's residual X,
+// with the plan's stand-ins around the projections: RMSNorm for lnMod and,
+// for attention, the V projection in double blocks and the attention half of
+// C as it was created (zeros) in single blocks.
+hipError_t encode(imq_dit_step* st, hipStream_t s) {
+  Enc c{st, s};
+  for (int b = 0; b < st->d.n_double; ++b) {
+    double_attn_in(c, b, st->X, nullptr, st->Q, st->K, st->V);
+    double_attn_out(c, b, st->V, st->X);
+    double_mlp(c, b, nullptr, st->X);
+  }
+  for (int b = 0; b < st->d.n_single; ++b) {
+    single_attn_in(c, b, st->X, nullptr, st->QKV, st->C);
+    single_attn_out(c, b, st->C, st->X);
+  }
+  return c.e;
+}
+
+// The head's input half (encodeDenoiseStep, DirectDiTStep.swift:917-941):
+// lat16 = T(lat / 16), then the image rows of x = float(T(lat16 .
+// x_embedder^T)) * 16 (cast ÷16, qmm, cast ×16).
+void head_embed(Enc& c, const float* lat, float* x) {
+  imq_dit_step* st = c.st;
+  const imq_dit_dims& d = st->d;
+  const int T = (int)st->dtype, C = st->lat_ch;
+  c.ok(imq::launch_prescale(lat, st->lat16, (size_t)d.l_img * C, 16.0f, T, c.s));
+  c.ok(imq::launch_qgemm_postscale(st->x_emb.w, st->x_emb.scales, st->x_emb.biases, st->lat16,
+                                   x + (size_t)d.l_txt * d.dim, C, d.dim, d.l_img, 16.0f, T, c.s));
+}
+
+// The head's output half (:947-965): proj_out on nh (the caller's norm_out
+// output / 16; without one, the stand-in T(RMSNorm(image rows of x) / 16),
+// the AdaLN modulation being outside the quantized-linear path) and the
+// Euler gate-add lat_out = lat_in + float(T(nh . proj_out^T)) * 16 dt, the
+// factor read from st->euler when the kernel runs.
+void head_out(Enc& c, const float* x, const void* nh, const float* lat_in, float* lat_out) {
+  imq_dit_step* st = c.st;
+  const imq_dit_dims& d = st->d;
+  const int T = (int)st->dtype, C = st->lat_ch;
+  if (!nh) {
+    c.ok(imq::launch_rmsnorm(x + (size_t)d.l_txt * d.dim, st->norm_w, st->nH, d.l_img, d.dim, kEps,
+                             T, c.s, 1.0f / 16.0f));
+    nh = st->nH;
+  }
+  c.ok(imq::launch_qgemm_gate_add(st->proj_out.w, st->proj_out.scales, st->proj_out.biases, nh,
+                                  lat_in, st->ones, lat_out, d.dim, C, d.l_img, 0.0f, T, c.s,
+                                  st->split_head, st->euler));
+}
+
+// One denoise step (encodeDenoiseStep, :908-971) on stream s, the inputs
+// already in the plan's buffers: the head's input half, the blocks, the
+// head's output half.
+hipError_t encode_denoise(imq_dit_step* st, hipStream_t s) {
+  Enc c{st, s};
+  head_embed(c, st->lat_in, st->X);
+  c.sync(encode(st, s));
+  head_out(c, st->X, nullptr, st->lat_in, st->lat_out);
+  return c.e;
 }
 
 void release_head(imq_dit_step* st) {
@@ -529,6 +621,120 @@ int imq_dit_step_denoise(imq_dit_step* st, const float* lat_in, const float* e_i
   }
   if (e == hipSuccess) e = hipMemcpyAsync(lat_out, st->lat_out, lat_bytes, hipMemcpyDefault, s);
   return e == hipSuccess ? IMQ_OK : hip_fail(st->ctx, e, fn);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Shared checks of the block-half entry points: a plan, a block of the kind
+// in range, every buffer given and 16-byte aligned (nullable ones may be
+// null), then the plan's device current.
+int check_half(imq_dit_step* st, const char* fn, int block, int count, const char* kind,
+               std::initializer_list<const void*> need, std::initializer_list<const void*> opt) {
+  if (!st) return fail(nullptr, IMQ_EINVAL, "%s: null step", fn);
+  if (block < 0 || block >= count)
+    return fail(st->ctx, IMQ_EINVAL, "%s: %s block %d out of range [0, %d)", fn, kind, block,
+                count);
+  for (const void* p : need)
+    if (!p) return fail(st->ctx, IMQ_EINVAL, "%s: null buffer", fn);
+  for (const void* p : need)
+    if (!aligned(p, 16)) return fail(st->ctx, IMQ_EINVAL, "%s: buffers must be 16-byte aligned", fn);
+  for (const void* p : opt)
+    if (p && !aligned(p, 16))
+      return fail(st->ctx, IMQ_EINVAL, "%s: buffers must be 16-byte aligned", fn);
+  return bind_device(st->ctx);
+}
+
+int finish(imq_dit_step* st, const Enc& c, const char* fn) {
+  return c.e == hipSuccess ? IMQ_OK : hip_fail(st->ctx, c.e, fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int imq_dit_double_attn_in(imq_dit_step* st, int block, const float* x, const void* nx, void* q,
+                           void* k, void* v, imq_stream stream) {
+  const char* fn = "imq_dit_double_attn_in";
+  int rc = check_half(st, fn, block, st ? st->d.n_double : 0, "double", {q, k, v}, {x, nx});
+  if (rc != IMQ_OK) return rc;
+  if (!x && !nx) return fail(st->ctx, IMQ_EINVAL, "%s: neither x nor nx given", fn);
+  Enc c{st, static_cast<hipStream_t>(stream)};
+  st->launches = 0;
+  double_attn_in(c, block, x, nx, q, k, v);
+  return finish(st, c, fn);
+}
+
+int imq_dit_double_attn_out(imq_dit_step* st, int block, const void* attn, float* x,
+                            imq_stream stream) {
+  const char* fn = "imq_dit_double_attn_out";
+  int rc = check_half(st, fn, block, st ? st->d.n_double : 0, "double", {attn, x}, {});
+  if (rc != IMQ_OK) return rc;
+  Enc c{st, static_cast<hipStream_t>(stream)};
+  st->launches = 0;
+  double_attn_out(c, block, attn, x);
+  return finish(st, c, fn);
+}
+
+int imq_dit_double_mlp(imq_dit_step* st, int block, const void* nx, float* x, imq_stream stream) {
+  const char* fn = "imq_dit_double_mlp";
+  int rc = check_half(st, fn, block, st ? st->d.n_double : 0, "double", {x}, {nx});
+  if (rc != IMQ_OK) return rc;
+  Enc c{st, static_cast<hipStream_t>(stream)};
+  st->launches = 0;
+  double_mlp(c, block, nx, x);
+  return finish(st, c, fn);
+}
+
+int imq_dit_single_attn_in(imq_dit_step* st, int block, const float* x, const void* nx, void* qkv,
+                           void* concat, imq_stream stream) {
+  const char* fn = "imq_dit_single_attn_in";
+  int rc = check_half(st, fn, block, st ? st->d.n_single : 0, "single", {qkv, concat}, {x, nx});
+  if (rc != IMQ_OK) return rc;
+  if (!x && !nx) return fail(st->ctx, IMQ_EINVAL, "%s: neither x nor nx given", fn);
+  Enc c{st, static_cast<hipStream_t>(stream)};
+  st->launches = 0;
+  single_attn_in(c, block, x, nx, qkv, concat);
+  return finish(st, c, fn);
+}
+
+int imq_dit_single_attn_out(imq_dit_step* st, int block, const void* concat, float* x,
+                            imq_stream stream) {
+  const char* fn = "imq_dit_single_attn_out";
+  int rc = check_half(st, fn, block, st ? st->d.n_single : 0, "single", {concat, x}, {});
+  if (rc != IMQ_OK) return rc;
+  Enc c{st, static_cast<hipStream_t>(stream)};
+  st->launches = 0;
+  single_attn_out(c, block, concat, x);
+  return finish(st, c, fn);
+}
+
+int imq_dit_head_embed(imq_dit_step* st, const float* lat, float* x, imq_stream stream) {
+  const char* fn = "imq_dit_head_embed";
+  if (!st) return fail(nullptr, IMQ_EINVAL, "%s: null step", fn);
+  if (!st->has_head) return fail(st->ctx, IMQ_EINVAL, "%s: no head set (imq_dit_step_set_head)", fn);
+  int rc = check_half(st, fn, 0, 1, "head", {lat, x}, {});
+  if (rc != IMQ_OK) return rc;
+  Enc c{st, static_cast<hipStream_t>(stream)};
+  st->launches = 0;
+  head_embed(c, lat, x);
+  return finish(st, c, fn);
+}
+
+int imq_dit_head_out(imq_dit_step* st, const float* x, const void* nh, const float* lat_in,
+                     float* lat_out, float dt, imq_stream stream) {
+  const char* fn = "imq_dit_head_out";
+  if (!st) return fail(nullptr, IMQ_EINVAL, "%s: null step", fn);
+  if (!st->has_head) return fail(st->ctx, IMQ_EINVAL, "%s: no head set (imq_dit_step_set_head)", fn);
+  int rc = check_half(st, fn, 0, 1, "head", {lat_in, lat_out}, {x, nh});
+  if (rc != IMQ_OK) return rc;
+  if (!x && !nh) return fail(st->ctx, IMQ_EINVAL, "%s: neither x nor nh given", fn);
+  Enc c{st, static_cast<hipStream_t>(stream)};
+  st->launches = 0;
+  c.sync(imq::launch_fill_f32(st->euler, 16.0f * dt, 1, c.s));
+  head_out(c, x, nh, lat_in, lat_out);
+  return finish(st, c, fn);
 }
 
 int imq_dit_step_launches(const imq_dit_step* st) { return st ? st->launches : 0; }

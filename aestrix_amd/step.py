@@ -203,6 +203,88 @@ class DitStep:
                 ctypes.c_void_p(st)), self._ctx)
         return out
 
+    # ---- block halves around the caller's attention (imq_dit_double_attn_in ...)
+
+    def _call(self, name: str, *args) -> None:
+        st = torch.cuda.current_stream(self.device).cuda_stream
+        ptrs = [a if isinstance(a, (int, float)) else
+                ctypes.c_void_p(a.data_ptr() if a is not None else 0) for a in args]
+        with torch.cuda.device(self.device):
+            _lib.check(getattr(self._L, name)(self._h, *ptrs, ctypes.c_void_p(st)), self._ctx)
+
+    def _joint(self, t: torch.Tensor | None, width: int, dtype: torch.dtype, what: str) -> None:
+        if t is None:
+            return
+        assert t.is_cuda and t.is_contiguous(), f"{what} must be a contiguous device tensor"
+        assert t.dtype == dtype, f"{what} must be {dtype}"
+        assert tuple(t.shape) == (self.dims.joint, width), f"{what} must be [J, {width}]"
+
+    def double_attn_in(self, block: int, x: torch.Tensor | None, q: torch.Tensor, k: torch.Tensor,
+                       v: torch.Tensor, nx: torch.Tensor | None = None) -> None:
+        """Double block ``block`` before attention: q, k, v [J, dim] (T, text rows
+        first) from nx (T [J, dim]) or, with nx None, the stand-in RMSNorm(x)."""
+        d = self.dims
+        self._joint(x, d.dim, torch.float32, "x")
+        self._joint(nx, d.dim, self.dtype, "nx")
+        for t, n in ((q, "q"), (k, "k"), (v, "v")):
+            self._joint(t, d.dim, self.dtype, n)
+        self._call("imq_dit_double_attn_in", int(block), x, nx, q, k, v)
+
+    def double_attn_out(self, block: int, attn: torch.Tensor, x: torch.Tensor) -> None:
+        """Double block ``block`` after attention: x += gated to_out / to_add_out of attn."""
+        self._joint(attn, self.dims.dim, self.dtype, "attn")
+        self._joint(x, self.dims.dim, torch.float32, "x")
+        self._call("imq_dit_double_attn_out", int(block), attn, x)
+
+    def double_mlp(self, block: int, x: torch.Tensor, nx: torch.Tensor | None = None) -> None:
+        """Double block ``block``'s two MLPs with their gated residual adds into x."""
+        self._joint(x, self.dims.dim, torch.float32, "x")
+        self._joint(nx, self.dims.dim, self.dtype, "nx")
+        self._call("imq_dit_double_mlp", int(block), nx, x)
+
+    def single_attn_in(self, block: int, x: torch.Tensor | None, qkv: torch.Tensor,
+                       concat: torch.Tensor, nx: torch.Tensor | None = None) -> None:
+        """Single block ``block`` before attention: qkv [J, 3 dim] and the MLP half
+        (columns [dim, dim + ff_inner)) of concat [J, dim + ff_inner]."""
+        d = self.dims
+        self._joint(x, d.dim, torch.float32, "x")
+        self._joint(nx, d.dim, self.dtype, "nx")
+        self._joint(qkv, 3 * d.dim, self.dtype, "qkv")
+        self._joint(concat, d.dim + d.ff_inner, self.dtype, "concat")
+        self._call("imq_dit_single_attn_in", int(block), x, nx, qkv, concat)
+
+    def single_attn_out(self, block: int, concat: torch.Tensor, x: torch.Tensor) -> None:
+        """Single block ``block`` after attention (concat[:, :dim] holds it): x +=
+        gated to_out of concat."""
+        d = self.dims
+        self._joint(concat, d.dim + d.ff_inner, self.dtype, "concat")
+        self._joint(x, d.dim, torch.float32, "x")
+        self._call("imq_dit_single_attn_out", int(block), concat, x)
+
+    def head_embed(self, lat: torch.Tensor, x: torch.Tensor) -> None:
+        """The image rows of x = float(T(T(lat / 16) . x_embedder^T)) * 16."""
+        assert lat.dtype == torch.float32 and lat.is_contiguous() and lat.shape[0] == self.dims.l_img
+        self._joint(x, self.dims.dim, torch.float32, "x")
+        self._call("imq_dit_head_embed", lat, x)
+
+    def head_out(self, x: torch.Tensor | None, lat_in: torch.Tensor, dt: float,
+                 lat_out: torch.Tensor, nh: torch.Tensor | None = None) -> None:
+        """lat_out = lat_in + float(T(nh . proj_out^T)) * 16 dt, nh the caller's
+        norm_out output / 16 or, with nh None, the stand-in T(RMSNorm(x image rows) / 16)."""
+        self._joint(x, self.dims.dim, torch.float32, "x")
+        if nh is not None:
+            assert nh.dtype == self.dtype and nh.is_contiguous()
+            assert tuple(nh.shape) == (self.dims.l_img, self.dims.dim)
+        assert lat_in.is_contiguous() and lat_out.is_contiguous()
+        assert lat_in.dtype == lat_out.dtype == torch.float32 and lat_in.shape == lat_out.shape
+        st = torch.cuda.current_stream(self.device).cuda_stream
+        with torch.cuda.device(self.device):
+            _lib.check(self._L.imq_dit_head_out(
+                self._h, ctypes.c_void_p(x.data_ptr() if x is not None else 0),
+                ctypes.c_void_p(nh.data_ptr() if nh is not None else 0),
+                ctypes.c_void_p(lat_in.data_ptr()), ctypes.c_void_p(lat_out.data_ptr()),
+                float(dt), ctypes.c_void_p(st)), self._ctx)
+
     @property
     def launches(self) -> int:
         return self._L.imq_dit_step_launches(self._h)

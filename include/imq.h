@@ -94,6 +94,8 @@ int imq_malloc(imq_ctx* ctx, size_t bytes, void** out);
 int imq_free(imq_ctx* ctx, void* ptr);
 int imq_memcpy_h2d(imq_ctx* ctx, void* dst, const void* src, size_t bytes, imq_stream stream);
 int imq_memcpy_d2h(imq_ctx* ctx, void* dst, const void* src, size_t bytes, imq_stream stream);
+/* Device to device (the reference's blit copies, DirectDiTStep.swift:639-648,667-670). */
+int imq_memcpy_d2d(imq_ctx* ctx, void* dst, const void* src, size_t bytes, imq_stream stream);
 
 /* ---- kernels ------------------------------------------------------------ */
 

@@ -12,10 +12,17 @@
  * RMSNorm of the fp32 residual stream before each block's projections.
  *
  * Not in the graph (outside the quantized-linear path): attention, RoPE, the
- * per-head Q/K norms and the LayerNorm modulation.  Where the reference feeds
- * the attention output into to_out / to_add_out, the step feeds the V
- * projection of the same rows; in single blocks the attention half of the
- * concat buffer keeps the values it was created with (zeros).
+ * per-head Q/K norms and the LayerNorm modulation.  imq_dit_step_run and
+ * imq_dit_step_denoise run stand-ins for them: RMSNorm with the plan's norm
+ * weight for every lnMod; where the reference feeds the attention output
+ * into to_out / to_add_out, the V projection of the same rows; in single
+ * blocks the attention half of the concat buffer keeps the values it was
+ * created with (zeros).  Their output is therefore NOT the model's: they
+ * time and check the quantized-linear work of a step at its real shapes.
+ * A caller that runs the real model drives the block halves further down
+ * (imq_dit_double_attn_in ... imq_dit_head_out) with its own attention core
+ * and LayerNorm modulation between them; run and denoise are exactly those
+ * halves with the stand-ins (same kernels, same bits).
  *
  * Data flow per double block (img rows = the l_img rows after the l_txt text
  * rows of the joint residual X, fp32 [l_txt + l_img, dim]):
@@ -102,7 +109,61 @@ int imq_dit_step_set_head(imq_dit_step* step, const imq_qweight* x_embedder,
 int imq_dit_step_denoise(imq_dit_step* step, const float* lat_in, const float* e_in,
                          float* lat_out, float dt, int use_graph, imq_stream stream);
 
-/* Kernel launches of the last pass encoded (eager run or graph capture). */
+/* ---- block halves around the caller's attention ---------------------------
+ * encodeDouble / encodeSingle (DirectDiTStep.swift:546-618) and the head of
+ * encodeDenoiseStep (:908-971) split where the reference runs work that is
+ * not quantized-linear (lnMod, per-head RMSNorm, RoPE, attention): a caller
+ * runs those itself between the calls below, in this order per step:
+ *
+ *   imq_dit_head_embed(lat) -> image rows of x
+ *   per double block b: [lnMod "img.msa" / "txt.msa" -> nx]
+ *                       imq_dit_double_attn_in(b, x, nx) -> q, k, v
+ *                       [per-head norms, RoPE, attention -> attn]
+ *                       imq_dit_double_attn_out(b, attn, x)
+ *                       [lnMod "img.mlp" / "txt.mlp" -> nx]
+ *                       imq_dit_double_mlp(b, nx, x)
+ *   per single block b: [lnMod "single" -> nx]
+ *                       imq_dit_single_attn_in(b, x, nx) -> qkv, concat[:, dim:]
+ *                       [per-head norms, RoPE, attention -> concat[:, :dim]]
+ *                       imq_dit_single_attn_out(b, concat, x)
+ *   [lnMod "out" -> nh = T(norm_out(x image rows) / 16)]
+ *   imq_dit_head_out(x, nh, lat_in, dt) -> lat_out
+ *
+ * Buffers are the caller's, device memory, 16-byte aligned, rows = tokens
+ * with the l_txt text rows first (J = l_txt + l_img rows in all):
+ *   x       fp32 [J, dim], the residual stream, updated in place;
+ *   nx      T [J, dim], the normalized block input; NULL runs the plan's
+ *           stand-in, nx = T(RMSNorm(x) * norm weight) (then x is read);
+ *   q, k, v T [J, dim] (text rows from add_q / add_k / add_v, image rows
+ *           from to_q / to_k / to_v);
+ *   attn    T [J, dim], the double block's attention output;
+ *   qkv     T [J, 3 dim], the single block's Q | K | V columns;
+ *   concat  T [J, dim + ff_inner], the single block's to_out input:
+ *           columns [0, dim) the attention output (the caller's, written
+ *           between the two single-block calls), [dim, dim + ff_inner) the
+ *           SwiGLU of the MLP rows (written by imq_dit_single_attn_in);
+ *   lat     fp32 [l_img, C] latents; nh T [l_img, dim] (NULL: the stand-in
+ *           T(RMSNorm(x image rows) / 16)).
+ * Gates are the plan's (imq_dit_step_set_conditioning).  Calls share the
+ * plan's scratch (the MLP's SwiGLU buffer, the stand-in norm output, the
+ * split-K workspaces): on one plan, one call at a time, on one stream.
+ * Asynchronous on stream; they may be captured into a graph. */
+int imq_dit_double_attn_in(imq_dit_step* step, int block, const float* x, const void* nx, void* q,
+                           void* k, void* v, imq_stream stream);
+int imq_dit_double_attn_out(imq_dit_step* step, int block, const void* attn, float* x,
+                            imq_stream stream);
+int imq_dit_double_mlp(imq_dit_step* step, int block, const void* nx, float* x, imq_stream stream);
+int imq_dit_single_attn_in(imq_dit_step* step, int block, const float* x, const void* nx, void* qkv,
+                           void* concat, imq_stream stream);
+int imq_dit_single_attn_out(imq_dit_step* step, int block, const void* concat, float* x,
+                            imq_stream stream);
+/* Need imq_dit_step_set_head. */
+int imq_dit_head_embed(imq_dit_step* step, const float* lat, float* x, imq_stream stream);
+int imq_dit_head_out(imq_dit_step* step, const float* x, const void* nh, const float* lat_in,
+                     float* lat_out, float dt, imq_stream stream);
+
+/* Kernel launches of the last pass encoded (eager run, graph capture, or the
+ * last block-half call). */
 int imq_dit_step_launches(const imq_dit_step* step);
 
 int imq_dit_step_destroy(imq_dit_step* step);

@@ -12,14 +12,20 @@ import ImarelloRuntime
 /// `DirectDiTPackedDenoiser` (Sources/ImarelloDirect/DirectDiTAdapter.swift:14-81) on the
 /// MI355X engine: the pipeline's noise and prompt embeds in, the final packed
 /// latents out, behind `PackedLatentDenoising.denoise`
-/// (Sources/ImarelloRuntime/ImarelloPipeline.swift:22-28).  Everything is built inside
-/// the call and freed on return (staged residency, as the reference's adapter).
+/// (Sources/ImarelloRuntime/ImarelloPipeline.swift:22-28).  Every quantized
+/// projection of a step runs on the engine's block halves; the step's other
+/// work (LayerNorm modulation, per-head norms, RoPE, attention) is the
+/// caller's `DiTBlockCore`, without which no denoiser can be made.  Everything
+/// else is built inside the call and freed on return (staged residency, as the
+/// reference's adapter).
 public final class HIPPackedDenoiser: PackedLatentDenoising {
     let transformerDirectory: URL
     let device: Int32
+    let core: DiTBlockCore
 
-    public init(transformerDirectory: URL, device: Int32 = 0) {
+    public init(transformerDirectory: URL, core: DiTBlockCore, device: Int32 = 0) {
         self.transformerDirectory = transformerDirectory
+        self.core = core
         self.device = device
     }
 
@@ -67,7 +73,9 @@ public final class HIPPackedDenoiser: PackedLatentDenoising {
         for step in 0 ..< steps {
             try onStep?(step)
             try engine.setStepConditioning(conditioning[step])
-            try engine.encodeDenoiseStep(latIn: cur, latOut: alt, e0: e0Buf, head: head, dt: dts[step])
+            try core.setStepConditioning(conditioning[step])
+            try engine.encodeDenoiseStep(latIn: cur, latOut: alt, e0: e0Buf, head: head, dt: dts[step],
+                                         core: core)
             swap(&cur, &alt)
         }
         let lat = try cur.download(Float.self, count: lImg * DirectDiTStepHIP.channels)

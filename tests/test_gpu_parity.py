@@ -608,7 +608,8 @@ def test_plain_c_caller_on_the_device():
 
 
 def test_pure_c_abi_memory_stream_and_kernel():
-    """Everything through the C ABI: imq_malloc / memcpy / stream / dequant / qmm."""
+    """Everything through the C ABI: imq_malloc / memcpy (h2d, d2d, d2h) / stream /
+    dequant / qmm."""
     note("pure C-ABI round trip")
     L = _lib.load()
     ctx = ops.context()
@@ -629,7 +630,12 @@ def test_pure_c_abi_memory_stream_and_kernel():
     _lib.check(L.imq_malloc(ctx, 3 * 128 * 2, ctypes.byref(y)), ctx)
     _lib.check(L.imq_dequantize(ctx, bufs["w"], bufs["s"], bufs["b"], deq, 256, 128, 64, 4,
                                 _lib.IMQ_BF16, stream), ctx)
-    _lib.check(L.imq_qmm_t(ctx, bufs["w"], bufs["s"], bufs["b"], bufs["x"], y, 256, 128, 3, 64,
+    # x through a device-to-device copy into a second buffer.
+    x2 = ctypes.c_void_p()
+    _lib.check(L.imq_malloc(ctx, p.x.nbytes, ctypes.byref(x2)), ctx)
+    _lib.check(L.imq_memcpy_d2d(ctx, x2, bufs["x"], p.x.nbytes, stream), ctx)
+    bufs["x2"] = x2
+    _lib.check(L.imq_qmm_t(ctx, bufs["w"], bufs["s"], bufs["b"], bufs["x2"], y, 256, 128, 3, 64,
                            4, _lib.IMQ_BF16, stream), ctx)
     deq_h = np.empty((128, 256), dtype=np.uint16)
     y_h = np.empty((3, 128), dtype=np.uint16)

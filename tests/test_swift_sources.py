@@ -56,6 +56,7 @@ def test_swift_calls_match_the_headers():
             assert n == decls[name], f"{os.path.basename(path)}: {name} with {n} args, header has {decls[name]}"
             seen.add(name)
     for needed in ("imq_qmm_t", "imq_dit_step_denoise", "imq_cond_step_conditioning",
+                   "imq_dit_double_attn_in", "imq_dit_single_attn_out", "imq_dit_head_out",
                    "imq_te_attn_out_mlp", "imq_load_qlinear_cat", "imq_qmm_postscale_ex"):
         assert needed in seen, needed
 
