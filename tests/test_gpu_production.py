@@ -278,6 +278,56 @@ def test_full_size_step_sampled_rows_and_graph_replays(dtype):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_full_size_block_qkv_projections_sampled_rows(dtype):
+    """The projections the stand-in step computes but never feeds on (its
+    attention stand-in uses V only): every double block's to_q / to_k / to_v
+    over the 4096 image rows and add_q / add_k / add_v over the 512 text rows,
+    and every single block's Q/K/V rows of to_qkv_mlp_proj over all 4608 rows,
+    at full size through the block halves on the stand-in norm of one residual,
+    checked on sampled rows against the oracle (MAE, normwise, cosine)."""
+    d = DitDims()
+    note(f"dit q/k/v projections {dtype} full size {d} seed=86")
+    tdt = TDT[dtype]
+    projs = random_projections(d, tdt, seed=86)
+    step = DitStep(d, projs)
+    txt_rows = sample_rows(d.l_txt, 8)
+    img_rows = sample_rows(d.l_img, 16)
+    rows = np.concatenate([txt_rows, d.l_txt + img_rows])
+    try:
+        rng = np.random.default_rng(86)
+        norm_w = (1.0 + 0.1 * rng.standard_normal(d.dim)).astype(np.float32)
+        step.set_conditioning(torch.from_numpy(norm_w).cuda(), None)
+        X = rng.standard_normal((d.joint, d.dim)).astype(np.float32)
+        x = torch.from_numpy(X).cuda()
+        q, k, v = (torch.empty((d.joint, d.dim), dtype=tdt, device="cuda") for _ in range(3))
+        qkv = torch.empty((d.joint, 3 * d.dim), dtype=tdt, device="cuda")
+        concat = torch.empty((d.joint, d.dim + d.ff_inner), dtype=tdt, device="cuda")
+        got = []
+        for b in range(d.n_double):
+            step.double_attn_in(b, x, q, k, v)
+            got.append([host_bits(t)[rows] for t in (q, k, v)])
+        for b in range(d.n_single):
+            step.single_attn_in(b, x, qkv, concat)
+            got.append([host_bits(qkv)[rows]])
+        assert np.array_equal(x.cpu().numpy(), X), "the input halves wrote the residual"
+        hp = [(q_.w.cpu().numpy().view(np.uint32), host_bits(q_.s), host_bits(q_.b)) for q_ in projs]
+    finally:
+        step.close()
+    nX = round_t(ref.rmsnorm_rows(X[rows], norm_w), dtype)
+    nt = len(txt_rows)
+    for b in range(d.n_double):
+        for i, name in enumerate("qkv"):
+            want_i = oracle_qmm(nX[nt:], *hp[12 * b + i], dtype)
+            want_t = oracle_qmm(nX[:nt], *hp[12 * b + 3 + i], dtype)
+            assert_close(t_values(got[b][i][nt:], dtype), want_i, f"double {b} to_{name} image rows")
+            assert_close(t_values(got[b][i][:nt], dtype), want_t, f"double {b} add_{name} text rows")
+    for b in range(d.n_single):
+        w, sb, bb = hp[12 * d.n_double + 2 * b]
+        want = oracle_qmm(nX, w[:3 * d.dim], sb[:3 * d.dim], bb[:3 * d.dim], dtype)
+        assert_close(t_values(got[d.n_double + b][0], dtype), want, f"single {b} Q/K/V rows")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
 def test_full_size_denoise_step_sampled_rows(dtype):
     """encodeDenoiseStep at full size: the x_embedder sandwich (K = 128), the 25
     blocks and the head (norm / 16, proj_out N = 128, Euler gate-add with 16 dt)

@@ -6,10 +6,11 @@ bit-exact dequant), RMSNorm in float64 rounded to T, and the reference's glue
 (oracle/ref.py glue_add_t = dq_add, glue_swiglu at scales 1 = dq_silu_mul).
 imq_qmm_add must equal imq_qgemm + dq_add on the device's own product bit for
 bit (same accumulator, same rounding).  The halves compound roundings
-(RMSNorm, three products, SiLU), so their bar is on each output: normwise
-error <= 1e-2 (mean relative error reported), on 32 sampled rows (every op is
-row-local) at the Qwen3 4B shapes (hidden 2560, q 4096, k / v 1024, inter
-9728)."""
+(RMSNorm, three products, SiLU), yet each output still meets the single
+qmm's bars: normwise error <= 1e-2, MAE <= 1e-3 and cosine >= 0.99999 (the
+layer output measured at MAE <= 7e-5, cosine >= 0.9999999), on 32 sampled
+rows (every op is row-local) at the Qwen3 4B shapes (hidden 2560, q 4096,
+k / v 1024, inter 9728)."""
 
 from __future__ import annotations
 
@@ -26,6 +27,8 @@ from oracle import ref
 pytestmark = pytest.mark.gpu
 
 NORMWISE_TOL = 1e-2
+MAE_TOL = 1e-3
+COSINE_MIN = 0.99999  # the reference's qmm parity bar (DirectQmmSpike.swift:141-153)
 
 
 @pytest.fixture(autouse=True)
@@ -75,10 +78,12 @@ def qmm_t(x_t: np.ndarray, q: Q, tdt, rows=None) -> np.ndarray:
 def check(got: np.ndarray, want: np.ndarray, what: str, tol: float = NORMWISE_TOL) -> None:
     d = np.abs(got.astype(np.float64) - want)
     normwise = d.max() / np.abs(want).max()
+    st = ref.error_stats_values(got.astype(np.float64), np.asarray(want, np.float64))
     note(f"  {what}: normwise={normwise:.3g} mean_rel={d.mean() / np.abs(want).mean():.3g} "
-         f"equal={np.mean(got == want):.4f}")
+         f"mae={st['mae']:.3g} cosine={st['cosine']:.8f} equal={np.mean(got == want):.4f}")
     assert np.all(np.isfinite(got))
     assert normwise <= tol, (what, normwise)
+    assert st["mae"] <= MAE_TOL and st["cosine"] >= COSINE_MIN, (what, st)
 
 
 # --------------------------------------------------------------------- RMSNorm

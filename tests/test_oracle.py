@@ -875,3 +875,57 @@ def test_c_qmm_t_f64_matches_pinned_float64_product(dtype):
                          p.scales if dtype == "bf16" else s16,
                          p.biases if dtype == "bf16" else b16, dtype)
     assert np.max(np.abs(bad - want)) > 1e-3 * np.max(np.abs(want))
+
+
+# ---------------------------------------------------------------- statistics
+def test_error_stats_known_answers():
+    """The parity bars' statistics (MAE, normwise max error, floored relative
+    error, cosine) on planted errors whose values follow by hand."""
+    o = np.array([[1.0, -2.0, 4.0, 0.0]])
+    y = o + np.array([[0.5, 0.0, -1.0, 0.0]])
+    s = ref.error_stats_values(y, o)
+    assert s["mae"] == pytest.approx(1.5 / 4)
+    assert s["max_abs"] == pytest.approx(1.0)
+    assert s["max_rel_normwise"] == pytest.approx(1.0 / 4.0)
+    # floor = max(|o|, 1e-3 rms(o)); the largest d / floor is 0.5 / 1.
+    assert s["max_rel_floored"] == pytest.approx(0.5)
+    # cosine of (1.5, -2, 3, 0) and (1, -2, 4, 0): 17.5 / (sqrt(15.25) sqrt(21)).
+    assert s["cosine"] == pytest.approx(17.5 / (np.sqrt(15.25) * np.sqrt(21.0)), rel=1e-12)
+    assert s["bit_exact_frac"] == pytest.approx(0.5)
+    # Scaling both by the same factor changes neither normwise nor cosine.
+    s2 = ref.error_stats_values(8.0 * y, 8.0 * o)
+    assert s2["max_rel_normwise"] == pytest.approx(s["max_rel_normwise"])
+    assert s2["cosine"] == pytest.approx(s["cosine"], rel=1e-12)
+    assert s2["mae"] == pytest.approx(8.0 * s["mae"])
+    # Identical outputs: no error, cosine 1; a sign flip: cosine -1.
+    z = ref.error_stats_values(o, o)
+    assert z["mae"] == 0 and z["max_rel_normwise"] == 0 and z["cosine"] == pytest.approx(1.0)
+    assert ref.error_stats_values(-o, o)["cosine"] == pytest.approx(-1.0)
+
+
+def test_error_stats_bf16_bits_known_answers():
+    """error_stats on bf16 bit patterns decodes them first: one output off by
+    one bf16 ulp at 1.0 (2^-7) among four."""
+    o_vals = np.array([1.0, 2.0, -0.5, 0.25], np.float32)
+    o = ref.f32_to_bf16(o_vals)
+    y = o.copy()
+    y[0] += 1  # 1.0 -> 1.0078125
+    s = ref.error_stats(y, o)
+    assert s["mae"] == pytest.approx(2.0 ** -7 / 4)
+    assert s["max_rel_normwise"] == pytest.approx(2.0 ** -7 / 2.0)
+    assert s["bit_exact_frac"] == pytest.approx(0.75)
+
+
+def test_error_stats_catch_a_dropped_term():
+    """A plausible kernel mistake -- one quantization group's contribution
+    dropped -- fails every bar the parity tests apply (MAE <= 1e-3, normwise
+    <= 1e-2, cosine >= 0.99999), while the correct product passes them."""
+    p = synth.make_problem(8, 64, 256, seed=5)
+    good = ref.qmm_t(p.x, p.w, p.scales, p.biases)
+    s_ok = ref.error_stats(good, good)
+    assert s_ok["mae"] <= 1e-3 and s_ok["max_rel_normwise"] <= 1e-2 and s_ok["cosine"] >= 0.99999
+    x_bad = p.x.copy()
+    x_bad[:, 64:128] = 0  # bf16 zero bits: the second group never enters the sum
+    bad = ref.qmm_t(x_bad, p.w, p.scales, p.biases)
+    s = ref.error_stats(bad, good)
+    assert s["mae"] > 1e-3 and s["max_rel_normwise"] > 1e-2 and s["cosine"] < 0.99999, s
