@@ -33,6 +33,24 @@ hipError_t launch_qgemv_swiglu(const uint32_t* w, const void* scales, const void
                                int gate_row, int up_row, float in_scale, float out_scale,
                                int dtype, hipStream_t stream);
 
+// The qGEMV on RMSNorm'd x: y = x' . deq(W)^T (launch_qgemv_norm) or the
+// SwiGLU pair of launch_qgemv_swiglu at in / out scale 1
+// (launch_qgemv_swiglu_norm), x' = T(x * rsqrt(mean(x^2) + eps) * nw) row by
+// row, bit for bit what launch_rmsnorm_t writes -- the text encoder's
+// RMSNorm before q/k/v or gate/up folded into the projection's x staging.
+// Only where qgemv_norm_fits (1 <= m <= kQgemvNormMaxM, 16-bit T, k % 8 == 0
+// and k <= 4096, x and nw 16-byte aligned, whole rows in one x tile; width 0
+// for the plain form); otherwise hipErrorInvalidValue.
+constexpr int kQgemvNormMaxM = 2;
+bool qgemv_norm_fits(int k, int n, int m, int width, int dtype, const void* x, const float* nw);
+hipError_t launch_qgemv_norm(const uint32_t* w, const void* scales, const void* biases,
+                             const void* x, const float* nw, float eps, void* y, int k, int n,
+                             int m, int dtype, hipStream_t stream);
+hipError_t launch_qgemv_swiglu_norm(const uint32_t* w, const void* scales, const void* biases,
+                                    const void* x, const float* nw, float eps, void* y, int ldy,
+                                    int k, int n, int m, int width, int gate_row, int up_row,
+                                    int dtype, hipStream_t stream);
+
 // fp32 scratch for split-K partial sums.  With too few output tiles to fill
 // the chip, the MFMA kernel splits K, writes each split's partial sums here
 // and a second kernel adds them; a null or short workspace runs unsplit.

@@ -115,9 +115,81 @@ struct GvPair {
   int gate_row, up_row, width, ldy;
   float in_scale, out_scale;
   const void* resid = nullptr;
+  // Non-null: x is RMSNorm'd in LDS before the products (x tile = whole rows).
+  const float* norm_w = nullptr;
+  float eps = 0.f;
 };
 
 bool is_pair(const GvPair* pr) { return pr && pr->width > 0; }
+
+// RMSNorm of the staged x rows in place: row m becomes T(x * rsqrt(mean(x^2)
+// + eps) * nw) with the arithmetic of the T-input RMSNorm kernel's 16-byte
+// form (rmsnorm_tin_vec_kernel, norm.hip): thread t takes the 8-value pieces
+// t and t + 256 of the row in that order, fma of each value's square, the
+// same xor-shuffle tree in the wave, the four wave sums added in order from
+// zero, __frsqrt_rn, and (x * inv) * w rounded to T per value -- so the
+// products see bit for bit the values the separate RMSNorm launch would
+// write.  The tile must hold whole rows (one K tile) of 16-bit T with at most
+// 512 pieces; the norm weights of the thread's pieces (nwv, loaded beside the
+// x staging) are already in registers.
+template <int T, int MR>
+__device__ __forceinline__ void norm_rows_in_lds(u32x4_t* xs, int M, int K, int vpr,
+                                                 const float4 (&nwv)[2][2], float eps) {
+  using E = Elem<T>;
+  using X = XTile<T>;
+  static_assert(X::kP == 4, "16-bit T: four 16-byte pieces per chunk of 32 values");
+  __shared__ float npart[MR][kWaves];
+  const int tid = threadIdx.x;
+  const int n8 = K >> 3;
+  auto slot = [&](int m, int e) { return m * vpr + (e >> 2) * 4 + ((e & 3) ^ X::swz(e >> 2)); };
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    if (m >= M) break;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + i * kThreads;
+      if (e >= n8) break;
+      const u32x4_t v = xs[slot(m, e)];
+      const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = E::param((uint16_t)(q[j] & 0xFFFFu));
+        const float hi = E::param((uint16_t)(q[j] >> 16));
+        acc = __builtin_fmaf(lo, lo, acc);
+        acc = __builtin_fmaf(hi, hi, acc);
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if ((tid & 63) == 0) npart[m][tid >> 6] = acc;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    if (m >= M) break;
+    float total = 0.f;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) total += npart[m][i];
+    const float inv = __frsqrt_rn(total / (float)K + eps);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + i * kThreads;
+      if (e >= n8) break;
+      const float ww[8] = {nwv[i][0].x, nwv[i][0].y, nwv[i][0].z, nwv[i][0].w,
+                           nwv[i][1].x, nwv[i][1].y, nwv[i][1].z, nwv[i][1].w};
+      u32x4_t& v = xs[slot(m, e)];
+      const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = E::pack2(E::param((uint16_t)(q[j] & 0xFFFFu)) * inv * ww[2 * j],
+                        E::param((uint16_t)(q[j] >> 16)) * inv * ww[2 * j + 1]);
+      v = u32x4_t{o[0], o[1], o[2], o[3]};
+    }
+  }
+  __syncthreads();
+}
 
 template <int T, int MR, int G, int U, int R, bool PAIR>
 __global__ __launch_bounds__(kThreads) void qgemv_kernel(
@@ -182,6 +254,21 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
       const uint32_t off = (uint32_t)((m * K + k0 + j * 32 + pc * X::kEpp) * E::kBytes);
       load_lds16(xr, off, 0u, xs + base + wave * 64);
     }
+    // The norm weights of this thread's pieces (clamped indices: no branch
+    // around the loads), beside the x staging and ahead of the weights.
+    float4 nwv[2][2];
+    if constexpr (T != kF32 && MR <= 2) {
+      if (pr.norm_w) {
+        const float4* nr = reinterpret_cast<const float4*>(pr.norm_w);
+        const int n8 = K >> 3;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int e = min(tid + i * kThreads, n8 - 1);
+          nwv[i][0] = nr[2 * e];
+          nwv[i][1] = nr[2 * e + 1];
+        }
+      }
+    }
     __builtin_amdgcn_sched_barrier(0);
     // 2. weight chunks and their scales/biases, chunk by chunk: loads retire
     //    in issue order, so chunk u's dot products then wait for chunk u's
@@ -204,6 +291,12 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
     IMQ_WAIT_VMCNT(3 * U * R);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (T != kF32 && MR <= 2) {
+      // RMSNorm'd x (the host passes a norm weight only when the tile is the
+      // whole row); its LDS traffic runs while the weights are in flight.
+      if (pr.norm_w) norm_rows_in_lds<T, MR>(xs, M, K, vpr, nwv, pr.eps);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -469,6 +562,44 @@ hipError_t launch_qgemv_resid_add(const uint32_t* w, const void* scales, const v
     case kBf16: return launch_t<kBf16>(w, scales, biases, x, y, k, n, m, &pr, stream);
     case kF16: return launch_t<kF16>(w, scales, biases, x, y, k, n, m, &pr, stream);
     default: return hipErrorInvalidValue;
+  }
+}
+
+bool qgemv_norm_fits(int k, int n, int m, int width, int dtype, const void* x, const float* nw) {
+  if (m < 1 || m > kQgemvNormMaxM || (dtype != kBf16 && dtype != kF16)) return false;
+  // The RMSNorm kernel's 16-byte form, at most two pieces per thread.
+  if (k % 8 != 0 || k / 8 > 2 * kThreads) return false;
+  if (((uintptr_t)x & 15u) != 0 || ((uintptr_t)nw & 15u) != 0) return false;
+  // The x tile must be the whole row.
+  const Plan p = width > 0 ? make_plan(k, 2 * width, m <= 1 ? 1 : 2, 2, 2)
+                           : make_plan(k, n, m <= 1 ? 1 : 2, 2);
+  return p.kt == k;
+}
+
+hipError_t launch_qgemv_norm(const uint32_t* w, const void* scales, const void* biases,
+                             const void* x, const float* nw, float eps, void* y, int k, int n,
+                             int m, int dtype, hipStream_t stream) {
+  if (!qgemv_norm_fits(k, n, m, 0, dtype, x, nw)) return hipErrorInvalidValue;
+  GvPair pr{0, 0, 0, 0, 1.0f, 1.0f};
+  pr.norm_w = nw;
+  pr.eps = eps;
+  switch (dtype) {
+    case kBf16: return launch_t<kBf16>(w, scales, biases, x, y, k, n, m, &pr, stream);
+    default: return launch_t<kF16>(w, scales, biases, x, y, k, n, m, &pr, stream);
+  }
+}
+
+hipError_t launch_qgemv_swiglu_norm(const uint32_t* w, const void* scales, const void* biases,
+                                    const void* x, const float* nw, float eps, void* y, int ldy,
+                                    int k, int n, int m, int width, int gate_row, int up_row,
+                                    int dtype, hipStream_t stream) {
+  if (!qgemv_norm_fits(k, n, m, width, dtype, x, nw)) return hipErrorInvalidValue;
+  GvPair pr{gate_row, up_row, width, ldy, 1.0f, 1.0f};
+  pr.norm_w = nw;
+  pr.eps = eps;
+  switch (dtype) {
+    case kBf16: return launch_t<kBf16>(w, scales, biases, x, y, k, n, m, &pr, stream);
+    default: return launch_t<kF16>(w, scales, biases, x, y, k, n, m, &pr, stream);
   }
 }
 

@@ -187,9 +187,18 @@ int imq_te_attn_in(imq_te* te, int layer, const void* x, void* qkv, int rows, im
     return fail(te->ctx, IMQ_EINVAL, "%s: x and qkv must be 2-byte aligned", fn);
   const imq_te_layer_weights& l = te->layers[layer];
   const auto st = static_cast<hipStream_t>(stream);
-  hipError_t e = imq::launch_rmsnorm_t(x, l.norm_in, te->h1, rows, te->hidden, te->eps,
-                                       (int)te->dtype, st);
-  if (e == hipSuccess) e = plain_qmm(te, l.qkv, te->h1, qkv, rows, st);
+  const int dt = (int)te->dtype;
+  hipError_t e;
+  if (rows <= imq::kDispatchGemvMaxM &&
+      imq::qgemv_norm_fits(l.qkv.k, l.qkv.n, rows, 0, dt, x, l.norm_in)) {
+    // 1-2 rows: the qGEMV normalizes x in its staging (one launch, the same
+    // bits as RMSNorm then q/k/v).
+    e = imq::launch_qgemv_norm(l.qkv.w, l.qkv.scales, l.qkv.biases, x, l.norm_in, te->eps, qkv,
+                               l.qkv.k, l.qkv.n, rows, dt, st);
+  } else {
+    e = imq::launch_rmsnorm_t(x, l.norm_in, te->h1, rows, te->hidden, te->eps, dt, st);
+    if (e == hipSuccess) e = plain_qmm(te, l.qkv, te->h1, qkv, rows, st);
+  }
   return e == hipSuccess ? IMQ_OK : hip_fail(te->ctx, e, fn);
 }
 
@@ -209,11 +218,17 @@ int imq_te_attn_out_mlp(imq_te* te, int layer, const void* x, const void* attn_o
   // takes the shape (for o_proj with the RMSNorm after it in its split-sum
   // kernel, one launch fewer), else the tile kernel.
   hipError_t e;
+  // 1-2 rows: gate/up's qGEMV normalizes r itself (the RMSNorm below is
+  // then not launched).
+  const imq_qweight& gu = l.gate_up;
+  const bool norm_in_gate_up = rows <= kGemvResidMaxRows && gu.n == 2 * in &&
+                               imq::qgemv_swiglu_fits(gu.k, gu.n, rows, dt) &&
+                               imq::qgemv_norm_fits(gu.k, gu.n, rows, in, dt, te->r, l.norm_post);
   if (rows <= kGemvResidMaxRows) {
     // 1-2 rows: the qGEMV with the residual add in its store, then RMSNorm.
     e = imq::launch_qgemv_resid_add(l.o.w, l.o.scales, l.o.biases, attn_o, x, te->r, te->nq, h,
                                     rows, dt, st);
-    if (e == hipSuccess)
+    if (e == hipSuccess && !norm_in_gate_up)
       e = imq::launch_rmsnorm_t(te->r, l.norm_post, te->h1, rows, h, te->eps, dt, st);
   } else if (resid_split(te, l.o, rows) &&
       imq::qskinny_resid_add_norm_fits(te->nq, h, rows, dt, x, te->r, l.norm_post, te->h1,
@@ -245,7 +260,10 @@ int imq_te_attn_out_mlp(imq_te* te, int layer, const void* x, const void* attn_o
                               imq::SplitWs{});
       if (e == hipSuccess)
         e = imq::launch_swiglu_t(te->split.p, g.n, rows, in, te->m, in, 1.0f, 1.0f, dt, st);
-    } else if (imq::qgemv_swiglu_fits(g.k, g.n, rows, dt))
+    } else if (norm_in_gate_up)
+      e = imq::launch_qgemv_swiglu_norm(g.w, g.scales, g.biases, te->r, l.norm_post, te->eps,
+                                        te->m, in, g.k, g.n, rows, in, 0, in, dt, st);
+    else if (imq::qgemv_swiglu_fits(g.k, g.n, rows, dt))
       e = imq::launch_qgemv_swiglu(g.w, g.scales, g.biases, te->h1, te->m, in, g.k, g.n, rows, in,
                                    0, in, 1.0f, 1.0f, dt, st);
     else if (g.n == 2 * in && resid_split(te, g, rows))

@@ -32,6 +32,16 @@ hipError_t launch_qgemv_resid_add(const uint32_t*, const void*, const void*, con
                                   const void*, void*, int, int, int, int, hipStream_t) {
   return hipErrorNoDevice;
 }
+bool qgemv_norm_fits(int, int, int, int, int, const void*, const float*) { return false; }
+hipError_t launch_qgemv_norm(const uint32_t*, const void*, const void*, const void*, const float*,
+                             float, void*, int, int, int, int, hipStream_t) {
+  return hipErrorNoDevice;
+}
+hipError_t launch_qgemv_swiglu_norm(const uint32_t*, const void*, const void*, const void*,
+                                    const float*, float, void*, int, int, int, int, int, int, int,
+                                    int, hipStream_t) {
+  return hipErrorNoDevice;
+}
 hipError_t launch_qgemm(const uint32_t*, const void*, const void*, const void*, void*, int, int,
                         int, int, hipStream_t, SplitWs) {
   return hipErrorNoDevice;

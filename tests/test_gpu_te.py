@@ -189,6 +189,34 @@ def test_layer_halves_match_oracle(dtype, rows):
     te.close()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 2])
+def test_layer_halves_at_one_and_two_rows_equal_the_unfused_ops(dtype, rows):
+    """At 1-2 rows the q/k/v and gate/up qGEMVs normalize their input in the
+    x staging instead of after a separate RMSNorm launch: the halves equal, bit
+    for bit, the same products on the RMSNorm kernel's output (imq.rmsnorm,
+    imq.qgemv, imq.qmm_swiglu on the qGEMV; the residual adds T(float(a) +
+    float(b)) in torch's fp32 and round-to-nearest-even)."""
+    note(f"TE halves at {rows} rows {dtype}: fused norm == rmsnorm + products")
+    layers = random_te_layers(1, dtype=dtype, seed=74)
+    te = TextEncoderLayers(layers, max_rows=16)
+    l = layers[0]
+    g = torch.Generator(device="cuda").manual_seed(74 + rows)
+    x = torch.randn((rows, 2560), device="cuda", generator=g).to(dtype)
+    attn_o = torch.randn((rows, 4096), device="cuda", generator=g).to(dtype)
+    qkv = te.attn_in(0, x)
+    y = te.attn_out_mlp(0, x, attn_o)
+    h1 = imq.rmsnorm(x, l.norm_in, 1e-6)
+    assert torch.equal(qkv, imq.qgemv(h1, l.qkv.w, l.qkv.s, l.qkv.b)), "attn_in"
+    r = (x.float() + imq.qgemv(attn_o, l.o.w, l.o.s, l.o.b).float()).to(dtype)
+    h2 = imq.rmsnorm(r, l.norm_post, 1e-6)
+    inter = l.down.k
+    m = imq.qmm_swiglu(h2, l.gate_up.w, l.gate_up.s, l.gate_up.b, inter, 0, inter)
+    want = (r.float() + imq.qgemv(m, l.down.w, l.down.s, l.down.b).float()).to(dtype)
+    assert torch.equal(y, want), "attn_out_mlp"
+    te.close()
+
+
 def test_layer_halves_under_graph_capture():
     """Both halves allocate nothing per call: a captured pair of calls over two
     layers replays bit-equal to eager, with other device work in between."""
