@@ -47,7 +47,7 @@ class QWeight(ctypes.Structure):
 class Plan(ctypes.Structure):
     """imq_plan."""
     _fields_ = [("kernel", ctypes.c_int), ("tile_rows", ctypes.c_int), ("splits", ctypes.c_int),
-                ("workspace_bytes", ctypes.c_size_t)]
+                ("workspace_bytes", ctypes.c_size_t), ("tile_cols", ctypes.c_int)]
 
 
 IMQ_ENTRY_QMM_T, IMQ_ENTRY_QGEMM, IMQ_ENTRY_QGEMV, IMQ_ENTRY_FUSED, IMQ_ENTRY_SWIGLU = 0, 1, 2, 3, 4

@@ -529,10 +529,10 @@ int imq_qmm_plan(imq_ctx* ctx, int entry, int k, int n, int m, imq_dtype dtype, 
   int rc = bind_device(ctx);
   if (rc != IMQ_OK) return rc;
   const bool w_fits_gemv = (size_t)n * (size_t)k / 2 < ((size_t)1 << 32);
-  auto tile = [&](bool fused, bool split) {
-    const imq::QgemmPlan p = imq::qgemm_plan(k, n, m, fused, split, 0);
+  auto tile = [&](bool fused, bool split, bool pair = false) {
+    const imq::QgemmPlan p = imq::qgemm_plan(k, n, m, fused, split, 0, pair);
     *out = imq_plan{p.big ? IMQ_KERNEL_TILE : IMQ_KERNEL_TILE_REG, p.tile_rows, p.splits,
-                    p.workspace_bytes};
+                    p.workspace_bytes, p.tile_cols};
     return IMQ_OK;
   };
   switch (entry) {
@@ -550,7 +550,7 @@ int imq_qmm_plan(imq_ctx* ctx, int entry, int k, int n, int m, imq_dtype dtype, 
         *out = imq_plan{IMQ_KERNEL_QGEMV, 0, 1, 0};
         return IMQ_OK;
       }
-      return tile(true, false);
+      return tile(true, false, true);
     case IMQ_ENTRY_QGEMM:
     case IMQ_ENTRY_FUSED:
       if (dtype == IMQ_F32) return fail(ctx, IMQ_EUNSUPPORTED, "%s: f32 has no MFMA kernel", fn);

@@ -76,14 +76,15 @@ size_t qgemm_split_bytes(int k, int n, int m, bool fused = false);
 // height in rows, its K splits and their fp32 workspace bytes.  fused: an
 // output stage other than the plain store over n weight rows (2 * width for a
 // SwiGLU pair); split: a workspace is available; cus: the compute units the
-// planner counts on (0: the device's).
+// planner counts on (0: the device's); pair: the stage is a gate/up pair.
 struct QgemmPlan {
   bool big;
   int tile_rows;
   int splits;
   size_t workspace_bytes;
+  int tile_cols;
 };
-QgemmPlan qgemm_plan(int k, int n, int m, bool fused, bool split, int cus);
+QgemmPlan qgemm_plan(int k, int n, int m, bool fused, bool split, int cus, bool pair = false);
 
 // Whether the buffer-load MFMA kernel (and so the fused epilogues) takes
 // these shapes: K % 256 == 0 and x, w addressable with 32-bit byte offsets.

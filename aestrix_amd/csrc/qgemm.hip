@@ -378,12 +378,12 @@ struct GroupParams {
   float s24[2], s20[2], b[2];
 };
 
-template <int T, int S>
+template <int T, int S, int NT>
 __device__ __forceinline__ GroupParams group_params(const uint4 (&sblk)[2], const uint4 (&bblk)[2],
                                                     int h) {
   GroupParams p;
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NT; ++nt) {
     const float sv = Elem<T>::param((typename Elem<T>::S)param_at<S>(sblk[nt], h));
     p.s24[nt] = sv * 0x1p24f;
     p.s20[nt] = sv * 0x1p20f;
@@ -403,22 +403,23 @@ __device__ __forceinline__ constexpr int a_split(int p) {
 
 // Weight loads of step gs into register set ST: per column tile the rows
 // 0-15 (i = 0) and 16-31 (i = 1), 64 bytes each.
-template <int MT, int ST>
+template <int MT, int NT, int ST>
 __device__ __forceinline__ void big_issue_w(uint32_t gs, const BigSrc<MT>& src,
                                             u32x4_t (&wr)[2][2][kBigKG]) {
 #pragma unroll
   for (int i = 0; i < kBigKG; ++i)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < NT; ++nt)
       wr[ST][nt][i] = load_b128(src.wr, src.w_off[nt][i], gs * 64u);
 }
 
 // The landed weight registers of a step into MFMA operand layout (see the
 // kernel's comment): afterwards wr[nt][0] holds words 0-3 and wr[nt][1]
 // words 4-7 of the lane's group.
+template <int NT>
 __device__ __forceinline__ void big_swap_w(u32x4_t (&wr)[2][kBigKG]) {
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt)
+  for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const auto r = __builtin_amdgcn_permlane16_swap(wr[nt][0][j], wr[nt][1][j], false, false);
@@ -441,7 +442,7 @@ __device__ __forceinline__ void big_issue_a(int p, uint32_t gs, const BigRing& r
 // LDS reads and weight dequant of k-slice t of a step into buffer B: lane
 // (r32, h) holds k = 64 h + 8 t .. +8 of its activation row and of its weight
 // row (word t of its group h), so the two operands agree.
-template <int T, int MT, int B>
+template <int T, int MT, int NT, int B>
 __device__ __forceinline__ void big_operands(int t, const uint4* at, const u32x4_t (&wr)[2][kBigKG],
                                              const GroupParams& gp, BigFrags<MT>& f, int arow0,
                                              int r32, int h) {
@@ -451,7 +452,7 @@ __device__ __forceinline__ void big_operands(int t, const uint4* at, const u32x4
     f.a[B][mt] = __builtin_bit_cast(
         u32x4_t, at[a_slot_kg<kBigKG>(arow0 + mt * 32 + r32, 8 * h + t)]);
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NT; ++nt) {
     const u32x4_t wv = wr[nt][q];
     const uint32_t word = (kk == 0) ? wv.x : (kk == 1) ? wv.y : (kk == 2) ? wv.z : wv.w;
     uint32_t p[4];
@@ -460,53 +461,53 @@ __device__ __forceinline__ void big_operands(int t, const uint4* at, const u32x4
   }
 }
 
-template <int T, int MT, int B>
-__device__ __forceinline__ void big_mfmas(const BigFrags<MT>& f, f32x16_t (&acc)[MT][2]) {
+template <int T, int MT, int NT, int B>
+__device__ __forceinline__ void big_mfmas(const BigFrags<MT>& f, f32x16_t (&acc)[MT][NT]) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma32<T>(f.a[B][mt], f.b[B][nt], acc[mt][nt]);
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma32<T>(f.a[B][mt], f.b[B][nt], acc[mt][nt]);
 }
 
 // One K-step.  S = g % kBigUnroll: stage and weight registers S % 2, dword S
 // of the scale / bias blocks in slot 0 (slot 1: the next four steps').
-template <int T, int MT, int S>
+template <int T, int MT, int NT, int S>
 __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
                                          const BigSrc<MT>& src, uint4 (&sblk)[2][2],
                                          uint4 (&bblk)[2][2], u32x4_t (&wr)[2][2][kBigKG],
-                                         BigFrags<MT>& f, f32x16_t (&acc)[MT][2], int wave,
+                                         BigFrags<MT>& f, f32x16_t (&acc)[MT][NT], int wave,
                                          int arow0, int r32, int h) {
   constexpr int ST = S % 2;
-  constexpr int kMfma = 2 * MT;
+  constexpr int kMfma = NT * MT;
   IMQ_WAIT_VM_LGKM_0();
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
   const uint4* at = ring.a[ST];
-  big_swap_w(wr[ST]);
-  const GroupParams gp = group_params<T, S>(sblk[0], bblk[0], h);
-  big_operands<T, MT, 0>(0, at, wr[ST], gp, f, arow0, r32, h);
+  big_swap_w<NT>(wr[ST]);
+  const GroupParams gp = group_params<T, S, NT>(sblk[0], bblk[0], h);
+  big_operands<T, MT, NT, 0>(0, at, wr[ST], gp, f, arow0, r32, h);
   if constexpr (S == 0) {
     // The next block (steps g+4 .. g+7) goes to slot 1; the K loop moves it to
     // slot 0 after step g+3.
     const uint32_t nb = (uint32_t)min(g + 4, steps - 2);
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < NT; ++nt) {
       sblk[1][nt] = load_param_block(src.sr, src.p_off[nt], nb);
       bblk[1][nt] = load_param_block(src.br, src.p_off[nt], nb);
     }
   }
   const uint32_t gs1 = (uint32_t)min(g + 1, steps - 1);
-  big_issue_w<MT, ST ^ 1>(gs1, src, wr);
+  big_issue_w<MT, NT, ST ^ 1>(gs1, src, wr);
   big_issue_a<MT, ST ^ 1>(0, gs1, ring, src, wave);
-  big_mfmas<T, MT, 1>(f, acc);  // the previous step's last k-slice
+  big_mfmas<T, MT, NT, 1>(f, acc);  // the previous step's last k-slice
   {
     // LDS reads first, then each deferred MFMA followed by a share of the
     // loads and of slice 0's dequant.
-    constexpr int kVmem = 2 * kBigKG + a_split<MT>(1) + (S == 0 ? 4 : 0);
+    constexpr int kVmem = NT * kBigKG + a_split<MT>(1) + (S == 0 ? 2 * NT : 0);
     constexpr int kVmemPer = (kVmem + kMfma - 1) / kMfma;
-    constexpr int kValuPer = (2 * 17 + 8 + kMfma - 1) / kMfma;
+    constexpr int kValuPer = (NT * 17 + 4 * NT + kMfma - 1) / kMfma;
 #pragma unroll
     for (int i = 0; i < MT; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
 #pragma unroll
@@ -522,17 +523,17 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
     __builtin_amdgcn_sched_barrier(0);
     if (t + 1 < kIssuePts) big_issue_a<MT, ST ^ 1>(t + 1, gs1, ring, src, wave);
     if (t & 1) {
-      big_operands<T, MT, 0>(t + 1, at, wr[ST], gp, f, arow0, r32, h);
-      big_mfmas<T, MT, 1>(f, acc);
+      big_operands<T, MT, NT, 0>(t + 1, at, wr[ST], gp, f, arow0, r32, h);
+      big_mfmas<T, MT, NT, 1>(f, acc);
     } else {
-      big_operands<T, MT, 1>(t + 1, at, wr[ST], gp, f, arow0, r32, h);
-      big_mfmas<T, MT, 0>(f, acc);
+      big_operands<T, MT, NT, 1>(t + 1, at, wr[ST], gp, f, arow0, r32, h);
+      big_mfmas<T, MT, NT, 0>(f, acc);
     }
     // Every MFMA of this k-slice is followed by a share of the next slice's
     // dequant VALU work, for the first MT one LDS read, and for the first few
     // one of the next step's activation loads, so a single wave keeps the
     // matrix core fed while it dequantizes.
-    constexpr int kValuPer = (2 * 17 + kMfma - 1) / kMfma;
+    constexpr int kValuPer = (NT * 17 + kMfma - 1) / kMfma;
     const int n_dma = t + 1 < kIssuePts ? a_split<MT>(t + 2) - a_split<MT>(t + 1) : 0;
 #pragma unroll
     for (int i = 0; i < kMfma; ++i) {
@@ -550,15 +551,15 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
 // of kCW * 2 bytes, its 16-byte chunk c at slot c ^ (4 * ((r / 4) % 2)): a
 // wave's 2-byte writes (rows r and r + 4 in its two lane halves) then hit
 // disjoint banks.
-template <class EP>
+template <class EP, int NT>
 constexpr int tile_cols() {
-  return EP::kPair ? kBigBN / 2 : kBigBN;
+  return EP::kPair ? kBigBN / 2 : 128 * NT;
 }
 
-template <int MT, class EP>
+template <int MT, int NT, class EP>
 __device__ __forceinline__ uint16_t* staged_at(const BigRing& ring, int row, int col) {
   constexpr int kHalf = BigCfg<MT>::kBM / 2;
-  constexpr int kCW = tile_cols<EP>();
+  constexpr int kCW = tile_cols<EP, NT>();
   const int chunk = (col >> 3) ^ (((row >> 2) & 1) << 2);
   uint16_t* base = reinterpret_cast<uint16_t*>(row < kHalf ? ring.a[0] : ring.a[1]);
   return base + (row % kHalf) * kCW + chunk * 8 + (col & 7);
@@ -567,8 +568,8 @@ __device__ __forceinline__ uint16_t* staged_at(const BigRing& ring, int row, int
 // Accumulator r of a 32x32 tile holds row 8*(r/4) + 4*h + r%4, column r32:
 // registers r and r+1 are rows one apart in the same column, rounded to T as a
 // pair.
-template <int T, int MT, class EP>
-__device__ __forceinline__ void big_stage_tile(const EP& ep, const f32x16_t (&acc)[MT][2],
+template <int T, int MT, int NT, class EP>
+__device__ __forceinline__ void big_stage_tile(const EP& ep, const f32x16_t (&acc)[MT][NT],
                                                const BigRing& ring, int wave, int r32, int h) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -577,18 +578,18 @@ __device__ __forceinline__ void big_stage_tile(const EP& ep, const f32x16_t (&ac
       const int row = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
       if constexpr (EP::kPair) {
         const int col = wave * 32 + r32;
-        const uint32_t v = Elem<T>::pack2(ep.value2(acc[mt][0][r], acc[mt][1][r]),
-                                          ep.value2(acc[mt][0][r + 1], acc[mt][1][r + 1]));
-        *staged_at<MT, EP>(ring, row, col) = (uint16_t)v;
-        *staged_at<MT, EP>(ring, row + 1, col) = (uint16_t)(v >> 16);
+        const uint32_t v = Elem<T>::pack2(ep.value2(acc[mt][0][r], acc[mt][NT - 1][r]),
+                                          ep.value2(acc[mt][0][r + 1], acc[mt][NT - 1][r + 1]));
+        *staged_at<MT, NT, EP>(ring, row, col) = (uint16_t)v;
+        *staged_at<MT, NT, EP>(ring, row + 1, col) = (uint16_t)(v >> 16);
       } else {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          const int col = wave * 64 + nt * 32 + r32;
+        for (int nt = 0; nt < NT; ++nt) {
+          const int col = wave * (32 * NT) + nt * 32 + r32;
           const uint32_t v =
               Elem<T>::pack2(ep.value(acc[mt][nt][r]), ep.value(acc[mt][nt][r + 1]));
-          *staged_at<MT, EP>(ring, row, col) = (uint16_t)v;
-          *staged_at<MT, EP>(ring, row + 1, col) = (uint16_t)(v >> 16);
+          *staged_at<MT, NT, EP>(ring, row, col) = (uint16_t)v;
+          *staged_at<MT, NT, EP>(ring, row + 1, col) = (uint16_t)(v >> 16);
         }
       }
     }
@@ -596,16 +597,16 @@ __device__ __forceinline__ void big_stage_tile(const EP& ep, const f32x16_t (&ac
 
 // Write the staged tile to output rows m0.., columns col0.. (< ncols): all of
 // a thread's LDS reads first, so their latencies overlap, then the stores.
-template <int MT, class EP>
+template <int MT, int NT, class EP>
 __device__ __forceinline__ void big_write_tile(const EP& ep, const BigRing& ring, int tid, int m0,
                                                int col0, int M, int ncols) {
-  constexpr int kCPR = tile_cols<EP>() / 8;  // 16-byte chunks per row
+  constexpr int kCPR = tile_cols<EP, NT>() / 8;  // 16-byte chunks per row
   constexpr int kIters = BigCfg<MT>::kBM * kCPR / kThreads;
   uint4 v[kIters];
 #pragma unroll
   for (int i = 0; i < kIters; ++i) {
     const int q = i * kThreads + tid;
-    v[i] = *reinterpret_cast<const uint4*>(staged_at<MT, EP>(ring, q / kCPR, (q % kCPR) * 8));
+    v[i] = *reinterpret_cast<const uint4*>(staged_at<MT, NT, EP>(ring, q / kCPR, (q % kCPR) * 8));
   }
   const int c = tid % kCPR;
   const int col = col0 + c * 8;
@@ -633,11 +634,17 @@ __device__ __forceinline__ void big_write_tile(const EP& ep, const BigRing& ring
 // workgroup's 256 weight rows are 128 gate rows and the 128 matching up rows:
 // a wave's column tile 0 holds gate rows, tile 1 the up rows of the same 32
 // output columns, so each lane has both accumulators of an output.
-template <int T, int MT, class EP>
+// NT = 1: each wave owns one 32-column tile, the workgroup tile is (32 MT) x
+// 128 -- twice the tiles of a shape at the same height, so a short M can keep
+// a taller tile (each dequantized weight fragment feeds MT MFMAs; at one or
+// two row tiles the dequant VALU work, not the matrix core, bounds a step).
+template <int T, int MT, int NT, class EP>
 __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, const EP ep,
     int M, int N, int K, int tiles_m, int tiles_n, int split_steps) {
+  static_assert(NT == 1 || NT == 2, "one or two 32-column tiles per wave");
+  static_assert(!EP::kPair || NT == 2, "a gate/up pair takes two column tiles per wave");
   using C = BigCfg<MT>;
   __shared__ uint4 a_st0[C::kSlots], a_st1[C::kSlots];
   const BigRing ring = {{a_st0, a_st1}};
@@ -650,9 +657,9 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   int tm, tn;
   tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * C::kBM;
-  const int n0 = tn * kBigBN;
+  const int n0 = tn * (128 * NT);
   const int arow0 = 0;                      // every wave covers all rows of the tile
-  const int ncol0 = n0 + wave * 64;         // this wave's first output column
+  const int ncol0 = n0 + wave * (32 * NT);  // this wave's first output column
   const int pcol0 = tn * (kBigBN / 2) + wave * 32;  // paired epilogue: first output column
   const int gpr = K >> 6;
   // K-steps [g0, g1) of split blockIdx.y (splits of `split_steps` steps, an
@@ -680,7 +687,7 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   // ncol0 + 32 nt + r32 (its scales and biases); its loads read row
   // ncol0 + 32 nt + 16 i + lane % 16, bytes [16 (lane / 16), +16) of the step.
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NT; ++nt) {
     int wrow = ncol0 + nt * 32 + r32;
     if constexpr (EP::kPair) wrow = (nt == 0 ? ep.gate_row : ep.up_row) + min(pcol0 + r32, ep.width - 1);
     src.p_off[nt] = (uint32_t)min(wrow, N - 1) * (uint32_t)gpr * 2u;
@@ -693,11 +700,11 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     }
   }
 
-  f32x16_t acc[MT][2];
+  f32x16_t acc[MT][NT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.f;
 
@@ -706,38 +713,38 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   uint4 sblk[2][2], bblk[2][2];
   u32x4_t wr[2][2][kBigKG];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NT; ++nt) {
     sblk[0][nt] = load_param_block(src.sr, src.p_off[nt], (uint32_t)g0);
     bblk[0][nt] = load_param_block(src.br, src.p_off[nt], (uint32_t)g0);
   }
-  big_issue_w<MT, 0>((uint32_t)g0, src, wr);
+  big_issue_w<MT, NT, 0>((uint32_t)g0, src, wr);
 #pragma unroll
   for (int p = 0; p < kIssuePts; ++p) big_issue_a<MT, 0>(p, (uint32_t)g0, ring, src, wave);
   BigFrags<MT> f;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) f.a[1][mt] = u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) f.b[1][nt] = u32x4_t{0u, 0u, 0u, 0u};
+  for (int nt = 0; nt < NT; ++nt) f.b[1][nt] = u32x4_t{0u, 0u, 0u, 0u};
 
   // g1 - g0 is even: full unrolls, then possibly two steps.  The ring stage
   // and scale blocks count from g0; loads past g1 are clamped to g1 - 1.
   int g = g0;
   for (; g + kBigUnroll <= g1; g += kBigUnroll) {
-    big_step<T, MT, 0>(g, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
-    big_step<T, MT, 1>(g + 1, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
-    big_step<T, MT, 2>(g + 2, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
-    big_step<T, MT, 3>(g + 3, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, NT, 0>(g, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, NT, 1>(g + 1, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, NT, 2>(g + 2, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, NT, 3>(g + 3, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < NT; ++nt) {
       sblk[0][nt] = sblk[1][nt];
       bblk[0][nt] = bblk[1][nt];
     }
   }
   if (g < g1) {
-    big_step<T, MT, 0>(g, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
-    big_step<T, MT, 1>(g + 1, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, NT, 0>(g, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, NT, 1>(g + 1, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
   }
-  big_mfmas<T, MT, 1>(f, acc);  // the last step's last k-slice
+  big_mfmas<T, MT, NT, 1>(f, acc);  // the last step's last k-slice
 
   if constexpr (EP::kPartial) {
     // Split-K partial sums: fp32 straight from the MFMA layout into split
@@ -762,7 +769,7 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
           const int col = ncol0 + nt * 32 + r32;
           if (col >= N) continue;
 #pragma unroll
@@ -782,16 +789,16 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   // clamped tail loads landed).
   IMQ_WAIT_VM_LGKM_0();
   __builtin_amdgcn_s_barrier();
-  big_stage_tile<T, MT>(ep, acc, ring, wave, r32, h);
+  big_stage_tile<T, MT, NT>(ep, acc, ring, wave, r32, h);
   __syncthreads();
   if constexpr (EP::kPair)
-    big_write_tile<MT>(ep, ring, tid, m0, tn * (kBigBN / 2), M, ep.width);
+    big_write_tile<MT, NT>(ep, ring, tid, m0, tn * (kBigBN / 2), M, ep.width);
   else
-    big_write_tile<MT>(ep, ring, tid, m0, n0, M, N);
+    big_write_tile<MT, NT>(ep, ring, tid, m0, n0, M, N);
   }
 }
 
-template <int T, int MT, class EP>
+template <int T, int MT, int NT, class EP>
 hipError_t launch_big(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                       const uint16_t* x, const EP& ep, int k, int n, int m, hipStream_t stream,
                       int splits = 1, int split_steps = 0) {
@@ -799,11 +806,11 @@ hipError_t launch_big(const uint32_t* w, const uint16_t* scales, const uint16_t*
   const int tiles_m = (m + BM - 1) / BM;
   int cols = n;  // weight rows the workgroups cover
   if constexpr (EP::kPair) cols = 2 * ep.width;
-  const int tiles_n = (cols + kBigBN - 1) / kBigBN;
+  const int tiles_n = (cols + 128 * NT - 1) / (128 * NT);
   if (splits <= 1) split_steps = k / (64 * kBigKG);
   const dim3 grid((unsigned)tiles_m * (unsigned)tiles_n, (unsigned)splits);
-  hipLaunchKernelGGL((qgemm_big_kernel<T, MT, EP>), grid, dim3(kThreads), 0, stream, w, scales,
-                     biases, x, ep, m, n, k, tiles_m, tiles_n, split_steps);
+  hipLaunchKernelGGL((qgemm_big_kernel<T, MT, NT, EP>), grid, dim3(kThreads), 0, stream, w,
+                     scales, biases, x, ep, m, n, k, tiles_m, tiles_n, split_steps);
   return hipGetLastError();
 }
 
@@ -896,10 +903,10 @@ hipError_t launch_reduce(const SplitWs& ws, int splits, int m, int ncols, int ld
   return hipGetLastError();
 }
 
-// Tile height and K split of the large-M kernel (small: 32- and 64-row tiles
-// allowed without a split -- the plain output stage is built for them, the
-// fused stages are not, the split-K partial sums always are; split: K may be
-// split).  Cost in units of about
+// Tile height, width and K split of the large-M kernel (small: 32- and 64-row
+// and 128-column tiles allowed without a split -- the plain store and the
+// residual add are built for them, the other fused stages are not, the
+// split-K partial sums always are; split: K may be split).  Cost in units of about
 // 0.36 us (a K-step of a 32-row slice of the tile): a round of tiles costs
 // split_steps * (MT + 1.5) plus 12 for its prologue and output; a split adds
 // the workspace traffic of its reduction (8 bytes per output and split, at
@@ -908,28 +915,54 @@ hipError_t launch_reduce(const SplitWs& ws, int splits, int m, int ncols, int ld
 // leave a round of 192-row tiles part empty: 1024 x 9216 at K = 3072 is 252
 // tiles in one round instead of 216 (58.4 -> 57.0 us), 2048 x 9216 is 468
 // tiles in two rounds instead of 396 in two (115.0 -> 105.6 us).
+//
+// 128-column tiles (one 32-column tile per wave, NT = 1) double the tiles of
+// a shape at a given height, so a short M keeps a taller tile.  What bounds a
+// K-step of a 32- or 64-row tile is its dequant VALU work, the same per wave
+// and weight fragment at any height (each fragment feeds MT MFMAs), not its
+// MFMAs: half the columns per wave halve it.  Cost of a NT = 1 step:
+// max(kNt1Floor, kNt1Step + kNt1PerRow * MT), fitted to forced plans timed on
+// the text-encoder and DiT shapes (M = 128-2048, same box: e.g. M = 512 K =
+// 2560 N = 6144 at 128 x 128 tiles 18.8 us against 21.5 at 64 x 256; N = 2560
+// K = 4096 unsplit at 64 x 128 20.0 against 23.4 split three ways at 64 x
+// 256).  The narrower tiles read 1.5x the activation and weight bytes per
+// flop of 256-column ones from L2: they are taken only where a split's
+// activation panel (M rows x its K range) fits one XCD's 4 MB L2 (at M = 512
+// K = 9216 unsplit 64 x 128 tiles ran at 57.6 us against 42.0 for 128 x 256
+// tiles split four ways), and a split of them is costed 3 units more.  Only
+// for stages other than a gate/up pair (whose wave holds gate and up
+// columns), unsplit only for the plain store.
+constexpr double kNt1Floor = 1.5, kNt1Step = -0.35, kNt1PerRow = 0.925;
+constexpr size_t kNt1MaxPanel = (size_t)4 << 20;
 struct BigPlan {
-  int mt, splits, split_steps;
+  int mt, nt, splits, split_steps;
 };
 
-BigPlan pick_big_plan(int m, int n, int k, int cus, bool small, bool split) {
-  const int tiles_n = (n + kBigBN - 1) / kBigBN;
+BigPlan pick_big_plan(int m, int n, int k, int cus, bool small, bool split, bool pair = false) {
   const int steps = k / (64 * kBigKG);
-  BigPlan best{8, 1, steps};
+  BigPlan best{8, 2, 1, steps};
   double best_cost = 1e30;
-  for (int mt : {8, 7, 6, 5, 4, 2, 1}) {
-    const long tiles = (long)((m + 32 * mt - 1) / (32 * mt)) * tiles_n;
-    const int max_splits = split && tiles < cus ? std::max(1, steps / 2) : 1;
-    for (int sp = 1; sp <= max_splits; ++sp) {
-      const int sps = ((steps + sp - 1) / sp + 1) / 2 * 2;  // even
-      const int eff = (steps + sps - 1) / sps;
-      if (eff != sp || (eff == 1 && mt < 4 && !small)) continue;
-      const long rounds = (tiles * eff + cus - 1) / cus;
-      double cost = (double)rounds * (sps * (mt + 1.5) + 12.0);
-      if (eff > 1) cost += (double)eff * m * n * 8.0 / 1.4e6 + 3.0;
-      if (cost < best_cost - 1e-9) {
-        best_cost = cost;
-        best = BigPlan{mt, eff, sps};
+  for (int nt : {2, 1}) {
+    if (nt == 1 && pair) continue;
+    const int tiles_n = (n + 128 * nt - 1) / (128 * nt);
+    for (int mt : {8, 7, 6, 5, 4, 2, 1}) {
+      const long tiles = (long)((m + 32 * mt - 1) / (32 * mt)) * tiles_n;
+      const int max_splits = split && tiles < cus ? std::max(1, steps / 2) : 1;
+      for (int sp = 1; sp <= max_splits; ++sp) {
+        const int sps = ((steps + sp - 1) / sp + 1) / 2 * 2;  // even
+        const int eff = (steps + sps - 1) / sps;
+        if (eff != sp || (eff == 1 && mt < 4 && !small)) continue;
+        if (nt == 1 && ((eff == 1 && !small) || (size_t)m * sps * 128 * 2 > kNt1MaxPanel))
+          continue;
+        const long rounds = (tiles * eff + cus - 1) / cus;
+        const double step =
+            nt == 2 ? mt + 1.5 : std::max(kNt1Floor, kNt1Step + kNt1PerRow * mt);
+        double cost = (double)rounds * (sps * step + 12.0);
+        if (eff > 1) cost += (double)eff * m * n * 8.0 / 1.4e6 + (nt == 2 ? 3.0 : 6.0);
+        if (cost < best_cost - 1e-9) {
+          best_cost = cost;
+          best = BigPlan{mt, nt, eff, sps};
+        }
       }
     }
   }
@@ -965,26 +998,48 @@ int device_cus() {
   return cus;
 }
 
+// Stages built for every tile height and for 128-column tiles: the plain
+// store, the split-K partial sums and the text encoder's residual add.
 template <int T, class EP>
-hipError_t launch_big_mt(int mt, const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
-                         const uint16_t* x, const EP& ep, int k, int n, int m, hipStream_t stream,
-                         int splits = 1, int split_steps = 0) {
-  // Plain and partial-sum stages are built for every tile height, the fused
-  // ones for 128 rows and more.
-  constexpr bool kSmall = EP::kPartial || (!EP::kPair && std::is_same<EP, EpStore<T>>::value);
+constexpr bool kAnyTile = EP::kPartial || (!EP::kPair && (std::is_same<EP, EpStore<T>>::value ||
+                                                          std::is_same<EP, EpResidAdd<T>>::value));
+
+template <int T, int NT, class EP>
+hipError_t launch_big_mt_nt(int mt, const uint32_t* w, const uint16_t* scales,
+                            const uint16_t* biases, const uint16_t* x, const EP& ep, int k, int n,
+                            int m, hipStream_t stream, int splits, int split_steps) {
+  // The other fused stages are built for 128 rows and more.
+  constexpr bool kSmall = kAnyTile<T, EP>;
   switch (mt) {
     case 1:
-      if constexpr (kSmall) return launch_big<T, 1>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
+      if constexpr (kSmall) return launch_big<T, 1, NT>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
       return hipErrorInvalidValue;
     case 2:
-      if constexpr (kSmall) return launch_big<T, 2>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
+      if constexpr (kSmall) return launch_big<T, 2, NT>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
       return hipErrorInvalidValue;
-    case 4: return launch_big<T, 4>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
-    case 5: return launch_big<T, 5>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
-    case 6: return launch_big<T, 6>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
-    case 7: return launch_big<T, 7>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
-    default: return launch_big<T, 8>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
+    case 4: return launch_big<T, 4, NT>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
+    case 5: return launch_big<T, 5, NT>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
+    case 6: return launch_big<T, 6, NT>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
+    case 7: return launch_big<T, 7, NT>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
+    default: return launch_big<T, 8, NT>(w, scales, biases, x, ep, k, n, m, stream, splits, split_steps);
   }
+}
+
+// nt = 1 (128-column tiles) is built for the kAnyTile stages other than a
+// gate/up pair's partial sums.
+template <int T, class EP>
+hipError_t launch_big_mt(int mt, int nt, const uint32_t* w, const uint16_t* scales,
+                         const uint16_t* biases, const uint16_t* x, const EP& ep, int k, int n,
+                         int m, hipStream_t stream, int splits = 1, int split_steps = 0) {
+  constexpr bool kNt1 = !EP::kPair && kAnyTile<T, EP>;
+  if (nt == 1) {
+    if constexpr (kNt1)
+      return launch_big_mt_nt<T, 1>(mt, w, scales, biases, x, ep, k, n, m, stream, splits,
+                                    split_steps);
+    return hipErrorInvalidValue;
+  }
+  return launch_big_mt_nt<T, 2>(mt, w, scales, biases, x, ep, k, n, m, stream, splits,
+                                split_steps);
 }
 
 // The large-M kernel with output stage ep (two groups per K-step, 2-stage
@@ -999,7 +1054,7 @@ hipError_t launch_big_ep(const uint32_t* w, const uint16_t* scales, const uint16
   // K % 256 != 0 (e.g. the DiT's x_embedder, K = 128) or operands past 32-bit
   // offsets: the register-staged kernel, one pass.
   if (!qgemm_big_supported(k, n, m)) return launch_tile<T, 4, 2>(w, scales, biases, x, ep, k, n, m, stream);
-  constexpr bool kSmall = !EP::kPair && std::is_same<EP, EpStore<T>>::value;
+  constexpr bool kSmall = kAnyTile<T, EP>;
   int cols = n;  // weight rows covered
   int width = n, gate_row = 0, up_row = 0;
   if constexpr (EP::kPair) {
@@ -1009,13 +1064,13 @@ hipError_t launch_big_ep(const uint32_t* w, const uint16_t* scales, const uint16
     up_row = ep.up_row;
   }
   const int cus = ws.cus > 0 ? ws.cus : device_cus();
-  BigPlan p = pick_big_plan(m, cols, k, cus, kSmall, ws.p != nullptr);
+  BigPlan p = pick_big_plan(m, cols, k, cus, kSmall, ws.p != nullptr, EP::kPair);
   if (p.splits > 1 && ws.bytes < (size_t)p.splits * m * cols * sizeof(float))
-    p = pick_big_plan(m, cols, k, cus, kSmall, false);  // no room for the partial sums
-  if (p.splits == 1) return launch_big_mt<T>(p.mt, w, scales, biases, x, ep, k, n, m, stream);
+    p = pick_big_plan(m, cols, k, cus, kSmall, false, EP::kPair);  // no room for the partial sums
+  if (p.splits == 1) return launch_big_mt<T>(p.mt, p.nt, w, scales, biases, x, ep, k, n, m, stream);
   const EpPartial<EP::kPair> part{ws.p, cols, width, gate_row, up_row};
-  const hipError_t e =
-      launch_big_mt<T>(p.mt, w, scales, biases, x, part, k, n, m, stream, p.splits, p.split_steps);
+  const hipError_t e = launch_big_mt<T>(p.mt, p.nt, w, scales, biases, x, part, k, n, m, stream,
+                                        p.splits, p.split_steps);
   if (e != hipSuccess) return e;
   return launch_reduce<T>(ws, p.splits, m, width, cols, ep, stream);
 }
@@ -1052,15 +1107,22 @@ hipError_t launch_qgemm(const uint32_t* w, const void* scales, const void* biase
 
 size_t qgemm_split_bytes(int k, int n, int m, bool fused) {
   if (!qgemm_big_supported(k, n, m)) return 0;
-  const BigPlan p = pick_big_plan(m, n, k, device_cus(), !fused, true);
-  return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
+  // The most a stage over these rows takes: a fused stage may be a gate/up
+  // pair (no 128-column tiles), the residual add (every tile) or another.
+  size_t bytes = 0;
+  for (int v = 0; v < (fused ? 3 : 1); ++v) {
+    const bool small = !fused || v == 2, pair = v == 1;
+    const BigPlan p = pick_big_plan(m, n, k, device_cus(), small, true, pair);
+    if (p.splits > 1) bytes = std::max(bytes, (size_t)p.splits * m * n * sizeof(float));
+  }
+  return bytes;
 }
 
-QgemmPlan qgemm_plan(int k, int n, int m, bool fused, bool split, int cus) {
-  if (!qgemm_big_supported(k, n, m)) return QgemmPlan{false, 128, 1, 0};
-  const BigPlan p = pick_big_plan(m, n, k, cus > 0 ? cus : device_cus(), !fused, split);
+QgemmPlan qgemm_plan(int k, int n, int m, bool fused, bool split, int cus, bool pair) {
+  if (!qgemm_big_supported(k, n, m)) return QgemmPlan{false, 128, 1, 0, 256};
+  const BigPlan p = pick_big_plan(m, n, k, cus > 0 ? cus : device_cus(), !fused, split, pair);
   return QgemmPlan{true, 32 * p.mt, p.splits,
-                   p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0};
+                   p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0, 128 * p.nt};
 }
 
 hipError_t launch_qgemm_postscale(const uint32_t* w, const void* scales, const void* biases,

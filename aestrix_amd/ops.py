@@ -416,6 +416,7 @@ def qmm_plan(m: int, n: int, k: int, dtype: torch.dtype = torch.bfloat16, entry:
     _lib.check(_lib.load().imq_qmm_plan(ctx, _ENTRIES[entry], k, n, m, _DTYPES.get(dtype, -1),
                                         ctypes.byref(out)), ctx)
     return {"kernel": _lib.KERNEL_NAMES[out.kernel], "tile_rows": out.tile_rows,
+            "tile_cols": out.tile_cols,
             "splits": out.splits, "workspace_bytes": out.workspace_bytes}
 
 

@@ -63,6 +63,10 @@ MAX_SCLK_MHZ = 2400.0  # the engine clock the dense MFMA peak is quoted at
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 TARGET = (4608, 18432, 3072)  # M, N, K
+# Text-encoder prefill and splice rows, and the reference's published qmm shape
+# (M = 512, K = 2560, N = 4096), through the regime dispatcher.
+MID_M_SHAPES = ((32, 9728, 2560), (128, 9728, 2560), (512, 9728, 2560), (512, 2560, 9728),
+                (512, 4096, 2560))
 
 
 def qmm_bytes(m: int, n: int, k: int) -> int:
@@ -761,6 +765,9 @@ def main() -> int:
                     help="run the whole DiT step benchmark only (for profiling runs)")
     ap.add_argument("--only-te", action="store_true",
                     help="run the text-encoder layer benchmark only (for profiling runs)")
+    ap.add_argument("--only-midm", action="store_true",
+                    help="run the mid-M shapes only (M = 32, 128, 512 through the dispatcher, the "
+                         "text-encoder layer at L = 512) and a calibration copy (for counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} requested, but this path runs on one GPU "
@@ -785,6 +792,16 @@ def main() -> int:
         return 0
     if args.only_te:
         bench_te_layer(torch)
+        return 0
+    if args.only_midm:
+        for (m, n, k) in MID_M_SHAPES:
+            bench_qgemm_shape(imq, synth, torch, m, n, k, dispatcher=True)
+        bench_te_layer(torch, rows_list=(512,))
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calibration copy: 268435456 bytes read and written")
         return 0
     if args.only_hbm:
         bench_qgemv(imq, synth, torch, ms_list=(1,), few_rows=(4, 8, 16))
@@ -871,8 +888,7 @@ def main() -> int:
         # when the output tiles are too few to fill the GPU).
         extra["qmm_small_m"] = {
             f"M{m}_N{n}_K{k}": bench_qgemm_shape(imq, synth, torch, m, n, k, dispatcher=True)
-            for (m, n, k) in ((32, 9728, 2560), (128, 9728, 2560), (512, 9728, 2560),
-                              (512, 2560, 9728), (512, 4096, 2560))
+            for (m, n, k) in MID_M_SHAPES
         }
         extra["dit_single_block"] = bench_dit_single_block(imq, torch)
         extra["dit_step"] = bench_dit_step(torch)

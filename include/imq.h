@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define IMQ_ABI_VERSION 1
+#define IMQ_ABI_VERSION 2
 
 typedef enum imq_status {
     IMQ_OK = 0,
@@ -206,6 +206,8 @@ typedef struct imq_plan {
     int tile_rows;          /* output rows per workgroup tile (tile kernels; 0 otherwise) */
     int splits;             /* K ranges summed by a second kernel (1: K not split) */
     size_t workspace_bytes; /* fp32 partial sums of a split plan (0 when not split) */
+    int tile_cols;          /* output columns per workgroup tile (tile kernels: 256, or 128 for
+                               short M; 0 otherwise) */
 } imq_plan;
 
 /* The plan of a call of `entry` with these sizes and dtype on ctx's device,

@@ -47,8 +47,8 @@ hipError_t launch_qgemm(const uint32_t*, const void*, const void*, const void*, 
   return hipErrorNoDevice;
 }
 size_t qgemm_split_bytes(int, int, int, bool) { return 0; }
-QgemmPlan qgemm_plan(int k, int n, int m, bool, bool, int) {
-  return QgemmPlan{qgemm_big_supported(k, n, m), 128, 1, 0};
+QgemmPlan qgemm_plan(int k, int n, int m, bool, bool, int, bool) {
+  return QgemmPlan{qgemm_big_supported(k, n, m), 128, 1, 0, 256};
 }
 bool qgemm_big_supported(int k, int n, int m) {
   return (size_t)m * k * 2 < ((size_t)1 << 31) && (size_t)n * k / 2 < ((size_t)1 << 31) &&

@@ -159,22 +159,27 @@ def test_gate_add_at_production_tile_heights(dtype, case):
     assert_close(got, want, f"gate_add M={m} K={k} rows={len(rows)}")
 
 
-# (M, N, K, tile rows, splits): the double blocks' Q/K/V over image rows and
-# text rows, the image rows' MLP-in width as a plain store (256-row tiles), and
-# the 1024-row MLP-in qGEMM (160-row tiles: 252 tiles in one round on 256 CUs).
-PLAIN = [(4096, 3072, 3072, 224, 1), (512, 3072, 3072, 32, 1), (4096, 18432, 3072, 256, 1),
-         (1024, 9216, 3072, 160, 1)]
+# (M, N, K, tile rows, tile columns, splits): the double blocks' Q/K/V over
+# image rows and text rows (64 x 128 tiles: 192 of them), the image rows'
+# MLP-in width as a plain store (256-row tiles), the 1024-row MLP-in qGEMM
+# (160-row tiles: 252 tiles in one round on 256 CUs), and the text encoder's
+# q/k/v, o and down at L = 512 (128- and 64-row tiles of 128 columns; down
+# split three ways).
+PLAIN = [(4096, 3072, 3072, 224, 256, 1), (512, 3072, 3072, 64, 128, 1),
+         (4096, 18432, 3072, 256, 256, 1), (1024, 9216, 3072, 160, 256, 1),
+         (512, 6144, 2560, 128, 128, 1), (512, 2560, 4096, 64, 128, 1),
+         (512, 2560, 9728, 128, 128, 3)]
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-@pytest.mark.parametrize("case", PLAIN, ids=[f"M{c[0]}_N{c[1]}" for c in PLAIN])
+@pytest.mark.parametrize("case", PLAIN, ids=[f"M{c[0]}_N{c[1]}_K{c[2]}" for c in PLAIN])
 def test_plain_qmm_at_production_tile_heights(dtype, case):
-    m, n, k, tile_rows, splits = case
+    m, n, k, tile_rows, tile_cols, splits = case
     note(f"qmm_t {dtype} M={m} N={n} K={k} seed=82")
     plan = imq.qmm_plan(m, n, k, TDT[dtype])
     note(f"  plan {plan}")
     assert plan["kernel"] == "tile" and plan["tile_rows"] == tile_rows
-    assert plan["splits"] == splits
+    assert plan["tile_cols"] == tile_cols and plan["splits"] == splits
     w_h, x, w, s, b = problem(m, n, k, dtype, seed=82)
     y = imq.quantized_matmul(x, w, s, b)
     rows = sample_rows(m, 32)

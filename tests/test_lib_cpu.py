@@ -57,7 +57,7 @@ def test_only_the_c_abi_is_exported():
 
 def test_status_strings_and_version():
     L = _lib.load()
-    assert L.imq_abi_version() == 1
+    assert L.imq_abi_version() == 2
     assert L.imq_status_string(0) == b"IMQ_OK"
     assert L.imq_status_string(1) == b"IMQ_EINVAL"
     assert L.imq_status_string(2) == b"IMQ_EUNSUPPORTED"

@@ -67,7 +67,7 @@ PAIRS = [
     ((2048, 2560, 9728), (128, 3072, 12288)),  # 60 MiB of scratch, then 15 MiB
     ((1024, 3072, 9216), (8, 9728, 2560)),     # split-K, then the few-row kernel
     ((40, 1000, 2560), (1, 2560, 9728)),       # split-K, then the qGEMV
-    ((4608, 3072, 3072), (300, 512, 768)),     # unsplit tiles, then split-K
+    ((4608, 3072, 3072), (64, 3072, 3072)),    # unsplit tiles, then split-K (128-column tiles)
     ((16, 2560, 9728), (12, 1000, 4608)),      # the few-row kernel's K split: 10, then 9 splits
 ]
 
