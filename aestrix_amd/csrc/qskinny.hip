@@ -786,38 +786,37 @@ hipError_t launch_lds_t(const uint32_t* w, const uint16_t* s, const uint16_t* b,
   return launch_lds_tw<T, TPW, kLdsWaves>(w, s, b, x, y, k, n, m, p.u, vec, stream);
 }
 
-// ---- K split: the multi-tile kernel over a range of K, for long K ----
+// ---- K split, rows per wave ----
 //
-// Workgroup (g, s) owns TPW 16-row tiles and the K pieces [s per, s per + per)
-// for TG groups of 16 tokens (M <= 16 TG tokens; each dequantized weight
-// fragment feeds one MFMA per group)
-// (512 k each, the last range shorter); it stages only its x slice [M, 512
-// per] in LDS (rows 1024 per + 16 bytes apart) and writes fp32 partial sums
-// to ws[s][m][n]; qskinny_reduce_kernel adds the splits in order and rounds
-// to T (deterministic).  The second launch costs about 2.9 us per call
-// ([2560 x 9728] M = 16: 13.7 us, 10.8 without it), but adding the splits in
-// the last-arriving workgroup of each tile group (arrival counters, no
-// waiting) measured slower in every form tried: device-scope fences in every
-// workgroup (each writes back and invalidates its XCD's L2) 84 us,
-// agent-scope atomic stores and loads of the partial sums 19 us, atomic
-// stores with one acquire fence in the last workgroup 16.8 us.  For [2560 x 9728] (160 row tiles, x of 16 rows 311
-// KB) the 16-row kernel re-reads all of x from L2 per tile (about 50 MB for
-// 12.5 MB of weights) on 160 workgroups; here each x byte is read once per
-// tile group and split and the grid fills the CUs.
-template <int T, int TPW, int W, int U, int TG>
-__global__ __launch_bounds__(64 * W) void qskinny_split_kernel(const uint32_t* __restrict__ w,
-                                                               const uint16_t* __restrict__ scales,
-                                                               const uint16_t* __restrict__ biases,
-                                                               const uint16_t* __restrict__ x,
-                                                               float* __restrict__ ws, int M,
-                                                               int N, int K, int per, bool vec) {
-  constexpr int kWeightLoads = 3 * U * TPW < 63 ? 3 * U * TPW : 63;
-  __shared__ f32x4_t part[W][TPW][TG][64];
+// For long K or more than 16 rows: workgroup (g, s) owns W x R 16-row tiles
+// (wave v the R tiles from row (g W + v) 16 R) and the K range of split s:
+// `per` pieces of 512 k, CH = 4 per chunks of 128 k.  Each wave runs the
+// whole range for its own tiles, so no sums cross waves, and the W waves
+// share one x slice [M, 512 per] in LDS (rows 1024 per + 16 bytes apart).
+// Its predecessor split the K range among the waves of a workgroup of one to
+// four tiles and added their sums in LDS: at 30 rows and [2560 x 9728] it
+// read some 98 MB of x slices from L2 for 12.5 MB of weights, and took 17.1
+// us (with the split sums) where this takes 12.5.  A wave issues every load
+// of its range before its first MFMA: its x pieces, then its scale and bias
+// blocks (8 groups of a row per 16-byte load), then the weights chunk by
+// chunk, and waits once for its x pieces (loads return in issue order)
+// before a barrier; the compiler's own waits then take the weights chunk by
+// chunk.  Fp32 partial sums go to ws[s][m][n]; qskinny_reduce_kernel (or a
+// fused-stage split sum) adds the splits in order (deterministic).
+template <int T, int R, int W, int TG, int CH>
+__global__ __launch_bounds__(64 * W) void qskinny_rows_kernel(const uint32_t* __restrict__ w,
+                                                              const uint16_t* __restrict__ scales,
+                                                              const uint16_t* __restrict__ biases,
+                                                              const uint16_t* __restrict__ x,
+                                                              float* __restrict__ ws, int M,
+                                                              int N, int K, int per, bool vec) {
+  static_assert(CH % 4 == 0 && CH * R + CH / 2 * R <= 63, "the loads after x fit vmcnt");
+  constexpr int kBlk = CH / 4;  // 16-byte scale (bias) blocks per row: 8 groups, 512 k each
   extern __shared__ uint4 xs[];  // x [M, 512 per], rows 1024 per + 16 bytes apart
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, h = lane >> 4;
-  const int n0 = blockIdx.x * (kRows * TPW);
+  const int n0 = ((int)blockIdx.x * W + wave) * (kRows * R);
   const int gpr = K >> 6;
   const int p0 = (int)blockIdx.y * per;
   const int np = min(per, (K >> 9) - p0);  // pieces of 512 k in this range (>= 1)
@@ -841,97 +840,97 @@ __global__ __launch_bounds__(64 * W) void qskinny_split_kernel(const uint32_t* _
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  uint32_t w_off[TPW], p_off[TPW];
+  // 2. Scale and bias blocks (groups 8 b .. 8 b + 7 from the range's first
+  //    group; a short last range repeats its last block, never used), then
+  //    the weights: lane (c, h) holds row c of each tile, bytes [16 h, +16) of
+  //    each chunk's 64 (chunks past a short range repeat its last one).
+  uint32_t w_off[R], p_off[R];
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    const uint32_t row = (uint32_t)min(n0 + kRows * t + c, N - 1);
-    w_off[t] = row * (uint32_t)(K / 2) + (uint32_t)h * 16u;
-    p_off[t] = (row * (uint32_t)gpr + (uint32_t)(h >> 1)) * 2u;
+  for (int r = 0; r < R; ++r) {
+    const uint32_t row = (uint32_t)min(n0 + kRows * r + c, N - 1);
+    w_off[r] = row * (uint32_t)(K / 2) + (uint32_t)h * 16u;
+    p_off[r] = row * (uint32_t)gpr * 2u;
   }
-  f32x4_t acc[TPW][TG];
+  uint4 sblk[kBlk][R], bblk[kBlk][R];
 #pragma unroll
-  for (int t = 0; t < TPW; ++t)
+  for (int b = 0; b < kBlk; ++b)
 #pragma unroll
-    for (int g = 0; g < TG; ++g) acc[t][g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < R; ++r) {
+      const uint32_t g = (uint32_t)(2 * c0 + 8 * min(b, (chunks - 1) / 4));
+      sblk[b][r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(sr, p_off[r], g * 2u, 0));
+      bblk[b][r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(br, p_off[r], g * 2u, 0));
+    }
+  u32x4_t wv[CH][R];
+#pragma unroll
+  for (int j = 0; j < CH; ++j)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      wv[j][r] = load_b128(wr, w_off[r], (uint32_t)(c0 + min(j, chunks - 1)) * 64u);
+  __builtin_amdgcn_sched_barrier(0);
+
+  f32x4_t acc[R][TG];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int g = 0; g < TG; ++g) acc[r][g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // B operand of token group g (16 tokens): row min(16 g + c, M - 1); columns
   // past M are never stored.
   int xrow[TG];
 #pragma unroll
   for (int g = 0; g < TG; ++g) xrow[g] = min(16 * g + c, M - 1);
-  bool first = true;
-  for (int ch0 = wave; ch0 < chunks; ch0 += W * U) {
-    u32x4_t wv[U][TPW];
-    uint16_t sv[U][TPW], bv[U][TPW];
+  IMQ_WAIT_VMCNT(2 * kBlk * R + CH * R);  // this wave's x pieces have landed
+  __builtin_amdgcn_s_barrier();           // and every other wave's
+  __builtin_amdgcn_sched_barrier(0);
+  // Every chunk runs, so that no load is sunk into a conditional block past
+  // the wait above; a chunk past a short range reads the range's last x
+  // chunk and dequantizes to zero (scale and bias 0), adding nothing.
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t ch = (uint32_t)(c0 + min(ch0 + u * W, chunks - 1));
+  for (int j = 0; j < CH; ++j) {
+    const bool valid = j < chunks;
+    const int jx = min(j, chunks - 1);
+    u32x4_t xf[TG][4];
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) {
-        wv[u][t] = load_b128(wr, w_off[t], ch * 64u);
-        sv[u][t] = __builtin_amdgcn_raw_buffer_load_b16(sr, p_off[t], ch * 4u, 0);
-        bv[u][t] = __builtin_amdgcn_raw_buffer_load_b16(br, p_off[t], ch * 4u, 0);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if (first) {
-      IMQ_WAIT_VMCNT(kWeightLoads);
-      __builtin_amdgcn_s_barrier();
-      first = false;
-    }
-    __builtin_amdgcn_sched_barrier(0);
+    for (int g = 0; g < TG; ++g)
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bool valid = ch0 + u * W < chunks;
-      const int j = min(ch0 + u * W, chunks - 1);
-      u32x4_t xf[TG][4];
+      for (int i = 0; i < 4; ++i)
+        xf[g][i] = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(xs) +
+                                                    xrow[g] * xstride + jx * 256 + (4 * h + i) * 16);
 #pragma unroll
-      for (int g = 0; g < TG; ++g)
+    for (int r = 0; r < R; ++r) {
+      // Group 2 j + h / 2 of the range: half h / 2 of dword j % 4 of block j / 4.
+      const uint4 sb = sblk[j / 4][r], bb = bblk[j / 4][r];
+      const uint32_t sw = (j % 4 == 0) ? sb.x : (j % 4 == 1) ? sb.y : (j % 4 == 2) ? sb.z : sb.w;
+      const uint32_t bw = (j % 4 == 0) ? bb.x : (j % 4 == 1) ? bb.y : (j % 4 == 2) ? bb.z : bb.w;
+      const int sh = 16 * (h >> 1);
+      const float sc = valid ? Elem<T>::param((uint16_t)(sw >> sh)) : 0.0f;
+      const float s24 = sc * 0x1p24f, s20 = sc * 0x1p20f;
+      const float b = valid ? Elem<T>::param((uint16_t)(bw >> sh)) : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          xf[g][i] = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(xs) +
-                                                      xrow[g] * xstride + j * 256 + (4 * h + i) * 16);
+      for (int i = 0; i < 4; ++i) {
+        uint32_t pq[4];
+        Elem<T>::dequant(wv[j][r][i], s24, s20, b, pq);
+        const u32x4_t a = u32x4_t{pq[0], pq[1], pq[2], pq[3]};
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) {
-        const float sc = valid ? Elem<T>::param(sv[u][t]) : 0.0f;
-        const float s24 = sc * 0x1p24f, s20 = sc * 0x1p20f;
-        const float b = valid ? Elem<T>::param(bv[u][t]) : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          uint32_t pq[4];
-          Elem<T>::dequant(wv[u][t][i], s24, s20, b, pq);
-          const u32x4_t a = u32x4_t{pq[0], pq[1], pq[2], pq[3]};
-#pragma unroll
-          for (int g = 0; g < TG; ++g) acc[t][g] = mfma16x16x32<T>(a, xf[g][i], acc[t][g]);
-        }
+        for (int g = 0; g < TG; ++g) acc[r][g] = mfma16x16x32<T>(a, xf[g][i], acc[r][g]);
       }
     }
   }
-  if (first) {
-    IMQ_WAIT_VMCNT(0);
-    __builtin_amdgcn_s_barrier();
-  }
 #pragma unroll
-  for (int t = 0; t < TPW; ++t)
+  for (int r = 0; r < R; ++r) {
+    const int f0 = n0 + kRows * r + 4 * h;
 #pragma unroll
-    for (int g = 0; g < TG; ++g) part[wave][t][g][lane] = acc[t][g];
-  __syncthreads();
-  if (wave >= TPW) return;
-  const int t = wave;
-  const int f0 = n0 + kRows * t + 4 * h;
+    for (int g = 0; g < TG; ++g) {
+      const int m = 16 * g + c;
+      if (m >= M) continue;
+      float* dst = ws + ((size_t)blockIdx.y * M + m) * N;
+      const f32x4_t sum = acc[r][g];
+      if (vec && f0 + 3 < N) {
+        *reinterpret_cast<float4*>(dst + f0) = make_float4(sum[0], sum[1], sum[2], sum[3]);
+      } else {
 #pragma unroll
-  for (int g = 0; g < TG; ++g) {
-    const int m = 16 * g + c;
-    if (m >= M) continue;
-    f32x4_t sum = part[0][t][g][lane];
-#pragma unroll
-    for (int i = 1; i < W; ++i) sum += part[i][t][g][lane];
-    float* dst = ws + ((size_t)blockIdx.y * M + m) * N;
-    if (vec && f0 + 3 < N) {
-      *reinterpret_cast<float4*>(dst + f0) = make_float4(sum[0], sum[1], sum[2], sum[3]);
-    } else {
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        if (f0 + v < N) dst[f0 + v] = sum[v];
+        for (int v = 0; v < 4; ++v)
+          if (f0 + v < N) dst[f0 + v] = sum[v];
+      }
     }
   }
 }
@@ -1069,144 +1068,105 @@ __global__ __launch_bounds__(256) void qskinny_reduce_norm_kernel(
   }
 }
 
+// A K split of the few-row product: `per` pieces of 512 k per split, rr
+// 16-row tiles per wave, rw waves per workgroup (qskinny_rows_kernel).
 struct SplitPlan {
-  int tpw, per, splits, u;
+  int per, splits, rr, rw;
   bool ok;
 };
 
-constexpr int kSplitWaves = 8;
-// Fewest rows for the K split: at M <= 5 all of x fits LDS up to K = 9728
-// and the unsplit kernels stay faster ([2560 x 9728] M = 4: 10.2 us unsplit,
-// 10.2 us for the best split plan).
+// Fewest rows for the K split of a plain product: at M <= 5 all of x fits
+// LDS up to K = 9728 and the unsplit kernels were as fast as the split that
+// the rows kernel replaced ([2560 x 9728] M = 4: 10.2 us either way).
 constexpr int kSplitMinM = 6;
 
-// Bytes of the split kernel's x slice in LDS.
+// Bytes of the rows kernel's x slice in LDS.
 size_t split_x_bytes(int per, int m) { return (size_t)m * (1024 * (size_t)per + 16); }
 
-// Taken, from M = 6, where the unsplit kernels would stream x per chunk from
-// L2 (x [M, K] past the 96 KiB LDS budget and not the multi-tile kernel's
-// case), and where it saves more than a quarter of the multi-tile kernel's
-// wave work (the plan rule below).  Its first planner (M >= 8, at most 128
-// row tiles or K >= 8192, least L2 traffic), measured with the weights from
-// HBM (same box, A/B builds): [2560 x 9728] M = 8 / 12
-// / 16 13.9 / 15.9 / 18.1 -> 13.2 / 13.5 / 13.8 us, [1000 x 4608] M = 12 9.5
-// -> 6.3 us, [1030 x 4608] M = 13 9.6 -> 6.6 us; elsewhere slower: M = 4 and
-// 5 at K = 9728 (x in LDS: 11.7 -> 12.2, 11.9 -> 12.9 us), [2560 x 4096] M =
-// 16 (9.4 -> 10.0), [3072 x 3072] at M = 4 / 8 / 16 (6.3 -> 8.3-8.9 us): there
-// the second launch and the partial sums cost more than the better-filled
-// grid saves.  17 to 32 rows (two token groups per weight fragment) take it
-// wherever the row tiles are fewer than 256 (now 512), against the tile kernel's 32-row
-// tiles and their split K (same box, A/B builds, M = 30 unless stated):
-// [2560 x 9728] 19.1 -> 17.0 us (M = 17 18.0 -> 15.9), [2560 x 4096] 14.7 ->
-// 13.2, [2560 x 2560] 11.4 -> 8.0, [1000 x 4608] 13.6 -> 7.2, [3072 x 3072]
-// 12.7 -> 12.4, M = 24 [1024 x 2560] 10.5 -> 5.8.
-//
-// Plan: among the (tiles per workgroup, pieces per split) whose x slice fits
-// 64 KB (80 KB for two token groups), the least wave work on the busiest CU:
-// ceil(workgroups / 256) x U x TPW x TG, U = the chunk rounds of a wave
-// (ceil(4 per / 8): an odd number of pieces leaves half the waves a dummy
-// round); ties go to more tiles per workgroup (fewer x slices), then to
-// fewer splits.  Measured against every plan forced in turn on 15 shapes
-// (same box, weights from HBM): within 1.4% of the fastest on average (5.8%
-// at most), 12.5% faster on average than the former choice (the least L2
-// traffic among grids of at least 256 workgroups): [2560 x 9728] M = 8 / 12
-// / 16 13.2 / 13.5 / 13.7 -> 11.1 / 11.6 / 12.5 us, M = 30 [2560 x 4096]
-// 13.3 -> 9.2, [3072 x 3072] 12.3 -> 8.5, [2560 x 2560] 7.9 -> 6.8,
-// [1024 x 9728] M = 16 10.1 -> 8.2 us.
-// resid: for the residual-add form, which the unsplit kernels do not have
-// (the tile kernel is its alternative): from 1 row, and where the unsplit
-// kernels would be preferred for a plain product.
-SplitPlan plan_split(int k, int n, int m, bool resid = false) {
-  SplitPlan best{0, 0, 0, 0, false};
-  if (k % 512 != 0 || k / 512 < 2 || m < (resid ? 1 : kSplitMinM) || m > 2 * kRows) return best;
+// The rows kernel's plan: 64-row workgroups (four waves of one tile), 128
+// where that leaves more than 800 workgroups; two 512-k pieces per split
+// from K = 8192, one below.  Forced plans on 12 shapes (M = 8-30, weights
+// from HBM, the split-sum launch included) put it within 4% of the fastest
+// rows plan on each ([19456 x 2560] M = 30: 128-row workgroups 15.8 us
+// against 17.0 at 64; [2560 x 9728]: two pieces 12.4 / 10.3 / 9.6 us at M =
+// 30 / 16 / 8 against 13.4 / 10.9 / 10.0 with one).
+SplitPlan rows_plan(int k, int n, int m) {
   const int pieces = k / 512;
+  const int per = pieces >= 16 ? 2 : 1;
+  const int splits = (pieces + per - 1) / per;
+  (void)m;
+  return SplitPlan{per, splits, (long)((n + 63) / 64) * splits > 800 ? 2 : 1, 4, true};
+}
+
+// Weight bytes from which the rows kernel's split runs where an unsplit
+// kernel would finish in one round of the CUs: [9728 x 2560] M = 16 (12.5
+// MB) 10.3 -> 9.6 us; [6144 x 2560] M = 16 (7.9 MB) ties (7.55 / 7.65).
+constexpr size_t kRowsOverOneRound = (size_t)10 << 20;
+
+// Whether (and how) the few-row product splits K: the rows kernel, from M =
+// 6 (from 1 row for the residual-add form, which the unsplit kernels do not
+// have) to 32, K % 512 == 0 with at least two pieces of 512.  Up to 16 rows
+// the unsplit kernels stay where they finish in one round of the CUs below
+// kRowsOverOneRound bytes of weights (the split's second launch costs more
+// than it saves: [2560 x 2560] M = 12 4.7 us unsplit, 6.1 split), and where
+// all of x fits LDS without the multi-tile kernel.  Past 16 rows it runs
+// wherever it plans; the tile kernel's 32-row tiles are its alternative (M =
+// 30, same box, the split-sum launch included: [9728 x 2560] 14.8 -> 11.7
+// us, [19456 x 2560] 18.9 -> 15.8, [6144 x 2560] 12.7 -> 9.1 against the
+// split kernel it replaced, [2560 x 9728] 17.6 -> 12.2).
+SplitPlan plan_split(int k, int n, int m, bool resid = false) {
+  const SplitPlan best{0, 0, 0, 0, false};
+  if (k % 512 != 0 || k / 512 < 2 || m < (resid ? 1 : kSplitMinM) || m > 2 * kRows) return best;
   const long tiles = (n + kRows - 1) / kRows;
-  // Up to 16 rows the unsplit kernels are the alternative: the multi-tile
-  // kernel where it plans (in one round of the CUs it stays; in more it is
-  // compared by the same wave work below), otherwise the kernels with all of
-  // x in LDS; past 16 rows (two token groups, this kernel only) the tile
-  // kernel is, from 512 row tiles on: M = 30 / 24 / 17 [6144 x 2560] 13.3 /
-  // 13.5 / 12.7 -> 12.8 / 12.1 / 10.1 us, [4096 x 2560] M = 30 12.6 -> 9.5
-  // split; [9728 x 2560] M = 30 / 20 15.0 / 13.8 on the tile kernel against
-  // 15.8 / 14.8 for the planned split, [19456 x 2560] M = 30 18.3 against 23
-  // or more for any split.
-  long lds_work = -1;
   if (m <= kRows && !resid) {
     const LdsPlan lp = plan_lds(k, n, m);
     if (lp.ok) {
       const long groups = (tiles + lp.tpw - 1) / lp.tpw;
-      if (groups <= 256) return best;
-      lds_work = (groups + 255) / 256 * ((k / kChunkK + kLdsWaves - 1) / kLdsWaves) * lp.tpw;
+      if (groups <= 256 && (size_t)n * k / 2 < kRowsOverOneRound) return best;
     } else if ((size_t)m * k * 2 <= (size_t)kXLdsMax) {
       return best;
     }
-  } else if (m > kRows && tiles >= 512) {
-    return best;
   }
-  const int tg = m > kRows ? 2 : 1;
-  long best_work = -1;
-  for (int tpw = 1; tpw <= 4; ++tpw) {
-    const long groups = (tiles + tpw - 1) / tpw;
-    for (int per = 1; per <= pieces; ++per) {
-      const int splits = (pieces + per - 1) / per;
-      if (splits < 2) continue;
-      // x slice budget: 64 KB beside the 32 KB of per-wave sums of one token
-      // group; 80 KB beside the 64 KB of two (32 rows then still take two
-      // 512-k pieces per split).
-      if (split_x_bytes(per, m) > (m > kRows ? 80 : 64) * 1024) continue;
-      const int u = std::max(1, std::min((per * 4 + kSplitWaves - 1) / kSplitWaves,
-                                         max_u_lds(tpw, kSplitWaves)));
-      const long work = (groups * splits + 255) / 256 * u * tpw * tg;
-      if (best_work < 0 || work < best_work ||
-          (work == best_work && (tpw > best.tpw || (tpw == best.tpw && splits < best.splits)))) {
-        best_work = work;
-        best = SplitPlan{tpw, per, splits, u, true};
-      }
-    }
-  }
-  // Against the multi-tile kernel in two or more rounds the split (a second
-  // launch, partial sums) must save more than a quarter of the wave work:
-  // [19456 x 2560] M = 12 / 16 (15 against 24) 21.6 / 22.4 -> 15.3 / 16.6 us.
-  // In one round the second launch costs more than the split saves:
-  // [2560 x 4096] M = 13 7.2 -> 8.3 us, [2560 x 2560] M = 12 4.7 -> 6.1,
-  // [1024 x 2560] M = 12 4.6 -> 5.3 us when split.
-  if (lds_work >= 0 && best.ok && best_work * 4 >= lds_work * 3) best.ok = false;
-  return best;
+  return rows_plan(k, n, m);
 }
 
-template <int T, int TPW, int U>
-hipError_t launch_split_tu(const uint32_t* w, const uint16_t* s, const uint16_t* b,
-                           const uint16_t* x, float* ws, int k, int n, int m, const SplitPlan& p,
-                           bool vec, hipStream_t stream) {
-  if constexpr (U > max_u_lds(TPW, kSplitWaves)) {
-    return hipErrorInvalidValue;
-  } else {
-    const dim3 grid((unsigned)((n + kRows * TPW - 1) / (kRows * TPW)), (unsigned)p.splits);
-    if (m > kRows)
-      hipLaunchKernelGGL((qskinny_split_kernel<T, TPW, kSplitWaves, U, 2>), grid,
-                         dim3(64 * kSplitWaves), split_x_bytes(p.per, m), stream, w, s, b, x, ws,
-                         m, n, k, p.per, vec);
-    else
-      hipLaunchKernelGGL((qskinny_split_kernel<T, TPW, kSplitWaves, U, 1>), grid,
-                         dim3(64 * kSplitWaves), split_x_bytes(p.per, m), stream, w, s, b, x, ws,
-                         m, n, k, p.per, vec);
-    return hipGetLastError();
-  }
+template <int T, int R, int W, int CH>
+hipError_t launch_rows_k(const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                         const uint16_t* x, float* ws, int k, int n, int m, const SplitPlan& p,
+                         bool vec, hipStream_t stream) {
+  const int wg_rows = kRows * R * W;
+  const dim3 grid((unsigned)((n + wg_rows - 1) / wg_rows), (unsigned)p.splits);
+  if (m > kRows)
+    hipLaunchKernelGGL((qskinny_rows_kernel<T, R, W, 2, CH>), grid, dim3(64 * W),
+                       split_x_bytes(p.per, m), stream, w, s, b, x, ws, m, n, k, p.per, vec);
+  else
+    hipLaunchKernelGGL((qskinny_rows_kernel<T, R, W, 1, CH>), grid, dim3(64 * W),
+                       split_x_bytes(p.per, m), stream, w, s, b, x, ws, m, n, k, p.per, vec);
+  return hipGetLastError();
 }
 
-template <int T, int TPW>
-hipError_t launch_split_t(const uint32_t* w, const uint16_t* s, const uint16_t* b,
+template <int T, int R, int W>
+hipError_t launch_rows_rw(const uint32_t* w, const uint16_t* s, const uint16_t* b,
                           const uint16_t* x, float* ws, int k, int n, int m, const SplitPlan& p,
                           bool vec, hipStream_t stream) {
-  switch (p.u) {
-    case 1: return launch_split_tu<T, TPW, 1>(w, s, b, x, ws, k, n, m, p, vec, stream);
-    case 2: return launch_split_tu<T, TPW, 2>(w, s, b, x, ws, k, n, m, p, vec, stream);
-    case 3: return launch_split_tu<T, TPW, 3>(w, s, b, x, ws, k, n, m, p, vec, stream);
-    case 4: return launch_split_tu<T, TPW, 4>(w, s, b, x, ws, k, n, m, p, vec, stream);
-    case 5:
-    case 6: return launch_split_tu<T, TPW, 6>(w, s, b, x, ws, k, n, m, p, vec, stream);
-    default: return launch_split_tu<T, TPW, 8>(w, s, b, x, ws, k, n, m, p, vec, stream);
+  if (p.per == 1) return launch_rows_k<T, R, W, 4>(w, s, b, x, ws, k, n, m, p, vec, stream);
+  if (p.per == 2) return launch_rows_k<T, R, W, 8>(w, s, b, x, ws, k, n, m, p, vec, stream);
+  return hipErrorInvalidValue;
+}
+
+// The rows kernel: 1 or 2 tiles per wave, 4 or 8 waves, 1 or 2 pieces of 512 k.
+template <int T>
+hipError_t launch_rows(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* x,
+                       float* ws, int k, int n, int m, const SplitPlan& p, bool vec,
+                       hipStream_t stream) {
+  if (p.rw == 4) {
+    if (p.rr == 1) return launch_rows_rw<T, 1, 4>(w, s, b, x, ws, k, n, m, p, vec, stream);
+    if (p.rr == 2) return launch_rows_rw<T, 2, 4>(w, s, b, x, ws, k, n, m, p, vec, stream);
+  } else if (p.rw == 8) {
+    if (p.rr == 1) return launch_rows_rw<T, 1, 8>(w, s, b, x, ws, k, n, m, p, vec, stream);
+    if (p.rr == 2) return launch_rows_rw<T, 2, 8>(w, s, b, x, ws, k, n, m, p, vec, stream);
   }
+  return hipErrorInvalidValue;
 }
 
 // Rows of the fused split sum + residual + RMSNorm: N % 8 == 0, at most 8192
@@ -1223,12 +1183,7 @@ hipError_t launch_split_partials(const uint32_t* w, const uint16_t* s, const uin
                                  const uint16_t* x, float* ws, int k, int n, int m,
                                  const SplitPlan& p, hipStream_t stream) {
   const bool vec = n % 4 == 0 && ((uintptr_t)ws & 15u) == 0;
-  switch (p.tpw) {
-    case 1: return launch_split_t<T, 1>(w, s, b, x, ws, k, n, m, p, vec, stream);
-    case 2: return launch_split_t<T, 2>(w, s, b, x, ws, k, n, m, p, vec, stream);
-    case 3: return launch_split_t<T, 3>(w, s, b, x, ws, k, n, m, p, vec, stream);
-    default: return launch_split_t<T, 4>(w, s, b, x, ws, k, n, m, p, vec, stream);
-  }
+  return launch_rows<T>(w, s, b, x, ws, k, n, m, p, vec, stream);
 }
 
 template <int T>

@@ -234,23 +234,24 @@ def test_split_k_dispatcher(m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k,splits", [(16, 2560, 9728, 10), (12, 2560, 9728, 10),
-                                          (12, 1000, 4608, 5), (8, 2560, 9728, 10),
-                                          (16, 1024, 9728, 10), (13, 1030, 4608, 5),
-                                          (6, 2560, 9728, 10), (16, 2560, 4096, 4),
-                                          (16, 19456, 2560, 3), (16, 4096, 9728, 10),
+                                          (12, 1000, 4608, 9), (8, 2560, 9728, 10),
+                                          (16, 1024, 9728, 10), (13, 1030, 4608, 9),
+                                          (6, 2560, 9728, 10), (16, 2560, 4096, 8),
+                                          (16, 19456, 2560, 5), (16, 4096, 9728, 10),
                                           (5, 2560, 9728, 1), (4, 2560, 9728, 1),
-                                          (16, 9728, 2560, 1), (16, 6144, 2560, 1),
-                                          (12, 12288, 2560, 1), (13, 2560, 4096, 1),
+                                          (16, 9728, 2560, 5), (16, 6144, 2560, 1),
+                                          (12, 12288, 2560, 5), (13, 2560, 4096, 1),
                                           (12, 2560, 2560, 1), (12, 1024, 2560, 1),
                                           (3, 2560, 9728, 1)])
 def test_few_row_split_plan(m, n, k, splits):
-    """imq_qmm_plan reports the few-row kernel's K split and its workspace:
-    taken from M = 6 where x does not fit LDS ([2560 x 9728], [1000 x 4608],
-    [2560 x 4096] at M = 16), and where it saves a quarter of the multi-tile
-    kernel's wave work ([19456 x 2560] M = 16: two rounds of 304 workgroups
-    of four tiles); not at M <= 5, nor where the multi-tile kernel fits one
-    round of the CUs ([9728 x 2560], [6144 x 2560], [12288 x 2560], [2560 x
-    4096] at M = 13, [2560 x 2560] and [1024 x 2560] at M = 12)."""
+    """imq_qmm_plan reports the few-row K split and its workspace: taken from
+    M = 6 where x does not fit LDS ([2560 x 9728], [1000 x 4608], [2560 x
+    4096] at M = 16), where the multi-tile kernel would need two rounds of the
+    CUs ([19456 x 2560] M = 16) or streams 10 MiB of weights or more
+    ([9728 x 2560] M = 16, [12288 x 2560] M = 12); not at M <= 5, nor where the
+    multi-tile kernel fits one round below that ([6144 x 2560], [2560 x 4096]
+    at M = 13, [2560 x 2560] and [1024 x 2560] at M = 12).  Splits: one 512-k
+    piece each below K = 8192, two from there."""
     plan = imq.qmm_plan(m, n, k, torch.bfloat16)
     assert plan["kernel"] == "few_row", plan
     assert plan["splits"] == splits, plan
@@ -258,21 +259,19 @@ def test_few_row_split_plan(m, n, k, splits):
 
 
 @pytest.mark.parametrize("m,n,k,splits", [(17, 2560, 9728, 10), (30, 2560, 9728, 10),
-                                          (32, 2560, 9728, 10), (30, 2560, 4096, 4),
-                                          (24, 1024, 2560, 3), (24, 1030, 4608, 5),
-                                          (30, 9728, 2560, 0), (30, 2560, 1024, 2),
-                                          (33, 2560, 9728, 0), (20, 2560, 2560, 3),
-                                          (30, 3072, 3072, 3), (24, 2560, 3840, 0),
-                                          (20, 17, 1024, 2), (30, 6144, 2560, 3),
-                                          (17, 6144, 2560, 3), (30, 4096, 2560, 3),
-                                          (20, 9728, 2560, 0), (30, 19456, 2560, 0)])
+                                          (32, 2560, 9728, 10), (30, 2560, 4096, 8),
+                                          (24, 1024, 2560, 5), (24, 1030, 4608, 9),
+                                          (30, 9728, 2560, 5), (30, 2560, 1024, 2),
+                                          (33, 2560, 9728, 0), (20, 2560, 2560, 5),
+                                          (30, 3072, 3072, 6), (24, 2560, 3840, 0),
+                                          (20, 17, 1024, 2), (30, 6144, 2560, 5),
+                                          (17, 6144, 2560, 5), (30, 4096, 2560, 5),
+                                          (20, 9728, 2560, 5), (30, 19456, 2560, 5)])
 def test_few_row_split_past_16_rows_plan(m, n, k, splits):
-    """17 to 32 rows take the few-row kernel's K split (two token groups per
-    weight fragment) where it plans one: fewer than 512 row tiles and K % 512
-    == 0 with at least two 512-k pieces; the splits are those of the plan
-    with the least wave work on the busiest CU (two pieces per split where
-    the x slice allows it).  The others here (splits 0) run the tile kernel:
-    608 and 1216 row tiles, 33 rows, K = 3840."""
+    """17 to 32 rows take the few-row K split (two token groups per weight
+    fragment) wherever K % 512 == 0 with at least two 512-k pieces, at any
+    count of row tiles; one piece per split below K = 8192, two from there.
+    The others here (splits 0) run the tile kernel: 33 rows, K = 3840."""
     plan = imq.qmm_plan(m, n, k, torch.bfloat16)
     if splits:
         assert plan["kernel"] == "few_row" and plan["splits"] == splits, plan
