@@ -1104,17 +1104,22 @@ size_t split_x_bytes(int per, int m) { return (size_t)m * (1024 * (size_t)per + 
 
 // The rows kernel's plan: 64-row workgroups (four waves of one tile), 128
 // where that leaves more than 800 workgroups; two 512-k pieces per split
-// from K = 8192, one below.  Forced plans on 12 shapes (M = 8-30, weights
+// from K = 8192, and from K = 4096 where that still leaves 160 workgroups of
+// 64 rows, one below.  Forced plans on 12 shapes (M = 8-30, weights
 // from HBM, the split-sum launch included) put it within 4% of the fastest
 // rows plan on each ([19456 x 2560] M = 30: 128-row workgroups 15.8 us
 // against 17.0 at 64; [2560 x 9728]: two pieces 12.4 / 10.3 / 9.6 us at M =
-// 30 / 16 / 8 against 13.4 / 10.9 / 10.0 with one).
+// 30 / 16 / 8 against 13.4 / 10.9 / 10.0 with one; [2560 x 4096] M = 30
+// 8.9 against 9.0; [6144 x 2560] and [3072 x 3072] one piece, 9.2 and 8.1
+// us against 10.8 and 8.5; [1000 x 4608] M = 12 / 24 one piece, 5.8 / 6.9 us
+// against 6.4 / 7.9 on 80 workgroups).
 SplitPlan rows_plan(int k, int n, int m) {
   const int pieces = k / 512;
-  const int per = pieces >= 16 ? 2 : 1;
+  const long groups = (n + 63) / 64;
+  const int per = pieces >= 16 || (pieces >= 8 && groups * ((pieces + 1) / 2) >= 160) ? 2 : 1;
   const int splits = (pieces + per - 1) / per;
   (void)m;
-  return SplitPlan{per, splits, (long)((n + 63) / 64) * splits > 800 ? 2 : 1, 4, true};
+  return SplitPlan{per, splits, groups * splits > 800 ? 2 : 1, 4, true};
 }
 
 // Weight bytes from which the rows kernel's split runs where an unsplit

@@ -236,7 +236,7 @@ def test_split_k_dispatcher(m, n, k):
 @pytest.mark.parametrize("m,n,k,splits", [(16, 2560, 9728, 10), (12, 2560, 9728, 10),
                                           (12, 1000, 4608, 9), (8, 2560, 9728, 10),
                                           (16, 1024, 9728, 10), (13, 1030, 4608, 9),
-                                          (6, 2560, 9728, 10), (16, 2560, 4096, 8),
+                                          (6, 2560, 9728, 10), (16, 2560, 4096, 4),
                                           (16, 19456, 2560, 5), (16, 4096, 9728, 10),
                                           (5, 2560, 9728, 1), (4, 2560, 9728, 1),
                                           (16, 9728, 2560, 5), (16, 6144, 2560, 1),
@@ -250,8 +250,9 @@ def test_few_row_split_plan(m, n, k, splits):
     CUs ([19456 x 2560] M = 16) or streams 10 MiB of weights or more
     ([9728 x 2560] M = 16, [12288 x 2560] M = 12); not at M <= 5, nor where the
     multi-tile kernel fits one round below that ([6144 x 2560], [2560 x 4096]
-    at M = 13, [2560 x 2560] and [1024 x 2560] at M = 12).  Splits: one 512-k
-    piece each below K = 8192, two from there."""
+    at M = 13, [2560 x 2560] and [1024 x 2560] at M = 12).  Splits: two 512-k
+    pieces each from K = 8192, and from K = 4096 where that leaves 160
+    workgroups of 64 rows ([2560 x 4096]; not [1000 x 4608]), else one."""
     plan = imq.qmm_plan(m, n, k, torch.bfloat16)
     assert plan["kernel"] == "few_row", plan
     assert plan["splits"] == splits, plan
@@ -259,7 +260,7 @@ def test_few_row_split_plan(m, n, k, splits):
 
 
 @pytest.mark.parametrize("m,n,k,splits", [(17, 2560, 9728, 10), (30, 2560, 9728, 10),
-                                          (32, 2560, 9728, 10), (30, 2560, 4096, 8),
+                                          (32, 2560, 9728, 10), (30, 2560, 4096, 4),
                                           (24, 1024, 2560, 5), (24, 1030, 4608, 9),
                                           (30, 9728, 2560, 5), (30, 2560, 1024, 2),
                                           (33, 2560, 9728, 0), (20, 2560, 2560, 5),
@@ -270,7 +271,7 @@ def test_few_row_split_plan(m, n, k, splits):
 def test_few_row_split_past_16_rows_plan(m, n, k, splits):
     """17 to 32 rows take the few-row K split (two token groups per weight
     fragment) wherever K % 512 == 0 with at least two 512-k pieces, at any
-    count of row tiles; one piece per split below K = 8192, two from there.
+    count of row tiles; pieces per split as for 16 rows and fewer.
     The others here (splits 0) run the tile kernel: 33 rows, K = 3840."""
     plan = imq.qmm_plan(m, n, k, torch.bfloat16)
     if splits:
