@@ -510,10 +510,12 @@ def bench_x_embedder(imq, synth, torch) -> dict:
     lat = torch.randn((m, k), device="cuda")
     y = torch.empty((m, n), device="cuda")
     x16 = torch.empty((m, k), dtype=torch.float16, device="cuda")
+    # Six sandwiches per captured graph (one launch pair per graph would time
+    # the graph launch more than the kernels).
     launches = [lambda: imq.cast_prescale(lat, 16.0, torch.float16, out=x16),
                 lambda: imq.qmm_postscale(x16, lin.weight, lin.scales, lin.biases, 16.0, out=y)]
-    ms = time_graph(launches, replays=10) * 2
-    qmm_ms = time_graph(launches[1:], replays=10)
+    ms = time_graph(launches * 6, replays=10) * 2
+    qmm_ms = time_graph(launches[1:] * 12, replays=10)
     tf = 2.0 * m * n * k / (qmm_ms * 1e-3) / 1e12
     byts = m * n * 4 + m * k * 2 + n * k // 2
     log(f"x_embedder sandwich M={m} N={n} K={k}: {ms * 1e3:.1f} us (qmm + post-scale "
