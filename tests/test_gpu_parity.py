@@ -333,7 +333,8 @@ def test_few_row_split_repeated_and_replayed():
                                    (14, 3000, 4096), (12, 1000, 4608), (13, 1030, 4608),
                                    (3, 1001, 1024), (7, 1030, 2560), (8, 17, 512),
                                    (17, 2560, 9728), (30, 2560, 4096), (32, 2560, 9728),
-                                   (24, 1030, 4608), (30, 1000, 4608), (20, 520, 9728)])
+                                   (24, 1030, 4608), (30, 1000, 4608), (20, 520, 9728),
+                                   (29, 19400, 2560), (20, 2100, 4608), (7, 4100, 9728)])
 def test_few_row_matrix_core_dispatch(dtype, m, n, k):
     """3 <= M <= 16 through the dispatcher.  The 16-row weight-streaming kernel
     stages x in LDS when M K 2, rounded up to whole wave instructions, fits
@@ -345,20 +346,25 @@ def test_few_row_matrix_core_dispatch(dtype, m, n, k):
     (partial row tiles; K = 512 is one span per wave pair), 1030 x 2560 at
     M = 7 (N % 4 != 0: single-element stores).
     12 <= M <= 16 with K <= 4096 (K % 512 == 0) take the multi-tile kernel
-    with x in LDS: [9728 x 2560] at M = 12 and 16 (three 16-row tiles per
-    workgroup, the last workgroup two), 3000 x 4096 at M = 14 (a partial last
-    tile), 1001 x 1024 at M = 16.  N = 1001 and 17 end in a partial row block
-    and take the single-element stores; K = 128 is one chunk; K % 128 != 0
-    (K = 192) runs the tiled kernel.  From M = 8, where x would stream from L2
-    and the 16-row workgroups are few or long, K is split over workgroups (fp32
-    partial sums added in order by a second kernel): [2560 x 9728] at M = 8 and
-    16, 1000 x 4608 at M = 12, 1030 x 4608 at M = 13 (N % 4 != 0: the
-    single-element partial stores and reduction).  17 to 32 rows run only that
-    split, with two token groups: [2560 x 9728] at M = 17 (the second group one
-    token) and 32, 2560 x 4096 at M = 30, 1030 x 4608 at M = 24, 1000 x 4608 at
-    M = 30, 520 x 9728 at M = 20 (a partial last row tile).  Oracle within tolerance, the same bits on
-    a second call, and one-hot rows reproduce the dequantized weights bit for
-    bit (a one-hot row has one nonzero product in one split)."""
+    with x in LDS where it fits one round of the CUs on less than 10 MiB of
+    weights: 3000 x 4096 at M = 14 (a partial last tile), 1001 x 1024 at M =
+    16.  N = 1001 and 17 end in a partial row block and take the
+    single-element stores; K = 128 is one chunk; K % 128 != 0 (K = 192) runs
+    the tiled kernel.  From M = 6 where x does not fit LDS, and from 12 rows
+    where the multi-tile kernel would stream 10 MiB or more ([9728 x 2560] at
+    M = 12 and 16), K is split (the rows-per-wave kernel; fp32 partial sums
+    added in order by a second kernel): [2560 x 9728] at M = 6, 8 and 16, 1000
+    x 4608 at M = 12, 1030 x 4608 at M = 13 (N % 4 != 0: the single-element
+    partial stores and reduction), 4100 x 9728 at M = 7 (a partial last
+    workgroup of 64 rows).  17 to 32 rows run only that split, with two token
+    groups: [2560 x 9728] at M = 17 (the second group one token) and 32, 2560
+    x 4096 at M = 30, 1030 x 4608 at M = 24, 1000 x 4608 at M = 30, 520 x 9728
+    at M = 20 (a partial last row tile), 19400 x 2560 at M = 29 (two tiles per
+    wave, the last tile partial), 2100 x 4608 at M = 20 (two 512-k pieces per
+    split, the last split one: its second chunk block clamped).  Oracle
+    within tolerance, the same bits on a second call, and one-hot rows
+    reproduce the dequantized weights bit for bit (a one-hot row has one
+    nonzero product in one split)."""
     note(f"few-row dispatch {dtype} M={m} N={n} K={k}")
     p = synth.make_problem(m, n, k, seed=23)
     x, w, s, b = synth.to_device(p)
