@@ -373,15 +373,24 @@ constexpr int kBigKG = 2;                // quantization groups per K-step
 constexpr int kBigSlices = 4 * kBigKG;   // k-slices of 16 per K-step
 constexpr int kBigUnroll = 4;            // K-steps per loop iteration (two scale blocks)
 
+// PD: how many K-steps ahead a step's loads are issued.  Tiles of up to 128
+// rows take two: a K-step of a 64 x 128 tile lasts about 0.4 us, less than a
+// weight load from HBM or the last-level cache takes to return, so with one
+// step of lead the wave waited on it (M = 512 [2560 x 4096] 25.8 us with the
+// weights from HBM against 20.4 with them cached).  Their LDS ring then has
+// four stages and the weights four register sets; taller tiles keep one step
+// of lead and two stages (the headline's 224-row tile fills the LDS with two).
 template <int MT>
 struct BigCfg {
   static constexpr int kBM = 32 * MT;
   static constexpr int kSlots = kBM * 8 * kBigKG;     // 16-byte LDS slots per stage
   static constexpr int kA = kSlots / kThreads;        // activation slots per thread per step
+  static constexpr int kPD = MT <= 4 ? 2 : 1;         // prefetch distance in K-steps
+  static constexpr int kStages = 2 * kPD;             // LDS stages and weight register sets
 };
 
 struct BigRing {
-  uint4* a[2];
+  uint4* a[4];
 };
 
 template <int MT>
@@ -450,7 +459,7 @@ __device__ __forceinline__ constexpr int a_split(int p) {
 // 0-15 (i = 0) and 16-31 (i = 1), 64 bytes each.
 template <int MT, int NT, int ST>
 __device__ __forceinline__ void big_issue_w(uint32_t gs, const BigSrc<MT>& src,
-                                            u32x4_t (&wr)[2][2][kBigKG]) {
+                                            u32x4_t (&wr)[BigCfg<MT>::kStages][2][kBigKG]) {
 #pragma unroll
   for (int i = 0; i < kBigKG; ++i)
 #pragma unroll
@@ -516,15 +525,34 @@ __device__ __forceinline__ void big_mfmas(const BigFrags<MT>& f, f32x16_t (&acc)
 
 // One K-step.  S = g % kBigUnroll: stage and weight registers S % 2, dword S
 // of the scale / bias blocks in slot 0 (slot 1: the next four steps').
+// Vector-memory loads a thread issues in a step with position S in its block:
+// the activation parts, the weights and, at S = 0, the next scale block.
+template <int MT, int NT, int S>
+constexpr int big_step_loads() {
+  return BigCfg<MT>::kA + NT * kBigKG + (S == 0 ? 2 * NT : 0);
+}
+
 template <int T, int MT, int NT, int S>
 __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
                                          const BigSrc<MT>& src, uint4 (&sblk)[2][2],
-                                         uint4 (&bblk)[2][2], u32x4_t (&wr)[2][2][kBigKG],
+                                         uint4 (&bblk)[2][2],
+                                         u32x4_t (&wr)[BigCfg<MT>::kStages][2][kBigKG],
                                          BigFrags<MT>& f, f32x16_t (&acc)[MT][NT], int wave,
                                          int arow0, int r32, int h) {
-  constexpr int ST = S % 2;
+  constexpr int PD = BigCfg<MT>::kPD;
+  constexpr int ST = S % BigCfg<MT>::kStages;       // this step's stage and weight set
+  constexpr int SN = (S + PD) % BigCfg<MT>::kStages;  // step g + PD's
   constexpr int kMfma = NT * MT;
-  IMQ_WAIT_VM_LGKM_0();
+  // This wave's loads of step g have landed: with one step of lead, all of
+  // its loads; with two, all but those the previous step issued (loads
+  // return in issue order).  After the barrier every wave's have.
+  if constexpr (PD == 1) {
+    IMQ_WAIT_VM_LGKM_0();
+  } else {
+    constexpr int n = big_step_loads<MT, NT, (S + kBigUnroll - 1) % kBigUnroll>();
+    static_assert(n <= 63, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4));  // vmcnt(n) lgkmcnt(0)
+  }
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
@@ -543,9 +571,9 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
       bblk[1][nt] = load_param_block(src.br, src.p_off[nt], nb);
     }
   }
-  const uint32_t gs1 = (uint32_t)min(g + 1, steps - 1);
-  big_issue_w<MT, NT, ST ^ 1>(gs1, src, wr);
-  big_issue_a<MT, ST ^ 1>(0, gs1, ring, src, wave);
+  const uint32_t gs1 = (uint32_t)min(g + PD, steps - 1);
+  big_issue_w<MT, NT, SN>(gs1, src, wr);
+  big_issue_a<MT, SN>(0, gs1, ring, src, wave);
   big_mfmas<T, MT, NT, 1>(f, acc);  // the previous step's last k-slice
   {
     // LDS reads first, then each deferred MFMA followed by a share of the
@@ -566,7 +594,7 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
 #pragma unroll
   for (int t = 0; t + 1 < kBigSlices; ++t) {
     __builtin_amdgcn_sched_barrier(0);
-    if (t + 1 < kIssuePts) big_issue_a<MT, ST ^ 1>(t + 1, gs1, ring, src, wave);
+    if (t + 1 < kIssuePts) big_issue_a<MT, SN>(t + 1, gs1, ring, src, wave);
     if (t & 1) {
       big_operands<T, MT, NT, 0>(t + 1, at, wr[ST], gp, f, arow0, r32, h);
       big_mfmas<T, MT, NT, 1>(f, acc);
@@ -691,8 +719,9 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   static_assert(NT == 1 || NT == 2, "one or two 32-column tiles per wave");
   static_assert(!EP::kPair || NT == 2, "a gate/up pair takes two column tiles per wave");
   using C = BigCfg<MT>;
-  __shared__ uint4 a_st0[C::kSlots], a_st1[C::kSlots];
-  const BigRing ring = {{a_st0, a_st1}};
+  constexpr int kExtra = C::kStages > 2 ? C::kSlots : 1;  // stages 2, 3 (two steps of lead)
+  __shared__ uint4 a_st0[C::kSlots], a_st1[C::kSlots], a_st2[kExtra], a_st3[kExtra];
+  const BigRing ring = {{a_st0, a_st1, a_st2, a_st3}};
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -753,10 +782,12 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.f;
 
-  // Prologue: the first scale block, the loads of step 0, and zero operands
-  // for the first step's deferred MFMAs (they add nothing).
+  // Prologue: the first scale block, the loads of the first PD steps (step
+  // g0 + 1's last: with two steps of lead the first step's wait leaves them
+  // in flight), and zero operands for the first step's deferred MFMAs (they
+  // add nothing).
   uint4 sblk[2][2], bblk[2][2];
-  u32x4_t wr[2][2][kBigKG];
+  u32x4_t wr[C::kStages][2][kBigKG];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     sblk[0][nt] = load_param_block(src.sr, src.p_off[nt], (uint32_t)g0);
@@ -765,6 +796,12 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
   big_issue_w<MT, NT, 0>((uint32_t)g0, src, wr);
 #pragma unroll
   for (int p = 0; p < kIssuePts; ++p) big_issue_a<MT, 0>(p, (uint32_t)g0, ring, src, wave);
+  if constexpr (C::kPD == 2) {
+    const uint32_t gn = (uint32_t)min(g0 + 1, g1 - 1);
+    big_issue_w<MT, NT, 1>(gn, src, wr);
+#pragma unroll
+    for (int p = 0; p < kIssuePts; ++p) big_issue_a<MT, 1>(p, gn, ring, src, wave);
+  }
   BigFrags<MT> f;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) f.a[1][mt] = u32x4_t{0u, 0u, 0u, 0u};
@@ -991,6 +1028,10 @@ BigPlan pick_big_plan(int m, int n, int k, int cus, bool small, bool split, bool
     if (nt == 1 && pair) continue;
     const int tiles_n = (n + 128 * nt - 1) / (128 * nt);
     for (int mt : {8, 7, 6, 5, 4, 2, 1}) {
+      // 32 x 128 tiles are not planned: that instantiation spills registers
+      // to scratch memory (the 32 x 256 tile or the few-row kernel take
+      // those shapes).
+      if (nt == 1 && mt == 1) continue;
       const long tiles = (long)((m + 32 * mt - 1) / (32 * mt)) * tiles_n;
       const int max_splits = split && tiles < cus ? std::max(1, steps / 2) : 1;
       for (int sp = 1; sp <= max_splits; ++sp) {
