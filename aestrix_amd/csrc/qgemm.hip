@@ -532,7 +532,12 @@ constexpr int big_step_loads() {
   return BigCfg<MT>::kA + NT * kBigKG + (S == 0 ? 2 * NT : 0);
 }
 
-template <int T, int MT, int NT, int S>
+// TAIL: one of the split's last two steps after the unrolled loop.  With
+// two steps of lead those issue no loads (every step they would load lies
+// past the split), and the second waits for everything: the count a step's
+// wait leaves in flight must match what the previous step really issued, and
+// loads whose registers are never read again are dropped by the compiler.
+template <int T, int MT, int NT, int S, bool TAIL = false>
 __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
                                          const BigSrc<MT>& src, uint4 (&sblk)[2][2],
                                          uint4 (&bblk)[2][2],
@@ -543,10 +548,11 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
   constexpr int ST = S % BigCfg<MT>::kStages;       // this step's stage and weight set
   constexpr int SN = (S + PD) % BigCfg<MT>::kStages;  // step g + PD's
   constexpr int kMfma = NT * MT;
+  constexpr bool kIssue = !(TAIL && PD == 2);  // this step issues the loads of step g + PD
   // This wave's loads of step g have landed: with one step of lead, all of
   // its loads; with two, all but those the previous step issued (loads
   // return in issue order).  After the barrier every wave's have.
-  if constexpr (PD == 1) {
+  if constexpr (PD == 1 || (TAIL && S == 1)) {
     IMQ_WAIT_VM_LGKM_0();
   } else {
     constexpr int n = big_step_loads<MT, NT, (S + kBigUnroll - 1) % kBigUnroll>();
@@ -561,7 +567,7 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
   big_swap_w<NT>(wr[ST]);
   const GroupParams gp = group_params<T, S, NT>(sblk[0], bblk[0], h);
   big_operands<T, MT, NT, 0>(0, at, wr[ST], gp, f, arow0, r32, h);
-  if constexpr (S == 0) {
+  if constexpr (S == 0 && kIssue) {
     // The next block (steps g+4 .. g+7) goes to slot 1; the K loop moves it to
     // slot 0 after step g+3.
     const uint32_t nb = (uint32_t)min(g + 4, steps - 2);
@@ -572,13 +578,16 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
     }
   }
   const uint32_t gs1 = (uint32_t)min(g + PD, steps - 1);
-  big_issue_w<MT, NT, SN>(gs1, src, wr);
-  big_issue_a<MT, SN>(0, gs1, ring, src, wave);
+  if constexpr (kIssue) {
+    big_issue_w<MT, NT, SN>(gs1, src, wr);
+    big_issue_a<MT, SN>(0, gs1, ring, src, wave);
+  }
   big_mfmas<T, MT, NT, 1>(f, acc);  // the previous step's last k-slice
   {
     // LDS reads first, then each deferred MFMA followed by a share of the
     // loads and of slice 0's dequant.
-    constexpr int kVmem = NT * kBigKG + a_split<MT>(1) + (S == 0 ? 2 * NT : 0);
+    constexpr int kVmem =
+        kIssue ? NT * kBigKG + a_split<MT>(1) + (S == 0 ? 2 * NT : 0) : 0;
     constexpr int kVmemPer = (kVmem + kMfma - 1) / kMfma;
     constexpr int kValuPer = (NT * 17 + 4 * NT + kMfma - 1) / kMfma;
 #pragma unroll
@@ -586,7 +595,7 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
 #pragma unroll
     for (int i = 0; i < kMfma; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x020, kVmemPer, 0);   // VMEM read
+      if (kVmemPer > 0) __builtin_amdgcn_sched_group_barrier(0x020, kVmemPer, 0);  // VMEM read
       __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);   // VALU
     }
   }
@@ -594,7 +603,7 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
 #pragma unroll
   for (int t = 0; t + 1 < kBigSlices; ++t) {
     __builtin_amdgcn_sched_barrier(0);
-    if (t + 1 < kIssuePts) big_issue_a<MT, SN>(t + 1, gs1, ring, src, wave);
+    if (kIssue && t + 1 < kIssuePts) big_issue_a<MT, SN>(t + 1, gs1, ring, src, wave);
     if (t & 1) {
       big_operands<T, MT, NT, 0>(t + 1, at, wr[ST], gp, f, arow0, r32, h);
       big_mfmas<T, MT, NT, 1>(f, acc);
@@ -607,7 +616,8 @@ __device__ __forceinline__ void big_step(int g, int steps, const BigRing& ring,
     // one of the next step's activation loads, so a single wave keeps the
     // matrix core fed while it dequantizes.
     constexpr int kValuPer = (NT * 17 + kMfma - 1) / kMfma;
-    const int n_dma = t + 1 < kIssuePts ? a_split<MT>(t + 2) - a_split<MT>(t + 1) : 0;
+    const int n_dma =
+        kIssue && t + 1 < kIssuePts ? a_split<MT>(t + 2) - a_split<MT>(t + 1) : 0;
 #pragma unroll
     for (int i = 0; i < kMfma; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // MFMA
@@ -823,8 +833,9 @@ __global__ __launch_bounds__(kThreads, 1) void qgemm_big_kernel(
     }
   }
   if (g < g1) {
-    big_step<T, MT, NT, 0>(g, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
-    big_step<T, MT, NT, 1>(g + 1, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, NT, 0, true>(g, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32, h);
+    big_step<T, MT, NT, 1, true>(g + 1, g1, ring, src, sblk, bblk, wr, f, acc, wave, arow0, r32,
+                                 h);
   }
   big_mfmas<T, MT, NT, 1>(f, acc);  // the last step's last k-slice
 
