@@ -2,26 +2,28 @@
 machine code (CPU only: the code objects are taken out of aestrix_amd/libimq.so
 with the ROCm LLVM tools and disassembled).
 
-Two kernels count their own loads instead of waiting for all of them:
+Several kernels count their own loads instead of waiting for all of them
+(loads complete in issue order):
 
 * qgemm_big_kernel: a K-step's top waits with `s_waitcnt vmcnt(n)` (n the
-  loads the previous step issued, left in flight) and then `s_barrier`.  Loads
-  complete in issue order, so the wait is right only if every path from the
-  previous step-top barrier to it issues at least n loads -- which the
-  compiler can break by dropping loads whose registers are never read again.
-* qskinny_rows_kernel: the wait before its first barrier leaves the scale,
-  bias and weight loads in flight (n of them) while the x slice's LDS DMA
-  lands; every path from the last DMA load to it must issue at least n loads.
+  loads the previous step issued, left in flight) and then `s_barrier`.  The
+  wait is right only if every path from the previous step-top barrier to it
+  issues at least n loads -- which the compiler can break by dropping loads
+  whose registers are never read again.
+* the qGEMV and the few-row kernels (qgemv_kernel, qskinny_*_kernel): x goes
+  to LDS by direct buffer->LDS loads, then the weight, scale and bias loads;
+  a `vmcnt(n)` and a barrier make x visible while those n stay in flight, so
+  every path from the last LDS load to the wait must issue at least n others
+  -- which a load sunk past the wait into a conditional block breaks.
 
 A min-over-paths dataflow over each kernel's control-flow graph (branch
-targets from the disassembly) checks both.
+targets from the disassembly) checks every such wait.
 """
 
 from __future__ import annotations
 
 import os
 import re
-import shutil
 import subprocess
 from pathlib import Path
 
@@ -34,7 +36,7 @@ TOOLS = {n: LLVM / n for n in ("llvm-objcopy", "clang-offload-bundler", "llvm-re
                                "llvm-objdump")}
 TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
 MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
-KERNELS = ("qgemm_big_kernel", "qskinny_rows_kernel")
+KERNELS = ("qgemm_big_kernel", "qskinny_", "qgemv_kernel")
 
 INSN = re.compile(r"^\s+(\S+)\s*([^/]*?)\s*//\s*([0-9A-Fa-f]+):")
 TARGET_RE = re.compile(r"<(\S+)\+0x([0-9a-f]+)>")
@@ -135,17 +137,25 @@ def _step_waits(insns):
     return res
 
 
+def _family(sym: str) -> str:
+    m = re.search(r"N_1\d+(\w+?_kernel)", sym)
+    return m.group(1) if m else sym
+
+
 def test_kernels_found(disasm):
-    big = [s for s in disasm if "qgemm_big_kernel" in s]
-    rows = [s for s in disasm if "qskinny_rows_kernel" in s]
-    assert len(big) >= 20 and len(rows) >= 8, (len(big), len(rows))
+    fams = {}
+    for sym in disasm:
+        fams[_family(sym)] = fams.get(_family(sym), 0) + 1
+    for fam, least in (("qgemm_big_kernel", 20), ("qskinny_rows_kernel", 8), ("qgemv_kernel", 20),
+                       ("qskinny_lds8_kernel", 4), ("qskinny_half_kernel", 4)):
+        assert fams.get(fam, 0) >= least, (fam, fams)
 
 
 def test_tile_kernel_step_waits_cover_the_previous_step(disasm):
     bad = []
     checked = 0
     for sym, insns in disasm.items():
-        if "qgemm_big_kernel" not in sym:
+        if _family(sym) != "qgemm_big_kernel":
             continue
         cnt = _min_counts(insns, lambda mn, l: _is_load(mn), lambda mn, l: mn == "s_barrier")
         for i, n in _step_waits(insns):
@@ -156,17 +166,21 @@ def test_tile_kernel_step_waits_cover_the_previous_step(disasm):
     assert not bad, bad
 
 
-def test_rows_kernel_x_wait_leaves_only_later_loads(disasm):
+def test_lds_dma_waits_leave_only_later_loads(disasm):
     bad = []
+    checked = 0
     for sym, insns in disasm.items():
-        if "qskinny_rows_kernel" not in sym:
+        if _family(sym) == "qgemm_big_kernel" or not any(_is_dma(mn, l) for _, mn, l in insns):
             continue
-        first_bar = next(i for i, (_, mn, _) in enumerate(insns) if mn == "s_barrier")
-        waits = [(i, n) for i, n in _step_waits(insns) if i + 1 == first_bar]
-        assert waits, f"{sym}: no wait before the first barrier"
+        waits = [(i, n) for i, n in _step_waits(insns) if n > 0]
+        if _family(sym) == "qskinny_rows_kernel":
+            assert waits, f"{sym}: no wait before the first barrier"
         cnt = _min_counts(insns, lambda mn, l: _is_load(mn) and not _is_dma(mn, l),
                           lambda mn, l: _is_dma(mn, l))
-        i, n = waits[0]
-        if cnt[i] < n:
-            bad.append((sym[-60:], f"vmcnt({n}) after {cnt[i]} loads since the last DMA"))
+        for i, n in waits:
+            checked += 1
+            if cnt[i] < n:
+                bad.append((sym[-60:], hex(insns[i][0]),
+                            f"vmcnt({n}) after {cnt[i]} loads since the last LDS load"))
+    assert checked > 400
     assert not bad, bad
