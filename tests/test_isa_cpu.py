@@ -10,7 +10,7 @@ Several kernels count their own loads instead of waiting for all of them
   wait is right only if every path from the previous step-top barrier to it
   issues at least n loads -- which the compiler can break by dropping loads
   whose registers are never read again.
-* the qGEMV and the few-row kernels (qgemv_kernel, qskinny_*_kernel): x goes
+* the qGEMV and the few-row kernels (qgemv_*kernel, qskinny_*_kernel): x goes
   to LDS by direct buffer->LDS loads, then the weight, scale and bias loads;
   a `vmcnt(n)` and a barrier make x visible while those n stay in flight, so
   every path from the last LDS load to the wait must issue at least n others
@@ -36,7 +36,7 @@ TOOLS = {n: LLVM / n for n in ("llvm-objcopy", "clang-offload-bundler", "llvm-re
                                "llvm-objdump")}
 TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
 MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
-KERNELS = ("qgemm_big_kernel", "qskinny_", "qgemv_kernel")
+KERNELS = ("qgemm_big_kernel", "qskinny_", "qgemv_")
 
 INSN = re.compile(r"^\s+(\S+)\s*([^/]*?)\s*//\s*([0-9A-Fa-f]+):")
 TARGET_RE = re.compile(r"<(\S+)\+0x([0-9a-f]+)>")
