@@ -107,6 +107,36 @@ def test_halves_with_standins_reproduce_step_run(tdt, d):
     step.close()
 
 
+def _random_dims(seed: int) -> list[DitDims]:
+    rng = np.random.default_rng(seed)
+    return [DitDims(l_img=16 * int(rng.integers(1, 40)), l_txt=16 * int(rng.integers(1, 20)),
+                    dim=256 * int(rng.integers(1, 6)), ff_inner=256 * int(rng.integers(1, 9)),
+                    n_double=int(rng.integers(1, 3)), n_single=int(rng.integers(1, 3)))
+            for _ in range(6)]
+
+
+@pytest.mark.parametrize("d", _random_dims(41), ids=lambda d: f"img{d.l_img}_txt{d.l_txt}_"
+                         f"dim{d.dim}_ff{d.ff_inner}_{d.n_double}x{d.n_single}")
+@pytest.mark.parametrize("tdt", [torch.float16, torch.bfloat16])
+def test_step_at_seeded_random_dims(tdt, d):
+    """Seeded random plans (row counts in steps of 16, dim and ff_inner in steps of 256, one or
+    two blocks of each kind), so the tile plans, K splits and partial tiles of both chains vary:
+    the captured graph gives imq_dit_step_run's eager bits, the halves with the stand-ins give
+    them too, and the residual stays finite."""
+    note(f"dit step at random dims {tdt} {d}")
+    step, _ = conditioned_step(d, tdt, seed=d.l_img + d.dim)
+    rng = np.random.default_rng(d.l_txt + d.ff_inner)
+    h = torch.from_numpy(rng.standard_normal((d.l_img, d.dim)).astype(np.float32)).cuda()
+    e = torch.from_numpy(rng.standard_normal((d.l_txt, d.dim)).astype(np.float32)).cuda()
+    want = step.run(h, e, use_graph=False)
+    assert torch.isfinite(want).all()
+    assert torch.equal(step.run(h, e, use_graph=True), want), "graph differs from eager"
+    x = torch.cat([e, h]).contiguous()
+    blocks_by_halves(step, d, x, Buffers(d, tdt))
+    assert torch.equal(x, want), "halves differ from imq_dit_step_run"
+    step.close()
+
+
 @pytest.mark.parametrize("d", [TINY, SPLIT], ids=["tiny", "split_k"])
 @pytest.mark.parametrize("tdt", [torch.float16, torch.bfloat16])
 def test_denoise_by_halves_reproduces_denoise(tdt, d):
