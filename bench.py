@@ -48,6 +48,8 @@ below its 2400 MHz maximum within about 0.7 s.
 from __future__ import annotations
 
 import argparse
+import contextlib
+import gc
 import json
 import os
 import sys
@@ -82,6 +84,26 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+@contextlib.contextmanager
+def no_gc(collect: bool = False):
+    """Python's cyclic collector off inside a timed region: a full collection
+    of this process's objects takes 20-40 ms, and inside a host-bound timed
+    loop (the conditioning chain's one-timestep calls) it would be timed as
+    the library's (20 calls of 45 us read as 2 ms each when one landed there).
+    collect: run one first -- only where a pre-warm follows, since the GPU
+    idles through it and its clock drops (timed right after one, the tile
+    kernel's shapes ran 15-18% slower)."""
+    was = gc.isenabled()
+    if collect and was:
+        gc.collect()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
+            gc.enable()
+
+
 def time_events(fn, reps: int) -> float:
     """Average milliseconds per fn() over reps back-to-back calls (HIP events on
     torch's current stream, the stream the library launches on)."""
@@ -89,12 +111,13 @@ def time_events(fn, reps: int) -> float:
 
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(reps):
-        fn()
-    end.record()
-    torch.cuda.synchronize()
+    with no_gc():
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
     return start.elapsed_time(end) / reps
 
 
@@ -202,15 +225,16 @@ def time_single(fn_list, flush, reps: int = 24) -> float:
     import torch
 
     times = []
-    for r in range(reps):
-        flush()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record()
-        fn_list[r % len(fn_list)]()
-        end.record()
-        torch.cuda.synchronize()
-        times.append(start.elapsed_time(end))
+    with no_gc():
+        for r in range(reps):
+            flush()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            fn_list[r % len(fn_list)]()
+            end.record()
+            torch.cuda.synchronize()
+            times.append(start.elapsed_time(end))
     times.sort()
     return times[len(times) // 2]
 
@@ -243,11 +267,12 @@ def time_graph(launches, replays: int = 5) -> float:
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(replays):
-        g.replay()
-    end.record()
-    torch.cuda.synchronize()
+    with no_gc():
+        start.record()
+        for _ in range(replays):
+            g.replay()
+        end.record()
+        torch.cuda.synchronize()
     return start.elapsed_time(end) / (replays * len(launches))
 
 
@@ -533,7 +558,7 @@ def bench_dense_bf16(torch, imq, x, w, s, b, gpu: GpuState, steps: int = 20) -> 
     n = w.shape[0]
     wt = imq.dequantize(w, s, b).t().contiguous()  # [K, N] bf16
     y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-    with StateSampler(gpu) as smp:
+    with StateSampler(gpu) as smp, no_gc(collect=True):
         t_pre = time.perf_counter()
         while time.perf_counter() - t_pre < PREWARM_S:
             for _ in range(20):
@@ -648,11 +673,12 @@ def bench_dit_single_block(imq, torch) -> dict:
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(20):
-        block()
-    e1.record()
-    torch.cuda.synchronize()
+    with no_gc():
+        e0.record()
+        for _ in range(20):
+            block()
+        e1.record()
+        torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / 20
     flop = 2.0 * J * dim * (3 * dim + 2 * ffi) + 2.0 * J * (dim + ffi) * dim
     log(f"dit single block (f16, fused SwiGLU + gated residual): {ms:.3f} ms "
@@ -670,17 +696,18 @@ def bench_dit_step(torch) -> dict:
     h = torch.randn((d.l_img, d.dim), device="cuda")
     e = torch.randn((d.l_txt, d.dim), device="cuda")
     out = torch.empty((d.joint, d.dim), device="cuda")
-    t_pre = time.perf_counter()
-    while time.perf_counter() - t_pre < PREWARM_S:
-        step.run(h, e, out)
+    with no_gc(collect=True):
+        t_pre = time.perf_counter()
+        while time.perf_counter() - t_pre < PREWARM_S:
+            step.run(h, e, out)
+            torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            step.run(h, e, out)
+        e1.record()
         torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(10):
-        step.run(h, e, out)
-    e1.record()
-    torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / 10
     finite = bool(torch.isfinite(out).all().item())
     flop = d.step_flops()
@@ -828,25 +855,28 @@ def main() -> int:
     with StateSampler(gpu) as smp:
         # Untimed pre-warm until PREWARM_S of wall time has passed (the GPU
         # leaves its idle clock and settles at its loaded clock and power),
-        # then the W warmup steps.
-        t_pre = time.perf_counter()
-        while time.perf_counter() - t_pre < PREWARM_S:
-            for _ in range(20):
+        # then the W warmup steps.  The collector is off from before the
+        # pre-warm (a collection after it would idle the GPU for tens of ms
+        # and let the clock rise again before the timed steps).
+        with no_gc(collect=True):
+            t_pre = time.perf_counter()
+            while time.perf_counter() - t_pre < PREWARM_S:
+                for _ in range(20):
+                    imq.quantized_matmul(x, w, s, b, out=y)
+                torch.cuda.synchronize()
+            steady_from = smp.elapsed() - STEADY_S
+            for _ in range(args.warmup):
                 imq.quantized_matmul(x, w, s, b, out=y)
             torch.cuda.synchronize()
-        steady_from = smp.elapsed() - STEADY_S
-        for _ in range(args.warmup):
-            imq.quantized_matmul(x, w, s, b, out=y)
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        start.record()
-        for _ in range(args.steps):
-            imq.quantized_matmul(x, w, s, b, out=y)
-        end.record()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            start.record()
+            for _ in range(args.steps):
+                imq.quantized_matmul(x, w, s, b, out=y)
+            end.record()
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t0
     loaded = smp.summary(since=steady_from)
     after = gpu.snapshot()
     ms = start.elapsed_time(end) / args.steps
