@@ -191,12 +191,15 @@ __device__ __forceinline__ void norm_rows_in_lds(u32x4_t* xs, int M, int K, int 
   __syncthreads();
 }
 
-template <int T, int MR, int G, int U, int R, bool PAIR>
+// NORM: x is RMSNorm'd in LDS (pr.norm_w) -- a template switch, so the other
+// forms carry none of its set-up.
+template <int T, int MR, int G, int U, int R, bool PAIR, bool NORM = false>
 __global__ __launch_bounds__(kThreads) void qgemv_kernel(
     const uint32_t* __restrict__ w, const typename Elem<T>::S* __restrict__ scales,
     const typename Elem<T>::S* __restrict__ biases, const typename Elem<T>::S* __restrict__ x,
     typename Elem<T>::S* __restrict__ y, int K, int N, int M, int kt, const GvPair pr) {
   static_assert(!PAIR || R == 2, "a gate/up pair is two rows per lane group");
+  static_assert(!NORM || (T != kF32 && MR <= 2), "the x norm: 16-bit T, at most two rows");
   using E = Elem<T>;
   using X = XTile<T>;
   constexpr int P = X::kP;
@@ -246,19 +249,21 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
     //    at the swizzled position; slots past the end load a clamped
     //    duplicate into the padding.
     for (int base = 0; base < xtotal; base += kThreads) {
-      const int sl = min(base + tid, xtotal - 1);
-      const int m = (MR == 1) ? 0 : sl / vpr;
-      const int idx = sl - m * vpr;
-      const int j = idx / P;
-      const int pc = (idx & (P - 1)) ^ X::swz(j);
-      const uint32_t off = (uint32_t)((m * K + k0 + j * 32 + pc * X::kEpp) * E::kBytes);
+      // Unsigned: the slot indices are non-negative, and signed division by
+      // a power of two costs three more instructions.
+      const unsigned sl = (unsigned)min(base + tid, xtotal - 1);
+      const unsigned m = (MR == 1) ? 0u : sl / (unsigned)vpr;
+      const unsigned idx = sl - m * (unsigned)vpr;
+      const int j = (int)(idx / (unsigned)P);
+      const int pc = (int)(idx & (unsigned)(P - 1)) ^ X::swz(j);
+      const uint32_t off = (uint32_t)(((int)m * K + k0 + j * 32 + pc * X::kEpp) * E::kBytes);
       load_lds16(xr, off, 0u, xs + base + wave * 64);
     }
     // The norm weights of this thread's pieces (clamped indices: no branch
     // around the loads), beside the x staging and ahead of the weights.
     float4 nwv[2][2];
-    if constexpr (T != kF32 && MR <= 2) {
-      if (pr.norm_w) {
+    if constexpr (NORM) {
+      {
         const float4* nr = reinterpret_cast<const float4*>(pr.norm_w);
         const int n8 = K >> 3;
 #pragma unroll
@@ -291,10 +296,10 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
     IMQ_WAIT_VMCNT(3 * U * R);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (T != kF32 && MR <= 2) {
+    if constexpr (NORM) {
       // RMSNorm'd x (the host passes a norm weight only when the tile is the
       // whole row); its LDS traffic runs while the weights are in flight.
-      if (pr.norm_w) norm_rows_in_lds<T, MR>(xs, M, K, vpr, nwv, pr.eps);
+      norm_rows_in_lds<T, MR>(xs, M, K, vpr, nwv, pr.eps);
       __builtin_amdgcn_sched_barrier(0);
     }
 
@@ -472,9 +477,19 @@ hipError_t launch_u(const uint32_t* w, const void* s, const void* b, const void*
     if constexpr (MR <= 4 && T != kF32) {
       constexpr int kOutsPerBlock = kWaves * (64 / G);
       const dim3 grid((pr->width + kOutsPerBlock - 1) / kOutsPerBlock);
-      hipLaunchKernelGGL((qgemv_kernel<T, MR, G, U, 2, true>), grid, dim3(kThreads), slots * 16,
-                         stream, w, static_cast<const ST*>(s), static_cast<const ST*>(b),
-                         static_cast<const ST*>(x), static_cast<ST*>(y), k, n, m, kt, *pr);
+      if (pr->norm_w) {
+        if constexpr (MR <= 2)
+          hipLaunchKernelGGL((qgemv_kernel<T, MR, G, U, 2, true, true>), grid, dim3(kThreads),
+                             slots * 16, stream, w, static_cast<const ST*>(s),
+                             static_cast<const ST*>(b), static_cast<const ST*>(x),
+                             static_cast<ST*>(y), k, n, m, kt, *pr);
+        else
+          return hipErrorInvalidValue;
+      } else {
+        hipLaunchKernelGGL((qgemv_kernel<T, MR, G, U, 2, true>), grid, dim3(kThreads), slots * 16,
+                           stream, w, static_cast<const ST*>(s), static_cast<const ST*>(b),
+                           static_cast<const ST*>(x), static_cast<ST*>(y), k, n, m, kt, *pr);
+      }
       return hipGetLastError();
     }
     return hipErrorInvalidValue;
@@ -482,10 +497,20 @@ hipError_t launch_u(const uint32_t* w, const void* s, const void* b, const void*
   constexpr int R = rows_per_lane(MR);
   constexpr int rows_per_block = kWaves * (64 / G) * R;
   const dim3 grid((n + rows_per_block - 1) / rows_per_block);
-  hipLaunchKernelGGL((qgemv_kernel<T, MR, G, U, R, false>), grid, dim3(kThreads), slots * 16,
-                     stream, w, static_cast<const ST*>(s), static_cast<const ST*>(b),
-                     static_cast<const ST*>(x), static_cast<ST*>(y), k, n, m, kt,
-                     pr ? *pr : GvPair{});
+  if (pr && pr->norm_w) {
+    if constexpr (T != kF32 && MR <= 2)
+      hipLaunchKernelGGL((qgemv_kernel<T, MR, G, U, R, false, true>), grid, dim3(kThreads),
+                         slots * 16, stream, w, static_cast<const ST*>(s),
+                         static_cast<const ST*>(b), static_cast<const ST*>(x),
+                         static_cast<ST*>(y), k, n, m, kt, *pr);
+    else
+      return hipErrorInvalidValue;
+  } else {
+    hipLaunchKernelGGL((qgemv_kernel<T, MR, G, U, R, false>), grid, dim3(kThreads), slots * 16,
+                       stream, w, static_cast<const ST*>(s), static_cast<const ST*>(b),
+                       static_cast<const ST*>(x), static_cast<ST*>(y), k, n, m, kt,
+                       pr ? *pr : GvPair{});
+  }
   return hipGetLastError();
 }
 

@@ -72,8 +72,11 @@ def disasm(tmp_path_factory) -> dict[str, list[tuple[int, str, str]]]:
                 .splitlines() if "FUNC" in line and any(k in line for k in KERNELS)]
         if not syms:
             continue
-        text = _run(str(TOOLS["llvm-objdump"]), "-d", f"--disassemble-symbols={','.join(syms)}",
-                    str(co))
+        # In batches: one argument naming every kernel is longer than the OS allows.
+        text = "\n".join(
+            _run(str(TOOLS["llvm-objdump"]), "-d",
+                 f"--disassemble-symbols={','.join(syms[i:i + 100])}", str(co))
+            for i in range(0, len(syms), 100))
         cur = None
         for line in text.splitlines():
             m = re.match(r"^[0-9a-f]+ <(\S+)>:$", line)
