@@ -63,6 +63,20 @@ struct XTile {
   static __device__ __forceinline__ int swz(int j) { return (j >> kSh) & (kP - 1); }
 };
 
+// Byte offset within the tile of row m's chunk j, already XORed with its
+// swizzle: piece v of the chunk is at that offset ^ 16 v.  A chunk's P pieces
+// start at a multiple of 16 P (rows are kl / 32 whole chunks long), so the
+// swizzle of every piece is one XOR of this offset.
+template <int T>
+__device__ __forceinline__ uint32_t x_piece0_t(int m, int M, int vpr, int j, int swz) {
+  return (uint32_t)(min(m, M - 1) * vpr + j * XTile<T>::kP + swz) * 16u;
+}
+
+__device__ __forceinline__ u32x4_t x_piece(const u32x4_t* xs, uint32_t xo, int v) {
+  return *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const char*>(xs) +
+                                           (xo ^ (uint32_t)(16 * v)));
+}
+
 // One scale or bias of T at byte offset voff + soff.
 template <int T>
 __device__ __forceinline__ typename Elem<T>::S load_param(__amdgpu_buffer_rsrc_t rs, uint32_t voff,
@@ -303,6 +317,9 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
       __builtin_amdgcn_sched_barrier(0);
     }
 
+    auto x_piece0 = [](int m, int M_, int vpr_, int j_, int swz_) {
+      return x_piece0_t<T>(m, M_, vpr_, j_, swz_);
+    };
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = min(gl + u * G, tch - 1);
@@ -322,13 +339,13 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
         }
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-          const u32x4_t* xp = xs + min(m, M - 1) * vpr + j * P;
+          const uint32_t xo = x_piece0(m, M, vpr, j, swz);
           float a[R];
 #pragma unroll
           for (int r = 0; r < R; ++r) a[r] = acc[r][m];
 #pragma unroll
           for (int v = 0; v < P; ++v) {
-            const u32x4_t xx = xp[v ^ swz];
+            const u32x4_t xx = x_piece(xs, xo, v);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
               a[r] = __builtin_fmaf(wf[r][4 * v + 0], __uint_as_float(xx.x), a[r]);
@@ -355,13 +372,13 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
         }
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-          const u32x4_t* xp = xs + min(m, M - 1) * vpr + j * P;
+          const uint32_t xo = x_piece0(m, M, vpr, j, swz);
           float a[R];
 #pragma unroll
           for (int r = 0; r < R; ++r) a[r] = acc[r][m];
 #pragma unroll
           for (int v = 0; v < P; ++v) {
-            const u32x4_t xx = xp[v ^ swz];
+            const u32x4_t xx = x_piece(xs, xo, v);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
               if constexpr (T == kBf16) {
