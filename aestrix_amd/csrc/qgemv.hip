@@ -68,7 +68,7 @@ struct XTile {
 // start at a multiple of 16 P (rows are kl / 32 whole chunks long), so the
 // swizzle of every piece is one XOR of this offset.
 template <int T>
-__device__ __forceinline__ uint32_t x_piece0_t(int m, int M, int vpr, int j, int swz) {
+__device__ __forceinline__ uint32_t x_piece0(int m, int M, int vpr, int j, int swz) {
   return (uint32_t)(min(m, M - 1) * vpr + j * XTile<T>::kP + swz) * 16u;
 }
 
@@ -277,15 +277,13 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
     // around the loads), beside the x staging and ahead of the weights.
     float4 nwv[2][2];
     if constexpr (NORM) {
-      {
-        const float4* nr = reinterpret_cast<const float4*>(pr.norm_w);
-        const int n8 = K >> 3;
+      const float4* nr = reinterpret_cast<const float4*>(pr.norm_w);
+      const int n8 = K >> 3;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int e = min(tid + i * kThreads, n8 - 1);
-          nwv[i][0] = nr[2 * e];
-          nwv[i][1] = nr[2 * e + 1];
-        }
+      for (int i = 0; i < 2; ++i) {
+        const int e = min(tid + i * kThreads, n8 - 1);
+        nwv[i][0] = nr[2 * e];
+        nwv[i][1] = nr[2 * e + 1];
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -317,9 +315,6 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
       __builtin_amdgcn_sched_barrier(0);
     }
 
-    auto x_piece0 = [](int m, int M_, int vpr_, int j_, int swz_) {
-      return x_piece0_t<T>(m, M_, vpr_, j_, swz_);
-    };
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = min(gl + u * G, tch - 1);
@@ -339,7 +334,7 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
         }
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-          const uint32_t xo = x_piece0(m, M, vpr, j, swz);
+          const uint32_t xo = x_piece0<T>(m, M, vpr, j, swz);
           float a[R];
 #pragma unroll
           for (int r = 0; r < R; ++r) a[r] = acc[r][m];
@@ -372,7 +367,7 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
         }
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-          const uint32_t xo = x_piece0(m, M, vpr, j, swz);
+          const uint32_t xo = x_piece0<T>(m, M, vpr, j, swz);
           float a[R];
 #pragma unroll
           for (int r = 0; r < R; ++r) a[r] = acc[r][m];
