@@ -97,26 +97,39 @@ __device__ __forceinline__ void dequant_word_f16(uint32_t word, float s24, float
   out[3] = pack_f16x2(__builtin_fmaf(s24, f16_hi(d2), b), __builtin_fmaf(s20, f16_hi(d3), b));
 }
 
+// -0.0f the compiler cannot see: fma(a, b, -0.0f) is a * b exactly (one
+// rounding, the product's own zero sign), and a literal -0.0f addend is
+// simplified into a multiply, which then needs the f16 -> f32 conversion of
+// the code as an instruction of its own; with this addend the fma stays a
+// v_fma_mix_f32 that reads the code's 16-bit half directly.
+__device__ __forceinline__ float opaque_neg_zero() {
+  float z;
+  asm volatile("v_mov_b32 %0, 0x80000000" : "=v"(z));
+  return z;
+}
+
 // The eight codes of a word as f32 weights fl32(fl32(s*q) + b), in k order:
 // two rounded operations, like the reference's `scale * q + bias` on Float.
-// With f32 scales (24-bit significands) s*q is not exact in f32, so an fma
-// would round differently; s24 = s * 2^24 and s20 = s * 2^20 are exact.
+// With f32 scales (24-bit significands) s*q is not exact in f32, so one fma
+// of all three would round differently: the product is rounded by an fma with
+// a -0 addend (nz, from opaque_neg_zero), the sum by an add.  s24 = s * 2^24
+// and s20 = s * 2^20 are exact.
 __device__ __forceinline__ void dequant_word_f32(uint32_t word, float s24, float s20, float b,
-                                                 float out[8]) {
+                                                 float nz, float out[8]) {
 #pragma clang fp contract(off)
   const uint32_t d0 = word & 0x000F000Fu;
   const uint32_t d1 = word & 0x00F000F0u;
   const uint32_t w8 = word >> 8;
   const uint32_t d2 = w8 & 0x000F000Fu;
   const uint32_t d3 = w8 & 0x00F000F0u;
-  out[0] = s24 * f16_lo(d0) + b;
-  out[1] = s20 * f16_lo(d1) + b;
-  out[2] = s24 * f16_lo(d2) + b;
-  out[3] = s20 * f16_lo(d3) + b;
-  out[4] = s24 * f16_hi(d0) + b;
-  out[5] = s20 * f16_hi(d1) + b;
-  out[6] = s24 * f16_hi(d2) + b;
-  out[7] = s20 * f16_hi(d3) + b;
+  out[0] = __builtin_fmaf(s24, f16_lo(d0), nz) + b;
+  out[1] = __builtin_fmaf(s20, f16_lo(d1), nz) + b;
+  out[2] = __builtin_fmaf(s24, f16_lo(d2), nz) + b;
+  out[3] = __builtin_fmaf(s20, f16_lo(d3), nz) + b;
+  out[4] = __builtin_fmaf(s24, f16_hi(d0), nz) + b;
+  out[5] = __builtin_fmaf(s20, f16_hi(d1), nz) + b;
+  out[6] = __builtin_fmaf(s24, f16_hi(d2), nz) + b;
+  out[7] = __builtin_fmaf(s20, f16_hi(d3), nz) + b;
 }
 
 // Element type T of x, scales, biases and y (the values of imq_dtype).

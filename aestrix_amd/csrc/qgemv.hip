@@ -250,6 +250,8 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[r][m] = 0.f;
+  [[maybe_unused]] float nz = 0.f;  // f32 dequant's -0 product addend
+  if constexpr (T == kF32) nz = opaque_neg_zero();
 
   for (int k0 = 0; k0 < K; k0 += kt) {
     const int kl = min(kt, K - k0);  // tile length
@@ -327,10 +329,10 @@ __global__ __launch_bounds__(kThreads) void qgemv_kernel(
         for (int r = 0; r < R; ++r) {
           const float sc = E::param(sv[r][u]);
           const float bi = E::param(bv[r][u]);
-          dequant_word_f32(q[r][u].x, sc * 0x1p24f, sc * 0x1p20f, bi, wf[r] + 0);
-          dequant_word_f32(q[r][u].y, sc * 0x1p24f, sc * 0x1p20f, bi, wf[r] + 8);
-          dequant_word_f32(q[r][u].z, sc * 0x1p24f, sc * 0x1p20f, bi, wf[r] + 16);
-          dequant_word_f32(q[r][u].w, sc * 0x1p24f, sc * 0x1p20f, bi, wf[r] + 24);
+          dequant_word_f32(q[r][u].x, sc * 0x1p24f, sc * 0x1p20f, bi, nz, wf[r] + 0);
+          dequant_word_f32(q[r][u].y, sc * 0x1p24f, sc * 0x1p20f, bi, nz, wf[r] + 8);
+          dequant_word_f32(q[r][u].z, sc * 0x1p24f, sc * 0x1p20f, bi, nz, wf[r] + 16);
+          dequant_word_f32(q[r][u].w, sc * 0x1p24f, sc * 0x1p20f, bi, nz, wf[r] + 24);
         }
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
