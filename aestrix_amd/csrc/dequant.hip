@@ -106,6 +106,58 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint32_t* __res
   }
 }
 
+// The same arithmetic with one quantization group per thread (16-bit T): the
+// group's 8 packed words in two 16-byte loads and its scale and bias in one
+// load each, against twelve loads per 64 output bytes in the per-word form
+// (whose texture path was busy for most of the kernel).  A thread's 128
+// output bytes are staged in LDS (rows padded to 144 bytes: eight consecutive
+// lanes cover all banks, writing or reading) and read back so that each wave
+// store writes 1 KiB contiguous.  Groups past the end load a clamped
+// duplicate and store nothing.
+constexpr int kStageRow = 9;  // 16-byte LDS slots per group: 8 of output + 1 of padding
+
+template <typename Out>
+__global__ __launch_bounds__(kThreads) void dequant_group_kernel(
+    const uint32_t* __restrict__ w, const typename Out::S* __restrict__ scales,
+    const typename Out::S* __restrict__ biases, u32x4_t* __restrict__ out, uint32_t groups) {
+  static_assert(Out::kWordBytes == 16, "16-bit outputs");
+  __shared__ u32x4_t stage[kThreads * kStageRow];
+  const uint32_t g0 = blockIdx.x * (uint32_t)kThreads;
+  const uint32_t g = min(g0 + threadIdx.x, groups - 1);
+  const u32x4_t* wp = reinterpret_cast<const u32x4_t*>(w) + 2 * (size_t)g;
+  const u32x4_t c0 = __builtin_nontemporal_load(wp);
+  const u32x4_t c1 = __builtin_nontemporal_load(wp + 1);
+  const float s = Out::load(scales[g]);
+  const float b = Out::load(biases[g]);
+  const uint32_t words[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  u32x4_t* row = stage + threadIdx.x * kStageRow;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t lo = words[i] & 0x0F0F0F0Fu;
+    const uint32_t hi = (words[i] >> 4) & 0x0F0F0F0Fu;
+    uint32_t o[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const float q0 = (float)((lo >> (8 * p)) & 0xFFu);
+      const float q1 = (float)((hi >> (8 * p)) & 0xFFu);
+      o[p] = Out::pack(affine(s, q0, b), affine(s, q1, b));
+    }
+    row[i] = u32x4_t{o[0], o[1], o[2], o[3]};
+  }
+  __syncthreads();
+  // Wave v's 64 groups are 8 KiB of contiguous output; its store j covers
+  // bytes [1 KiB j, 1 KiB (j + 1)): lane l takes 16 bytes of group 8 j + l / 8.
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int grp = 64 * wv + 8 * j + (lane >> 3);
+    if (g0 + (uint32_t)grp < groups)
+      __builtin_nontemporal_store(stage[grp * kStageRow + (lane & 7)],
+                                  out + (size_t)(g0 + (uint32_t)grp) * 8 + (lane & 7));
+  }
+}
+
 // Rows gathered by index (DirectTEEncoder.embedRow, :106-123, for a batch of
 // token ids): output row r is deq(W[rows[r]]); ids are clamped to [0, n) so a
 // bad id never reads outside W.  One thread per packed word, as above.
@@ -165,9 +217,17 @@ hipError_t launch_out(const uint32_t* w, const void* scales, const void* biases,
     const uint32_t words = (uint32_t)((total - w0 < max_words) ? (total - w0) : max_words);
     const dim3 grid((words + kWordsPerBlock - 1) / kWordsPerBlock);
     u32x4_t* op = reinterpret_cast<u32x4_t*>(out) + w0 * (Out::kWordBytes / 16);
-    hipLaunchKernelGGL(dequant_kernel<Out>, grid, dim3(kThreads), 0, stream, w + w0,
-                       static_cast<const S*>(scales) + w0 / 8, static_cast<const S*>(biases) + w0 / 8,
-                       op, words);
+    if constexpr (Out::kWordBytes == 16) {
+      const uint32_t groups = words / 8;  // rows hold whole groups: K % 64 == 0
+      hipLaunchKernelGGL(dequant_group_kernel<Out>, dim3((groups + kThreads - 1) / kThreads),
+                         dim3(kThreads), 0, stream, w + w0,
+                         static_cast<const S*>(scales) + w0 / 8,
+                         static_cast<const S*>(biases) + w0 / 8, op, groups);
+    } else {
+      hipLaunchKernelGGL(dequant_kernel<Out>, grid, dim3(kThreads), 0, stream, w + w0,
+                         static_cast<const S*>(scales) + w0 / 8,
+                         static_cast<const S*>(biases) + w0 / 8, op, words);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
