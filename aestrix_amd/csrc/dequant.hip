@@ -110,11 +110,12 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint32_t* __res
 // group's 8 packed words in two 16-byte loads and its scale and bias in one
 // load each, against twelve loads per 64 output bytes in the per-word form
 // (whose texture path was busy for most of the kernel).  A thread's 128
-// output bytes are staged in LDS (rows padded to 144 bytes: eight consecutive
-// lanes cover all banks, writing or reading) and read back so that each wave
-// store writes 1 KiB contiguous.  Groups past the end load a clamped
-// duplicate and store nothing.
-constexpr int kStageRow = 9;  // 16-byte LDS slots per group: 8 of output + 1 of padding
+// output bytes are staged in LDS and read back so that each wave store writes
+// 1 KiB contiguous; a group's 16-byte piece i sits in slot i ^ (group % 8) of
+// its row, so neither the writes (16 lanes: 16 rows, one piece each) nor the
+// reads (16 lanes: two rows) meet in a bank.  Groups past the end load a
+// clamped duplicate and store nothing.
+constexpr int kStageRow = 8;  // 16-byte LDS slots per group
 
 template <typename Out>
 __global__ __launch_bounds__(kThreads) void dequant_group_kernel(
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(kThreads) void dequant_group_kernel(
       const float q1 = (float)((hi >> (8 * p)) & 0xFFu);
       o[p] = Out::pack(affine(s, q0, b), affine(s, q1, b));
     }
-    row[i] = u32x4_t{o[0], o[1], o[2], o[3]};
+    row[i ^ (threadIdx.x & 7)] = u32x4_t{o[0], o[1], o[2], o[3]};
   }
   __syncthreads();
   // Wave v's 64 groups are 8 KiB of contiguous output; its store j covers
@@ -153,7 +154,7 @@ __global__ __launch_bounds__(kThreads) void dequant_group_kernel(
   for (int j = 0; j < 8; ++j) {
     const int grp = 64 * wv + 8 * j + (lane >> 3);
     if (g0 + (uint32_t)grp < groups)
-      __builtin_nontemporal_store(stage[grp * kStageRow + (lane & 7)],
+      __builtin_nontemporal_store(stage[grp * kStageRow + ((lane ^ grp) & 7)],
                                   out + (size_t)(g0 + (uint32_t)grp) * 8 + (lane & 7));
   }
 }
