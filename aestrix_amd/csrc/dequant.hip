@@ -114,18 +114,27 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint32_t* __res
 // 1 KiB contiguous; a group's 16-byte piece i sits in slot i ^ (group % 8) of
 // its row, so neither the writes (16 lanes: 16 rows, one piece each) nor the
 // reads (16 lanes: two rows) meet in a bank.  Groups past the end load a
-// clamped duplicate and store nothing.
+// clamped duplicate and store nothing.  GATHER: output group g is group
+// g % gpr of W's row rows[g / gpr] (the rows form below), the id clamped to
+// [0, n) so that a bad id never reads outside W.
 constexpr int kStageRow = 8;  // 16-byte LDS slots per group
 
-template <typename Out>
+template <typename Out, bool GATHER = false>
 __global__ __launch_bounds__(kThreads) void dequant_group_kernel(
     const uint32_t* __restrict__ w, const typename Out::S* __restrict__ scales,
-    const typename Out::S* __restrict__ biases, u32x4_t* __restrict__ out, uint32_t groups) {
+    const typename Out::S* __restrict__ biases, u32x4_t* __restrict__ out, uint32_t groups,
+    const int32_t* __restrict__ rows = nullptr, uint32_t gpr = 0, int n = 0) {
   static_assert(Out::kWordBytes == 16, "16-bit outputs");
   __shared__ u32x4_t stage[kThreads * kStageRow];
   const uint32_t g0 = blockIdx.x * (uint32_t)kThreads;
-  const uint32_t g = min(g0 + threadIdx.x, groups - 1);
-  const u32x4_t* wp = reinterpret_cast<const u32x4_t*>(w) + 2 * (size_t)g;
+  const uint32_t go = min(g0 + threadIdx.x, groups - 1);
+  size_t g = go;  // the source group
+  if constexpr (GATHER) {
+    const uint32_t r = go / gpr;
+    const int id = min(max(rows[r], 0), n - 1);
+    g = (size_t)id * gpr + (go - r * gpr);
+  }
+  const u32x4_t* wp = reinterpret_cast<const u32x4_t*>(w) + 2 * g;
   const u32x4_t c0 = __builtin_nontemporal_load(wp);
   const u32x4_t c1 = __builtin_nontemporal_load(wp + 1);
   const float s = Out::load(scales[g]);
@@ -202,6 +211,18 @@ hipError_t launch_rows_out(const uint32_t* w, const void* scales, const void* bi
                            hipStream_t stream) {
   using S = typename Out::S;
   const uint32_t wpr = (uint32_t)(k / 8), total = (uint32_t)count * wpr;
+  // The grouped kernel loads 16 bytes of codes at a time: W 16-byte aligned
+  // (the entry point asks only for 4).
+  if constexpr (Out::kWordBytes == 16) {
+    if (((uintptr_t)w & 15u) == 0) {
+      const uint32_t gpr = wpr / 8, groups = (uint32_t)count * gpr;  // K % 64 == 0
+      hipLaunchKernelGGL((dequant_group_kernel<Out, true>),
+                         dim3((groups + kThreads - 1) / kThreads), dim3(kThreads), 0, stream, w,
+                         static_cast<const S*>(scales), static_cast<const S*>(biases),
+                         static_cast<u32x4_t*>(out), groups, rows, gpr, n);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL(dequant_rows_kernel<Out>, dim3((total + kThreads - 1) / kThreads),
                      dim3(kThreads), 0, stream, w, static_cast<const S*>(scales),
                      static_cast<const S*>(biases), rows, static_cast<u32x4_t*>(out), total, wpr, n);
